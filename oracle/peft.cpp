@@ -1,0 +1,243 @@
+// ORACLE — test infrastructure only. CPU restatement of HOS's LoRA PEFT model and
+// training step:
+//   t_const (frozen base, transposed f32 [in,out])   src/peft.rs:24-33
+//   PeftModel::build_multi (LoRA branch)              src/peft.rs:134-231
+//   PeftModel::loss_g / forward                       src/peft.rs:447-604
+//   cmd_peft step loop (zero_grad, accumulate, AdamW) src/main.rs:2583-2601
+//   train_minibatch                                   src/train.rs:33-52
+// Extensions the benchmark configs need, each reducing exactly to the reference when
+// switched to the reference's setting:
+//   * LoRA targets beyond q/v (k, o, gate, up, down), applied as `y += (x·A·B)·(α/r)`
+//     right after the base projection, in the order q, k, v (then biases), o, gate, up, down;
+//     targets = q|v reproduces src/peft.rs:508-512 exactly.
+//   * LoRA A/B supplied by the caller (the reference draws A with Tensor::randn,
+//     src/tensor.rs:241-256, and B = 0; randn_uniform restates that draw).
+#include <map>
+#include <string>
+
+#include "autograd.hpp"
+#include "oracle.h"
+
+namespace orc {
+
+struct Lora {
+  Tensor A, B;  // A [in, r], B [r, out]
+};
+
+struct BaseLayer {
+  Tensor attn_norm, wq, wk, wv, wo, bq, bk, bv, ffn_norm, w_gate, w_up, w_down;
+  Lora lora[7];  // q k v o gate up down
+};
+
+struct Model {
+  orc_cfg c;
+  Tensor tok_embd, out_norm, out;
+  std::vector<BaseLayer> layers;
+  std::unique_ptr<AdamW> opt;
+  float lora_scale() const { return c.lora_alpha / (float)c.lora_rank; }
+
+  std::vector<Tensor> params() const {
+    // LoRA factors per layer, in target order (src/peft.rs:295-302 lists aq,bq,av,bv).
+    std::vector<Tensor> p;
+    for (auto& l : layers)
+      for (int t = 0; t < 7; t++)
+        if (l.lora[t].A) {
+          p.push_back(l.lora[t].A);
+          p.push_back(l.lora[t].B);
+        }
+    return p;
+  }
+};
+
+static const int kTargetBits[7] = {ORC_T_Q, ORC_T_K, ORC_T_V, ORC_T_O, ORC_T_GATE, ORC_T_UP, ORC_T_DOWN};
+
+void target_dims(const orc_cfg& c, int t, size_t* in, size_t* out) {
+  size_t d = c.dim, qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim, f = c.ffn_dim;
+  switch (t) {
+    case 0: *in = d; *out = qd; break;
+    case 1: *in = d; *out = kvd; break;
+    case 2: *in = d; *out = kvd; break;
+    case 3: *in = qd; *out = d; break;
+    case 4: *in = d; *out = f; break;
+    case 5: *in = d; *out = f; break;
+    default: *in = f; *out = d; break;
+  }
+}
+
+Model* model_create(const orc_cfg* cfg) {
+  auto* m = new Model();
+  m->c = *cfg;
+  m->layers.resize(cfg->n_layers);
+  size_t r = cfg->lora_rank;
+  for (auto& l : m->layers)
+    for (int t = 0; t < 7; t++)
+      if (cfg->lora_targets & kTargetBits[t]) {
+        size_t in, out;
+        target_dims(*cfg, t, &in, &out);
+        l.lora[t].A = param(std::vector<float>(in * r, 0.0f), {in, r});
+        l.lora[t].B = param(std::vector<float>(r * out, 0.0f), {r, out});
+      }
+  return m;
+}
+
+// t_const, src/peft.rs:24-33: W [out,in] row-major (GGUF) -> constant [in,out].
+static Tensor t_const(const std::vector<float>& d, size_t out, size_t inn) {
+  std::vector<float> t(out * inn);
+  for (size_t o = 0; o < out; o++)
+    for (size_t i = 0; i < inn; i++) t[i * out + o] = d[o * inn + i];
+  return constant(std::move(t), {inn, out});
+}
+
+// Tensor names follow GGUF (src/model.rs:760-880). Bytes are dequantized with the
+// restated dequant_into, as Weight::to_f32 does (src/model.rs:251-273).
+int model_set_tensor(Model* m, const std::string& name, const uint8_t* bytes, uint32_t type, size_t rows, size_t cols) {
+  std::vector<float> f(rows * cols);
+  int rc = dequant_into(bytes, type, rows * cols, f.data());
+  if (rc) return rc;
+  const orc_cfg& c = m->c;
+  if (name == "token_embd.weight") {
+    m->tok_embd = constant(f, {rows, cols});
+    if (!m->out) m->out = t_const(f, rows, cols);  // tied head until output.weight arrives
+    return 0;
+  }
+  if (name == "output.weight") { m->out = t_const(f, rows, cols); return 0; }
+  if (name == "output_norm.weight") { m->out_norm = constant(f, {rows * cols}); return 0; }
+  if (name.rfind("blk.", 0) != 0) return ORC_E_INVALID;
+  size_t dot = name.find('.', 4);
+  int li = std::stoi(name.substr(4, dot - 4));
+  if (li < 0 || li >= c.n_layers) return ORC_E_INVALID;
+  std::string leaf = name.substr(dot + 1);
+  BaseLayer& l = m->layers[li];
+  if (leaf == "attn_norm.weight") l.attn_norm = constant(f, {rows * cols});
+  else if (leaf == "ffn_norm.weight") l.ffn_norm = constant(f, {rows * cols});
+  else if (leaf == "attn_q.weight") l.wq = t_const(f, rows, cols);
+  else if (leaf == "attn_k.weight") l.wk = t_const(f, rows, cols);
+  else if (leaf == "attn_v.weight") l.wv = t_const(f, rows, cols);
+  else if (leaf == "attn_output.weight") l.wo = t_const(f, rows, cols);
+  else if (leaf == "ffn_gate.weight") l.w_gate = t_const(f, rows, cols);
+  else if (leaf == "ffn_up.weight") l.w_up = t_const(f, rows, cols);
+  else if (leaf == "ffn_down.weight") l.w_down = t_const(f, rows, cols);
+  else if (leaf == "attn_q.bias") l.bq = constant(f, {rows * cols});
+  else if (leaf == "attn_k.bias") l.bk = constant(f, {rows * cols});
+  else if (leaf == "attn_v.bias") l.bv = constant(f, {rows * cols});
+  else return ORC_E_INVALID;
+  return 0;
+}
+
+static Tensor lora_apply(const Model* m, const Lora& lo, const Tensor& y, const Tensor& x) {
+  if (!lo.A) return y;
+  return add(y, scale(matmul(matmul(x, lo.A), lo.B), m->lora_scale()));
+}
+
+// PeftModel::forward (LoRA path), src/peft.rs:474-604.
+Tensor model_forward(const Model* m, const std::vector<size_t>& ids) {
+  const orc_cfg& c = m->c;
+  size_t t = ids.size(), hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv_heads;
+  size_t qd = nh * hd, group = nh / nkv;
+  float sc = 1.0f / std::sqrt((float)hd);
+  std::vector<size_t> pos(t);
+  for (size_t i = 0; i < t; i++) pos[i] = i;
+  std::vector<float> mk(nh * t * t, 0.0f);
+  for (size_t h = 0; h < nh; h++)
+    for (size_t i = 0; i < t; i++)
+      for (size_t j = i + 1; j < t; j++) mk[(h * t + i) * t + j] = -1e9f;
+  Tensor mask = constant(std::move(mk), {nh * t, t});
+
+  Tensor x = embedding(m->tok_embd, ids);
+  for (const BaseLayer& bl : m->layers) {
+    Tensor xn = rmsnorm_eps(x, bl.attn_norm, c.rms_eps);
+    Tensor q = matmul(xn, bl.wq);
+    Tensor k = matmul(xn, bl.wk);
+    Tensor v = matmul(xn, bl.wv);
+    q = lora_apply(m, bl.lora[0], q, xn);
+    k = lora_apply(m, bl.lora[1], k, xn);
+    v = lora_apply(m, bl.lora[2], v, xn);
+    if (bl.bq) q = add(q, bl.bq);
+    if (bl.bk) k = add(k, bl.bk);
+    if (bl.bv) v = add(v, bl.bv);
+    q = rope(q, nh, hd, c.rope_base, c.rope_neox != 0, pos);
+    k = rope(k, nkv, hd, c.rope_base, c.rope_neox != 0, pos);
+    Tensor qh = reshape(transpose12_4d(reshape(q, {1, t, nh, hd})), {nh, t, hd});
+    Tensor kh = reshape(transpose12_4d(reshape(k, {1, t, nkv, hd})), {nkv, t, hd});
+    Tensor vh = reshape(transpose12_4d(reshape(v, {1, t, nkv, hd})), {nkv, t, hd});
+    kh = repeat_interleave_dim0(kh, group);
+    vh = repeat_interleave_dim0(vh, group);
+    Tensor scores = scale(bmm(qh, transpose_last2(kh)), sc);
+    Tensor att = reshape(softmax_rows(add(reshape(scores, {nh * t, t}), mask)), {nh, t, t});
+    Tensor ctx = reshape(transpose12_4d(reshape(bmm(att, vh), {1, nh, t, hd})), {t, qd});
+    Tensor o = lora_apply(m, bl.lora[3], matmul(ctx, bl.wo), ctx);
+    x = add(x, o);
+    Tensor xn2 = rmsnorm_eps(x, bl.ffn_norm, c.rms_eps);
+    Tensor gt = lora_apply(m, bl.lora[4], matmul(xn2, bl.w_gate), xn2);
+    Tensor up = lora_apply(m, bl.lora[5], matmul(xn2, bl.w_up), xn2);
+    Tensor hmid = mul(silu(gt), up);
+    Tensor dn = lora_apply(m, bl.lora[6], matmul(hmid, bl.w_down), hmid);
+    x = add(x, dn);
+  }
+  return matmul(rmsnorm_eps(x, m->out_norm, c.rms_eps), m->out);
+}
+
+// One optimizer-step's gradient: zero_grad, then for each of the B sequences
+// loss(seq)·(1/B) backward, summing the scaled losses (src/main.rs:2583-2596).
+float model_loss_grad(Model* m, const int32_t* ids, const int32_t* tgts, int B, int T) {
+  for (auto& p : m->params()) zero_grad(p);
+  float mean_loss = 0.0f;
+  for (int b = 0; b < B; b++) {
+    std::vector<size_t> id(T), tg(T);
+    for (int i = 0; i < T; i++) {
+      id[i] = (size_t)ids[b * T + i];
+      tg[i] = (size_t)tgts[b * T + i];
+    }
+    Tensor loss = scale(cross_entropy(model_forward(m, id), tg), 1.0f / (float)B);
+    backward(loss);
+    mean_loss += loss->data[0];
+  }
+  return mean_loss;
+}
+
+// AdamW::step over the LoRA params; decay = (ndim == 2), src/main.rs:2571 (all LoRA
+// factors are 2-D). The optimizer is created on first use with (lr, wd), as cmd_peft
+// builds it once before the loop (src/main.rs:2581).
+void model_adamw(Model* m, float lr, float wd) {
+  auto ps = m->params();
+  if (!m->opt) m->opt.reset(new AdamW(ps, lr, wd));
+  m->opt->lr = lr;
+  m->opt->wd = wd;
+  std::vector<bool> decay(ps.size());
+  for (size_t i = 0; i < ps.size(); i++) decay[i] = ps[i]->shape.size() == 2;
+  m->opt->step(ps, decay);
+}
+
+}  // namespace orc
+
+// ---- LoRA factor access for the extern "C" surface ----
+extern "C" {
+void orc_model_destroy(void* mh) { delete (orc::Model*)mh; }
+int orc_model_set_lora(void* mh, int layer, int target, const float* A, const float* B) {
+  auto* m = (orc::Model*)mh;
+  if (layer < 0 || layer >= m->c.n_layers || target < 0 || target > 6) return ORC_E_INVALID;
+  auto& lo = m->layers[layer].lora[target];
+  if (!lo.A) return ORC_E_INVALID;
+  std::memcpy(lo.A->data.data(), A, lo.A->data.size() * 4);
+  std::memcpy(lo.B->data.data(), B, lo.B->data.size() * 4);
+  return 0;
+}
+int orc_model_get_lora(void* mh, int layer, int target, float* A, float* B) {
+  auto* m = (orc::Model*)mh;
+  if (layer < 0 || layer >= m->c.n_layers || target < 0 || target > 6) return ORC_E_INVALID;
+  auto& lo = m->layers[layer].lora[target];
+  if (!lo.A) return ORC_E_INVALID;
+  if (A) std::memcpy(A, lo.A->data.data(), lo.A->data.size() * 4);
+  if (B) std::memcpy(B, lo.B->data.data(), lo.B->data.size() * 4);
+  return 0;
+}
+int orc_model_get_lora_grad(void* mh, int layer, int target, float* dA, float* dB) {
+  auto* m = (orc::Model*)mh;
+  if (layer < 0 || layer >= m->c.n_layers || target < 0 || target > 6) return ORC_E_INVALID;
+  auto& lo = m->layers[layer].lora[target];
+  if (!lo.A) return ORC_E_INVALID;
+  if (dA) std::memcpy(dA, lo.A->grad.data(), lo.A->grad.size() * 4);
+  if (dB) std::memcpy(dB, lo.B->grad.data(), lo.B->grad.size() * 4);
+  return 0;
+}
+}
