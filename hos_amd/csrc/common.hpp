@@ -1,0 +1,60 @@
+// Shared definitions for the MI355X (gfx950) LoRA fine-tune backend.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/hos_hip.h"
+
+namespace hos {
+
+typedef _Float16 half_t;
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Host-side error carrying a HOS_E_* status code across the C ABI.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define HOS_HIP_CHECK(expr)                                                                     \
+  do {                                                                                          \
+    hipError_t e_ = (expr);                                                                     \
+    if (e_ != hipSuccess)                                                                       \
+      throw ::hos::Error(HOS_E_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));      \
+  } while (0)
+
+#define HOS_REQUIRE(cond, code, msg)                \
+  do {                                              \
+    if (!(cond)) throw ::hos::Error((code), (msg)); \
+  } while (0)
+
+inline int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// Device-resident repacked quantized weight (see quant.hip). rows = N (out), cols = K (in).
+//   Q8_0: q = int8 [N][K],     s = f32 d              per (row, 32 cols)
+//   Q4_K: q = u8   [N][K/2]    (col 2i low nibble, 2i+1 high), s = f32 {d·sc, dmin·m} per (row, 32)
+//   Q6_K: q = int8 [N][K],     s = f32 d·sc           per (row, 16 cols)
+struct QWeight {
+  uint32_t type = 0;
+  int64_t rows = 0, cols = 0;
+  void* q = nullptr;
+  float* s = nullptr;
+  size_t q_bytes = 0, s_bytes = 0;
+};
+
+// An fp16 GEMM operand with an exact power-of-two scale per row:
+//   data[m][k] = fp16(x[m][k] · 2^e[m]),  rinv[m] = 2^-e[m].
+struct H16 {
+  half_t* data;
+  float* rinv;
+};
+
+}  // namespace hos

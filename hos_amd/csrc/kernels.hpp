@@ -1,0 +1,70 @@
+// Kernel-facing declarations shared by the .hip translation units.
+#pragma once
+#include "common.hpp"
+
+namespace hos {
+
+enum : uint32_t { GGUF_F32 = 0, GGUF_Q8_0 = 8, GGUF_Q4_K = 12, GGUF_Q6_K = 14 };
+
+// Plain-old-data view of a QWeight passed to kernels by value.
+struct QWeightView {
+  uint32_t type;
+  long long rows, cols;
+  const void* q;
+  const float* s;
+};
+inline QWeightView view(const QWeight& w) { return QWeightView{w.type, w.rows, w.cols, w.q, w.s}; }
+
+// One dequantized element, bit-identical to Gguf::dequant_into (src/gguf.rs):
+//   Q8_0  q·d                 (:354-367)
+//   Q4_K  (d·sc)·q − dmin·m   (:385-413; d·sc and dmin·m are precomputed in f32 at repack)
+//   Q6_K  (d·sc)·q            (:449-477)
+__device__ __forceinline__ float deq_q8(int8_t q, float d) { return __fmul_rn((float)q, d); }
+__device__ __forceinline__ float deq_q4k(uint32_t q, float2 dm) {
+  return __fsub_rn(__fmul_rn(dm.x, (float)q), dm.y);
+}
+__device__ __forceinline__ float deq_q6k(int8_t q, float s) { return __fmul_rn(s, (float)q); }
+
+__device__ __forceinline__ float deq_one(const QWeightView& w, long long r, long long c) {
+  long long i = r * w.cols + c;
+  if (w.type == GGUF_Q8_0) return deq_q8(((const int8_t*)w.q)[i], w.s[i >> 5]);
+  if (w.type == GGUF_Q4_K) {
+    uint8_t b = ((const uint8_t*)w.q)[i >> 1];
+    uint32_t q = (i & 1) ? (b >> 4) : (b & 15u);
+    return deq_q4k(q, ((const float2*)w.s)[i >> 5]);
+  }
+  return deq_q6k(((const int8_t*)w.q)[i], w.s[i >> 4]);
+}
+
+// ---- quant.hip ----
+size_t gguf_bytes_for(uint32_t t, size_t n);
+size_t block_elems(uint32_t t);
+void qweight_sizes(uint32_t type, long long rows, long long cols, size_t* q_bytes, size_t* s_bytes);
+void repack_weight(const uint8_t* src_dev, QWeight& w, hipStream_t st);
+void launch_dequant(const QWeight& w, float* out_dev, hipStream_t st);
+void launch_quantize(const float* x_dev, size_t n, uint32_t type, uint8_t* out_dev, hipStream_t st);
+
+// ---- qgemm.hip ----
+// Epilogue of the fp16 GEMMs: out[m][n] = (beta ? out[m][n] : 0) + rinv[m]·acc[m][n] (+ bias[n]).
+struct GemmEpi {
+  float* out;
+  long long ldo;
+  const float* bias;  // may be null
+  int accumulate;     // 1: out += result
+};
+// Y[M, W.rows] = A[M, W.cols] · deq(W)ᵀ, A an fp16 row-scaled operand with row stride lda.
+void launch_qgemm_fwd(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
+                      hipStream_t st);
+// dX[M, W.cols] = dY[M, W.rows] · deq(W), dY an fp16 row-scaled operand with row stride lda.
+void launch_qgemm_dx(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
+                     hipStream_t st);
+// f32 [M, K] (row stride ldx) -> fp16 row-scaled operand (row stride K).
+void launch_to_h16(const float* x, long long ldx, long long M, long long K, H16 out, hipStream_t st);
+
+// ---- gemm_f32.hip ----
+// C[M,N] = alpha·Σ_k A(m,k)·B(k,n) + beta·C, A(m,k) = A[m·sam + k·sak], B(k,n) = B[k·sbk + n·sbn].
+void launch_gemm_f32(long long M, long long N, long long K, float alpha, const float* A, long long sam,
+                     long long sak, const float* B, long long sbk, long long sbn, float beta, float* C, long long ldc,
+                     float* ws, size_t ws_bytes, hipStream_t st);
+
+}  // namespace hos

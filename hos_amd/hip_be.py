@@ -1,0 +1,149 @@
+"""Python mirror of the reference's GPU boundary (the Rust `Gpu` method set, src/metal_be_stub.rs:35-208)
+over the C ABI of libhos_hip.so.
+
+Method names, argument order and meaning follow the Rust surface: ``matmul_f32_keyed(a, m, k, b, n, b_key)``
+returns ``C = A·B``; ``matmul_abt_keyed(a, m, n, b, k, b_key)`` returns ``A·Bᵀ``; ``matmul_atb_keyed(a, k, m, b,
+n, a_key)`` returns ``Aᵀ·B``; ``b_key=None`` means "no caching". Where the reference panics, this raises
+``HosError`` carrying the C status code.
+"""
+import ctypes
+
+import numpy as np
+
+from ._lib import lib
+
+GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 8, 12, 14
+BLOCK = {GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
+
+STATUS = {1: "Io", 2: "Format", 3: "MissingTensor", 4: "UnsupportedQuant", 5: "UnsupportedArch",
+          6: "MissingMeta", 7: "Spec", 8: "Device", 9: "Invalid", 10: "OutOfMemory"}
+
+
+class HosError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"[{STATUS.get(code, code)}] {msg}")
+        self.code = code
+
+
+def _p(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def bytes_for(ggml_type, n):
+    """bytes_for (src/gguf.rs:548-561); 0 for unsupported types."""
+    return lib().hos_hip_bytes_for(ggml_type, n)
+
+
+class Gpu:
+    """One device context (Gpu::new). Not thread-safe, like the reference's thread-local Gpu."""
+
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        rc = lib().hos_hip_create(device, ctypes.byref(h))
+        if rc:
+            raise HosError(rc, f"hos_hip_create(device={device}) failed (no usable HIP device?)")
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().hos_hip_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def _chk(self, rc):
+        if rc:
+            raise HosError(rc, lib().hos_hip_last_error(self.h).decode())
+
+    def arch(self):
+        buf = ctypes.create_string_buffer(64)
+        self._chk(lib().hos_hip_device_arch(self.h, buf, 64))
+        return buf.value.decode()
+
+    def synchronize(self):
+        self._chk(lib().hos_hip_synchronize(self.h))
+
+    # ---- keyed f32 GEMMs (src/metal_be.rs:2338-2366, 2434-2446) ----
+    def matmul_f32_keyed(self, a, m, k, b, n, b_key=None):
+        a, b = _f32(a), _f32(b)
+        out = np.empty((m, n), np.float32)
+        self._chk(lib().hos_hip_matmul_f32_keyed(self.h, _p(a), m, k, _p(b), n, b_key or 0, _p(out)))
+        return out
+
+    def matmul_abt_keyed(self, a, m, n, b, k, b_key=None):
+        a, b = _f32(a), _f32(b)
+        out = np.empty((m, k), np.float32)
+        self._chk(lib().hos_hip_matmul_abt_keyed(self.h, _p(a), m, n, _p(b), k, b_key or 0, _p(out)))
+        return out
+
+    def matmul_atb_keyed(self, a, k, m, b, n, a_key=None):
+        a, b = _f32(a), _f32(b)
+        out = np.empty((k, n), np.float32)
+        self._chk(lib().hos_hip_matmul_atb_keyed(self.h, _p(a), k, m, _p(b), n, a_key or 0, _p(out)))
+        return out
+
+    def evict(self, key):
+        self._chk(lib().hos_hip_evict(self.h, key))
+
+    def clear_cache(self):
+        self._chk(lib().hos_hip_clear_cache(self.h))
+
+    # ---- quantized frozen weights ----
+    def upload_quant(self, key, raw, ggml_type, rows, cols):
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        self._chk(lib().hos_hip_upload_quant(self.h, key, _p(raw), raw.size, ggml_type, rows, cols))
+        return (key, ggml_type, rows, cols)
+
+    def dequant(self, key, rows, cols):
+        out = np.empty((rows, cols), np.float32)
+        self._chk(lib().hos_hip_dequant(self.h, key, _p(out)))
+        return out
+
+    def qgemm_fwd(self, key, x, rows):
+        """Y = X·deq(W)ᵀ for an uploaded W [rows, cols]; x: [t, cols]."""
+        x = _f32(x)
+        out = np.empty((x.shape[0], rows), np.float32)
+        self._chk(lib().hos_hip_qgemm_fwd(self.h, key, _p(x), x.shape[0], _p(out)))
+        return out
+
+    def qgemm_dx(self, key, dy, cols):
+        """dX = dY·deq(W) for an uploaded W [rows, cols]; dy: [t, rows]."""
+        dy = _f32(dy)
+        out = np.empty((dy.shape[0], cols), np.float32)
+        self._chk(lib().hos_hip_qgemm_dx(self.h, key, _p(dy), dy.shape[0], _p(out)))
+        return out
+
+    def quantize(self, x, ggml_type):
+        """quantize(x, type) of src/gguf_write.rs:41-50, on the device."""
+        x = _f32(x).ravel()
+        out = np.empty(bytes_for(ggml_type, x.size), np.uint8)
+        self._chk(lib().hos_hip_quantize(self.h, _p(x), x.size, ggml_type, _p(out)))
+        return out
+
+    # ---- device memory ----
+    def alloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self._chk(lib().hos_hip_dev_alloc(self.h, nbytes, ctypes.byref(p)))
+        return p
+
+    def free(self, p):
+        self._chk(lib().hos_hip_dev_free(self.h, p))
+
+    def h2d(self, dst, arr):
+        arr = np.ascontiguousarray(arr)
+        self._chk(lib().hos_hip_h2d(self.h, dst, _p(arr), arr.nbytes))
+
+    def d2h(self, src, shape, dtype):
+        out = np.empty(shape, dtype)
+        self._chk(lib().hos_hip_d2h(self.h, _p(out), src, out.nbytes))
+        return out
+
+    def time_qgemm(self, which, key, in_dev, t, out_dev, iters):
+        ms = ctypes.c_float()
+        self._chk(lib().hos_hip_time_qgemm(self.h, which, key, in_dev, t, out_dev, iters, ctypes.byref(ms)))
+        return ms.value

@@ -1,0 +1,171 @@
+/*
+ * hos_hip.h — C ABI of the MI355X (gfx950) backend for HOS's LoRA fine-tuning path.
+ *
+ * The reference reaches its GPU through the Rust `Gpu` method set that src/tensor.rs
+ * calls (src/metal_be_stub.rs:35-208, implemented by src/metal_be.rs). This header is
+ * the same surface as a plain C ABI (plain pointers and sizes, no torch types), plus
+ * the quantized-weight GEMMs and the device-resident LoRA training step that the
+ * reference runs on the CPU (src/peft.rs, src/tensor.rs, src/main.rs:2583-2601).
+ *
+ * Conventions
+ *  - Every entry point returns an int status: HOS_OK (0) or an HOS_E_* code; the
+ *    message is in hos_hip_last_error(ctx). Codes 1-7 mirror HosError
+ *    (src/error.rs:12-27); the reference panics at this boundary instead, and the
+ *    Rust shim (hip_be.rs) turns a non-zero status back into a panic.
+ *  - Host pointers are caller-owned and only read/written during the call. Device
+ *    memory is owned by the library (keyed caches, the training model) or by the
+ *    caller when it comes from hos_hip_dev_alloc.
+ *  - A context is bound to one device and one thread, like the reference's
+ *    thread-local Gpu (src/tensor.rs:30-32). Calls are synchronous unless the name
+ *    ends in _dev / _async (those enqueue on the context's stream).
+ *  - ggml_type values are GGUF ids (src/gguf.rs:22-30): 0 F32, 8 Q8_0, 12 Q4_K, 14 Q6_K.
+ */
+#ifndef HOS_HIP_H
+#define HOS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  HOS_OK = 0,
+  HOS_E_IO = 1,                /* HosError::Io */
+  HOS_E_FORMAT = 2,            /* HosError::Format */
+  HOS_E_MISSING_TENSOR = 3,    /* HosError::MissingTensor */
+  HOS_E_UNSUPPORTED_QUANT = 4, /* HosError::UnsupportedQuant */
+  HOS_E_UNSUPPORTED_ARCH = 5,  /* HosError::UnsupportedArch */
+  HOS_E_MISSING_META = 6,      /* HosError::MissingMeta */
+  HOS_E_SPEC = 7,              /* HosError::Spec */
+  HOS_E_DEVICE = 8,            /* HIP runtime failure */
+  HOS_E_INVALID = 9,           /* bad argument: null pointer, shape, unknown key */
+  HOS_E_OOM = 10               /* device allocation failed */
+};
+
+typedef struct hos_ctx hos_ctx;
+
+/* ---- context: Gpu::new (src/metal_be_stub.rs:36-38, src/metal_be.rs:1942-1954) ---- */
+int hos_hip_create(int device, hos_ctx** out);
+void hos_hip_destroy(hos_ctx* ctx);
+const char* hos_hip_last_error(const hos_ctx* ctx);
+int hos_hip_synchronize(hos_ctx* ctx);
+/* gfx arch name of the context's device, e.g. "gfx950". */
+int hos_hip_device_arch(hos_ctx* ctx, char* buf, size_t len);
+
+/* ---- keyed f32 GEMMs: the training matmuls of src/tensor.rs:53-97 ----
+ * matmul_f32_keyed  C[m,n] = A[m,k]·B[k,n]          src/metal_be_stub.rs:108-118, metal_be.rs:2434-2446
+ * matmul_abt_keyed  C[m,k] = A[m,n]·B[k,n]ᵀ         src/metal_be_stub.rs:119-129, metal_be.rs:2338-2351
+ * matmul_atb_keyed  C[k,n] = A[m,k]ᵀ·B[m,n]         src/metal_be_stub.rs:130-140, metal_be.rs:2353-2366
+ * key != 0 caches that operand on the device under the key (a frozen weight), like
+ * buf_keyed (src/metal_be.rs:2322-2334); key == 0 means "no caching" (None). */
+int hos_hip_matmul_f32_keyed(hos_ctx* ctx, const float* a, size_t m, size_t k, const float* b, size_t n,
+                             uint64_t b_key, float* out);
+int hos_hip_matmul_abt_keyed(hos_ctx* ctx, const float* a, size_t m, size_t n, const float* b, size_t k,
+                             uint64_t b_key, float* out);
+int hos_hip_matmul_atb_keyed(hos_ctx* ctx, const float* a, size_t k, size_t m, const float* b, size_t n,
+                             uint64_t a_key, float* out);
+/* Gpu::evict / Gpu::clear_cache (src/metal_be.rs:2416-2428). Evicting an absent key is a no-op. */
+int hos_hip_evict(hos_ctx* ctx, uint64_t key);
+int hos_hip_clear_cache(hos_ctx* ctx);
+
+/* ---- quantized frozen weights ----
+ * upload_quant: Gpu::upload_quant (src/metal_be_stub.rs:45-53). `bytes` is one GGUF
+ * tensor [rows, cols] row-major (cols % block == 0). Repacked once on the device. */
+int hos_hip_upload_quant(hos_ctx* ctx, uint64_t key, const uint8_t* bytes, size_t nbytes, uint32_t ggml_type,
+                         size_t rows, size_t cols);
+/* Bit-exact Gguf::dequant_into (src/gguf.rs:330-505) of an uploaded weight, computed by the
+ * same device function the GEMMs use. out: rows·cols floats (host). */
+int hos_hip_dequant(hos_ctx* ctx, uint64_t key, float* out);
+/* Y[t, rows] = X[t, cols]·deq(W)ᵀ — the frozen-base forward x·t_const(W) (src/peft.rs:24-33,
+ * src/tensor.rs:316-327). Host pointers. */
+int hos_hip_qgemm_fwd(hos_ctx* ctx, uint64_t key, const float* x, size_t t, float* y);
+/* dX[t, cols] = dY[t, rows]·deq(W) — the frozen-base backward dA = g·Bᵀ (src/tensor.rs:347-360). */
+int hos_hip_qgemm_dx(hos_ctx* ctx, uint64_t key, const float* dy, size_t t, float* dx);
+/* Device-pointer variants (no host copies; enqueue + return). */
+int hos_hip_qgemm_fwd_dev(hos_ctx* ctx, uint64_t key, const float* x_dev, size_t t, float* y_dev);
+int hos_hip_qgemm_dx_dev(hos_ctx* ctx, uint64_t key, const float* dy_dev, size_t t, float* dx_dev);
+/* Time `iters` launches of the fp16-MFMA GEMM kernel alone (which: 0 fwd, 1 dx) on an input
+ * already converted to the fp16 row-scaled operand, with HIP events on the context stream.
+ * Returns the mean kernel time in ms. */
+int hos_hip_time_qgemm(hos_ctx* ctx, int which, uint64_t key, const float* in_dev, size_t t, float* out_dev,
+                       int iters, float* avg_ms);
+/* quantize(x, ggml_type) of src/gguf_write.rs:41-50 (Q8_0 :178-196, Q4_K :355-416,
+ * Q6_K :426-495), run on the device; byte-identical to the reference encoders.
+ * x: n floats (host), out: bytes_for(type, n) bytes (host). */
+int hos_hip_quantize(hos_ctx* ctx, const float* x, size_t n, uint32_t ggml_type, uint8_t* out);
+/* bytes_for (src/gguf.rs:548-561); 0 for an unsupported type. */
+size_t hos_hip_bytes_for(uint32_t ggml_type, size_t n);
+
+/* ---- device memory (GpuBuf / download_buf analogue, src/metal_be_stub.rs:13-20) ---- */
+int hos_hip_dev_alloc(hos_ctx* ctx, size_t nbytes, void** dptr);
+int hos_hip_dev_free(hos_ctx* ctx, void* dptr);
+int hos_hip_h2d(hos_ctx* ctx, void* dst_dev, const void* src_host, size_t nbytes);
+int hos_hip_d2h(hos_ctx* ctx, void* dst_host, const void* src_dev, size_t nbytes);
+
+/* ---- the LoRA training model: PeftModel (src/peft.rs) + AdamW (src/tensor.rs:2923-2976) ----
+ * Llama/Qwen2-family decoder with a frozen quantized base and LoRA on the selected
+ * projections. The reference adapts q and v only (src/peft.rs:52-59, 508-512); targets
+ * extend that the same way (y += (x·A·B)·α/r after the base projection). */
+enum {
+  HOS_T_Q = 1,
+  HOS_T_K = 2,
+  HOS_T_V = 4,
+  HOS_T_O = 8,
+  HOS_T_GATE = 16,
+  HOS_T_UP = 32,
+  HOS_T_DOWN = 64
+};
+
+/* Config: src/model.rs:622-644 (Config) + src/peft.rs:121-126 (PeftCfg). */
+typedef struct {
+  int n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab;
+  float rms_eps, rope_base;
+  int rope_neox, attn_bias;
+  int lora_rank;
+  float lora_alpha;
+  uint32_t lora_targets;
+  int max_batch, max_seq; /* sizes the device-resident activation arena */
+} hos_peft_cfg;
+
+typedef struct hos_peft hos_peft;
+
+/* PeftModel::build_multi (src/peft.rs:134-231): allocates the model on ctx's device. */
+int hos_peft_create(hos_ctx* ctx, const hos_peft_cfg* cfg, hos_peft** out);
+void hos_peft_destroy(hos_peft* p);
+const char* hos_peft_last_error(const hos_peft* p);
+/* One GGUF tensor by its GGUF name (src/model.rs:713-921): token_embd.weight, output.weight
+ * (absent = tied to token_embd), output_norm.weight, blk.N.{attn_norm, attn_q, attn_k, attn_v,
+ * attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight, blk.N.attn_{q,k,v}.bias.
+ * Norm weights and biases: F32. Linear weights: Q8_0, Q4_K or Q6_K. */
+int hos_peft_set_tensor(hos_peft* p, const char* name, const uint8_t* bytes, size_t nbytes, uint32_t ggml_type,
+                        size_t rows, size_t cols);
+/* LoRA factors of one (layer, target index 0..6 = q,k,v,o,gate,up,down), reference layout:
+ * A [in, r], B [r, out] row-major (src/peft.rs:187-199). */
+int hos_peft_set_lora(hos_peft* p, int layer, int target, const float* A, const float* B);
+int hos_peft_get_lora(hos_peft* p, int layer, int target, float* A, float* B);
+int hos_peft_get_lora_grad(hos_peft* p, int layer, int target, float* dA, float* dB);
+/* zero_grad + for each of B sequences: loss(seq)·(1/B), backward (src/main.rs:2583-2596,
+ * src/train.rs:33-52). ids/targets: [B, T] int32 (host). *loss = Σ_b loss_b / B. */
+int hos_peft_loss_grad(hos_peft* p, const int32_t* ids, const int32_t* targets, int B, int T, float* loss);
+/* AdamW::step over all LoRA factors (β 0.9/0.95, eps 1e-8, decay on 2-D params). */
+int hos_peft_adamw(hos_peft* p, float lr, float wd);
+/* One optimizer step (loss_grad + adamw) on device-resident ids/targets; enqueues only.
+ * loss_dev receives the step's loss (one float, device). */
+int hos_peft_step_dev(hos_peft* p, const int32_t* ids_dev, const int32_t* targets_dev, int B, int T, float lr,
+                      float wd, float* loss_dev);
+/* Logits [T, vocab] of one sequence (PeftModel::logits, src/peft.rs:462-464). */
+int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out);
+/* Per-kernel-class timing with HIP events around every launch (off by default). */
+int hos_peft_profile(hos_peft* p, int enable);
+/* Accumulated stats of one kernel class since profiling was enabled: launches, total ms,
+ * algorithmic flops and HBM bytes. Classes: "qgemm_fwd", "qgemm_dx", "lora", "attn_fwd",
+ * "attn_bwd", "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert". */
+int hos_peft_kernel_stats(hos_peft* p, const char* cls, long long* launches, double* total_ms, double* flops,
+                          double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HOS_HIP_H */
