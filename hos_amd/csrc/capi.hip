@@ -67,7 +67,8 @@ struct hos_ctx {
   std::string err;
   std::unordered_map<uint64_t, QWeight> qw;
   std::unordered_map<uint64_t, DevMem> f32cache;
-  DevMem ws, t0, t1, t2, t3, t4;
+  DevMem ws, t0, t1, t2, t3, t4, t5;
+  int passes = 1;
   static constexpr size_t kWs = 256ull << 20;
 };
 
@@ -115,21 +116,31 @@ const float* operand(hos_ctx* c, const float* host, size_t n, uint64_t key, DevM
   return (const float*)scratch.p;
 }
 
+// fp16 operand scratch (+ residual plane when the context runs multi-pass GEMMs).
+H16 operand_h16(hos_ctx* c, long long K, size_t t) {
+  c->t2.ensure(t * K * 2);
+  c->t3.ensure(t * 4 + 4);
+  H16 a{(half_t*)c->t2.p, (float*)c->t3.p, nullptr};
+  if (c->passes > 1) {
+    c->t5.ensure(t * K * 2);
+    a.lo = (half_t*)c->t5.p;
+  }
+  return a;
+}
+
 void qgemm_dev(hos_ctx* c, bool dx, uint64_t key, const float* in_dev, size_t t, float* out_dev) {
   const QWeight& w = get_qw(c, key);
   long long K = dx ? w.rows : w.cols;
   long long N = dx ? w.cols : w.rows;
   HOS_REQUIRE(in_dev && out_dev, HOS_E_INVALID, "qgemm: null pointer");
-  c->t2.ensure(t * K * 2);
-  c->t3.ensure(t * 4 + 4);
-  H16 a{(half_t*)c->t2.p, (float*)c->t3.p};
+  H16 a = operand_h16(c, K, t);
   launch_to_h16(in_dev, K, (long long)t, K, a, c->stream);
   c->ws.ensure(hos_ctx::kWs);
-  GemmEpi epi{out_dev, N, nullptr, 0};
+  GemmEpi epi{out_dev, N, nullptr, 0, nullptr};
   if (dx)
-    launch_qgemm_dx(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->stream);
+    launch_qgemm_dx(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->passes, c->stream);
   else
-    launch_qgemm_fwd(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->stream);
+    launch_qgemm_fwd(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->passes, c->stream);
 }
 
 }  // namespace
@@ -304,17 +315,15 @@ int hos_hip_time_qgemm(hos_ctx* c, int which, uint64_t key, const float* in_dev,
     const QWeight& w = get_qw(c, key);
     bool dx = which == 1;
     long long K = dx ? w.rows : w.cols, N = dx ? w.cols : w.rows;
-    c->t2.ensure(t * K * 2);
-    c->t3.ensure(t * 4 + 4);
-    H16 a{(half_t*)c->t2.p, (float*)c->t3.p};
+    H16 a = operand_h16(c, K, t);
     launch_to_h16(in_dev, K, (long long)t, K, a, c->stream);
     c->ws.ensure(hos_ctx::kWs);
-    GemmEpi epi{out_dev, N, nullptr, 0};
+    GemmEpi epi{out_dev, N, nullptr, 0, nullptr};
     auto run = [&] {
       if (dx)
-        launch_qgemm_dx(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->stream);
+        launch_qgemm_dx(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->passes, c->stream);
       else
-        launch_qgemm_fwd(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->stream);
+        launch_qgemm_fwd(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->passes, c->stream);
     };
     run();  // warm-up
     hipEvent_t e0, e1;
@@ -349,6 +358,13 @@ int hos_hip_quantize(hos_ctx* c, const float* x, size_t n, uint32_t type, uint8_
 }
 
 size_t hos_hip_bytes_for(uint32_t type, size_t n) { return gguf_bytes_for(type, n); }
+
+int hos_hip_set_gemm_passes(hos_ctx* c, int passes) {
+  return guard(c, [&] {
+    HOS_REQUIRE(passes >= 1 && passes <= 3, HOS_E_INVALID, "gemm passes must be 1, 2 or 3");
+    c->passes = passes;
+  });
+}
 
 int hos_hip_dev_alloc(hos_ctx* c, size_t nbytes, void** dptr) {
   return guard(c, [&] {

@@ -51,10 +51,16 @@ struct QWeight {
 };
 
 // An fp16 GEMM operand with an exact power-of-two scale per row:
-//   data[m][k] = fp16(x[m][k] · 2^e[m]),  rinv[m] = 2^-e[m].
+//   data[m][k] = fp16(x[m][k] · 2^e[m]),  rinv[m] = 2^-e[m],
+//   lo[m][k]   = fp16(x[m][k] · 2^e[m] − data[m][k])  (the rounding residual; null when not kept).
+// data + lo carries x to ~22 bits, which the multi-pass GEMMs use.
 struct H16 {
   half_t* data;
   float* rinv;
+  half_t* lo = nullptr;
 };
+inline H16 h16_offset(H16 a, long long cols) {
+  return H16{a.data + cols, a.rinv, a.lo ? a.lo + cols : nullptr};
+}
 
 }  // namespace hos

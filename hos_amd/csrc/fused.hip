@@ -1,0 +1,328 @@
+// Bandwidth-bound fused kernels of the LoRA training step (one workgroup per row where a row
+// reduction is needed; wave64 shuffle + LDS reductions; coalesced row-major access).
+//
+//   embed_rows     Tensor::embedding of the frozen table (src/tensor.rs:2438-2457), dequant fused
+//   rmsnorm_fwd    src/tensor.rs:2500-2517, also emitting the fp16 row-scaled GEMM operand
+//   rmsnorm_bwd    src/tensor.rs:2521-2540 (gx only: norm weights are frozen), accumulated into dx
+//   rope_apply     src/tensor.rs:2750-2814, fwd rotation and its transpose (bwd), bit-exact
+//   swiglu_fwd     silu(g)·u (src/tensor.rs:2082-2087, :458-462), fp16 operand out
+//   swiglu_bwd     mul + silu VJPs (src/tensor.rs:466-477, :2088-2098)
+//   ce_fwd_bwd     cross_entropy + its VJP (src/tensor.rs:2709-2743), fp16 dlogits out
+//   adamw          AdamW::step (src/tensor.rs:2952-2975), bit-exact given the same gradient
+#include "fused.hpp"
+
+namespace hos {
+
+namespace {
+
+constexpr int RB = 256;  // threads per row workgroup
+
+__device__ __forceinline__ float warp_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float warp_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+// Block-wide reductions for RB = 256 threads (4 waves). `red` holds 8 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = warp_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = warp_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// fp16 operand element (+ its rounding residual when the operand keeps one).
+__device__ __forceinline__ void put_h16(float v, _Float16* hi, _Float16* lo, long long i) {
+  _Float16 h = (_Float16)v;
+  hi[i] = h;
+  if (lo) lo[i] = (_Float16)(v - (float)h);
+}
+
+// Power-of-two scale that maps a row max-abs into [2^14, 2^15) (exact in fp16 and f32).
+__device__ __forceinline__ int row_exp(float amax) {
+  if (!(amax > 0.0f) || amax >= 3.0e38f) return 0;
+  int ex;
+  frexpf(amax, &ex);
+  int e = 15 - ex;
+  return e > 100 ? 100 : (e < -100 ? -100 : e);
+}
+
+__global__ void embed_kernel(QWeightView table, const int32_t* __restrict__ ids, float* __restrict__ x, int M,
+                             int d) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * d) return;
+  int m = (int)(i / d), c = (int)(i % d);
+  x[i] = deq_one(table, ids[m], c);
+}
+
+__global__ void __launch_bounds__(RB) rmsnorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          float eps, int d, float* __restrict__ xn,
+                                                          _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                          float* __restrict__ rinv, float* __restrict__ inv_out) {
+  __shared__ float red[8];
+  const int row = blockIdx.x;
+  const float* xr = x + (long long)row * d;
+  float ss = 0.0f;
+  for (int c = threadIdx.x; c < d; c += RB) ss += xr[c] * xr[c];
+  ss = block_sum(ss, red) / (float)d;
+  float inv = 1.0f / sqrtf(ss + eps);
+  float amax = 0.0f;
+  for (int c = threadIdx.x; c < d; c += RB) {
+    float y = xr[c] * inv * w[c];
+    amax = fmaxf(amax, fabsf(y));
+    if (xn) xn[(long long)row * d + c] = y;
+  }
+  amax = block_max(amax, red);
+  int e = row_exp(amax);
+  float sc = ldexpf(1.0f, e);
+  for (int c = threadIdx.x; c < d; c += RB) put_h16(xr[c] * inv * w[c] * sc, xh, xl, (long long)row * d + c);
+  if (threadIdx.x == 0) {
+    rinv[row] = ldexpf(1.0f, -e);
+    inv_out[row] = inv;
+  }
+}
+
+// dx += g·w·inv − inv³·x/d·Σ(g·w·x)
+__global__ void __launch_bounds__(RB) rmsnorm_bwd_kernel(const float* __restrict__ g, const float* __restrict__ x,
+                                                          const float* __restrict__ inv_in,
+                                                          const float* __restrict__ w, int d, float* __restrict__ dx) {
+  __shared__ float red[8];
+  const int row = blockIdx.x;
+  const float* gr = g + (long long)row * d;
+  const float* xr = x + (long long)row * d;
+  float s = 0.0f;
+  for (int c = threadIdx.x; c < d; c += RB) s += gr[c] * w[c] * xr[c];
+  s = block_sum(s, red);
+  float inv = inv_in[row];
+  float k = inv * inv * inv / (float)d * s;
+  float* dr = dx + (long long)row * d;
+  for (int c = threadIdx.x; c < d; c += RB) dr[c] += gr[c] * w[c] * inv - xr[c] * k;
+}
+
+// RoPE on [M, ld] rows, heads at column col0 + h·hd. tab: (sin, cos) per (position, i), built on the host
+// with the same powf/sinf/cosf calls as the reference. inverse: apply Rᵀ (the backward).
+__global__ void rope_kernel(float* __restrict__ buf, long long ld, int col0, int n_heads, int hd, int T,
+                            const float2* __restrict__ tab, int neox, int inverse, int M) {
+#pragma clang fp contract(off)
+  const int half = hd >> 1;
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  long long total = (long long)M * n_heads * half;
+  if (i >= total) return;
+  int p = (int)(i % half);
+  long long t2 = i / half;
+  int h = (int)(t2 % n_heads);
+  int m = (int)(t2 / n_heads);
+  float2 sc = tab[(m % T) * half + p];
+  float s = sc.x, c = sc.y;
+  float* base = buf + (long long)m * ld + col0 + h * hd;
+  int ia = neox ? p : 2 * p, ib = neox ? p + half : 2 * p + 1;
+  float a = base[ia], b = base[ib];
+  if (!inverse) {
+    base[ia] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    base[ib] = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+  } else {
+    base[ia] = __fadd_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    base[ib] = __fadd_rn(__fmul_rn(-a, s), __fmul_rn(b, c));
+  }
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// gu rows = [gate (F) | up (F)] -> h = silu(gate)·up: f32 (optional) + fp16 operand.
+__global__ void __launch_bounds__(RB) swiglu_fwd_kernel(const float* __restrict__ gu, int F, float* __restrict__ h,
+                                                         _Float16* __restrict__ hh, _Float16* __restrict__ hl,
+                                                         float* __restrict__ rinv) {
+  __shared__ float red[8];
+  const int row = blockIdx.x;
+  const float* g = gu + (long long)row * 2 * F;
+  const float* u = g + F;
+  float amax = 0.0f;
+  for (int c = threadIdx.x; c < F; c += RB) {
+    float v = silu_f(g[c]) * u[c];
+    amax = fmaxf(amax, fabsf(v));
+    if (h) h[(long long)row * F + c] = v;
+  }
+  amax = block_max(amax, red);
+  int e = row_exp(amax);
+  float sc = ldexpf(1.0f, e);
+  for (int c = threadIdx.x; c < F; c += RB) put_h16(silu_f(g[c]) * u[c] * sc, hh, hl, (long long)row * F + c);
+  if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
+}
+
+// dh -> d[gate | up] (f32 optional, fp16 operand with row scale)
+__global__ void __launch_bounds__(RB) swiglu_bwd_kernel(const float* __restrict__ gu, const float* __restrict__ dh,
+                                                         int F, float* __restrict__ dgu, _Float16* __restrict__ dgh,
+                                                         _Float16* __restrict__ dgl, float* __restrict__ rinv) {
+  __shared__ float red[8];
+  const int row = blockIdx.x;
+  const float* g = gu + (long long)row * 2 * F;
+  const float* u = g + F;
+  const float* d = dh + (long long)row * F;
+  float amax = 0.0f;
+  for (int c = threadIdx.x; c < F; c += RB) {
+    float x = g[c];
+    float s = 1.0f / (1.0f + expf(-x));
+    float dg = d[c] * u[c] * (s + x * s * (1.0f - s));
+    float du = d[c] * (x / (1.0f + expf(-x)));
+    amax = fmaxf(amax, fmaxf(fabsf(dg), fabsf(du)));
+    if (dgu) {
+      dgu[(long long)row * 2 * F + c] = dg;
+      dgu[(long long)row * 2 * F + F + c] = du;
+    }
+  }
+  amax = block_max(amax, red);
+  int e = row_exp(amax);
+  float sc = ldexpf(1.0f, e);
+  for (int c = threadIdx.x; c < F; c += RB) {
+    float x = g[c];
+    float s = 1.0f / (1.0f + expf(-x));
+    float dg = d[c] * u[c] * (s + x * s * (1.0f - s));
+    float du = d[c] * (x / (1.0f + expf(-x)));
+    put_h16(dg * sc, dgh, dgl, (long long)row * 2 * F + c);
+    put_h16(du * sc, dgh, dgl, (long long)row * 2 * F + F + c);
+  }
+  if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
+}
+
+// Softmax cross-entropy of one row + its gradient (p − onehot)·gscale as an fp16 operand.
+__global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits, int V,
+                                                 const int32_t* __restrict__ targets, float gscale,
+                                                 float* __restrict__ row_loss, _Float16* __restrict__ dl,
+                                                 _Float16* __restrict__ dll, float* __restrict__ rinv) {
+  __shared__ float red[8];
+  const int row = blockIdx.x;
+  const float* lr = logits + (long long)row * V;
+  float mx = -INFINITY;
+  for (int c = threadIdx.x; c < V; c += RB) mx = fmaxf(mx, lr[c]);
+  mx = block_max(mx, red);
+  float sum = 0.0f;
+  for (int c = threadIdx.x; c < V; c += RB) sum += expf(lr[c] - mx);
+  sum = block_sum(sum, red);
+  const int t = targets[row];
+  float pt = expf(lr[t] - mx) / sum;
+  if (threadIdx.x == 0) row_loss[row] = -logf(fmaxf(pt, 1e-12f));
+  // max |p − onehot| = max(1/sum, 1 − p_t) (the row max has p = 1/sum)
+  float amax = fmaxf(1.0f / sum, 1.0f - pt) * fabsf(gscale);
+  int e = row_exp(amax);
+  float sc = ldexpf(1.0f, e);
+  for (int c = threadIdx.x; c < V; c += RB) {
+    float p = expf(lr[c] - mx) / sum;
+    if (c == t) p -= 1.0f;
+    put_h16(p * gscale * sc, dl, dll, (long long)row * V + c);
+  }
+  if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
+}
+
+// loss = Σ_b (Σ_t term[b,t] / T) · (1/B), in sequence order (src/main.rs:2588-2596).
+__global__ void loss_reduce_kernel(const float* __restrict__ row_loss, int B, int T, float* __restrict__ loss) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float mean = 0.0f;
+  for (int b = 0; b < B; b++) {
+    float s = 0.0f;
+    for (int t = 0; t < T; t++) s += row_loss[b * T + t];
+    s = s / (float)T;
+    mean += s * (1.0f / (float)B);
+  }
+  *loss = mean;
+}
+
+__global__ void adamw_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+                             float* __restrict__ v, long long n, float lr, float b1, float b2, float eps, float wd,
+                             float bc1, float bc2, int decay) {
+#pragma clang fp contract(off)
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float gi = g[i];
+  float mi = __fadd_rn(__fmul_rn(b1, m[i]), __fmul_rn(__fsub_rn(1.0f, b1), gi));
+  float vi = __fadd_rn(__fmul_rn(b2, v[i]), __fmul_rn(__fmul_rn(__fsub_rn(1.0f, b2), gi), gi));
+  m[i] = mi;
+  v[i] = vi;
+  float mh = __fdiv_rn(mi, bc1), vh = __fdiv_rn(vi, bc2);
+  float u = __fdiv_rn(__fmul_rn(lr, mh), __fadd_rn(__fsqrt_rn(vh), eps));
+  if (decay) u = __fadd_rn(u, __fmul_rn(__fmul_rn(lr, wd), p[i]));
+  p[i] = __fsub_rn(p[i], u);
+}
+
+__global__ void fill_kernel(float* __restrict__ p, long long n, float v) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void copy_rows_kernel(const float* __restrict__ src, long long lds, float* __restrict__ dst,
+                                 long long ldd, int cols, long long total) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  long long r = i / cols;
+  int c = (int)(i % cols);
+  dst[r * ldd + c] = src[r * lds + c];
+}
+
+}  // namespace
+
+void launch_embed(const QWeight& table, const int32_t* ids, float* x, int M, int d, hipStream_t st) {
+  long long n = (long long)M * d;
+  embed_kernel<<<ceil_div(n, 256), 256, 0, st>>>(view(table), ids, x, M, d);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_rmsnorm_fwd(const float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
+                        hipStream_t st) {
+  rmsnorm_fwd_kernel<<<M, RB, 0, st>>>(x, w, eps, d, xn, out.data, out.lo, out.rinv, inv);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
+                        hipStream_t st) {
+  rmsnorm_bwd_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,
+                 bool inverse, int M, hipStream_t st) {
+  long long n = (long long)M * n_heads * (hd / 2);
+  rope_kernel<<<ceil_div(n, 256), 256, 0, st>>>(buf, ld, col0, n_heads, hd, T, tab, neox, inverse, M);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_swiglu_fwd(const float* gu, int M, int F, float* h, H16 out, hipStream_t st) {
+  swiglu_fwd_kernel<<<M, RB, 0, st>>>(gu, F, h, out.data, out.lo, out.rinv);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_swiglu_bwd(const float* gu, const float* dh, int M, int F, float* dgu, H16 out, hipStream_t st) {
+  swiglu_bwd_kernel<<<M, RB, 0, st>>>(gu, dh, F, dgu, out.data, out.lo, out.rinv);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_ce(const float* logits, int M, int V, const int32_t* targets, float gscale, float* row_loss, H16 dl,
+               hipStream_t st) {
+  ce_kernel<<<M, RB, 0, st>>>(logits, V, targets, gscale, row_loss, dl.data, dl.lo, dl.rinv);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_loss_reduce(const float* row_loss, int B, int T, float* loss, hipStream_t st) {
+  loss_reduce_kernel<<<1, 64, 0, st>>>(row_loss, B, T, loss);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_adamw(float* p, const float* g, float* m, float* v, long long n, float lr, float b1, float b2, float eps,
+                  float wd, float bc1, float bc2, bool decay, hipStream_t st) {
+  adamw_kernel<<<ceil_div(n, 256), 256, 0, st>>>(p, g, m, v, n, lr, b1, b2, eps, wd, bc1, bc2, decay);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_fill(float* p, long long n, float v, hipStream_t st) {
+  if (n <= 0) return;
+  fill_kernel<<<ceil_div(n, 256), 256, 0, st>>>(p, n, v);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_copy_rows(const float* src, long long lds, float* dst, long long ldd, int rows, int cols,
+                      hipStream_t st) {
+  long long n = (long long)rows * cols;
+  if (n <= 0) return;
+  copy_rows_kernel<<<ceil_div(n, 256), 256, 0, st>>>(src, lds, dst, ldd, cols, n);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace hos

@@ -1,0 +1,28 @@
+// Launchers of the fused bandwidth-bound kernels and attention (fused.hip, attention.hip).
+#pragma once
+#include "kernels.hpp"
+
+namespace hos {
+void launch_embed(const QWeight& table, const int32_t* ids, float* x, int M, int d, hipStream_t st);
+void launch_rmsnorm_fwd(const float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
+                        hipStream_t st);
+void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
+                        hipStream_t st);
+void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,
+                 bool inverse, int M, hipStream_t st);
+void launch_swiglu_fwd(const float* gu, int M, int F, float* h, H16 out, hipStream_t st);
+void launch_swiglu_bwd(const float* gu, const float* dh, int M, int F, float* dgu, H16 out, hipStream_t st);
+void launch_ce(const float* logits, int M, int V, const int32_t* targets, float gscale, float* row_loss, H16 dl,
+               hipStream_t st);
+void launch_loss_reduce(const float* row_loss, int B, int T, float* loss, hipStream_t st);
+void launch_adamw(float* p, const float* g, float* m, float* v, long long n, float lr, float b1, float b2, float eps,
+                  float wd, float bc1, float bc2, bool decay, hipStream_t st);
+void launch_fill(float* p, long long n, float v, hipStream_t st);
+void launch_copy_rows(const float* src, long long lds, float* dst, long long ldd, int rows, int cols,
+                      hipStream_t st);
+void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,
+                     float* o, long long ldo, float* lse, hipStream_t st);
+void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
+                     long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
+                     long long ldd, hipStream_t st);
+}  // namespace hos

@@ -45,20 +45,22 @@ void launch_dequant(const QWeight& w, float* out_dev, hipStream_t st);
 void launch_quantize(const float* x_dev, size_t n, uint32_t type, uint8_t* out_dev, hipStream_t st);
 
 // ---- qgemm.hip ----
-// Epilogue of the fp16 GEMMs: out[m][n] = (beta ? out[m][n] : 0) + rinv[m]·acc[m][n] (+ bias[n]).
+// Epilogue of the fp16 GEMMs: v = rinv[m]·acc[m][n] (+ bias[n]);
+//   accumulate: out += v;  else resid: out = resid + v (resid may alias out);  else out = v.
 struct GemmEpi {
   float* out;
   long long ldo;
-  const float* bias;  // may be null
-  int accumulate;     // 1: out += result
+  const float* bias;   // may be null
+  int accumulate;      // 1: out += v
+  const float* resid;  // may be null; same row stride as out
 };
 // Y[M, W.rows] = A[M, W.cols] · deq(W)ᵀ, A an fp16 row-scaled operand with row stride lda.
 void launch_qgemm_fwd(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
-                      hipStream_t st);
+                      int passes, hipStream_t st);
 // dX[M, W.cols] = dY[M, W.rows] · deq(W), dY an fp16 row-scaled operand with row stride lda.
 void launch_qgemm_dx(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
-                     hipStream_t st);
-// f32 [M, K] (row stride ldx) -> fp16 row-scaled operand (row stride K).
+                     int passes, hipStream_t st);
+// f32 [M, K] (row stride ldx) -> fp16 row-scaled operand (row stride K); residual too when out.lo is set.
 void launch_to_h16(const float* x, long long ldx, long long M, long long K, H16 out, hipStream_t st);
 
 // ---- gemm_f32.hip ----

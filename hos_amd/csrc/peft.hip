@@ -1,22 +1,728 @@
-// Placeholder: the LoRA training model is not wired yet.
-#include "ctx.hpp"
+// Device-resident LoRA training step: PeftModel (src/peft.rs) + AdamW (src/tensor.rs:2923-2976) on gfx950.
+//
+// The reference builds a dynamic autograd graph per sequence and walks it in reverse
+// (src/tensor.rs:2844-2881). Here the graph of PeftModel::forward (src/peft.rs:474-604) is fixed, so
+// the forward and its reverse pass are a static schedule of kernels over all B·T rows at once: the
+// reference's batch is B sequences accumulated with loss·(1/B) (src/main.rs:2583-2596), which is the
+// same sum as one pass over B·T rows with the CE gradient scaled by 1/(B·T) and attention kept
+// within each sequence. Everything stays in HBM between kernels; the host only enqueues.
+//
+// Frozen linear weights: quantized (Q8_0/Q4_K/Q6_K), dequantized inside the fp16-MFMA GEMMs.
+// LoRA factors, their gradients and AdamW moments: one flat f32 arena, updated by one kernel.
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
 
-struct hos_peft {
-  std::string err = "not implemented";
+#include "ctx.hpp"
+#include "fused.hpp"
+
+using namespace hos;
+
+namespace {
+
+// LoRA targets in order: q k v o gate up down.
+enum { TQ, TK, TV, TO, TG, TU, TD, NT };
+
+struct LayerW {
+  QWeight w[NT];                // base projection per target slot
+  float* attn_norm = nullptr;   // [d]
+  float* ffn_norm = nullptr;    // [d]
+  float* bias[3] = {nullptr, nullptr, nullptr};  // q k v
 };
 
-extern "C" {
-int hos_peft_create(hos_ctx*, const hos_peft_cfg*, hos_peft** out) { if (out) *out = nullptr; return HOS_E_INVALID; }
-void hos_peft_destroy(hos_peft* p) { delete p; }
-const char* hos_peft_last_error(const hos_peft* p) { return p ? p->err.c_str() : "null"; }
-int hos_peft_set_tensor(hos_peft*, const char*, const uint8_t*, size_t, uint32_t, size_t, size_t) { return HOS_E_INVALID; }
-int hos_peft_set_lora(hos_peft*, int, int, const float*, const float*) { return HOS_E_INVALID; }
-int hos_peft_get_lora(hos_peft*, int, int, float*, float*) { return HOS_E_INVALID; }
-int hos_peft_get_lora_grad(hos_peft*, int, int, float*, float*) { return HOS_E_INVALID; }
-int hos_peft_loss_grad(hos_peft*, const int32_t*, const int32_t*, int, int, float*) { return HOS_E_INVALID; }
-int hos_peft_adamw(hos_peft*, float, float) { return HOS_E_INVALID; }
-int hos_peft_step_dev(hos_peft*, const int32_t*, const int32_t*, int, int, float, float, float*) { return HOS_E_INVALID; }
-int hos_peft_logits(hos_peft*, const int32_t*, int, float*) { return HOS_E_INVALID; }
-int hos_peft_profile(hos_peft*, int) { return HOS_E_INVALID; }
-int hos_peft_kernel_stats(hos_peft*, const char*, long long*, double*, double*, double*) { return HOS_E_INVALID; }
+struct LayerAct {
+  float *x, *xn1, *inv1, *qkv, *o, *lse, *x2, *xn2, *inv2, *gu, *h, *u;
+};
+
+struct ProfRec {
+  std::string cls;
+  hipEvent_t e0, e1;
+  double flops, bytes;
+};
+struct ProfAcc {
+  long long launches = 0;
+  double ms = 0, flops = 0, bytes = 0;
+};
+
+// compiler-rt __powisf2 (Rust f32::powi): square-and-multiply, as the reference's bias corrections use.
+float powi_f32(float a, int b) {
+  bool recip = b < 0;
+  float r = 1.0f;
+  while (true) {
+    if (b & 1) r *= a;
+    b /= 2;
+    if (b == 0) break;
+    a *= a;
+  }
+  return recip ? 1.0f / r : r;
 }
+
+}  // namespace
+
+struct hos_peft {
+  hos_ctx* ctx = nullptr;
+  hipStream_t st = nullptr;
+  hos_peft_cfg c{};
+  std::string err;
+  int d = 0, qd = 0, kvd = 0, W3 = 0, F = 0, V = 0, r = 0, L = 0, Mmax = 0, passes = 3;
+  float lscale = 0.0f;
+
+  std::vector<LayerW> lw;
+  QWeight tok, out;
+  bool out_set = false;
+  float* out_norm = nullptr;
+
+  // LoRA arena: offsets (floats) of A and B per (layer, target); -1 when not adapted
+  std::vector<long long> offA, offB;
+  long long nparams = 0;
+  float *P = nullptr, *G = nullptr, *M1 = nullptr, *V1 = nullptr;
+  uint64_t adam_t = 0;
+
+  std::vector<LayerAct> act;
+  float* xfinal = nullptr;  // residual stream after the last layer
+  float* invf = nullptr;
+  H16 hs{};                 // fp16 operand scratch [Mmax, hs_cols]
+  float* logits = nullptr;
+  H16 dl{};
+  float *row_loss = nullptr, *loss = nullptr;
+  float *dx = nullptr, *dxn = nullptr, *dqkv = nullptr, *dout = nullptr, *dh = nullptr, *dgu = nullptr,
+        *du = nullptr, *dvec = nullptr;
+  float* ws = nullptr;
+  size_t ws_bytes = 0;
+  float2* rope_tab = nullptr;
+  int32_t *ids = nullptr, *tgts = nullptr;
+  std::vector<void*> allocs;
+
+  bool prof = false;
+  std::vector<ProfRec> recs;
+  std::map<std::string, ProfAcc> acc;
+
+  // ---------------- helpers ----------------
+  template <class T>
+  T* alloc(size_t n) {
+    void* p = nullptr;
+    if (n == 0) n = 1;
+    hipError_t e = hipMalloc(&p, n * sizeof(T));
+    if (e != hipSuccess) throw Error(HOS_E_OOM, "hipMalloc(" + std::to_string(n * sizeof(T)) + ") failed");
+    allocs.push_back(p);
+    return (T*)p;
+  }
+  bool has(int t) const { return (c.lora_targets >> t) & 1u; }
+  void dims(int t, int* in, int* outd) const {
+    switch (t) {
+      case TQ: *in = d; *outd = qd; break;
+      case TK: *in = d; *outd = kvd; break;
+      case TV: *in = d; *outd = kvd; break;
+      case TO: *in = qd; *outd = d; break;
+      case TG: *in = d; *outd = F; break;
+      case TU: *in = d; *outd = F; break;
+      default: *in = F; *outd = d; break;
+    }
+  }
+
+  struct Scope {
+    hos_peft* p;
+    hipEvent_t e0{}, e1{};
+    const char* cls;
+    double fl, by;
+    Scope(hos_peft* p_, const char* cls_, double fl_, double by_) : p(p_), cls(cls_), fl(fl_), by(by_) {
+      if (p->prof) {
+        HOS_HIP_CHECK(hipEventCreate(&e0));
+        HOS_HIP_CHECK(hipEventCreate(&e1));
+        HOS_HIP_CHECK(hipEventRecord(e0, p->st));
+      }
+    }
+    ~Scope() {
+      if (p->prof) {
+        (void)hipEventRecord(e1, p->st);
+        p->recs.push_back(ProfRec{cls, e0, e1, fl, by});
+      }
+    }
+  };
+
+  double wbytes(const QWeight& w) const { return (double)(w.q_bytes + w.s_bytes); }
+
+  // fp16 GEMMs on frozen weights
+  void qfwd(const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo, const float* bias,
+            const float* resid, int accumulate) {
+    Scope s(this, "qgemm_fwd", 2.0 * M * w.rows * w.cols * passes,
+            2.0 * M * w.cols + wbytes(w) + 4.0 * M * w.rows * (resid || accumulate ? 2 : 1));
+    GemmEpi e{out, ldo, bias, accumulate, resid};
+    launch_qgemm_fwd(w, a, lda, M, e, ws, ws_bytes, passes, st);
+  }
+  void qdx(const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo, int accumulate) {
+    Scope s(this, "qgemm_dx", 2.0 * M * w.rows * w.cols * passes,
+            2.0 * M * w.rows + wbytes(w) + 4.0 * M * w.cols * (accumulate ? 2 : 1));
+    GemmEpi e{out, ldo, nullptr, accumulate, nullptr};
+    launch_qgemm_dx(w, a, lda, M, e, ws, ws_bytes, passes, st);
+  }
+  // f32 GEMM C = alpha·A·B + beta·C (strided)
+  void g32(long long M, long long N, long long K, float alpha, const float* A, long long sam, long long sak,
+           const float* B, long long sbk, long long sbn, float beta, float* C, long long ldc) {
+    Scope s(this, "lora", 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N * (beta != 0.0f ? 2 : 1)));
+    launch_gemm_f32(M, N, K, alpha, A, sam, sak, B, sbk, sbn, beta, C, ldc, ws, ws_bytes, st);
+  }
+  void to16(const float* x, long long ldx, int M, int K) {
+    Scope s(this, "convert", 0, 6.0 * M * K);
+    launch_to_h16(x, ldx, M, K, hs, st);
+  }
+
+  // ---- LoRA pieces (reference layout: A [in, r], B [r, out]) ----
+  // u[:, t·r..] = x · A_t
+  void lora_down(int l, int t, const float* x, long long ldx, int M) {
+    int in, o;
+    dims(t, &in, &o);
+    const float* A = P + offA[l * NT + t];
+    g32(M, r, in, 1.0f, x, ldx, 1, A, r, 1, 0.0f, act[l].u + t * r, NT * r);
+  }
+  // y += s · u_t · B_t
+  void lora_up(int l, int t, float* y, long long ldy, int M) {
+    int in, o;
+    dims(t, &in, &o);
+    const float* B = P + offB[l * NT + t];
+    g32(M, o, r, lscale, act[l].u + t * r, NT * r, 1, B, o, 1, 1.0f, y, ldy);
+  }
+  // Given dy (grad of the adapted projection output): dB_t, dA_t, and dx_in += s·(dy·B_tᵀ)·A_tᵀ.
+  void lora_bwd(int l, int t, const float* x, long long ldx, const float* dy, long long ldy, float* dxin,
+                long long lddx, int M) {
+    int in, o;
+    dims(t, &in, &o);
+    const float* A = P + offA[l * NT + t];
+    const float* B = P + offB[l * NT + t];
+    float* dA = G + offA[l * NT + t];
+    float* dB = G + offB[l * NT + t];
+    const float* u = act[l].u + t * r;
+    // dB = s·uᵀ·dy   [r, o]
+    g32(r, o, M, lscale, u, 1, NT * r, dy, ldy, 1, 0.0f, dB, o);
+    // du = s·dy·Bᵀ   [M, r]
+    g32(M, r, o, lscale, dy, ldy, 1, B, 1, o, 0.0f, du, r);
+    // dA = xᵀ·du     [in, r]
+    g32(in, r, M, 1.0f, x, 1, ldx, du, r, 1, 0.0f, dA, r);
+    // dx += du·Aᵀ    [M, in]
+    g32(M, in, r, 1.0f, du, r, 1, A, 1, r, 1.0f, dxin, lddx);
+  }
+
+  void check_ready() {
+    HOS_REQUIRE(tok.q != nullptr, HOS_E_MISSING_TENSOR, "missing tensor 'token_embd.weight'");
+    HOS_REQUIRE(out_norm != nullptr, HOS_E_MISSING_TENSOR, "missing tensor 'output_norm.weight'");
+    for (int l = 0; l < L; l++) {
+      const char* names[NT] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+      for (int t = 0; t < NT; t++)
+        HOS_REQUIRE(lw[l].w[t].q != nullptr, HOS_E_MISSING_TENSOR,
+                    "missing tensor 'blk." + std::to_string(l) + "." + names[t] + ".weight'");
+      HOS_REQUIRE(lw[l].attn_norm && lw[l].ffn_norm, HOS_E_MISSING_TENSOR,
+                  "missing norm weights of blk." + std::to_string(l));
+      if (c.attn_bias)
+        HOS_REQUIRE(lw[l].bias[0] && lw[l].bias[1] && lw[l].bias[2], HOS_E_MISSING_TENSOR,
+                    "missing attention biases of blk." + std::to_string(l));
+    }
+  }
+
+  // ---------------- forward ----------------
+  void forward(int B, int T, bool need_logits_only) {
+    const int M = B * T;
+    {
+      Scope s(this, "embed", 0, 4.0 * M * d + (double)M * d);
+      launch_embed(tok, ids, act[0].x, M, d, st);
+    }
+    for (int l = 0; l < L; l++) {
+      LayerAct& a = act[l];
+      LayerW& w = lw[l];
+      float* xnext = (l + 1 < L) ? act[l + 1].x : xfinal;
+      const bool lqkv = has(TQ) || has(TK) || has(TV);
+      {
+        Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lqkv ? 2 : 1) + 2.0 * M * d);
+        launch_rmsnorm_fwd(a.x, w.attn_norm, c.rms_eps, M, d, lqkv ? a.xn1 : nullptr, hs, a.inv1, st);
+      }
+      qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0);
+      qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0);
+      qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0);
+      const int qcol[3] = {0, qd, qd + kvd};
+      for (int t = TQ; t <= TV; t++)
+        if (has(t)) {
+          lora_down(l, t, a.xn1, d, M);
+          lora_up(l, t, a.qkv + qcol[t], W3, M);
+        }
+      {
+        Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
+        launch_rope(a.qkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
+        launch_rope(a.qkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
+      }
+      {
+        Scope s(this, "attn_fwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 2,
+                4.0 * M * (W3 + qd) + 4.0 * B * c.n_heads * T);
+        launch_attn_fwd(a.qkv, W3, qd, qd + kvd, B, T, c.n_heads, c.n_kv_heads, c.head_dim, a.o, qd, a.lse, st);
+      }
+      to16(a.o, qd, M, qd);
+      qfwd(w.w[TO], hs, qd, M, a.x2, d, nullptr, a.x, 0);
+      if (has(TO)) {
+        lora_down(l, TO, a.o, qd, M);
+        lora_up(l, TO, a.x2, d, M);
+      }
+      const bool lgu = has(TG) || has(TU);
+      {
+        Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lgu ? 2 : 1) + 2.0 * M * d);
+        launch_rmsnorm_fwd(a.x2, w.ffn_norm, c.rms_eps, M, d, lgu ? a.xn2 : nullptr, hs, a.inv2, st);
+      }
+      qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0);
+      qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0);
+      if (has(TG)) {
+        lora_down(l, TG, a.xn2, d, M);
+        lora_up(l, TG, a.gu, 2LL * F, M);
+      }
+      if (has(TU)) {
+        lora_down(l, TU, a.xn2, d, M);
+        lora_up(l, TU, a.gu + F, 2LL * F, M);
+      }
+      {
+        Scope s(this, "swiglu", 0, 8.0 * M * F + 2.0 * M * F + (has(TD) ? 4.0 * M * F : 0));
+        launch_swiglu_fwd(a.gu, M, F, has(TD) ? a.h : nullptr, hs, st);
+      }
+      qfwd(w.w[TD], hs, F, M, xnext, d, nullptr, a.x2, 0);
+      if (has(TD)) {
+        lora_down(l, TD, a.h, F, M);
+        lora_up(l, TD, xnext, d, M);
+      }
+    }
+    {
+      Scope s(this, "rmsnorm", 0, 4.0 * M * d + 2.0 * M * d);
+      launch_rmsnorm_fwd(xfinal, out_norm, c.rms_eps, M, d, nullptr, hs, invf, st);
+    }
+    qfwd(out_set ? out : tok, hs, d, M, logits, V, nullptr, nullptr, 0);
+    (void)need_logits_only;
+  }
+
+  // ---------------- loss + backward ----------------
+  void loss_backward(int B, int T) {
+    const int M = B * T;
+    {
+      Scope s(this, "ce", 0, 4.0 * M * V + 2.0 * M * V);
+      float gscale = (1.0f / (float)B) / (float)T;  // scale(1/B) then CE's g/n (src/tensor.rs:2736-2741)
+      launch_ce(logits, M, V, tgts, gscale, row_loss, dl, st);
+      launch_loss_reduce(row_loss, B, T, loss, st);
+    }
+    const QWeight& head = out_set ? out : tok;
+    qdx(head, dl, V, M, dxn, d, 0);
+    {
+      Scope s(this, "rmsnorm", 0, 4.0 * M * d * 3 + 4.0 * M * d);
+      launch_fill(dx, (long long)M * d, 0.0f, st);
+      launch_rmsnorm_bwd(dxn, xfinal, invf, out_norm, M, d, dx, st);
+    }
+    for (int l = L - 1; l >= 0; l--) {
+      LayerAct& a = act[l];
+      LayerW& w = lw[l];
+      // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA) ----
+      to16(dx, d, M, d);
+      qdx(w.w[TD], hs, d, M, dh, F, 0);
+      if (has(TD)) lora_bwd(l, TD, a.h, F, dx, d, dh, F, M);
+      {
+        Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (dgu ? 8.0 * M * F : 0));
+        launch_swiglu_bwd(a.gu, dh, M, F, (has(TG) || has(TU)) ? dgu : nullptr, hs, st);
+      }
+      H16 hu = h16_offset(hs, F);
+      qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0);
+      qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1);
+      if (has(TG)) lora_bwd(l, TG, a.xn2, d, dgu, 2LL * F, dxn, d, M);
+      if (has(TU)) lora_bwd(l, TU, a.xn2, d, dgu + F, 2LL * F, dxn, d, M);
+      {
+        Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
+        launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st);
+      }
+      // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
+      to16(dx, d, M, d);
+      qdx(w.w[TO], hs, d, M, dout, qd, 0);
+      if (has(TO)) lora_bwd(l, TO, a.o, qd, dx, d, dout, qd, M);
+      {
+        Scope s(this, "attn_bwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 5,
+                4.0 * M * (W3 * 2 + qd * 2) + 8.0 * B * c.n_heads * T);
+        launch_attn_bwd(a.qkv, W3, qd, qd + kvd, a.o, dout, qd, a.lse, dvec, B, T, c.n_heads, c.n_kv_heads,
+                        c.head_dim, dqkv, W3, st);
+      }
+      {
+        Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
+        launch_rope(dqkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+        launch_rope(dqkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+      }
+      to16(dqkv, W3, M, W3);
+      H16 hk = h16_offset(hs, qd), hv = h16_offset(hs, qd + kvd);
+      qdx(w.w[TQ], hs, W3, M, dxn, d, 0);
+      qdx(w.w[TK], hk, W3, M, dxn, d, 1);
+      qdx(w.w[TV], hv, W3, M, dxn, d, 1);
+      const int qcol[3] = {0, qd, qd + kvd};
+      for (int t = TQ; t <= TV; t++)
+        if (has(t)) lora_bwd(l, t, a.xn1, d, dqkv + qcol[t], W3, dxn, d, M);
+      {
+        Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
+        launch_rmsnorm_bwd(dxn, a.x, a.inv1, w.attn_norm, M, d, dx, st);
+      }
+    }
+  }
+
+  void adamw(float lr, float wd) {
+    adam_t += 1;
+    float bc1 = 1.0f - powi_f32(0.9f, (int)adam_t);
+    float bc2 = 1.0f - powi_f32(0.95f, (int)adam_t);
+    Scope s(this, "adamw", 0, 4.0 * nparams * 7);
+    // every LoRA factor is 2-D, so decay applies to all (src/main.rs:2571)
+    launch_adamw(P, G, M1, V1, nparams, lr, 0.9f, 0.95f, 1e-8f, wd, bc1, bc2, true, st);
+  }
+
+  void collect_prof() {
+    if (recs.empty()) return;
+    HOS_HIP_CHECK(hipStreamSynchronize(st));
+    for (auto& rc : recs) {
+      float ms = 0;
+      (void)hipEventElapsedTime(&ms, rc.e0, rc.e1);
+      ProfAcc& a = acc[rc.cls];
+      a.launches++;
+      a.ms += ms;
+      a.flops += rc.flops;
+      a.bytes += rc.bytes;
+      (void)hipEventDestroy(rc.e0);
+      (void)hipEventDestroy(rc.e1);
+    }
+    recs.clear();
+  }
+
+  void init(hos_ctx* cx, const hos_peft_cfg* cfg) {
+    ctx = cx;
+    st = hos_internal_stream(cx);
+    c = *cfg;
+    HOS_REQUIRE(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.ffn_dim > 0 && c.vocab > 0,
+                HOS_E_INVALID, "peft: bad model dimensions");
+    HOS_REQUIRE(c.n_heads % c.n_kv_heads == 0, HOS_E_INVALID, "peft: n_heads must be a multiple of n_kv_heads");
+    HOS_REQUIRE(c.head_dim == 64, HOS_E_UNSUPPORTED_ARCH, "peft: head_dim must be 64");
+    HOS_REQUIRE(c.lora_rank > 0 && c.max_batch > 0 && c.max_seq > 0, HOS_E_INVALID, "peft: bad rank/batch/seq");
+    HOS_REQUIRE(c.dim % 32 == 0 && c.ffn_dim % 32 == 0, HOS_E_INVALID, "peft: dim and ffn_dim must be multiples of 32");
+    L = c.n_layers;
+    d = c.dim;
+    qd = c.n_heads * c.head_dim;
+    kvd = c.n_kv_heads * c.head_dim;
+    W3 = qd + 2 * kvd;
+    F = c.ffn_dim;
+    V = c.vocab;
+    r = c.lora_rank;
+    lscale = c.lora_alpha / (float)r;  // src/peft.rs:195
+    Mmax = c.max_batch * c.max_seq;
+    passes = c.gemm_passes == 0 ? 3 : c.gemm_passes;
+    HOS_REQUIRE(passes >= 1 && passes <= 3, HOS_E_INVALID, "peft: gemm_passes must be 0 (default), 1, 2 or 3");
+    const size_t M = (size_t)Mmax;
+    lw.resize(L);
+    // LoRA arena
+    offA.assign((size_t)L * NT, -1);
+    offB.assign((size_t)L * NT, -1);
+    long long off = 0;
+    for (int l = 0; l < L; l++)
+      for (int t = 0; t < NT; t++)
+        if (has(t)) {
+          int in, o;
+          dims(t, &in, &o);
+          offA[l * NT + t] = off;
+          off += (long long)in * r;
+          offB[l * NT + t] = off;
+          off += (long long)r * o;
+        }
+    nparams = off;
+    P = alloc<float>(nparams);
+    G = alloc<float>(nparams);
+    M1 = alloc<float>(nparams);
+    V1 = alloc<float>(nparams);
+    launch_fill(P, nparams, 0.0f, st);
+    launch_fill(G, nparams, 0.0f, st);
+    launch_fill(M1, nparams, 0.0f, st);
+    launch_fill(V1, nparams, 0.0f, st);
+    // activations
+    act.resize(L);
+    for (int l = 0; l < L; l++) {
+      LayerAct& a = act[l];
+      a.x = alloc<float>(M * d);
+      a.xn1 = (has(TQ) || has(TK) || has(TV)) ? alloc<float>(M * d) : nullptr;
+      a.inv1 = alloc<float>(M);
+      a.qkv = alloc<float>(M * W3);
+      a.o = alloc<float>(M * qd);
+      a.lse = alloc<float>(M * c.n_heads);
+      a.x2 = alloc<float>(M * d);
+      a.xn2 = (has(TG) || has(TU)) ? alloc<float>(M * d) : nullptr;
+      a.inv2 = alloc<float>(M);
+      a.gu = alloc<float>(M * 2 * F);
+      a.h = has(TD) ? alloc<float>(M * F) : nullptr;
+      a.u = alloc<float>(M * NT * r);
+    }
+    xfinal = alloc<float>(M * d);
+    invf = alloc<float>(M);
+    size_t hcols = std::max<size_t>({(size_t)d, (size_t)W3, (size_t)qd, 2 * (size_t)F});
+    hs.data = alloc<half_t>(M * hcols);
+    hs.rinv = alloc<float>(M);
+    hs.lo = passes > 1 ? alloc<half_t>(M * hcols) : nullptr;
+    logits = alloc<float>(M * V);
+    dl.data = alloc<half_t>(M * V);
+    dl.rinv = alloc<float>(M);
+    dl.lo = passes > 1 ? alloc<half_t>(M * V) : nullptr;
+    row_loss = alloc<float>(M);
+    loss = alloc<float>(1);
+    dx = alloc<float>(M * d);
+    dxn = alloc<float>(M * d);
+    dqkv = alloc<float>(M * W3);
+    dout = alloc<float>(M * qd);
+    dh = alloc<float>(M * F);
+    dgu = (has(TG) || has(TU)) ? alloc<float>(M * 2 * F) : nullptr;
+    du = alloc<float>(M * r);
+    dvec = alloc<float>(M * c.n_heads);
+    ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(d, F) * 4 * 8, 1ull << 30));
+    ws = alloc<float>(ws_bytes / 4);
+    ids = alloc<int32_t>(M);
+    tgts = alloc<int32_t>(M);
+    // RoPE (sin, cos) table with the reference's f32 powf/sinf/cosf (src/tensor.rs:2769-2778)
+    const int half = c.head_dim / 2;
+    std::vector<float2> tab((size_t)c.max_seq * half);
+    for (int p = 0; p < c.max_seq; p++)
+      for (int i = 0; i < half; i++) {
+        float freq = 1.0f / powf(c.rope_base, 2.0f * (float)i / (float)c.head_dim);
+        float ang = (float)p * freq;
+        tab[(size_t)p * half + i] = make_float2(sinf(ang), cosf(ang));
+      }
+    rope_tab = alloc<float2>(tab.size());
+    HOS_HIP_CHECK(hipMemcpyAsync(rope_tab, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice, st));
+    HOS_HIP_CHECK(hipStreamSynchronize(st));
+  }
+
+  void release() {
+    (void)hipStreamSynchronize(st);
+    for (auto& rc : recs) {
+      (void)hipEventDestroy(rc.e0);
+      (void)hipEventDestroy(rc.e1);
+    }
+    recs.clear();
+    for (auto& l : lw)
+      for (auto& w : l.w) free_qweight(w);
+    free_qweight(tok);
+    free_qweight(out);
+    for (void* p : allocs) (void)hipFree(p);
+    allocs.clear();
+  }
+
+  void set_f32(float** dst, const uint8_t* bytes, size_t nbytes, uint32_t type, size_t n, const std::string& name) {
+    HOS_REQUIRE(type == GGUF_F32, HOS_E_UNSUPPORTED_QUANT, "tensor '" + name + "' must be F32");
+    HOS_REQUIRE(nbytes == n * 4, HOS_E_FORMAT, "tensor '" + name + "' has " + std::to_string(nbytes) + " bytes");
+    if (!*dst) *dst = alloc<float>(n);
+    HOS_HIP_CHECK(hipMemcpyAsync(*dst, bytes, nbytes, hipMemcpyHostToDevice, st));
+    HOS_HIP_CHECK(hipStreamSynchronize(st));
+  }
+  void set_q(QWeight& w, const uint8_t* bytes, size_t nbytes, uint32_t type, size_t rows, size_t cols, size_t want_r,
+             size_t want_c, const std::string& name) {
+    HOS_REQUIRE(rows == want_r && cols == want_c, HOS_E_FORMAT,
+                "tensor '" + name + "' has shape [" + std::to_string(rows) + "," + std::to_string(cols) +
+                    "], expected [" + std::to_string(want_r) + "," + std::to_string(want_c) + "]");
+    free_qweight(w);
+    upload_qweight(st, bytes, nbytes, type, rows, cols, w);
+  }
+
+  void set_tensor(const std::string& name, const uint8_t* bytes, size_t nbytes, uint32_t type, size_t rows,
+                  size_t cols) {
+    HOS_REQUIRE(bytes != nullptr, HOS_E_INVALID, "null bytes");
+    if (name == "token_embd.weight") return set_q(tok, bytes, nbytes, type, rows, cols, V, d, name);
+    if (name == "output.weight") {
+      set_q(out, bytes, nbytes, type, rows, cols, V, d, name);
+      out_set = true;
+      return;
+    }
+    if (name == "output_norm.weight") return set_f32(&out_norm, bytes, nbytes, type, (size_t)d, name);
+    HOS_REQUIRE(name.rfind("blk.", 0) == 0, HOS_E_INVALID, "unknown tensor '" + name + "'");
+    size_t dot = name.find('.', 4);
+    HOS_REQUIRE(dot != std::string::npos, HOS_E_INVALID, "unknown tensor '" + name + "'");
+    int li = std::atoi(name.substr(4, dot - 4).c_str());
+    HOS_REQUIRE(li >= 0 && li < L, HOS_E_INVALID, "layer index out of range in '" + name + "'");
+    std::string leaf = name.substr(dot + 1);
+    LayerW& w = lw[li];
+    if (leaf == "attn_norm.weight") return set_f32(&w.attn_norm, bytes, nbytes, type, (size_t)d, name);
+    if (leaf == "ffn_norm.weight") return set_f32(&w.ffn_norm, bytes, nbytes, type, (size_t)d, name);
+    if (leaf == "attn_q.bias") return set_f32(&w.bias[0], bytes, nbytes, type, (size_t)qd, name);
+    if (leaf == "attn_k.bias") return set_f32(&w.bias[1], bytes, nbytes, type, (size_t)kvd, name);
+    if (leaf == "attn_v.bias") return set_f32(&w.bias[2], bytes, nbytes, type, (size_t)kvd, name);
+    const char* names[NT] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
+                             "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
+    for (int t = 0; t < NT; t++)
+      if (leaf == names[t]) {
+        int in, o;
+        dims(t, &in, &o);
+        return set_q(w.w[t], bytes, nbytes, type, rows, cols, (size_t)o, (size_t)in, name);
+      }
+    throw Error(HOS_E_INVALID, "unknown tensor '" + name + "'");
+  }
+
+  void check_bt(int B, int T) {
+    HOS_REQUIRE(B > 0 && T > 0 && T <= c.max_seq && B * T <= Mmax, HOS_E_INVALID,
+                "batch " + std::to_string(B) + " x seq " + std::to_string(T) + " exceeds max_batch/max_seq");
+  }
+};
+
+namespace {
+template <class F>
+int pguard(hos_peft* p, F&& f) {
+  if (!p) return HOS_E_INVALID;
+  try {
+    HOS_HIP_CHECK(hipSetDevice(hos_internal_device(p->ctx)));
+    f();
+    p->err.clear();
+    return HOS_OK;
+  } catch (const Error& e) {
+    p->err = e.what();
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    p->err = "host allocation failed";
+    return HOS_E_OOM;
+  } catch (const std::exception& e) {
+    p->err = e.what();
+    return HOS_E_DEVICE;
+  }
+}
+int lora_index(hos_peft* p, int layer, int target) {
+  HOS_REQUIRE(layer >= 0 && layer < p->L && target >= 0 && target < NT, HOS_E_INVALID, "bad layer/target");
+  HOS_REQUIRE(p->has(target), HOS_E_INVALID, "target " + std::to_string(target) + " is not adapted");
+  return layer * NT + target;
+}
+void check_ids(hos_peft* p, const int32_t* ids, int n) {
+  for (int i = 0; i < n; i++)
+    HOS_REQUIRE(ids[i] >= 0 && ids[i] < p->V, HOS_E_INVALID, "token id " + std::to_string(ids[i]) + " out of range");
+}
+}  // namespace
+
+extern "C" {
+
+int hos_peft_create(hos_ctx* ctx, const hos_peft_cfg* cfg, hos_peft** out) {
+  if (!ctx || !cfg || !out) return HOS_E_INVALID;
+  *out = nullptr;
+  auto* p = new hos_peft();
+  p->ctx = ctx;
+  int rc = pguard(p, [&] { p->init(ctx, cfg); });
+  if (rc) {
+    // keep the error readable through the context
+    std::fprintf(stderr, "hos_peft_create: %s\n", p->err.c_str());
+    p->release();
+    delete p;
+    return rc;
+  }
+  *out = p;
+  return HOS_OK;
+}
+
+void hos_peft_destroy(hos_peft* p) {
+  if (!p) return;
+  (void)hipSetDevice(hos_internal_device(p->ctx));
+  p->release();
+  delete p;
+}
+
+const char* hos_peft_last_error(const hos_peft* p) { return p ? p->err.c_str() : "null model"; }
+
+int hos_peft_set_tensor(hos_peft* p, const char* name, const uint8_t* bytes, size_t nbytes, uint32_t type, size_t rows,
+                        size_t cols) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(name != nullptr, HOS_E_INVALID, "null name");
+    p->set_tensor(name, bytes, nbytes, type, rows, cols);
+  });
+}
+
+int hos_peft_set_lora(hos_peft* p, int layer, int target, const float* A, const float* B) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(A && B, HOS_E_INVALID, "null factor");
+    int i = lora_index(p, layer, target), in, o;
+    p->dims(target, &in, &o);
+    HOS_HIP_CHECK(hipMemcpyAsync(p->P + p->offA[i], A, (size_t)in * p->r * 4, hipMemcpyHostToDevice, p->st));
+    HOS_HIP_CHECK(hipMemcpyAsync(p->P + p->offB[i], B, (size_t)p->r * o * 4, hipMemcpyHostToDevice, p->st));
+    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+  });
+}
+
+static int get_pair(hos_peft* p, const float* base, int layer, int target, float* A, float* B) {
+  return pguard(p, [&] {
+    int i = lora_index(p, layer, target), in, o;
+    p->dims(target, &in, &o);
+    if (A) HOS_HIP_CHECK(hipMemcpyAsync(A, base + p->offA[i], (size_t)in * p->r * 4, hipMemcpyDeviceToHost, p->st));
+    if (B) HOS_HIP_CHECK(hipMemcpyAsync(B, base + p->offB[i], (size_t)p->r * o * 4, hipMemcpyDeviceToHost, p->st));
+    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+  });
+}
+int hos_peft_get_lora(hos_peft* p, int layer, int target, float* A, float* B) {
+  return p ? get_pair(p, p->P, layer, target, A, B) : HOS_E_INVALID;
+}
+int hos_peft_get_lora_grad(hos_peft* p, int layer, int target, float* dA, float* dB) {
+  return p ? get_pair(p, p->G, layer, target, dA, dB) : HOS_E_INVALID;
+}
+
+int hos_peft_loss_grad(hos_peft* p, const int32_t* ids, const int32_t* targets, int B, int T, float* loss) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(ids && targets && loss, HOS_E_INVALID, "null pointer");
+    p->check_ready();
+    p->check_bt(B, T);
+    check_ids(p, ids, B * T);
+    check_ids(p, targets, B * T);
+    HOS_HIP_CHECK(hipMemcpyAsync(p->ids, ids, (size_t)B * T * 4, hipMemcpyHostToDevice, p->st));
+    HOS_HIP_CHECK(hipMemcpyAsync(p->tgts, targets, (size_t)B * T * 4, hipMemcpyHostToDevice, p->st));
+    p->forward(B, T, false);
+    p->loss_backward(B, T);
+    HOS_HIP_CHECK(hipMemcpyAsync(loss, p->loss, 4, hipMemcpyDeviceToHost, p->st));
+    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+  });
+}
+
+int hos_peft_adamw(hos_peft* p, float lr, float wd) {
+  return pguard(p, [&] {
+    p->adamw(lr, wd);
+    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+  });
+}
+
+int hos_peft_step_dev(hos_peft* p, const int32_t* ids_dev, const int32_t* targets_dev, int B, int T, float lr, float wd,
+                      float* loss_dev) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(ids_dev && targets_dev, HOS_E_INVALID, "null pointer");
+    p->check_ready();
+    p->check_bt(B, T);
+    HOS_HIP_CHECK(hipMemcpyAsync(p->ids, ids_dev, (size_t)B * T * 4, hipMemcpyDeviceToDevice, p->st));
+    HOS_HIP_CHECK(hipMemcpyAsync(p->tgts, targets_dev, (size_t)B * T * 4, hipMemcpyDeviceToDevice, p->st));
+    p->forward(B, T, false);
+    p->loss_backward(B, T);
+    p->adamw(lr, wd);
+    if (loss_dev) HOS_HIP_CHECK(hipMemcpyAsync(loss_dev, p->loss, 4, hipMemcpyDeviceToDevice, p->st));
+  });
+}
+
+int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(ids && out, HOS_E_INVALID, "null pointer");
+    p->check_ready();
+    p->check_bt(1, T);
+    check_ids(p, ids, T);
+    HOS_HIP_CHECK(hipMemcpyAsync(p->ids, ids, (size_t)T * 4, hipMemcpyHostToDevice, p->st));
+    p->forward(1, T, true);
+    HOS_HIP_CHECK(hipMemcpyAsync(out, p->logits, (size_t)T * p->V * 4, hipMemcpyDeviceToHost, p->st));
+    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+  });
+}
+
+int hos_peft_profile(hos_peft* p, int enable) {
+  return pguard(p, [&] {
+    p->collect_prof();
+    p->prof = enable != 0;
+    if (enable) p->acc.clear();
+  });
+}
+
+int hos_peft_kernel_stats(hos_peft* p, const char* cls, long long* launches, double* total_ms, double* flops,
+                          double* bytes) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(cls != nullptr, HOS_E_INVALID, "null class");
+    p->collect_prof();
+    auto it = p->acc.find(cls);
+    ProfAcc a = it == p->acc.end() ? ProfAcc{} : it->second;
+    if (launches) *launches = a.launches;
+    if (total_ms) *total_ms = a.ms;
+    if (flops) *flops = a.flops;
+    if (bytes) *bytes = a.bytes;
+  });
+}
+
+}  // extern "C"

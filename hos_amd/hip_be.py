@@ -68,6 +68,10 @@ class Gpu:
     def synchronize(self):
         self._chk(lib().hos_hip_synchronize(self.h))
 
+    def set_gemm_passes(self, passes):
+        """qGEMM precision: 1 fp16 pass, 2 (activation hi+lo), 3 (activation and weight hi+lo)."""
+        self._chk(lib().hos_hip_set_gemm_passes(self.h, passes))
+
     # ---- keyed f32 GEMMs (src/metal_be.rs:2338-2366, 2434-2446) ----
     def matmul_f32_keyed(self, a, m, k, b, n, b_key=None):
         a, b = _f32(a), _f32(b)

@@ -1,0 +1,145 @@
+"""Host-side mirror of HOS's LoRA training API (src/peft.rs PeftModel, src/tensor.rs AdamW) over the C ABI.
+
+``PeftModel.loss_grad(ids, targets)`` is one optimizer step's gradient (zero_grad, then B sequences with
+``loss·(1/B)`` backward, src/main.rs:2583-2596); ``adamw(lr, wd)`` is ``AdamW::step``; ``step`` does both.
+The model lives on one device; the host only enqueues.
+"""
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from ._lib import PeftCfg, lib
+from .hip_be import Gpu, HosError
+
+TARGETS = ("q", "k", "v", "o", "gate", "up", "down")
+TARGET_BITS = {t: 1 << i for i, t in enumerate(TARGETS)}
+
+
+@dataclass
+class ModelConfig:
+    """src/model.rs:622-644 (Config) + src/peft.rs:121-126 (PeftCfg) + the batch shape."""
+    name: str
+    n_layers: int
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn_dim: int
+    vocab: int
+    rms_eps: float = 1e-5
+    rope_base: float = 10000.0
+    rope_neox: bool = False
+    attn_bias: bool = False
+    tied: bool = True
+    lora_rank: int = 8
+    lora_alpha: float = 16.0
+    lora_targets: tuple = ("q", "v")
+    quant: int = 8            # GGUF type of the linear weights
+    head_quant: int = 8       # GGUF type of token_embd / output
+    batch: int = 1
+    seq: int = 128
+    lr: float = 1e-3
+    gemm_passes: int = 0      # qGEMM precision passes (0 = library default)
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def target_mask(self):
+        m = 0
+        for t in self.lora_targets:
+            m |= TARGET_BITS[t]
+        return m
+
+    def target_dims(self, t):
+        """(in, out) of the projection adapted by target t."""
+        d, qd, kvd, f = self.dim, self.n_heads * self.head_dim, self.n_kv_heads * self.head_dim, self.ffn_dim
+        return {"q": (d, qd), "k": (d, kvd), "v": (d, kvd), "o": (qd, d), "gate": (d, f), "up": (d, f),
+                "down": (f, d)}[t]
+
+
+class PeftModel:
+    def __init__(self, gpu: Gpu, cfg: ModelConfig, max_batch=None, max_seq=None):
+        self.gpu, self.cfg = gpu, cfg
+        c = PeftCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
+                    cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank,
+                    cfg.lora_alpha, cfg.target_mask, max_batch or cfg.batch, max_seq or cfg.seq, cfg.gemm_passes)
+        h = ctypes.c_void_p()
+        rc = lib().hos_peft_create(gpu.h, ctypes.byref(c), ctypes.byref(h))
+        if rc:
+            raise HosError(rc, "hos_peft_create failed (see stderr)")
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().hos_peft_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def _chk(self, rc):
+        if rc:
+            raise HosError(rc, lib().hos_peft_last_error(self.h).decode())
+
+    def set_tensor(self, name, raw, ggml_type, rows, cols):
+        raw = np.ascontiguousarray(raw).view(np.uint8).ravel()
+        self._chk(lib().hos_peft_set_tensor(self.h, name.encode(), raw.ctypes.data, raw.size, ggml_type, rows, cols))
+
+    def load(self, tensors):
+        for name, (raw, t, rows, cols) in tensors.items():
+            self.set_tensor(name, raw, t, rows, cols)
+
+    def set_lora(self, layer, target, A, B):
+        ti = TARGETS.index(target) if isinstance(target, str) else target
+        A = np.ascontiguousarray(A, np.float32)
+        B = np.ascontiguousarray(B, np.float32)
+        self._chk(lib().hos_peft_set_lora(self.h, layer, ti, A.ctypes.data, B.ctypes.data))
+
+    def _pair(self, fn, layer, target):
+        t = TARGETS[target] if isinstance(target, int) else target
+        i, o = self.cfg.target_dims(t)
+        A = np.empty((i, self.cfg.lora_rank), np.float32)
+        B = np.empty((self.cfg.lora_rank, o), np.float32)
+        self._chk(fn(self.h, layer, TARGETS.index(t), A.ctypes.data, B.ctypes.data))
+        return A, B
+
+    def get_lora(self, layer, target):
+        return self._pair(lib().hos_peft_get_lora, layer, target)
+
+    def get_lora_grad(self, layer, target):
+        return self._pair(lib().hos_peft_get_lora_grad, layer, target)
+
+    def loss_grad(self, ids, targets):
+        ids = np.ascontiguousarray(ids, np.int32)
+        tg = np.ascontiguousarray(targets, np.int32)
+        B, T = ids.shape
+        loss = ctypes.c_float()
+        self._chk(lib().hos_peft_loss_grad(self.h, ids.ctypes.data, tg.ctypes.data, B, T, ctypes.byref(loss)))
+        return loss.value
+
+    def adamw(self, lr, wd=0.0):
+        self._chk(lib().hos_peft_adamw(self.h, lr, wd))
+
+    def step(self, ids, targets, lr, wd=0.0):
+        loss = self.loss_grad(ids, targets)
+        self.adamw(lr, wd)
+        return loss
+
+    def step_dev(self, ids_dev, tgt_dev, B, T, lr, wd=0.0, loss_dev=None):
+        self._chk(lib().hos_peft_step_dev(self.h, ids_dev, tgt_dev, B, T, lr, wd, loss_dev))
+
+    def logits(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32).ravel()
+        out = np.empty((ids.size, self.cfg.vocab), np.float32)
+        self._chk(lib().hos_peft_logits(self.h, ids.ctypes.data, ids.size, out.ctypes.data))
+        return out
+
+    def profile(self, on):
+        self._chk(lib().hos_peft_profile(self.h, int(on)))
+
+    def kernel_stats(self, cls):
+        n = ctypes.c_longlong()
+        ms, fl, by = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        self._chk(lib().hos_peft_kernel_stats(self.h, cls.encode(), ctypes.byref(n), ctypes.byref(ms),
+                                              ctypes.byref(fl), ctypes.byref(by)))
+        return {"launches": n.value, "ms": ms.value, "flops": fl.value, "bytes": by.value}

@@ -95,6 +95,10 @@ int hos_hip_time_qgemm(hos_ctx* ctx, int which, uint64_t key, const float* in_de
  * Q6_K :426-495), run on the device; byte-identical to the reference encoders.
  * x: n floats (host), out: bytes_for(type, n) bytes (host). */
 int hos_hip_quantize(hos_ctx* ctx, const float* x, size_t n, uint32_t ggml_type, uint8_t* out);
+/* Precision of this context's qGEMMs: 1 = single fp16 pass (both operands rounded to 11 bits),
+ * 2 = activation carried as fp16 hi + lo (2 MFMA passes), 3 = weight split too (3 passes). Default 1.
+ * (The reference has no counterpart: its GPU GEMMs are f32, src/metal_be.rs:1095-1142.) */
+int hos_hip_set_gemm_passes(hos_ctx* ctx, int passes);
 /* bytes_for (src/gguf.rs:548-561); 0 for an unsupported type. */
 size_t hos_hip_bytes_for(uint32_t ggml_type, size_t n);
 
@@ -127,6 +131,7 @@ typedef struct {
   float lora_alpha;
   uint32_t lora_targets;
   int max_batch, max_seq; /* sizes the device-resident activation arena */
+  int gemm_passes;        /* qGEMM precision passes, as hos_hip_set_gemm_passes; 0 = default (3) */
 } hos_peft_cfg;
 
 typedef struct hos_peft hos_peft;
