@@ -1,0 +1,174 @@
+#!/usr/bin/env python3
+"""Benchmark: LoRA fine-tune tokens/s (fwd + bwd + AdamW) on a quantized base, one MI355X.
+
+Workload: Qwen2.5-0.5B architecture (24 layers, d 896, 14/2 heads, QKV bias,
+SwiGLU 4864, vocab 151936, NEOX RoPE 1e6), random-init ~N(0, 0.02) quantized on the device with HOS's own
+quantizers to Q4_K (Q8_0 for the 896-wide rows a 256-element super-block cannot tile), LoRA r=16 on all
+seven projections, batch 4 x 512 uniform-random tokens, AdamW lr 1e-4. One step = one optimizer step over
+the whole batch; inputs are resident in HBM before the timed region.
+
+Also reported: the dominant kernel against its roofline (HIP events around every launch inside the timed
+region), the isolated configs[1] dX GEMM (4096^3, Q4_K) against bf16/fp16 MFMA peak, and the CPU
+baseline (the oracle's restatement of HOS's CPU training path on this host's cores, a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+PEAK_HBM_GBS = 8000.0
+METRIC = "fine-tune tokens/sec (fwd+bwd+AdamW) on Q4_K base; dX-GEMM % MFMA peak"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="qwen2.5-0.5b")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline sample")
+    ap.add_argument("--cpu-seq", type=int, default=128, help="tokens in the CPU baseline sample")
+    return ap.parse_args()
+
+
+def dx_gemm_probe(gpu):
+    """dX = dY·deq(W), dY [4096,4096] ~N(0,1e-2), W [4096,4096] ~N(0,0.02) -> Q4_K."""
+    from hos_amd.hip_be import GGML_Q4_K
+    T = N = K = 4096
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    gpu.upload_quant(0xD0, gpu.quantize(w, GGML_Q4_K), GGML_Q4_K, N, K)
+    dy = (rng.standard_normal((T, N), dtype=np.float32) * np.float32(1e-2))
+    din, dout = gpu.alloc(T * N * 4), gpu.alloc(T * K * 4)
+    gpu.h2d(din, dy)
+    out = {}
+    for passes in (1, 3):
+        gpu.set_gemm_passes(passes)
+        ms = gpu.time_qgemm(1, 0xD0, din, T, dout, 20)
+        tf = 2.0 * T * N * K / (ms * 1e-3) / 1e12
+        out[f"passes{passes}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                                  "frac_of_peak": round(tf / PEAK_MFMA_TFLOPS, 4)}
+    gpu.set_gemm_passes(1)
+    gpu.free(din)
+    gpu.free(dout)
+    gpu.evict(0xD0)
+    return out
+
+
+def cpu_baseline(cfg, tensors, seq):
+    """The oracle (C++ restatement of HOS's CPU path, OpenMP row-parallel) on one sequence of `seq` tokens:
+    forward + backward + AdamW, timed on this host's cores."""
+    import types
+    from oracle import binding as o
+    from hos_amd import synth
+    oc = types.SimpleNamespace(**{k: getattr(cfg, k) for k in (
+        "n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "rms_eps", "rope_base",
+        "rope_neox", "attn_bias", "lora_rank", "lora_alpha")})
+    oc.lora_targets = cfg.target_mask
+    m = o.OracleModel(oc)
+    for name, (raw, t, rows, cols) in tensors.items():
+        m.set_tensor(name, raw, t, rows, cols)
+    for (l, t), (A, B) in synth.lora_init(cfg, seed=5).items():
+        m.set_lora(l, ("q", "k", "v", "o", "gate", "up", "down").index(t), A, B)
+    ids, tg = synth.tokens(cfg, 1, seq, seed=8)
+    t0 = time.perf_counter()
+    m.loss_grad(ids, tg)
+    m.adamw(cfg.lr, 0.0)
+    dt = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+    return {"value": round(seq / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"1 sequence x {seq} tokens (fwd+bwd+AdamW), {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards as data parallel over sequences, described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    from hos_amd import Gpu, synth
+    from hos_amd.peft import PeftModel
+
+    cfg = synth.CONFIGS[args.config]
+    gpu = Gpu(0)
+    t_setup = time.perf_counter()
+    tensors = synth.build_tensors(gpu, cfg, seed=1234)
+    pm = PeftModel(gpu, cfg)
+    pm.load(tensors)
+    for (l, t), (A, B) in synth.lora_init(cfg, seed=5).items():
+        pm.set_lora(l, t, A, B)
+    B, T = cfg.batch, cfg.seq
+    ids, tg = synth.tokens(cfg, B, T, seed=8)
+    ids_dev, tg_dev, loss_dev = gpu.alloc(ids.nbytes), gpu.alloc(tg.nbytes), gpu.alloc(4)
+    gpu.h2d(ids_dev, ids)
+    gpu.h2d(tg_dev, tg)
+    setup_s = time.perf_counter() - t_setup
+    print(f"[bench] setup {setup_s:.1f}s", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        pm.step_dev(ids_dev, tg_dev, B, T, cfg.lr, 0.0, loss_dev)
+    gpu.synchronize()
+
+    pm.profile(True)
+    gpu.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        pm.step_dev(ids_dev, tg_dev, B, T, cfg.lr, 0.0, loss_dev)
+    gpu.synchronize()
+    dt = time.perf_counter() - t0
+    loss = float(gpu.d2h(loss_dev, (1,), np.float32)[0])
+    classes = ["qgemm_fwd", "qgemm_dx", "lora", "attn_fwd", "attn_bwd", "rmsnorm", "swiglu", "rope", "ce", "adamw",
+               "embed", "convert"]
+    stats = {c: pm.kernel_stats(c) for c in classes}
+    pm.profile(False)
+
+    toks = B * T * args.steps
+    value = toks / dt
+    ms_step = dt / args.steps * 1e3
+    f_tok = synth.algorithmic_flops_per_token(cfg, T)
+    kernel_ms = {c: round(s["ms"] / args.steps, 3) for c, s in stats.items()}
+    dom = max(stats, key=lambda c: stats[c]["ms"])
+    ds = stats[dom]
+    avg_launch_s = ds["ms"] / max(ds["launches"], 1) * 1e-3
+    if ds["flops"] > 0:
+        achieved = ds["flops"] / max(ds["launches"], 1) / avg_launch_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": None, "kernel": dom,
+                "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"] // args.steps}
+    else:
+        achieved = ds["bytes"] / max(ds["launches"], 1) / avg_launch_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom,
+                "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"] // args.steps}
+
+    dx = dx_gemm_probe(gpu)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, tensors, args.cpu_seq)
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16 MFMA x3 (hi/lo split) + f32", "data": "synthetic",
+        "config": {"workload": f"{cfg.name} LoRA r{cfg.lora_rank} on q,k,v,o,gate,up,down; Q4_K base "
+                               "(Q8_0 for 896-wide rows); AdamW", "global_batch": B, "seq_len": T,
+                   "parallelism": "dp1", "gemm_passes": 3},
+        "roofline": roof,
+        "mfma_roofline_frac_step": round(value * f_tok / 1e12 / PEAK_MFMA_TFLOPS, 4),
+        "dx_gemm_cfg1_4096cubed_q4k": dx,
+        "cpu_baseline": cpu,
+        "gpu_over_cpu": round(value / cpu["value"], 1) if cpu else None,
+        "kernel_ms_per_step": kernel_ms,
+        "loss": round(loss, 5),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,4 +1,5 @@
-// Causal GQA softmax attention, forward and backward, without materialising [H, T, T].
+// Causal GQA softmax attention, forward and backward, on fp32 MFMA (v_mfma_f32_32x32x2f32), without
+// materialising [H, T, T].
 //
 // Semantics of PeftModel::forward (src/peft.rs:479-489, 530-553): scores = (q·kᵀ)·(1/√hd), the
 // strictly-upper triangle masked (−1e9 there gives exactly zero probability, as skipping does),
@@ -6,87 +7,128 @@
 // (repeat_interleave_dim0, src/tensor.rs:2819-2841). Backward = the bmm/softmax/repeat VJPs
 // (src/tensor.rs:2260-2272, :2481-2490, :2831-2840) in flash form: P is recomputed from the saved
 // log-sum-exp, dS = P∘(dP − rowsum(dO∘O)), and GQA gradients are summed over the group.
+// 1/√64 = 2^-3 is folded into q exactly.
 //
-// Layout: qkv [M, ld] rows m = b·T + t, q heads at cols h·64, k at kcol + g·64, v at vcol + g·64.
-// f32 throughout; 64×64 tiles in LDS; 4 threads per row (each owns 16 of the 64 columns).
+// MFMA layout used throughout (32×32 tiles): the D matrix X[i][j] sits with column j = lane%32 and
+// rows i = 8·(r/4) + 4·(lane/32) + r%4 in register r. Read back as an A operand, register r of that
+// layout supplies row (lane%32) of Xᵀ at contraction index κ(r, lane/32) = 8·(r/4) + 4·(lane/32) + r%4,
+// so a score tile feeds the next MFMA straight from registers provided the other operand is gathered
+// in the same κ order. Per wave: 32 queries (or keys) × 64 head dims; one wave per workgroup.
 #include "fused.hpp"
 
 namespace hos {
 namespace {
 
-constexpr int HD = 64, BLK = 64, LP = HD + 1;  // padded LDS row
+constexpr int HD = 64, TB = 32, LP = HD + 1;  // tile rows, padded LDS row (floats)
 
-__global__ void __launch_bounds__(256) attn_fwd_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
-                                                       int T, int nh, int group, float scale, float* __restrict__ o,
-                                                       long long ldo, float* __restrict__ lse) {
-  __shared__ float Ks[BLK][LP];
-  __shared__ float Vs[BLK][LP];
-  __shared__ float Ps[BLK][BLK + 1];
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int g = h / group;
-  const int tid = threadIdx.x, i = tid >> 2, c = tid & 3;
-  const int qi = qb * BLK + i;  // query position
-  const bool valid = qi < T;
-  const long long rowq = (long long)b * T + (valid ? qi : T - 1);
-  float q[HD];
-#pragma unroll
-  for (int d = 0; d < HD; d++) q[d] = qkv[rowq * ld + h * HD + d];
-  float mrun = -INFINITY, lrun = 0.0f, acc[16];
-#pragma unroll
-  for (int d = 0; d < 16; d++) acc[d] = 0.0f;
+__device__ __forceinline__ int kap(int s, int h) { return 8 * (s >> 2) + 4 * h + (s & 3); }
 
-  for (int kb = 0; kb <= qb; kb++) {
+// Load rows [r0, r0+32) × 64 cols (row stride ld, col offset col) into LDS [32][LP], clamping rows ≥ T
+// to T-1 (masked later); scaled by `mul`.
+__device__ __forceinline__ void load_tile(float (*dst)[LP], const float* __restrict__ src, long long base_row, int r0,
+                                          int T, long long ld, int col, float mul) {
+  const int lane = threadIdx.x;
+  for (int e = lane; e < TB * HD / 4; e += 64) {
+    int r = e / (HD / 4), c4 = e % (HD / 4);
+    int t = r0 + r;
+    long long row = base_row + (t < T ? t : T - 1);
+    float4 v = *(const float4*)(src + row * ld + col + 4 * c4);
+    dst[r][4 * c4] = v.x * mul;
+    dst[r][4 * c4 + 1] = v.y * mul;
+    dst[r][4 * c4 + 2] = v.z * mul;
+    dst[r][4 * c4 + 3] = v.w * mul;
+  }
+}
+
+// B-operand fragment of a [32 rows][64] matrix held in registers: frag[s] = X[row0 + lane%32][2s + lane/32].
+__device__ __forceinline__ void load_frag(float* frag, const float* __restrict__ src, long long base_row, int r0,
+                                          int T, long long ld, int col, float mul) {
+  const int lane = threadIdx.x;
+  int t = r0 + (lane & 31);
+  long long row = base_row + (t < T ? t : T - 1);
+  const float* p = src + row * ld + col + (lane >> 5);
+#pragma unroll
+  for (int s = 0; s < 32; s++) frag[s] = p[2 * s] * mul;
+}
+
+__global__ void __launch_bounds__(64) attn_fwd_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+                                                      int T, int nh, int group, float* __restrict__ o, long long ldo,
+                                                      float* __restrict__ lse) {
+  __shared__ float Ks[TB][LP];
+  __shared__ float Vs[TB][LP];
+  __shared__ float xch[TB];
+  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
+  const int lane = threadIdx.x, hl = lane >> 5, q0 = qb * TB;
+  const int myq = q0 + (lane & 31);  // this lane's query in the Sᵀ layout
+  const long long base = (long long)b * T;
+  float qf[32];
+  load_frag(qf, qkv, base, q0, T, ld, h * HD, 0.125f);
+  f16v O0, O1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) O0[r] = O1[r] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  const int nkb = min(qb + 1, (T + TB - 1) / TB);
+  for (int kb = 0; kb < nkb; kb++) {
+    const int k0 = kb * TB;
     __syncthreads();
-    for (int e = tid; e < BLK * HD; e += 256) {
-      int r = e / HD, d = e % HD;
-      int kt = kb * BLK + r;
-      long long row = (long long)b * T + (kt < T ? kt : T - 1);
-      Ks[r][d] = qkv[row * ld + kcol + g * HD + d];
-      Vs[r][d] = qkv[row * ld + vcol + g * HD + d];
-    }
+    load_tile(Ks, qkv, base, k0, T, ld, kcol + g * HD, 1.0f);
+    load_tile(Vs, qkv, base, k0, T, ld, vcol + g * HD, 1.0f);
     __syncthreads();
-    float s[16], mloc = -INFINITY;
+    f16v S;
 #pragma unroll
-    for (int jj = 0; jj < 16; jj++) {
-      int j = c * 16 + jj, kt = kb * BLK + j;
-      float dot = 0.0f;
+    for (int r = 0; r < 16; r++) S[r] = 0.0f;
 #pragma unroll
-      for (int d = 0; d < HD; d++) dot += q[d] * Ks[j][d];
-      float sv = dot * scale;
-      if (kt > qi || kt >= T) sv = -INFINITY;
-      s[jj] = sv;
-      mloc = fmaxf(mloc, sv);
+    for (int s = 0; s < 32; s++) S = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[lane & 31][2 * s + hl], qf[s], S, 0, 0, 0);
+    // S[r] = score(key k0 + kap(r, hl), query myq)
+    float mb = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      int key = k0 + kap(r, hl);
+      if (key > myq || key >= T) S[r] = -INFINITY;
+      mb = fmaxf(mb, S[r]);
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 1));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 2));
-    float mnew = fmaxf(mrun, mloc);
-    float alpha = (mrun == -INFINITY) ? 0.0f : expf(mrun - mnew);
-    float psum = 0.0f;
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    const float mn = fmaxf(m, mb);
+    const float alpha = (m == -INFINITY) ? 0.0f : expf(m - mn);
+    float ps = 0.0f;
+    float p[16];
 #pragma unroll
-    for (int jj = 0; jj < 16; jj++) {
-      float p = (s[jj] == -INFINITY) ? 0.0f : expf(s[jj] - mnew);
-      Ps[i][c * 16 + jj] = p;
-      psum += p;
+    for (int r = 0; r < 16; r++) {
+      p[r] = (S[r] == -INFINITY) ? 0.0f : expf(S[r] - mn);
+      ps += p[r];
     }
-    psum += __shfl_xor(psum, 1);
-    psum += __shfl_xor(psum, 2);
-    lrun = lrun * alpha + psum;
-    mrun = mnew;
+    ps += __shfl_xor(ps, 32);
+    l = l * alpha + ps;
+    m = mn;
+    // rescale O rows (queries q0 + kap(r, hl) in the O layout) by their alpha
+    if (lane < 32) xch[lane] = alpha;
     __syncthreads();
 #pragma unroll
-    for (int d = 0; d < 16; d++) acc[d] *= alpha;
-    for (int j = 0; j < BLK; j++) {
-      float p = Ps[i][j];
+    for (int r = 0; r < 16; r++) {
+      float a = xch[kap(r, hl)];
+      O0[r] *= a;
+      O1[r] *= a;
+    }
 #pragma unroll
-      for (int d = 0; d < 16; d++) acc[d] += p * Vs[j][c * 16 + d];
+    for (int s = 0; s < 16; s++) {
+      const float* vr = Vs[kap(s, hl)];
+      O0 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], vr[lane & 31], O0, 0, 0, 0);
+      O1 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], vr[32 + (lane & 31)], O1, 0, 0, 0);
     }
   }
-  if (!valid) return;
-  float inv = 1.0f / lrun;
-  float* orow = o + ((long long)b * T + qi) * ldo + h * HD + c * 16;
+  __syncthreads();
+  if (lane < 32) xch[lane] = l;
+  __syncthreads();
+  if (lane < 32 && myq < T) lse[((long long)b * nh + h) * T + myq] = m + logf(l);
 #pragma unroll
-  for (int d = 0; d < 16; d++) orow[d] = acc[d] * inv;
-  if (c == 0) lse[((long long)b * nh + h) * T + qi] = mrun + logf(lrun);
+  for (int r = 0; r < 16; r++) {
+    int q = q0 + kap(r, hl);
+    if (q >= T) continue;
+    float inv = 1.0f / xch[kap(r, hl)];
+    float* orow = o + (base + q) * ldo + h * HD;
+    orow[lane & 31] = O0[r] * inv;
+    orow[32 + (lane & 31)] = O1[r] * inv;
+  }
 }
 
 // Dvec[b,h,t] = Σ_d dO·O over the head's 64 columns.
@@ -104,149 +146,162 @@ __global__ void attn_dvec_kernel(const float* __restrict__ o, const float* __res
   dvec[i] = s;
 }
 
-// dQ for one (query block, head): dQ = scale·Σ_j dS[i][j]·K[j].
-__global__ void __launch_bounds__(256) attn_dq_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
-                                                      const float* __restrict__ dout, long long ldd,
-                                                      const float* __restrict__ lse, const float* __restrict__ dvec,
-                                                      int T, int nh, int group, float scale, float* __restrict__ dq,
-                                                      long long ldq) {
-  __shared__ float Ks[BLK][LP];
-  __shared__ float Vs[BLK][LP];
-  __shared__ float Ss[BLK][BLK + 1];
+// dQ for 32 queries of head h: Sᵀ and dPᵀ with lanes on queries, dQ = (dS·K)·2^-3.
+__global__ void __launch_bounds__(64) attn_dq_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+                                                     const float* __restrict__ dout, long long ldd,
+                                                     const float* __restrict__ lse, const float* __restrict__ dvec,
+                                                     int T, int nh, int group, float* __restrict__ dq,
+                                                     long long ldq) {
+  __shared__ float Ks[TB][LP];
+  __shared__ float Vs[TB][LP];
   const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
-  const int tid = threadIdx.x, i = tid >> 2, c = tid & 3;
-  const int qi = qb * BLK + i;
-  const bool valid = qi < T;
-  const long long row = (long long)b * T + (valid ? qi : T - 1);
-  float q[HD], dov[HD];
-#pragma unroll
-  for (int d = 0; d < HD; d++) {
-    q[d] = qkv[row * ld + h * HD + d];
-    dov[d] = dout[row * ldd + h * HD + d];
-  }
-  const long long si = ((long long)b * nh + h) * T + (valid ? qi : T - 1);
+  const int lane = threadIdx.x, hl = lane >> 5, q0 = qb * TB;
+  const int myq = q0 + (lane & 31);
+  const long long base = (long long)b * T;
+  float qf[32], df[32];
+  load_frag(qf, qkv, base, q0, T, ld, h * HD, 0.125f);
+  load_frag(df, dout, base, q0, T, ldd, h * HD, 1.0f);
+  const long long si = ((long long)b * nh + h) * T + (myq < T ? myq : T - 1);
   const float L = lse[si], Dv = dvec[si];
-  float acc[16];
+  f16v A0, A1;
 #pragma unroll
-  for (int d = 0; d < 16; d++) acc[d] = 0.0f;
-  for (int kb = 0; kb <= qb; kb++) {
+  for (int r = 0; r < 16; r++) A0[r] = A1[r] = 0.0f;
+  const int nkb = min(qb + 1, (T + TB - 1) / TB);
+  for (int kb = 0; kb < nkb; kb++) {
+    const int k0 = kb * TB;
     __syncthreads();
-    for (int e = tid; e < BLK * HD; e += 256) {
-      int r = e / HD, d = e % HD;
-      int kt = kb * BLK + r;
-      long long rr = (long long)b * T + (kt < T ? kt : T - 1);
-      Ks[r][d] = qkv[rr * ld + kcol + g * HD + d];
-      Vs[r][d] = qkv[rr * ld + vcol + g * HD + d];
+    load_tile(Ks, qkv, base, k0, T, ld, kcol + g * HD, 1.0f);
+    load_tile(Vs, qkv, base, k0, T, ld, vcol + g * HD, 1.0f);
+    __syncthreads();
+    f16v S, dP;
+#pragma unroll
+    for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 32; s++) {
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[lane & 31][2 * s + hl], qf[s], S, 0, 0, 0);
+      dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[lane & 31][2 * s + hl], df[s], dP, 0, 0, 0);
     }
-    __syncthreads();
-#pragma unroll 4
-    for (int jj = 0; jj < 16; jj++) {
-      int j = c * 16 + jj, kt = kb * BLK + j;
-      float dot = 0.0f, dp = 0.0f;
+    float ds[16];
 #pragma unroll
-      for (int d = 0; d < HD; d++) {
-        dot += q[d] * Ks[j][d];
-        dp += dov[d] * Vs[j][d];
-      }
-      float p = (kt > qi || kt >= T) ? 0.0f : expf(dot * scale - L);
-      Ss[i][j] = p * (dp - Dv);
+    for (int r = 0; r < 16; r++) {
+      int key = k0 + kap(r, hl);
+      float pv = (key > myq || key >= T || myq >= T) ? 0.0f : expf(S[r] - L);
+      ds[r] = pv * (dP[r] - Dv);
     }
-    __syncthreads();
-    for (int j = 0; j < BLK; j++) {
-      float ds = Ss[i][j];
 #pragma unroll
-      for (int d = 0; d < 16; d++) acc[d] += ds * Ks[j][c * 16 + d];
+    for (int s = 0; s < 16; s++) {
+      const float* kr = Ks[kap(s, hl)];
+      A0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], kr[lane & 31], A0, 0, 0, 0);
+      A1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], kr[32 + (lane & 31)], A1, 0, 0, 0);
     }
   }
-  if (!valid) return;
-  float* out = dq + row * ldq + h * HD + c * 16;
 #pragma unroll
-  for (int d = 0; d < 16; d++) out[d] = acc[d] * scale;
+  for (int r = 0; r < 16; r++) {
+    int q = q0 + kap(r, hl);
+    if (q >= T) continue;
+    float* out = dq + (base + q) * ldq + h * HD;
+    out[lane & 31] = A0[r] * 0.125f;
+    out[32 + (lane & 31)] = A1[r] * 0.125f;
+  }
 }
 
-// dK, dV for one (key block, kv head), summed over the group's query heads and all query blocks ≥ kb.
-__global__ void __launch_bounds__(256) attn_dkdv_kernel(const float* __restrict__ qkv, long long ld, int kcol,
-                                                        int vcol, const float* __restrict__ dout, long long ldd,
-                                                        const float* __restrict__ lse,
-                                                        const float* __restrict__ dvec, int T, int nh, int group,
-                                                        float scale, float* __restrict__ dkv, long long ldk) {
-  __shared__ float Qs[BLK][LP];
-  __shared__ float Ds[BLK][LP];
-  __shared__ float Ls[BLK], Dvs[BLK];
-  const int kb = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, j = tid >> 2, c = tid & 3;
-  const int kt = kb * BLK + j;
-  const bool valid = kt < T;
-  const long long row = (long long)b * T + (valid ? kt : T - 1);
-  float k[HD], v[HD];
+// dK, dV for 32 keys against query head h (kv head g = h / group): S and dP with lanes on keys.
+// With group > 1 each head's contribution goes to part[(b·T + key)][h][2·64] and attn_group_sum adds
+// the group in head order; with group == 1 it is written in place.
+__global__ void __launch_bounds__(64) attn_dkdv_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+                                                       const float* __restrict__ dout, long long ldd,
+                                                       const float* __restrict__ lse,
+                                                       const float* __restrict__ dvec, int T, int nh, int group,
+                                                       float* __restrict__ dkv, long long ldk,
+                                                       float* __restrict__ part) {
+  __shared__ float Qs[TB][LP];
+  __shared__ float Ds[TB][LP];
+  __shared__ float Ls[TB], Dvs[TB];
+  const int kb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
+  const int lane = threadIdx.x, hl = lane >> 5, k0 = kb * TB;
+  const int mykey = k0 + (lane & 31);
+  const long long base = (long long)b * T;
+  float kf[32], vf[32];
+  load_frag(kf, qkv, base, k0, T, ld, kcol + g * HD, 1.0f);
+  load_frag(vf, qkv, base, k0, T, ld, vcol + g * HD, 1.0f);
+  f16v K0, K1, V0, V1;
 #pragma unroll
-  for (int d = 0; d < HD; d++) {
-    k[d] = qkv[row * ld + kcol + g * HD + d];
-    v[d] = qkv[row * ld + vcol + g * HD + d];
-  }
-  float dk[16], dv[16];
-#pragma unroll
-  for (int d = 0; d < 16; d++) dk[d] = dv[d] = 0.0f;
-  const int nqb = (T + BLK - 1) / BLK;
-  for (int hh = 0; hh < group; hh++) {
-    const int h = g * group + hh;
+  for (int r = 0; r < 16; r++) K0[r] = K1[r] = V0[r] = V1[r] = 0.0f;
+  const int nqb = (T + TB - 1) / TB;
+  {
     for (int qb = kb; qb < nqb; qb++) {
+      const int q0 = qb * TB;
       __syncthreads();
-      for (int e = tid; e < BLK * HD; e += 256) {
-        int r = e / HD, d = e % HD;
-        int qt = qb * BLK + r;
-        long long rr = (long long)b * T + (qt < T ? qt : T - 1);
-        Qs[r][d] = qkv[rr * ld + h * HD + d];
-        Ds[r][d] = dout[rr * ldd + h * HD + d];
-      }
-      if (tid < BLK) {
-        int qt = qb * BLK + tid;
+      load_tile(Qs, qkv, base, q0, T, ld, h * HD, 0.125f);
+      load_tile(Ds, dout, base, q0, T, ldd, h * HD, 1.0f);
+      if (lane < TB) {
+        int qt = q0 + lane;
         long long si = ((long long)b * nh + h) * T + (qt < T ? qt : T - 1);
-        Ls[tid] = lse[si];
-        Dvs[tid] = dvec[si];
+        Ls[lane] = lse[si];
+        Dvs[lane] = dvec[si];
       }
       __syncthreads();
-      // this thread's 16 queries i = c·16 .. c·16+15 against key j
-      float pl[16], sl[16];
+      f16v S, dP;
 #pragma unroll
-      for (int ii = 0; ii < 16; ii++) {
-        int i = c * 16 + ii, qt = qb * BLK + i;
-        float dot = 0.0f, dp = 0.0f;
+      for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
 #pragma unroll
-        for (int d = 0; d < HD; d++) {
-          dot += Qs[i][d] * k[d];
-          dp += Ds[i][d] * v[d];
-        }
-        float p = (kt > qt || qt >= T || !valid) ? 0.0f : expf(dot * scale - Ls[i]);
-        pl[ii] = p;
-        sl[ii] = p * (dp - Dvs[i]);
+      for (int s = 0; s < 32; s++) {
+        S = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[lane & 31][2 * s + hl], kf[s], S, 0, 0, 0);
+        dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Ds[lane & 31][2 * s + hl], vf[s], dP, 0, 0, 0);
       }
-      // the 4 lanes of key j (consecutive lanes) each hold 16 of the 64 queries: exchange by shuffle
-      const int lane = tid & 63;
+      // S[r] = score(query q0 + kap(r, hl), key mykey)
+      float p[16], ds[16];
 #pragma unroll
-      for (int src = 0; src < 4; src++) {
+      for (int r = 0; r < 16; r++) {
+        int qi = kap(r, hl), q = q0 + qi;
+        float pv = (mykey > q || q >= T || mykey >= T) ? 0.0f : expf(S[r] - Ls[qi]);
+        p[r] = pv;
+        ds[r] = pv * (dP[r] - Dvs[qi]);
+      }
 #pragma unroll
-        for (int ii = 0; ii < 16; ii++) {
-          float p = __shfl(pl[ii], (lane & ~3) | src);
-          float ds = __shfl(sl[ii], (lane & ~3) | src);
-          int i = src * 16 + ii;
-#pragma unroll
-          for (int d = 0; d < 16; d++) {
-            dv[d] += p * Ds[i][c * 16 + d];
-            dk[d] += ds * Qs[i][c * 16 + d];
-          }
-        }
+      for (int s = 0; s < 16; s++) {
+        const float* dr = Ds[kap(s, hl)];
+        const float* qr = Qs[kap(s, hl)];
+        V0 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], dr[lane & 31], V0, 0, 0, 0);
+        V1 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], dr[32 + (lane & 31)], V1, 0, 0, 0);
+        K0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], qr[lane & 31], K0, 0, 0, 0);
+        K1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], qr[32 + (lane & 31)], K1, 0, 0, 0);
       }
     }
   }
-  if (!valid) return;
-  float* dkr = dkv + row * ldk + kcol + g * HD + c * 16;
-  float* dvr = dkv + row * ldk + vcol + g * HD + c * 16;
+  // Q in LDS carried the 2^-3 scale, so K0/K1 already hold dK = dSᵀ·Q·scale.
 #pragma unroll
-  for (int d = 0; d < 16; d++) {
-    dkr[d] = dk[d] * scale;
-    dvr[d] = dv[d];
+  for (int r = 0; r < 16; r++) {
+    int key = k0 + kap(r, hl);
+    if (key >= T) continue;
+    float *kr, *vr;
+    if (group == 1) {
+      kr = dkv + (base + key) * ldk + kcol + g * HD;
+      vr = dkv + (base + key) * ldk + vcol + g * HD;
+    } else {
+      kr = part + ((base + key) * nh + h) * 2 * HD;
+      vr = kr + HD;
+    }
+    kr[lane & 31] = K0[r];
+    kr[32 + (lane & 31)] = K1[r];
+    vr[lane & 31] = V0[r];
+    vr[32 + (lane & 31)] = V1[r];
   }
+}
+
+// dK/dV of kv head g = Σ over its group's heads, in head order (deterministic).
+__global__ void attn_group_sum(const float* __restrict__ part, int M, int nh, int nkv, int group,
+                               float* __restrict__ dkv, long long ldk, int kcol, int vcol) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * nkv * 2 * HD) return;
+  int c = (int)(i % (2 * HD));
+  long long t = i / (2 * HD);
+  int g = (int)(t % nkv);
+  long long m = t / nkv;
+  float s = 0.0f;
+  for (int hh = 0; hh < group; hh++) s += part[(m * nh + g * group + hh) * 2 * HD + c];
+  int col = (c < HD ? kcol : vcol) + g * HD + (c % HD);
+  dkv[m * ldk + col] = s;
 }
 
 }  // namespace
@@ -254,25 +309,32 @@ __global__ void __launch_bounds__(256) attn_dkdv_kernel(const float* __restrict_
 void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,
                      float* o, long long ldo, float* lse, hipStream_t st) {
   HOS_REQUIRE(hd == HD, HOS_E_INVALID, "attention: head_dim must be 64");
-  dim3 grid(ceil_div(T, BLK), nh, B);
-  attn_fwd_kernel<<<grid, 256, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nh / nkv, 1.0f / sqrtf((float)hd), o, ldo, lse);
+  HOS_REQUIRE(ld % 4 == 0 && kcol % 4 == 0 && vcol % 4 == 0, HOS_E_INVALID, "attention: unaligned qkv layout");
+  dim3 grid(ceil_div(T, TB), nh, B);
+  attn_fwd_kernel<<<grid, 64, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nh / nkv, o, ldo, lse);
   HOS_HIP_CHECK(hipGetLastError());
 }
 
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
-                     long long ldd, hipStream_t st) {
+                     long long ldd, float* part, hipStream_t st) {
   HOS_REQUIRE(hd == HD, HOS_E_INVALID, "attention: head_dim must be 64");
-  float scale = 1.0f / sqrtf((float)hd);
+  HOS_REQUIRE(nh == nkv || part != nullptr, HOS_E_INVALID, "attention: GQA backward needs a partial buffer");
+  HOS_REQUIRE(ldo % 4 == 0, HOS_E_INVALID, "attention: unaligned dO layout");
   long long n = (long long)B * nh * T;
   attn_dvec_kernel<<<ceil_div(n, 256), 256, 0, st>>>(o, dout, ldo, T, nh, B, dvec);
   HOS_HIP_CHECK(hipGetLastError());
-  dim3 gq(ceil_div(T, BLK), nh, B);
-  attn_dq_kernel<<<gq, 256, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, scale, dqkv, ldd);
+  dim3 gq(ceil_div(T, TB), nh, B);
+  attn_dq_kernel<<<gq, 64, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd);
   HOS_HIP_CHECK(hipGetLastError());
-  dim3 gk(ceil_div(T, BLK), nkv, B);
-  attn_dkdv_kernel<<<gk, 256, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, scale, dqkv, ldd);
+  dim3 gk(ceil_div(T, TB), nh, B);
+  attn_dkdv_kernel<<<gk, 64, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd, part);
   HOS_HIP_CHECK(hipGetLastError());
+  if (nh != nkv) {
+    long long ne = (long long)B * T * nkv * 2 * HD;
+    attn_group_sum<<<ceil_div(ne, 256), 256, 0, st>>>(part, B * T, nh, nkv, nh / nkv, dqkv, ldd, kcol, vcol);
+    HOS_HIP_CHECK(hipGetLastError());
+  }
 }
 
 }  // namespace hos

@@ -24,5 +24,5 @@ void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, 
                      float* o, long long ldo, float* lse, hipStream_t st);
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
-                     long long ldd, hipStream_t st);
+                     long long ldd, float* part, hipStream_t st);
 }  // namespace hos

@@ -20,9 +20,10 @@ inline QWeightView view(const QWeight& w) { return QWeightView{w.type, w.rows, w
 //   Q4_K  (d·sc)·q − dmin·m   (:385-413; d·sc and dmin·m are precomputed in f32 at repack)
 //   Q6_K  (d·sc)·q            (:449-477)
 __device__ __forceinline__ float deq_q8(int8_t q, float d) { return __fmul_rn((float)q, d); }
-__device__ __forceinline__ float deq_q4k(uint32_t q, float2 dm) {
-  return __fsub_rn(__fmul_rn(dm.x, (float)q), dm.y);
-}
+// (d·sc)·q is exact in f32 (d: 11 significant bits, sc ≤ 63, q ≤ 15 → ≤ 21 bits), so the reference's
+// multiply-then-subtract rounds once, at the subtraction — exactly what one fused multiply-add does.
+__device__ __forceinline__ float deq_q4k(uint32_t q, float2 dm) { return __builtin_fmaf(dm.x, (float)q, -dm.y); }
+__device__ __forceinline__ float deq_q4k_f(float q, float2 dm) { return __builtin_fmaf(dm.x, q, -dm.y); }
 __device__ __forceinline__ float deq_q6k(int8_t q, float s) { return __fmul_rn(s, (float)q); }
 
 __device__ __forceinline__ float deq_one(const QWeightView& w, long long r, long long c) {
@@ -47,12 +48,20 @@ void launch_quantize(const float* x_dev, size_t n, uint32_t type, uint8_t* out_d
 // ---- qgemm.hip ----
 // Epilogue of the fp16 GEMMs: v = rinv[m]·acc[m][n] (+ bias[n]);
 //   accumulate: out += v;  else resid: out = resid + v (resid may alias out);  else out = v.
+// Optional rank-r update fused into the epilogue (a LoRA branch): v += scale · Σ_j U[m][j] · L(j, n),
+// U row-major with row stride ldu, L(j, n) = L[j·slj + n·sln]. rank 0 = none.
 struct GemmEpi {
   float* out;
   long long ldo;
   const float* bias;   // may be null
   int accumulate;      // 1: out += v
   const float* resid;  // may be null; same row stride as out
+  const float* U = nullptr;
+  long long ldu = 0;
+  const float* L = nullptr;
+  long long slj = 0, sln = 0;
+  int rank = 0;
+  float scale = 0.0f;
 };
 // Y[M, W.rows] = A[M, W.cols] · deq(W)ᵀ, A an fp16 row-scaled operand with row stride lda.
 void launch_qgemm_fwd(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,

@@ -88,7 +88,7 @@ struct hos_peft {
   H16 dl{};
   float *row_loss = nullptr, *loss = nullptr;
   float *dx = nullptr, *dxn = nullptr, *dqkv = nullptr, *dout = nullptr, *dh = nullptr, *dgu = nullptr,
-        *du = nullptr, *dvec = nullptr;
+        *du = nullptr, *dvec = nullptr, *attn_part = nullptr;
   float* ws = nullptr;
   size_t ws_bytes = 0;
   float2* rope_tab = nullptr;
@@ -145,17 +145,30 @@ struct hos_peft {
   double wbytes(const QWeight& w) const { return (double)(w.q_bytes + w.s_bytes); }
 
   // fp16 GEMMs on frozen weights
+  // `lo` carries an optional fused LoRA rank-r update (GemmEpi U/L fields).
   void qfwd(const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo, const float* bias,
-            const float* resid, int accumulate) {
-    Scope s(this, "qgemm_fwd", 2.0 * M * w.rows * w.cols * passes,
+            const float* resid, int accumulate, GemmEpi lo = GemmEpi{}) {
+    // algorithmic flops (2·M·N·K), independent of the precision passes
+    Scope s(this, "qgemm_fwd", 2.0 * M * w.rows * w.cols,
             2.0 * M * w.cols + wbytes(w) + 4.0 * M * w.rows * (resid || accumulate ? 2 : 1));
-    GemmEpi e{out, ldo, bias, accumulate, resid};
+    GemmEpi e = lo;
+    e.out = out;
+    e.ldo = ldo;
+    e.bias = bias;
+    e.accumulate = accumulate;
+    e.resid = resid;
     launch_qgemm_fwd(w, a, lda, M, e, ws, ws_bytes, passes, st);
   }
-  void qdx(const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo, int accumulate) {
-    Scope s(this, "qgemm_dx", 2.0 * M * w.rows * w.cols * passes,
+  void qdx(const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo, int accumulate,
+           GemmEpi lo = GemmEpi{}) {
+    Scope s(this, "qgemm_dx", 2.0 * M * w.rows * w.cols,
             2.0 * M * w.rows + wbytes(w) + 4.0 * M * w.cols * (accumulate ? 2 : 1));
-    GemmEpi e{out, ldo, nullptr, accumulate, nullptr};
+    GemmEpi e = lo;
+    e.out = out;
+    e.ldo = ldo;
+    e.bias = nullptr;
+    e.accumulate = accumulate;
+    e.resid = nullptr;
     launch_qgemm_dx(w, a, lda, M, e, ws, ws_bytes, passes, st);
   }
   // f32 GEMM C = alpha·A·B + beta·C (strided)
@@ -169,39 +182,83 @@ struct hos_peft {
     launch_to_h16(x, ldx, M, K, hs, st);
   }
 
-  // ---- LoRA pieces (reference layout: A [in, r], B [r, out]) ----
-  // u[:, t·r..] = x · A_t
-  void lora_down(int l, int t, const float* x, long long ldx, int M) {
+  // ---- LoRA pieces (reference factors: A [in, r], B [r, out]) ----
+  // Targets sharing an input form a group (q/k/v, o, gate/up, down). A group's adapted A factors sit
+  // side by side as one [in, G·r] matrix, so one GEMM gives u = x·[A_1 … A_G] and one gives
+  // [dA_1 … dA_G] = xᵀ·[du_1 … du_G]. u and du live in [M, 7·r] buffers, target t at column ucol(t).
+  static int group_of(int t) { return t <= TV ? 0 : (t == TO ? 1 : (t <= TU ? 2 : 3)); }
+  static int group_first(int g) { return g == 0 ? TQ : (g == 1 ? TO : (g == 2 ? TG : TD)); }
+  static int group_last(int g) { return g == 0 ? TV : (g == 1 ? TO : (g == 2 ? TU : TD)); }
+  int gcount(int g) const {
+    int n = 0;
+    for (int t = group_first(g); t <= group_last(g); t++) n += has(t);
+    return n;
+  }
+  int slot(int t) const {
+    int n = 0;
+    for (int u = group_first(group_of(t)); u < t; u++) n += has(u);
+    return n;
+  }
+  long long ldA(int t) const { return (long long)gcount(group_of(t)) * r; }
+  int ucol(int t) const { return group_first(group_of(t)) * r + slot(t) * r; }
+
+  // u[:, group columns] = x · A_group (forward)
+  void lora_down(int l, int g, const float* x, long long ldx, int M) {
+    const int t0 = group_first(g), n = gcount(g);
+    if (n == 0) return;
+    int in, o;
+    dims(t0, &in, &o);
+    int first = t0;
+    while (!has(first)) first++;
+    g32(M, (long long)n * r, in, 1.0f, x, ldx, 1, P + offA[l * NT + first], (long long)n * r, 1, 0.0f,
+        act[l].u + ucol(first), NT * r);
+  }
+  // Epilogue term y += s·u_t·B_t of the base forward GEMM
+  GemmEpi up_epi(int l, int t) {
+    GemmEpi e{};
+    if (!has(t)) return e;
     int in, o;
     dims(t, &in, &o);
-    const float* A = P + offA[l * NT + t];
-    g32(M, r, in, 1.0f, x, ldx, 1, A, r, 1, 0.0f, act[l].u + t * r, NT * r);
+    e.U = act[l].u + ucol(t);
+    e.ldu = NT * r;
+    e.L = P + offB[l * NT + t];
+    e.slj = o;
+    e.sln = 1;
+    e.rank = r;
+    e.scale = lscale;
+    return e;
   }
-  // y += s · u_t · B_t
-  void lora_up(int l, int t, float* y, long long ldy, int M) {
+  // From dy (grad of the adapted projection's output): dB_t = s·u_tᵀ·dy, du_t = s·dy·B_tᵀ.
+  void lora_grad_b(int l, int t, const float* dy, long long ldy, int M) {
     int in, o;
     dims(t, &in, &o);
     const float* B = P + offB[l * NT + t];
-    g32(M, o, r, lscale, act[l].u + t * r, NT * r, 1, B, o, 1, 1.0f, y, ldy);
+    g32(r, o, M, lscale, act[l].u + ucol(t), 1, NT * r, dy, ldy, 1, 0.0f, G + offB[l * NT + t], o);
+    g32(M, r, o, lscale, dy, ldy, 1, B, 1, o, 0.0f, du + ucol(t), NT * r);
   }
-  // Given dy (grad of the adapted projection output): dB_t, dA_t, and dx_in += s·(dy·B_tᵀ)·A_tᵀ.
-  void lora_bwd(int l, int t, const float* x, long long ldx, const float* dy, long long ldy, float* dxin,
-                long long lddx, int M) {
+  // Epilogue term dx_in += du_t·A_tᵀ of the base dX GEMM
+  GemmEpi down_epi(int l, int t) {
+    GemmEpi e{};
+    if (!has(t)) return e;
+    e.U = du + ucol(t);
+    e.ldu = NT * r;
+    e.L = P + offA[l * NT + t];  // L(j, col) = A_t[col, j]
+    e.slj = 1;
+    e.sln = ldA(t);
+    e.rank = r;
+    e.scale = 1.0f;
+    return e;
+  }
+  // [dA_1 … dA_G] = xᵀ·[du_1 … du_G]
+  void lora_grad_a(int l, int g, const float* x, long long ldx, int M) {
+    const int n = gcount(g);
+    if (n == 0) return;
+    int first = group_first(g);
+    while (!has(first)) first++;
     int in, o;
-    dims(t, &in, &o);
-    const float* A = P + offA[l * NT + t];
-    const float* B = P + offB[l * NT + t];
-    float* dA = G + offA[l * NT + t];
-    float* dB = G + offB[l * NT + t];
-    const float* u = act[l].u + t * r;
-    // dB = s·uᵀ·dy   [r, o]
-    g32(r, o, M, lscale, u, 1, NT * r, dy, ldy, 1, 0.0f, dB, o);
-    // du = s·dy·Bᵀ   [M, r]
-    g32(M, r, o, lscale, dy, ldy, 1, B, 1, o, 0.0f, du, r);
-    // dA = xᵀ·du     [in, r]
-    g32(in, r, M, 1.0f, x, 1, ldx, du, r, 1, 0.0f, dA, r);
-    // dx += du·Aᵀ    [M, in]
-    g32(M, in, r, 1.0f, du, r, 1, A, 1, r, 1.0f, dxin, lddx);
+    dims(first, &in, &o);
+    g32(in, (long long)n * r, M, 1.0f, x, 1, ldx, du + ucol(first), NT * r, 1, 0.0f, G + offA[l * NT + first],
+        (long long)n * r);
   }
 
   void check_ready() {
@@ -236,15 +293,10 @@ struct hos_peft {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lqkv ? 2 : 1) + 2.0 * M * d);
         launch_rmsnorm_fwd(a.x, w.attn_norm, c.rms_eps, M, d, lqkv ? a.xn1 : nullptr, hs, a.inv1, st);
       }
-      qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0);
-      qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0);
-      qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0);
-      const int qcol[3] = {0, qd, qd + kvd};
-      for (int t = TQ; t <= TV; t++)
-        if (has(t)) {
-          lora_down(l, t, a.xn1, d, M);
-          lora_up(l, t, a.qkv + qcol[t], W3, M);
-        }
+      lora_down(l, 0, a.xn1, d, M);
+      qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0, up_epi(l, TQ));
+      qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0, up_epi(l, TK));
+      qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0, up_epi(l, TV));
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
         launch_rope(a.qkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
@@ -256,35 +308,22 @@ struct hos_peft {
         launch_attn_fwd(a.qkv, W3, qd, qd + kvd, B, T, c.n_heads, c.n_kv_heads, c.head_dim, a.o, qd, a.lse, st);
       }
       to16(a.o, qd, M, qd);
-      qfwd(w.w[TO], hs, qd, M, a.x2, d, nullptr, a.x, 0);
-      if (has(TO)) {
-        lora_down(l, TO, a.o, qd, M);
-        lora_up(l, TO, a.x2, d, M);
-      }
+      lora_down(l, 1, a.o, qd, M);
+      qfwd(w.w[TO], hs, qd, M, a.x2, d, nullptr, a.x, 0, up_epi(l, TO));
       const bool lgu = has(TG) || has(TU);
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lgu ? 2 : 1) + 2.0 * M * d);
         launch_rmsnorm_fwd(a.x2, w.ffn_norm, c.rms_eps, M, d, lgu ? a.xn2 : nullptr, hs, a.inv2, st);
       }
-      qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0);
-      qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0);
-      if (has(TG)) {
-        lora_down(l, TG, a.xn2, d, M);
-        lora_up(l, TG, a.gu, 2LL * F, M);
-      }
-      if (has(TU)) {
-        lora_down(l, TU, a.xn2, d, M);
-        lora_up(l, TU, a.gu + F, 2LL * F, M);
-      }
+      lora_down(l, 2, a.xn2, d, M);
+      qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, up_epi(l, TG));
+      qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0, up_epi(l, TU));
       {
         Scope s(this, "swiglu", 0, 8.0 * M * F + 2.0 * M * F + (has(TD) ? 4.0 * M * F : 0));
         launch_swiglu_fwd(a.gu, M, F, has(TD) ? a.h : nullptr, hs, st);
       }
-      qfwd(w.w[TD], hs, F, M, xnext, d, nullptr, a.x2, 0);
-      if (has(TD)) {
-        lora_down(l, TD, a.h, F, M);
-        lora_up(l, TD, xnext, d, M);
-      }
+      lora_down(l, 3, a.h, F, M);
+      qfwd(w.w[TD], hs, F, M, xnext, d, nullptr, a.x2, 0, up_epi(l, TD));
     }
     {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d + 2.0 * M * d);
@@ -315,44 +354,48 @@ struct hos_peft {
       LayerW& w = lw[l];
       // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA) ----
       to16(dx, d, M, d);
-      qdx(w.w[TD], hs, d, M, dh, F, 0);
-      if (has(TD)) lora_bwd(l, TD, a.h, F, dx, d, dh, F, M);
+      if (has(TD)) lora_grad_b(l, TD, dx, d, M);
+      qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD));
+      lora_grad_a(l, 3, a.h, F, M);
       {
         Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (dgu ? 8.0 * M * F : 0));
         launch_swiglu_bwd(a.gu, dh, M, F, (has(TG) || has(TU)) ? dgu : nullptr, hs, st);
       }
+      if (has(TG)) lora_grad_b(l, TG, dgu, 2LL * F, M);
+      if (has(TU)) lora_grad_b(l, TU, dgu + F, 2LL * F, M);
       H16 hu = h16_offset(hs, F);
-      qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0);
-      qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1);
-      if (has(TG)) lora_bwd(l, TG, a.xn2, d, dgu, 2LL * F, dxn, d, M);
-      if (has(TU)) lora_bwd(l, TU, a.xn2, d, dgu + F, 2LL * F, dxn, d, M);
+      qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG));
+      qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU));
+      lora_grad_a(l, 2, a.xn2, d, M);
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
         launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st);
       }
       // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
       to16(dx, d, M, d);
-      qdx(w.w[TO], hs, d, M, dout, qd, 0);
-      if (has(TO)) lora_bwd(l, TO, a.o, qd, dx, d, dout, qd, M);
+      if (has(TO)) lora_grad_b(l, TO, dx, d, M);
+      qdx(w.w[TO], hs, d, M, dout, qd, 0, down_epi(l, TO));
+      lora_grad_a(l, 1, a.o, qd, M);
       {
         Scope s(this, "attn_bwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 5,
                 4.0 * M * (W3 * 2 + qd * 2) + 8.0 * B * c.n_heads * T);
         launch_attn_bwd(a.qkv, W3, qd, qd + kvd, a.o, dout, qd, a.lse, dvec, B, T, c.n_heads, c.n_kv_heads,
-                        c.head_dim, dqkv, W3, st);
+                        c.head_dim, dqkv, W3, attn_part, st);
       }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
         launch_rope(dqkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
         launch_rope(dqkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
       }
-      to16(dqkv, W3, M, W3);
-      H16 hk = h16_offset(hs, qd), hv = h16_offset(hs, qd + kvd);
-      qdx(w.w[TQ], hs, W3, M, dxn, d, 0);
-      qdx(w.w[TK], hk, W3, M, dxn, d, 1);
-      qdx(w.w[TV], hv, W3, M, dxn, d, 1);
       const int qcol[3] = {0, qd, qd + kvd};
       for (int t = TQ; t <= TV; t++)
-        if (has(t)) lora_bwd(l, t, a.xn1, d, dqkv + qcol[t], W3, dxn, d, M);
+        if (has(t)) lora_grad_b(l, t, dqkv + qcol[t], W3, M);
+      to16(dqkv, W3, M, W3);
+      H16 hk = h16_offset(hs, qd), hv = h16_offset(hs, qd + kvd);
+      qdx(w.w[TQ], hs, W3, M, dxn, d, 0, down_epi(l, TQ));
+      qdx(w.w[TK], hk, W3, M, dxn, d, 1, down_epi(l, TK));
+      qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV));
+      lora_grad_a(l, 0, a.xn1, d, M);
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
         launch_rmsnorm_bwd(dxn, a.x, a.inv1, w.attn_norm, M, d, dx, st);
@@ -413,17 +456,24 @@ struct hos_peft {
     // LoRA arena
     offA.assign((size_t)L * NT, -1);
     offB.assign((size_t)L * NT, -1);
+    HOS_REQUIRE(r <= 32, HOS_E_INVALID, "peft: LoRA rank must be <= 32");
     long long off = 0;
     for (int l = 0; l < L; l++)
-      for (int t = 0; t < NT; t++)
-        if (has(t)) {
-          int in, o;
-          dims(t, &in, &o);
-          offA[l * NT + t] = off;
-          off += (long long)in * r;
-          offB[l * NT + t] = off;
-          off += (long long)r * o;
-        }
+      for (int g = 0; g < 4; g++) {
+        const int n = gcount(g);
+        if (n == 0) continue;
+        int in, o;
+        dims(group_first(g), &in, &o);
+        const long long abase = off;  // the group's A factors: one [in, n·r] matrix
+        off += (long long)in * n * r;
+        for (int t = group_first(g); t <= group_last(g); t++)
+          if (has(t)) {
+            dims(t, &in, &o);
+            offA[l * NT + t] = abase + (long long)slot(t) * r;
+            offB[l * NT + t] = off;
+            off += (long long)r * o;
+          }
+      }
     nparams = off;
     P = alloc<float>(nparams);
     G = alloc<float>(nparams);
@@ -468,8 +518,9 @@ struct hos_peft {
     dout = alloc<float>(M * qd);
     dh = alloc<float>(M * F);
     dgu = (has(TG) || has(TU)) ? alloc<float>(M * 2 * F) : nullptr;
-    du = alloc<float>(M * r);
+    du = alloc<float>(M * NT * r);
     dvec = alloc<float>(M * c.n_heads);
+    if (c.n_heads != c.n_kv_heads) attn_part = alloc<float>(M * c.n_heads * 2 * c.head_dim);
     ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(d, F) * 4 * 8, 1ull << 30));
     ws = alloc<float>(ws_bytes / 4);
     ids = alloc<int32_t>(M);
@@ -630,7 +681,9 @@ int hos_peft_set_lora(hos_peft* p, int layer, int target, const float* A, const 
     HOS_REQUIRE(A && B, HOS_E_INVALID, "null factor");
     int i = lora_index(p, layer, target), in, o;
     p->dims(target, &in, &o);
-    HOS_HIP_CHECK(hipMemcpyAsync(p->P + p->offA[i], A, (size_t)in * p->r * 4, hipMemcpyHostToDevice, p->st));
+    const size_t rb = (size_t)p->r * 4;
+    HOS_HIP_CHECK(hipMemcpy2DAsync(p->P + p->offA[i], (size_t)p->ldA(target) * 4, A, rb, rb, (size_t)in,
+                                   hipMemcpyHostToDevice, p->st));
     HOS_HIP_CHECK(hipMemcpyAsync(p->P + p->offB[i], B, (size_t)p->r * o * 4, hipMemcpyHostToDevice, p->st));
     HOS_HIP_CHECK(hipStreamSynchronize(p->st));
   });
@@ -640,7 +693,10 @@ static int get_pair(hos_peft* p, const float* base, int layer, int target, float
   return pguard(p, [&] {
     int i = lora_index(p, layer, target), in, o;
     p->dims(target, &in, &o);
-    if (A) HOS_HIP_CHECK(hipMemcpyAsync(A, base + p->offA[i], (size_t)in * p->r * 4, hipMemcpyDeviceToHost, p->st));
+    const size_t rb = (size_t)p->r * 4;
+    if (A)
+      HOS_HIP_CHECK(hipMemcpy2DAsync(A, rb, base + p->offA[i], (size_t)p->ldA(target) * 4, rb, (size_t)in,
+                                     hipMemcpyDeviceToHost, p->st));
     if (B) HOS_HIP_CHECK(hipMemcpyAsync(B, base + p->offB[i], (size_t)p->r * o * 4, hipMemcpyDeviceToHost, p->st));
     HOS_HIP_CHECK(hipStreamSynchronize(p->st));
   });

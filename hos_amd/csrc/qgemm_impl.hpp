@@ -1,0 +1,451 @@
+// Dequant-fused quantized-weight GEMM kernel templates on fp16 MFMA (v_mfma_f32_32x32x16_f16, fp32
+// accumulate); instantiated per quant type in qgemm_q8 / qgemm_q4k / qgemm_q6k.
+//
+//   fwd: Y[M, N]  = A[M, K] · deq(W)ᵀ   W [N, K]  — the frozen-base forward x·t_const(W)
+//   dx : dX[M, K] = dY[M, N] · deq(W)   W [N, K]  — the frozen-base backward g·Bᵀ
+//        (src/tensor.rs:316-327 and :347-360; src/peft.rs:24-33 transposes W to [in,out])
+//
+// Each BK-deep slab of the contraction streams the packed weight from HBM, dequantizes it in registers
+// with the bit-exact device functions of kernels.hpp and stores it row-major in LDS exactly as the rows
+// arrive (a run of E consecutive values per thread, one coalesced load, one vector LDS store):
+//   fwd: W rows are output columns, runs go along the contraction → B fragments are plain 128-bit reads;
+//   dx:  W rows are the contraction, runs go along the output → B fragments are read transposed with
+//        ds_read_b64_tr_b16 (in a 16-lane group, lane L addressing row cb + L/4, columns jb + 4·(L%4) .. +3
+//        hands lane i the rows cb .. cb+3 of column jb + i; two reads give the 8-deep run an MFMA lane needs).
+// The activation operand arrives as fp16 with an exact power-of-two scale per row; the epilogue
+// multiplies that scale back out and applies bias / residual / a fused rank-r (LoRA) update.
+//
+// Precision passes (NP): one fp16 product rounds both operands to 11 bits (~3e-4 relative per GEMM).
+//   NP = 1: A·W
+//   NP = 2: A_hi·W + A_lo·W                       (activation carried to ~22 bits)
+//   NP = 3: A_hi·W_hi + A_lo·W_hi + A_hi·W_lo     (both operands to ~22 bits; dropped A_lo·W_lo ~2^-22)
+// where W_hi = fp16(w), W_lo = fp16(w − W_hi) of the f32 dequantized w.
+//
+// Work decomposition: 256 threads = 4 waves (2×2), workgroup tile BM×BN, wave tile (BM/2)×(BN/2) of
+// 32×32 MFMA tiles, LDS double-buffered when both stages fit in 64 KB, register prefetch of the next slab,
+// optional split-K reduced deterministically by splitk_reduce.
+#pragma once
+#include <cstdio>
+#include <cstdlib>
+
+#include "kernels.hpp"
+
+namespace hos {
+namespace {
+
+typedef short s4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ h8 zero_h8() {
+  h8 z;
+#pragma unroll
+  for (int i = 0; i < 8; i++) z[i] = (_Float16)0.0f;
+  return z;
+}
+
+// Signed byte i of a word as float (one bit-field extract + one convert).
+__device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
+// Unsigned byte i as float (maps to v_cvt_f32_ubyte<i>).
+__device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
+
+// Four consecutive dequantized values from one packed source: Q4_K a 16-bit half-word (4 nibbles),
+// Q8_0/Q6_K a 32-bit word (4 int8). Same arithmetic as deq_q4k / deq_q8 / deq_q6k.
+template <uint32_t QT>
+__device__ __forceinline__ void deq4(uint32_t src, float2 s, float* v) {
+  if constexpr (QT == GGUF_Q4_K) {
+    const uint32_t lo = src & 0x0F0Fu, hi = (src >> 4) & 0x0F0Fu;  // nibbles of cols 0,2 | 1,3
+    v[0] = deq_q4k_f(ubyte(lo, 0), s);
+    v[1] = deq_q4k_f(ubyte(hi, 0), s);
+    v[2] = deq_q4k_f(ubyte(lo, 1), s);
+    v[3] = deq_q4k_f(ubyte(hi, 1), s);
+  } else if constexpr (QT == GGUF_Q8_0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = __fmul_rn(sbyte(src, i), s.x);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = __fmul_rn(s.x, sbyte(src, i));
+  }
+}
+
+// A run of E consecutive values of one W row (E ∈ {8, 16, 32}; it never leaves a 32-value Q8_0/Q4_K group;
+// Q6_K's 16-value groups give a second scale for E = 32).
+template <uint32_t QT, int E>
+struct Run {
+  static constexpr int VPW = QT == GGUF_Q4_K ? 8 : 4;  // values per 32-bit word
+  static constexpr int NW = E / VPW;
+  uint32_t q[NW];
+  float2 s[2];
+  bool ok;
+};
+
+template <uint32_t QT, int E>
+__device__ __forceinline__ void run_load(const QWeightView& w, long long row, int col, bool ok, Run<QT, E>& r) {
+  r.ok = ok;
+  if (!ok) {
+    row = 0;
+    col = 0;
+  }
+  const long long e = row * w.cols + col;
+  const uint32_t* src = (const uint32_t*)((const uint8_t*)w.q + (QT == GGUF_Q4_K ? (e >> 1) : e));
+  if constexpr (Run<QT, E>::NW == 1) {
+    r.q[0] = src[0];
+  } else if constexpr (Run<QT, E>::NW == 2) {
+    uint2 v = *(const uint2*)src;
+    r.q[0] = v.x;
+    r.q[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < Run<QT, E>::NW; i += 4) {
+      uint4 v = *(const uint4*)(src + i);
+      r.q[i] = v.x;
+      r.q[i + 1] = v.y;
+      r.q[i + 2] = v.z;
+      r.q[i + 3] = v.w;
+    }
+  }
+  if constexpr (QT == GGUF_Q4_K) {
+    r.s[0] = ((const float2*)w.s)[e >> 5];
+  } else if constexpr (QT == GGUF_Q8_0) {
+    r.s[0].x = w.s[e >> 5];
+  } else {
+    r.s[0].x = w.s[e >> 4];
+    if constexpr (E > 16) r.s[1].x = w.s[(e >> 4) + 1];
+  }
+}
+
+// Dequantize a run and store it as E/8 h8 vectors at dst (hi) and dst + lo_off (lo, when SPLIT).
+template <uint32_t QT, int E, bool SPLIT>
+__device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, int lo_off) {
+#pragma unroll
+  for (int v = 0; v < E / 8; v++) {
+    h8 hv, lv;
+    if (!r.ok) {
+      hv = lv = zero_h8();
+    } else {
+      float f[8];
+      const float2 sc = (QT == GGUF_Q6_K && v >= 2) ? r.s[1] : r.s[0];
+      if constexpr (QT == GGUF_Q4_K) {
+        deq4<QT>(r.q[v] & 0xffffu, sc, f);
+        deq4<QT>(r.q[v] >> 16, sc, f + 4);
+      } else {
+        deq4<QT>(r.q[2 * v], sc, f);
+        deq4<QT>(r.q[2 * v + 1], sc, f + 4);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        _Float16 h = (_Float16)f[i];
+        hv[i] = h;
+        if constexpr (SPLIT) lv[i] = (_Float16)(f[i] - (float)h);
+      }
+    }
+    *(h8*)(dst + 8 * v) = hv;
+    if constexpr (SPLIT) *(h8*)(dst + lo_off + 8 * v) = lv;
+  }
+}
+
+template <int BM, int BN, int BK, bool DX, int NP>
+struct Geo {
+  static constexpr int TM = BM / 64, TN = BN / 64;      // 32×32 tiles per wave
+  static constexpr int AROW = BK + 8;                   // A tile row (halves)
+  static constexpr int A_H8 = BM * BK / 8 / 256;        // A h8 vectors per thread
+  static constexpr int E = BN * BK / 256;               // B values per thread
+  static constexpr int BROW = DX ? BN + 16 : BK + 8;    // B tile row (halves)
+  static constexpr int BROWS = DX ? BK : BN;            // B tile rows
+  static constexpr int TPR = (DX ? BN : BK) / E;        // threads per B tile row
+  static constexpr int NA = NP >= 2 ? 2 : 1, NB = NP >= 3 ? 2 : 1;
+  static constexpr int ATILE = BM * AROW, BTILE = BROWS * BROW;
+  static constexpr int BUF = NA * ATILE + NB * BTILE;   // halves per stage
+  static constexpr int STAGES = BUF * 2 * 2 <= 65536 ? 2 : 1;
+  static constexpr int EPI = (BM * 32 + 32 * BN) * 2;   // halves for the fused rank-r staging
+  static constexpr int SMEM = (STAGES * BUF > EPI) ? STAGES * BUF : EPI;
+};
+
+// ---- the GEMM ----
+// out[m][n] (over n < Nout) = Σ_c A[m][c] · B(n, c); contraction C split over gridDim.z.
+template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
+__global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float16* __restrict__ A,
+                                                    const _Float16* __restrict__ Alo, const float* __restrict__ rinv,
+                                                    long long lda, int M, int Nout, int C, int c_per_split,
+                                                    GemmEpi epi, float* __restrict__ ws) {
+  using G = Geo<BM, BN, BK, DX, NP>;
+  static_assert(G::E == 8 || G::E == 16 || G::E == 32, "B run length");
+  static_assert(BK % 32 == 0 || (BK == 32), "slab depth");
+  constexpr bool ALO = NP >= 2, BLO = NP >= 3;
+  __shared__ __attribute__((aligned(16))) _Float16 smem[G::SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int cbeg = blockIdx.z * c_per_split;
+  const int cend = min(C, cbeg + c_per_split);
+  const int nslab = (cend - cbeg) / BK;
+
+  f16v acc[G::TM][G::TN];
+#pragma unroll
+  for (int i = 0; i < G::TM; i++)
+#pragma unroll
+    for (int j = 0; j < G::TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+  // Raw (still quantized / still in registers) data of the next slab, in flight from HBM while the
+  // current slab is multiplied.
+  struct Regs {
+    h8 a[G::A_H8], al[G::A_H8];
+    Run<QT, G::E> b;
+  };
+  Regs R0;
+  // this thread's B run: tile row br, first column bc
+  const int br = tid / G::TPR, bc = G::E * (tid % G::TPR);
+
+  auto load = [&](Regs& R, int c0) {
+#pragma unroll
+    for (int v = 0; v < G::A_H8; v++) {
+      int idx = tid + 256 * v;  // h8 index within the BM×BK tile
+      int row = idx / (BK / 8), cv = idx % (BK / 8);
+      int m = m0 + row;
+      long long off = (long long)m * lda + c0 + 8 * cv;
+      R.a[v] = m < M ? *(const h8*)(A + off) : zero_h8();
+      if constexpr (ALO) R.al[v] = m < M ? *(const h8*)(Alo + off) : zero_h8();
+    }
+    if constexpr (DX) {
+      const int col = n0 + bc;  // output column run; rows are the contraction
+      run_load<QT, G::E>(w, c0 + br, col, col < w.cols, R.b);
+    } else {
+      const long long row = n0 + br;  // W row = output column; run along the contraction
+      run_load<QT, G::E>(w, row, c0 + bc, row < w.rows, R.b);
+    }
+  };
+  auto store = [&](const Regs& R, _Float16* buf) {
+#pragma unroll
+    for (int v = 0; v < G::A_H8; v++) {
+      int idx = tid + 256 * v;
+      int row = idx / (BK / 8), cv = idx % (BK / 8);
+      *(h8*)(buf + row * G::AROW + 8 * cv) = R.a[v];
+      if constexpr (ALO) *(h8*)(buf + G::ATILE + row * G::AROW + 8 * cv) = R.al[v];
+    }
+    _Float16* bs = buf + G::NA * G::ATILE;
+    run_store<QT, G::E, BLO>(R.b, bs + br * G::BROW + bc, G::BTILE);
+  };
+
+  if (nslab > 0) {
+    load(R0, cbeg);
+    store(R0, smem);
+  }
+  __syncthreads();
+
+  for (int s = 0; s < nslab; s++) {
+    const int buf = G::STAGES == 2 ? (s & 1) : 0;
+    const bool more = s + 1 < nslab;
+    if (more) load(R0, cbeg + (s + 1) * BK);
+    const _Float16* as = smem + buf * G::BUF;
+    const _Float16* bs = as + G::NA * G::ATILE;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      h8 af[G::TM], afl[G::TM], bf[G::TN], bfl[G::TN];
+      const int koff = kk + 8 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < G::TM; i++) {
+        int ro = (wm * (BM / 2) + 32 * i + (lane & 31)) * G::AROW + koff;
+        af[i] = *(const h8*)(as + ro);
+        if constexpr (ALO) afl[i] = *(const h8*)(as + G::ATILE + ro);
+      }
+#pragma unroll
+      for (int j = 0; j < G::TN; j++) {
+        if constexpr (DX) {
+          // 16-lane group g: columns 16·(g%2) .. +15 of this 32-wide tile, contraction kk + 8·(g/2) .. +7
+          const int g = lane >> 4, L = lane & 15;
+          const int col = wn * (BN / 2) + 32 * j + 16 * (g & 1) + 4 * (L & 3);
+          const int row = kk + 8 * (g >> 1) + (L >> 2);
+          const _Float16* p = bs + row * G::BROW + col;
+          typedef __attribute__((address_space(3))) s4v* lds_s4;
+          s4v x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p));
+          s4v x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p + 4 * G::BROW));
+          __builtin_memcpy(&bf[j], &x0, 8);
+          __builtin_memcpy((char*)&bf[j] + 8, &x1, 8);
+          if constexpr (BLO) {
+            s4v y0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p + G::BTILE));
+            s4v y1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p + G::BTILE + 4 * G::BROW));
+            __builtin_memcpy(&bfl[j], &y0, 8);
+            __builtin_memcpy((char*)&bfl[j] + 8, &y1, 8);
+          }
+        } else {
+          int ro = (wn * (BN / 2) + 32 * j + (lane & 31)) * G::BROW + koff;
+          bf[j] = *(const h8*)(bs + ro);
+          if constexpr (BLO) bfl[j] = *(const h8*)(bs + G::BTILE + ro);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < G::TM; i++)
+#pragma unroll
+        for (int j = 0; j < G::TN; j++) {
+          if constexpr (BLO) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], acc[i][j], 0, 0, 0);
+          if constexpr (ALO) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    if (more) {
+      if constexpr (G::STAGES == 1) __syncthreads();  // everyone is done reading the single stage
+      store(R0, smem + (G::STAGES == 2 ? (buf ^ 1) : 0) * G::BUF);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: D[i][j] of a 32×32 tile lives at lane j + 32·((i/4)&1), register (i&3) + 4·(i/8)
+  const bool split = gridDim.z > 1;
+  // fused rank-r update: stage U [BM][r] and L [r][BN] in the (now free) LDS
+  float* Us = (float*)smem;
+  float* Ls = Us + BM * 32;
+  const int rank = split ? 0 : epi.rank;
+  if (rank > 0) {
+    for (int e = tid; e < BM * rank; e += 256) {
+      int rr = e / rank, jj = e % rank, row = m0 + rr;
+      Us[rr * 32 + jj] = row < M ? epi.U[(long long)row * epi.ldu + jj] : 0.0f;
+    }
+    for (int e = tid; e < rank * BN; e += 256) {
+      int jj = e / BN, cc = e % BN, col = n0 + cc;
+      Ls[jj * BN + cc] = col < Nout ? epi.L[(long long)jj * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < G::TM; i++)
+#pragma unroll
+    for (int j = 0; j < G::TN; j++) {
+      const int cc = wn * (BN / 2) + 32 * j + (lane & 31);
+      const int col = n0 + cc;
+      if (col >= Nout) continue;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int rr = wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int row = m0 + rr;
+        if (row >= M) continue;
+        float v = acc[i][j][r];
+        if (split) {
+          ws[((long long)blockIdx.z * M + row) * Nout + col] = v;
+        } else {
+          v *= rinv[row];
+          if (epi.bias) v += epi.bias[col];
+          if (rank > 0) {
+            float lv = 0.0f;
+            for (int q = 0; q < rank; q++) lv += Us[rr * 32 + q] * Ls[q * BN + cc];
+            v += lv;
+          }
+          long long off = (long long)row * epi.ldo + col;
+          float* o = epi.out + off;
+          *o = epi.accumulate ? *o + v : (epi.resid ? epi.resid[off] + v : v);
+        }
+      }
+    }
+}
+
+// Deterministic split-K reduction + the same epilogue. Workgroup = 16 rows × 256 columns; the fused
+// rank-r term reads U rows from LDS and this thread's column of L from registers.
+constexpr int RED_ROWS = 16;
+__global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ ws, int splits, int M, int N,
+                                                     const float* __restrict__ rinv, GemmEpi epi) {
+  __shared__ float Us[RED_ROWS][33];
+  const int r0 = blockIdx.y * RED_ROWS, col = blockIdx.x * 256 + threadIdx.x;
+  const int rank = epi.rank;
+  float lc[32];
+  if (rank > 0) {
+    for (int e = threadIdx.x; e < RED_ROWS * rank; e += 256) {
+      int rr = e / rank, q = e % rank, row = r0 + rr;
+      Us[rr][q] = row < M ? epi.U[(long long)row * epi.ldu + q] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < 32; q++)
+      lc[q] = (q < rank && col < N) ? epi.L[(long long)q * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
+    __syncthreads();
+  }
+  if (col >= N) return;
+  for (int rr = 0; rr < RED_ROWS; rr++) {
+    const int row = r0 + rr;
+    if (row >= M) break;
+    const long long i = (long long)row * N + col;
+    float v = 0.0f;
+    for (int z = 0; z < splits; z++) v += ws[(long long)z * M * N + i];
+    v *= rinv[row];
+    if (epi.bias) v += epi.bias[col];
+    if (rank > 0) {
+      float lv = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 32; q++)
+        if (q < rank) lv += Us[rr][q] * lc[q];
+      v += lv;
+    }
+    long long off = (long long)row * epi.ldo + col;
+    float* o = epi.out + off;
+    *o = epi.accumulate ? *o + v : (epi.resid ? epi.resid[off] + v : v);
+  }
+}
+
+template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
+void launch_shape(const QWeight& w, H16 a, long long lda, long long M, int Nout, int C, int per, int splits,
+                  GemmEpi epi, float* ws, hipStream_t st) {
+  dim3 grid(ceil_div(Nout, BN), ceil_div(M, BM), splits);
+  qgemm_kernel<QT, DX, BM, BN, BK, NP>
+      <<<grid, 256, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, (int)M, Nout, C, per, epi, ws);
+}
+
+template <uint32_t QT, bool DX, int NP>
+void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
+                  hipStream_t st) {
+  const int Nout = DX ? (int)w.cols : (int)w.rows;
+  const int C = DX ? (int)w.rows : (int)w.cols;
+  HOS_REQUIRE(C % 32 == 0, HOS_E_INVALID, "qgemm: contraction length must be a multiple of 32");
+  HOS_REQUIRE((lda % 8) == 0, HOS_E_INVALID, "qgemm: activation row stride must be a multiple of 8");
+  HOS_REQUIRE(NP == 1 || a.lo != nullptr, HOS_E_INVALID, "qgemm: multi-pass precision needs the operand residual");
+  HOS_REQUIRE(epi.rank >= 0 && epi.rank <= 32, HOS_E_INVALID, "qgemm: fused rank-r update supports r <= 32");
+  // Tile choice: the largest tile that still gives ~1.25 waves of workgroups over the 256 CUs; only when
+  // even 64×64 tiles leave the chip idle is the contraction split (deterministic reduction after).
+  auto ntiles = [&](int bm, int bn) { return ceil_div(M, bm) * ceil_div(Nout, bn); };
+  int bm = 64, bn = 64, bk = 32;
+  if (ntiles(128, 128) >= 320) {
+    bm = 128;
+    bn = 128;
+  } else if (ntiles(64, 128) >= 320) {
+    bm = 64;
+    bn = 128;
+  } else if (ntiles(128, 64) >= 320) {
+    bm = 128;
+    bn = 64;
+  }
+  if (C % 64 == 0 && ((bm == 64 && bn == 64) || (NP == 1 && bm == 128 && bn == 128))) bk = 64;
+  if (const char* ov = std::getenv("HOS_QGEMM_TILE")) {  // tuning override: "BMxBNxBK"
+    int x = 0, y = 0, z = 0;
+    if (std::sscanf(ov, "%dx%dx%d", &x, &y, &z) == 3 && (z == 32 || (z == 64 && C % 64 == 0)) &&
+        ((x == 128 && y == 128) || (x == 64 && y == 128) || (x == 128 && y == 64) || (x == 64 && y == 64))) {
+      bm = x;
+      bn = y;
+      bk = z;
+    }
+  }
+  int tiles = ntiles(bm, bn);
+  int nslab = C / bk;
+  int splits = 1;
+  while (tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
+         (size_t)(splits * 2) * M * Nout * sizeof(float) <= ws_bytes)
+    splits *= 2;
+  int per = ceil_div(nslab, splits) * bk;
+  splits = ceil_div(C, per);
+#define HOS_QG(BM_, BN_, BK_) \
+  if (bm == BM_ && bn == BN_ && bk == BK_) launch_shape<QT, DX, BM_, BN_, BK_, NP>(w, a, lda, M, Nout, C, per, splits, epi, ws, st)
+  HOS_QG(128, 128, 64);
+  else HOS_QG(128, 128, 32);
+  else HOS_QG(64, 128, 32);
+  else HOS_QG(128, 64, 32);
+  else HOS_QG(64, 64, 32);
+  else HOS_QG(64, 128, 64);
+  else HOS_QG(128, 64, 64);
+  else HOS_QG(64, 64, 64);
+#undef HOS_QG
+  HOS_HIP_CHECK(hipGetLastError());
+  if (splits > 1) {
+    dim3 rg(ceil_div(Nout, 256), ceil_div(M, RED_ROWS));
+    splitk_reduce<<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
+    HOS_HIP_CHECK(hipGetLastError());
+  }
+}
+
+}  // namespace
+}  // namespace hos

@@ -1,0 +1,19 @@
+// qGEMM instantiations for GGUF_Q4_K (all tile shapes, both directions, 1-3 precision passes).
+#include "qgemm_impl.hpp"
+
+namespace hos {
+
+void qgemm_launch_q4k(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
+                        float* ws, size_t ws_bytes, hipStream_t st) {
+  if (dx) {
+    if (passes == 1) launch_typed<GGUF_Q4_K, true, 1>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else if (passes == 2) launch_typed<GGUF_Q4_K, true, 2>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else launch_typed<GGUF_Q4_K, true, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+  } else {
+    if (passes == 1) launch_typed<GGUF_Q4_K, false, 1>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else if (passes == 2) launch_typed<GGUF_Q4_K, false, 2>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else launch_typed<GGUF_Q4_K, false, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+  }
+}
+
+}  // namespace hos

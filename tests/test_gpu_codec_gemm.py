@@ -54,7 +54,9 @@ def test_dequant_bit_exact(gpu, t):
 
 @pytest.mark.parametrize("passes", [1, 2, 3])
 @pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K])
-@pytest.mark.parametrize("shape", [(256, 512, 512), (200, 576, 768), (128, 1152, 256)])
+@pytest.mark.parametrize("shape", [(256, 512, 512), (200, 576, 768), (128, 1152, 256),
+                                   # large enough for the 128-row / 128-column tile variants
+                                   (2560, 2048, 2048), (1280, 4096, 1024)])
 def test_qgemm_fwd_and_dx(gpu, t, shape, passes):
     T, N, K = shape  # W [N, K]
     print(f"qgemm type {t} T={T} N={N} K={K} passes={passes}", flush=True)
