@@ -34,7 +34,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="qwen2.5-0.5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline sample")
-    ap.add_argument("--cpu-seq", type=int, default=128, help="tokens in the CPU baseline sample")
+    ap.add_argument("--cpu-seq", type=int, default=256, help="tokens in the CPU baseline sample")
     return ap.parse_args()
 
 
@@ -124,7 +124,7 @@ def main():
     gpu.synchronize()
     dt = time.perf_counter() - t0
     loss = float(gpu.d2h(loss_dev, (1,), np.float32)[0])
-    classes = ["qgemm_fwd", "qgemm_dx", "lora", "attn_fwd", "attn_bwd", "rmsnorm", "swiglu", "rope", "ce", "adamw",
+    classes = ["qgemm_fwd", "qgemm_dx", "lora_down", "lora_db", "lora_du", "lora_da", "attn_fwd", "attn_bwd", "rmsnorm", "swiglu", "rope", "ce", "adamw",
                "embed", "convert"]
     stats = {c: pm.kernel_stats(c) for c in classes}
     pm.profile(False)
@@ -161,7 +161,7 @@ def main():
                    "parallelism": "dp1", "gemm_passes": 3},
         "roofline": roof,
         "mfma_roofline_frac_step": round(value * f_tok / 1e12 / PEAK_MFMA_TFLOPS, 4),
-        "dx_gemm_cfg1_4096cubed_q4k": dx,
+        "dx_gemm_4096cubed_q4k": dx,
         "cpu_baseline": cpu,
         "gpu_over_cpu": round(value / cpu["value"], 1) if cpu else None,
         "kernel_ms_per_step": kernel_ms,

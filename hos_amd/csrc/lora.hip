@@ -1,0 +1,346 @@
+// LoRA factor GEMMs on fp32 MFMA (v_mfma_f32_16x16x4f32), shaped for the skinny products of a
+// rank-r adapter (src/peft.rs:508-512 forward; the matmul VJPs of src/tensor.rs:340-391 backward):
+//
+//   rows:  C[M, n]  = α · X[M, K] · Bᵀ        x·A (down-projection), s·dy·Bᵀ (du)
+//   cols:  C(j, c)  = α · Σ_m S[m, j] · G[m, c]   s·uᵀ·dy (dB), xᵀ·du (dA)
+//
+// One side is the adapter rank (n or j ≤ 96), the other a full activation [M, K] read once from HBM,
+// so both kernels are bandwidth-bound: the big operand is streamed with 16-byte loads, the small one
+// is read from L2. The contraction order inside an MFMA is free, so a lane's float4 of 4 consecutive
+// k (rows kernel) or 4 consecutive output columns (cols kernel) feeds 4 MFMAs directly.
+//
+// The long contraction is split across workgroups for parallelism. Each workgroup reduces its four
+// waves in LDS in a fixed order and writes its partial block; a reduce launch sums the partials in
+// split order. Deterministic. (An in-kernel "last workgroup reduces" variant with device-scope fences
+// measured 3-4x slower here: every release fence writes back the XCD's L2.)
+#include <cstdlib>
+
+#include "lora.hpp"
+
+namespace hos {
+namespace {
+
+__device__ __forceinline__ f4v mfma16(float a, float b, f4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Four waves hold partial sums of the same E-element block (element ids given by pos()). Sum them in
+// the fixed order (w0 + w2) + (w1 + w3) through a [2][E] LDS buffer; the result lands in red[0][·].
+template <int NV, class Pos>
+__device__ __forceinline__ void wave_reduce(float (&v)[NV], float* red, int E, Pos pos) {
+  const int wave = threadIdx.x >> 6;
+  if (wave >= 2)
+#pragma unroll
+    for (int i = 0; i < NV; i++) red[(wave - 2) * E + pos(i)] = v[i];
+  __syncthreads();
+  if (wave < 2)
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] += red[wave * E + pos(i)];
+  __syncthreads();
+  if (wave == 1)
+#pragma unroll
+    for (int i = 0; i < NV; i++) red[pos(i)] = v[i];
+  __syncthreads();
+  if (wave == 0)
+#pragma unroll
+    for (int i = 0; i < NV; i++) red[pos(i)] += v[i];
+  __syncthreads();
+}
+
+// Sum of the S partials of element e of block bx, in split order (4 loads in flight).
+__device__ __forceinline__ float sum_parts(const float* part, int S, int gx, int bx, int E, int e) {
+  const long long stride = (long long)gx * E;
+  const float* p = part + (long long)bx * E + e;
+  float v = 0.0f;
+  int s = 0;
+  for (; s + 4 <= S; s += 4) {
+    float a0 = p[s * stride], a1 = p[(s + 1) * stride], a2 = p[(s + 2) * stride], a3 = p[(s + 3) * stride];
+    v += a0;
+    v += a1;
+    v += a2;
+    v += a3;
+  }
+  for (; s < S; s++) v += p[s * stride];
+  return v;
+}
+
+// Block result in red[0..E): write it (no split) or store this split's partial for the reduce launch.
+// store(e, value) writes one finished element of the output.
+template <class Store>
+__device__ __forceinline__ void finish_block(const float* red, int E, float* part, Store store) {
+  if (gridDim.y == 1) {
+    for (int e = threadIdx.x; e < E; e += 256) store(e, red[e]);
+    return;
+  }
+  float* mine = part + ((long long)blockIdx.y * gridDim.x + blockIdx.x) * E;
+  for (int e = threadIdx.x; e < E; e += 256) mine[e] = red[e];
+}
+
+// ---------------- rows: C[M, n] = α·X·Bᵀ ----------------
+// Workgroup: 32 rows × all n columns × a k-chunk; wave w takes the chunk's 16-wide k steps w, w+4, …
+// Lane (q = lane/16, p = lane%16): rows m0+16t+p, k-slot q (k = step + 4q .. +3 as one float4).
+template <int NJ>
+__global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk, float alpha,
+                                                        const float* __restrict__ X, long long ldx,
+                                                        const float* __restrict__ Bt, long long ldb, RowsSeg sg,
+                                                        float* __restrict__ C, long long ldc, float* part) {
+  constexpr int NC = NJ * 16, E = 32 * NC;
+  __shared__ float red[2 * E];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
+  const int m0 = blockIdx.x * 32;
+  const int kb = blockIdx.y * kchunk, ke = min(K, kb + kchunk);
+  const int n = sg.nt * sg.r;
+
+  const float* bp[NJ];
+  int klo[NJ], khi[NJ];
+#pragma unroll
+  for (int jt = 0; jt < NJ; jt++) {
+    const int j = jt * 16 + p;
+    if (j < n) {
+      const int t = j / sg.r, jj = j - t * sg.r;
+      bp[jt] = Bt + sg.boff[t] + (long long)jj * ldb - sg.kbeg[t];
+      klo[jt] = sg.kbeg[t];
+      khi[jt] = sg.kend[t];
+    } else {
+      bp[jt] = Bt;
+      klo[jt] = 0;
+      khi[jt] = 0;
+    }
+  }
+  const float* xr[2];
+  bool rv[2];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int row = m0 + 16 * t + p;
+    rv[t] = row < M;
+    xr[t] = X + (long long)(rv[t] ? row : 0) * ldx;
+  }
+
+  f4v acc[2][NJ];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int jt = 0; jt < NJ; jt++) acc[t][jt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll 2
+  for (int k = kb + 16 * wave; k < ke; k += 64) {
+    const int kk = k + 4 * q;
+    const bool kin = kk < ke;
+    float4 xa[2], bv[NJ];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+      xa[t] = (rv[t] && kin) ? *reinterpret_cast<const float4*>(xr[t] + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int jt = 0; jt < NJ; jt++)
+      bv[jt] = (kin && kk >= klo[jt] && kk < khi[jt]) ? *reinterpret_cast<const float4*>(bp[jt] + kk)
+                                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int jt = 0; jt < NJ; jt++) {
+        acc[t][jt] = mfma16(xa[t].x, bv[jt].x, acc[t][jt]);
+        acc[t][jt] = mfma16(xa[t].y, bv[jt].y, acc[t][jt]);
+        acc[t][jt] = mfma16(xa[t].z, bv[jt].z, acc[t][jt]);
+        acc[t][jt] = mfma16(xa[t].w, bv[jt].w, acc[t][jt]);
+      }
+  }
+
+  // flatten: element (row 16t+4q+i, col 16jt+p) of the 32×NC block
+  float v[2 * NJ * 4];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int jt = 0; jt < NJ; jt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[(t * NJ + jt) * 4 + i] = acc[t][jt][i];
+  wave_reduce(v, red, E, [&](int idx) {
+    const int i = idx & 3, tj = idx >> 2, t = tj / NJ, jt = tj % NJ;
+    return (16 * t + 4 * q + i) * NC + 16 * jt + p;
+  });
+  finish_block(red, E, part, [&](int e, float val) {
+    const int rr = e / NC, c = e % NC, row = m0 + rr;
+    if (row < M && c < n) C[(long long)row * ldc + c] = alpha * val;
+  });
+}
+
+// ---------------- cols: C(j, c) = α·Σ_m S[m, j]·G[m, c] ----------------
+// Workgroup: 64 columns of one segment × all j × an m-chunk; wave w takes the chunk's 4-row steps
+// w, w+4, … Lane (q, p): m = step + q, columns c0+4p .. +3 (one float4; component e is MFMA tile e).
+template <int NS>
+__global__ void __launch_bounds__(256) lora_cols_kernel(int M, int ns, int mchunk, float alpha,
+                                                        const float* __restrict__ Sm, long long lds,
+                                                        const float* __restrict__ Gm, long long ldg, ColsSeg sg,
+                                                        float* __restrict__ C, long long scj, long long scc,
+                                                        float* part) {
+  constexpr int NJR = NS * 16, E = NJR * 64;
+  __shared__ float red[2 * E];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
+  int t = 0;
+#pragma unroll
+  for (int i = 1; i < 4; i++)
+    if (i < sg.nseg && (int)blockIdx.x >= sg.blk0[i]) t = i;
+  const int c0 = ((int)blockIdx.x - sg.blk0[t]) * 64, len = sg.len[t];
+  const int mb = blockIdx.y * mchunk, me = min(M, mb + mchunk);
+  const bool cv = c0 + 4 * p < len;
+  const float* gcol = Gm + sg.gbeg[t] + c0 + 4 * p;
+  const float* scol = Sm + sg.soff[t];
+
+  f4v acc[NS][4];
+#pragma unroll
+  for (int js = 0; js < NS; js++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[js][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll 4
+  for (int m4 = mb + 4 * wave; m4 < me; m4 += 16) {
+    const int m = m4 + q;
+    const bool mv = m < me;
+    const float4 g = (mv && cv) ? *reinterpret_cast<const float4*>(gcol + (long long)m * ldg)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    float s[NS];
+#pragma unroll
+    for (int js = 0; js < NS; js++) {
+      const int j = js * 16 + p;
+      s[js] = (mv && j < ns) ? scol[(long long)m * lds + j] : 0.0f;
+    }
+#pragma unroll
+    for (int js = 0; js < NS; js++) {
+      acc[js][0] = mfma16(s[js], g.x, acc[js][0]);
+      acc[js][1] = mfma16(s[js], g.y, acc[js][1]);
+      acc[js][2] = mfma16(s[js], g.z, acc[js][2]);
+      acc[js][3] = mfma16(s[js], g.w, acc[js][3]);
+    }
+  }
+
+  // flatten: element (j = 16js+4q+i, column 4p+e) of the NJR×64 block
+  float v[NS * 16];
+#pragma unroll
+  for (int js = 0; js < NS; js++)
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[(js * 4 + e) * 4 + i] = acc[js][e][i];
+  wave_reduce(v, red, E, [&](int idx) {
+    const int i = idx & 3, e = (idx >> 2) & 3, js = idx >> 4;
+    return (16 * js + 4 * q + i) * 64 + 4 * p + e;
+  });
+  const long long ocol = sg.ocol[t];
+  finish_block(red, E, part, [&](int e, float val) {
+    const int j = e / 64, c = c0 + e % 64;
+    if (j < ns && c < len) C[(long long)j * scj + (ocol + c) * scc] = alpha * val;
+  });
+}
+
+// Separate-launch reductions of the partials (one thread per output element of every block).
+__global__ void lora_rows_reduce(const float* __restrict__ part, int S, int gx, int NC, int M, int n, float alpha,
+                                 float* __restrict__ C, long long ldc) {
+  const int E = 32 * NC;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)gx * E) return;
+  const int bx = (int)(i / E), e = (int)(i % E), rr = e / NC, c = e % NC, row = bx * 32 + rr;
+  if (row >= M || c >= n) return;
+  C[(long long)row * ldc + c] = alpha * sum_parts(part, S, gx, bx, E, e);
+}
+__global__ void lora_cols_reduce(const float* __restrict__ part, int S, int gx, int NJR, int ns, ColsSeg sg,
+                                 float alpha, float* __restrict__ C, long long scj, long long scc) {
+  const int E = NJR * 64;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)gx * E) return;
+  const int bx = (int)(i / E), e = (int)(i % E);
+  int t = 0;
+  for (int k = 1; k < sg.nseg; k++)
+    if (bx >= sg.blk0[k]) t = k;
+  const int j = e / 64, c = (bx - sg.blk0[t]) * 64 + e % 64;
+  if (j >= ns || c >= sg.len[t]) return;
+  C[(long long)j * scj + ((long long)sg.ocol[t] + c) * scc] = alpha * sum_parts(part, S, gx, bx, E, e);
+}
+
+int ceil_div_i(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// Workgroups a launch aims for; the long contraction is split until the grid reaches it.
+int split_target() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = std::getenv("HOS_LORA_WGS");
+    v = e ? std::max(1, std::atoi(e)) : 1024;
+  }
+  return v;
+}
+
+}  // namespace
+
+void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
+                      long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
+                      hipStream_t st) {
+  const int n = sg.nt * sg.r;
+  if (M <= 0 || n <= 0) return;
+  HOS_REQUIRE(n <= 96 && sg.nt >= 1 && sg.nt <= 4, HOS_E_INVALID, "lora_rows: n = nt·r must be <= 96");
+  HOS_REQUIRE(K % 4 == 0 && ldx % 4 == 0 && ldb % 4 == 0 && ((uintptr_t)X & 15) == 0 && ((uintptr_t)Bt & 15) == 0,
+              HOS_E_INVALID, "lora_rows: K, strides and pointers must be 16-byte aligned");
+  for (int t = 0; t < sg.nt; t++)
+    HOS_REQUIRE(sg.kbeg[t] % 4 == 0 && sg.kend[t] % 4 == 0 && sg.boff[t] % 4 == 0 && sg.kbeg[t] >= 0 &&
+                    sg.kend[t] <= K,
+                HOS_E_INVALID, "lora_rows: segment bounds must be multiples of 4 within K");
+  const int gx = ceil_div_i(M, 32);
+  int S = std::max(1, std::min(ceil_div_i(split_target(), gx), ceil_div_i(K, 64)));
+  int kchunk = ceil_div_i(ceil_div_i(K, S), 64) * 64;
+  S = std::max(1, ceil_div_i(K, kchunk));
+  const int NJ = (n + 15) / 16;
+  HOS_REQUIRE(S == 1 || (size_t)S * gx * 32 * NJ * 16 * 4 <= ws_bytes, HOS_E_INVALID, "lora_rows: workspace too small");
+  dim3 grid(gx, S);
+#define ROWS(NJV)                                                                                         \
+  case NJV:                                                                                               \
+    lora_rows_kernel<NJV><<<grid, 256, 0, st>>>((int)M, (int)K, kchunk, alpha, X, ldx, Bt, ldb, sg, C, ldc, \
+                                                ws);                                             \
+    break;
+  switch (NJ) {
+    ROWS(1) ROWS(2) ROWS(3) ROWS(4) ROWS(5) ROWS(6)
+    default: throw Error(HOS_E_INVALID, "lora_rows: bad width");
+  }
+#undef ROWS
+  HOS_HIP_CHECK(hipGetLastError());
+  if (S > 1) {
+    const long long tot = (long long)gx * 32 * NJ * 16;
+    lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, NJ * 16, (int)M, n, alpha, C, ldc);
+    HOS_HIP_CHECK(hipGetLastError());
+  }
+}
+
+void launch_lora_cols(long long M, int ns, float alpha, const float* Sm, long long lds, const float* Gm, long long ldg,
+                      ColsSeg sg, float* C, long long scj, long long scc, float* ws, size_t ws_bytes,
+                      hipStream_t st) {
+  if (M <= 0 || ns <= 0 || sg.nseg <= 0) return;
+  HOS_REQUIRE(ns <= 96 && sg.nseg <= 4, HOS_E_INVALID, "lora_cols: ns must be <= 96, at most 4 segments");
+  HOS_REQUIRE(ldg % 4 == 0 && ((uintptr_t)Gm & 15) == 0, HOS_E_INVALID, "lora_cols: G must be 16-byte aligned");
+  int gx = 0;
+  for (int t = 0; t < sg.nseg; t++) {
+    HOS_REQUIRE(sg.gbeg[t] % 4 == 0 && sg.len[t] % 4 == 0 && sg.len[t] > 0, HOS_E_INVALID,
+                "lora_cols: segment columns must be multiples of 4");
+    sg.blk0[t] = gx;
+    gx += ceil_div_i(sg.len[t], 64);
+  }
+  int S = std::max(1, std::min(ceil_div_i(split_target(), gx), ceil_div_i(M, 16)));
+  int mchunk = ceil_div_i(ceil_div_i(M, S), 16) * 16;
+  S = std::max(1, ceil_div_i(M, mchunk));
+  const int NS = (ns + 15) / 16;
+  HOS_REQUIRE(S == 1 || (size_t)S * gx * NS * 16 * 64 * 4 <= ws_bytes, HOS_E_INVALID, "lora_cols: workspace too small");
+  dim3 grid(gx, S);
+#define COLS(NSV)                                                                                            \
+  case NSV:                                                                                                  \
+    lora_cols_kernel<NSV><<<grid, 256, 0, st>>>((int)M, ns, mchunk, alpha, Sm, lds, Gm, ldg, sg, C, scj, scc, \
+                                                ws);                                                \
+    break;
+  switch (NS) {
+    COLS(1) COLS(2) COLS(3) COLS(4) COLS(5) COLS(6)
+    default: throw Error(HOS_E_INVALID, "lora_cols: bad width");
+  }
+#undef COLS
+  HOS_HIP_CHECK(hipGetLastError());
+  if (S > 1) {
+    const long long tot = (long long)gx * NS * 16 * 64;
+    lora_cols_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, NS * 16, ns, sg, alpha, C, scj, scc);
+    HOS_HIP_CHECK(hipGetLastError());
+  }
+}
+
+}  // namespace hos

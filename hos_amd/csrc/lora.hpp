@@ -1,0 +1,33 @@
+// LoRA factor GEMMs (lora.hip): skinny fp32-MFMA products with a deterministic split reduction.
+#pragma once
+#include <algorithm>
+
+#include "kernels.hpp"
+
+namespace hos {
+
+// Output columns of the rows kernel come in nt slots of r columns (one per adapter target). Slot t
+// contracts over X columns [kbeg[t], kend[t]) against Bt[boff[t] + jj·ldb + (k − kbeg[t])], jj < r.
+struct RowsSeg {
+  int nt = 0, r = 0;
+  int kbeg[4] = {0, 0, 0, 0}, kend[4] = {0, 0, 0, 0};
+  long long boff[4] = {0, 0, 0, 0};
+};
+// C[m, j] = α·Σ_k X[m, k]·B(j, k) for m < M, j < nt·r. X rows 16-byte aligned, K % 4 == 0.
+void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
+                      long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
+                      hipStream_t st);
+
+// Column segments of the cols kernel: segment t covers G columns [gbeg, gbeg + len), uses S columns
+// starting at soff and writes output columns starting at ocol. blk0 is filled in by the launcher.
+struct ColsSeg {
+  int nseg = 0;
+  int gbeg[4] = {0, 0, 0, 0}, len[4] = {0, 0, 0, 0}, soff[4] = {0, 0, 0, 0}, ocol[4] = {0, 0, 0, 0};
+  int blk0[4] = {0, 0, 0, 0};
+};
+// C[j·scj + (ocol + c)·scc] = α·Σ_m S[m, soff + j]·G[m, gbeg + c] for j < ns, c < len, per segment.
+void launch_lora_cols(long long M, int ns, float alpha, const float* Sm, long long lds, const float* Gm, long long ldg,
+                      ColsSeg sg, float* C, long long scj, long long scc, float* ws, size_t ws_bytes,
+                      hipStream_t st);
+
+}  // namespace hos

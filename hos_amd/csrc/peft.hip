@@ -17,6 +17,7 @@
 
 #include "ctx.hpp"
 #include "fused.hpp"
+#include "lora.hpp"
 
 using namespace hos;
 
@@ -74,8 +75,9 @@ struct hos_peft {
   bool out_set = false;
   float* out_norm = nullptr;
 
-  // LoRA arena: offsets (floats) of A and B per (layer, target); -1 when not adapted
-  std::vector<long long> offA, offB;
+  // LoRA arena offsets (floats): per (layer, group) the stacked At and Bcat blocks; per (layer, target)
+  // the first row of A_tᵀ in At and the first column of B_t in Bcat; -1 when not adapted
+  std::vector<long long> offAg, offBg, offA, offB;
   long long nparams = 0;
   float *P = nullptr, *G = nullptr, *M1 = nullptr, *V1 = nullptr;
   uint64_t adam_t = 0;
@@ -171,21 +173,18 @@ struct hos_peft {
     e.resid = nullptr;
     launch_qgemm_dx(w, a, lda, M, e, ws, ws_bytes, passes, st);
   }
-  // f32 GEMM C = alpha·A·B + beta·C (strided)
-  void g32(long long M, long long N, long long K, float alpha, const float* A, long long sam, long long sak,
-           const float* B, long long sbk, long long sbn, float beta, float* C, long long ldc) {
-    Scope s(this, "lora", 2.0 * M * N * K, 4.0 * (M * K + K * N + M * N * (beta != 0.0f ? 2 : 1)));
-    launch_gemm_f32(M, N, K, alpha, A, sam, sak, B, sbk, sbn, beta, C, ldc, ws, ws_bytes, st);
-  }
   void to16(const float* x, long long ldx, int M, int K) {
     Scope s(this, "convert", 0, 6.0 * M * K);
     launch_to_h16(x, ldx, M, K, hs, st);
   }
 
   // ---- LoRA pieces (reference factors: A [in, r], B [r, out]) ----
-  // Targets sharing an input form a group (q/k/v, o, gate/up, down). A group's adapted A factors sit
-  // side by side as one [in, G·r] matrix, so one GEMM gives u = x·[A_1 … A_G] and one gives
-  // [dA_1 … dA_G] = xᵀ·[du_1 … du_G]. u and du live in [M, 7·r] buffers, target t at column ucol(t).
+  // Targets sharing an input form a group (q/k/v, o, gate/up, down). Per layer and group the arena
+  // holds the adapted targets' A factors transposed and stacked, At [G·r][in] (row slot·r + j is
+  // column j of A_t), then their B factors side by side, Bcat [r][Σ out] (B_t at column bcol(t)).
+  // One rows-GEMM gives u = x·[A_1 … A_G] for the whole group, one cols-GEMM gives every dA, one
+  // cols-GEMM every dB and one rows-GEMM every du. u and du live in [M, 7·r] buffers, target t at
+  // column ucol(t).
   static int group_of(int t) { return t <= TV ? 0 : (t == TO ? 1 : (t <= TU ? 2 : 3)); }
   static int group_first(int g) { return g == 0 ? TQ : (g == 1 ? TO : (g == 2 ? TG : TD)); }
   static int group_last(int g) { return g == 0 ? TV : (g == 1 ? TO : (g == 2 ? TU : TD)); }
@@ -199,66 +198,126 @@ struct hos_peft {
     for (int u = group_first(group_of(t)); u < t; u++) n += has(u);
     return n;
   }
-  long long ldA(int t) const { return (long long)gcount(group_of(t)) * r; }
-  int ucol(int t) const { return group_first(group_of(t)) * r + slot(t) * r; }
-
-  // u[:, group columns] = x · A_group (forward)
-  void lora_down(int l, int g, const float* x, long long ldx, int M) {
-    const int t0 = group_first(g), n = gcount(g);
-    if (n == 0) return;
-    int in, o;
-    dims(t0, &in, &o);
-    int first = t0;
-    while (!has(first)) first++;
-    g32(M, (long long)n * r, in, 1.0f, x, ldx, 1, P + offA[l * NT + first], (long long)n * r, 1, 0.0f,
-        act[l].u + ucol(first), NT * r);
+  int first_adapted(int g) const {
+    int t = group_first(g);
+    while (t <= group_last(g) && !has(t)) t++;
+    return t;
   }
-  // Epilogue term y += s·u_t·B_t of the base forward GEMM
+  int ucol(int t) const { return group_first(group_of(t)) * r + slot(t) * r; }
+  int out_dim(int t) const {
+    int in, o;
+    dims(t, &in, &o);
+    return o;
+  }
+  int in_dim(int t) const {
+    int in, o;
+    dims(t, &in, &o);
+    return in;
+  }
+  // Bcat width of a group and column of target t in it
+  int bw(int g) const {
+    int w = 0;
+    for (int t = group_first(g); t <= group_last(g); t++)
+      if (has(t)) w += out_dim(t);
+    return w;
+  }
+  int bcol(int t) const {
+    int w = 0;
+    for (int u = group_first(group_of(t)); u < t; u++)
+      if (has(u)) w += out_dim(u);
+    return w;
+  }
+  // column of target t's output inside the buffer its group's projections write (fused q|k|v, gate|up)
+  int ycol(int t) const { return t == TK ? qd : (t == TV ? qd + kvd : (t == TU ? F : 0)); }
+
+  void lora_rows(const char* cls, long long M, long long K, float alpha, const float* X, long long ldx,
+                 const float* Bt, long long ldb, const RowsSeg& sg, float* C, long long ldc) {
+    Scope s(this, cls, 2.0 * M * K * sg.nt * sg.r, 4.0 * (M * K + (double)M * sg.nt * sg.r));
+    launch_lora_rows(M, K, alpha, X, ldx, Bt, ldb, sg, C, ldc, ws, ws_bytes, st);
+  }
+  void lora_cols(const char* cls, long long M, int ns, float alpha, const float* Sm, long long lds, const float* Gm,
+                 long long ldg, const ColsSeg& sg, float* C, long long scj, long long scc) {
+    double cols = 0;
+    for (int t = 0; t < sg.nseg; t++) cols += sg.len[t];
+    Scope s(this, cls, 2.0 * M * ns * cols, 4.0 * (M * cols + (double)M * ns + ns * cols));
+    launch_lora_cols(M, ns, alpha, Sm, lds, Gm, ldg, sg, C, scj, scc, ws, ws_bytes, st);
+  }
+
+  // u[:, group columns] = x · [A_1 … A_G]   (forward)
+  void lora_down(int l, int g, const float* x, long long ldx, int M) {
+    const int n = gcount(g);
+    if (n == 0) return;
+    const int first = first_adapted(g), in = in_dim(first);
+    RowsSeg sg;
+    sg.nt = n;
+    sg.r = r;
+    for (int i = 0; i < n; i++) {
+      sg.kbeg[i] = 0;
+      sg.kend[i] = in;
+      sg.boff[i] = (long long)i * r * in;
+    }
+    lora_rows("lora_down", M, in, 1.0f, x, ldx, P + offAg[l * 4 + g], in, sg, act[l].u + ucol(first), NT * r);
+  }
+  // Epilogue term y += s·u_t·B_t of the base forward GEMM: L(j, n) = Bcat[j·bw + bcol(t) + n]
   GemmEpi up_epi(int l, int t) {
     GemmEpi e{};
     if (!has(t)) return e;
-    int in, o;
-    dims(t, &in, &o);
     e.U = act[l].u + ucol(t);
     e.ldu = NT * r;
     e.L = P + offB[l * NT + t];
-    e.slj = o;
+    e.slj = bw(group_of(t));
     e.sln = 1;
     e.rank = r;
     e.scale = lscale;
     return e;
   }
-  // From dy (grad of the adapted projection's output): dB_t = s·u_tᵀ·dy, du_t = s·dy·B_tᵀ.
-  void lora_grad_b(int l, int t, const float* dy, long long ldy, int M) {
-    int in, o;
-    dims(t, &in, &o);
-    const float* B = P + offB[l * NT + t];
-    g32(r, o, M, lscale, act[l].u + ucol(t), 1, NT * r, dy, ldy, 1, 0.0f, G + offB[l * NT + t], o);
-    g32(M, r, o, lscale, dy, ldy, 1, B, 1, o, 0.0f, du + ucol(t), NT * r);
+  // From dy, the gradient of the group's fused projection output (row stride ldy, target t at column
+  // ycol(t)): dB_t = s·u_tᵀ·dy_t for every adapted t (one launch), du_t = s·dy_t·B_tᵀ (one launch).
+  void lora_grad_b(int l, int g, const float* dy, long long ldy, long long kspan, int M) {
+    const int n = gcount(g);
+    if (n == 0) return;
+    ColsSeg cs;
+    RowsSeg rs;
+    rs.nt = n;
+    rs.r = r;
+    for (int t = group_first(g); t <= group_last(g); t++) {
+      if (!has(t)) continue;
+      const int i = cs.nseg++;
+      cs.gbeg[i] = ycol(t);
+      cs.len[i] = out_dim(t);
+      cs.soff[i] = ucol(t);
+      cs.ocol[i] = bcol(t);
+      rs.kbeg[i] = ycol(t);
+      rs.kend[i] = ycol(t) + out_dim(t);
+      rs.boff[i] = bcol(t);
+    }
+    const int w = bw(g);
+    lora_cols("lora_db", M, r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1);
+    lora_rows("lora_du", M, kspan, lscale, dy, ldy, P + offBg[l * 4 + g], w, rs, du + ucol(first_adapted(g)),
+              NT * r);
   }
-  // Epilogue term dx_in += du_t·A_tᵀ of the base dX GEMM
+  // Epilogue term dx_in += du_t·A_tᵀ of the base dX GEMM: L(j, col) = At[(slot·r + j)·in + col]
   GemmEpi down_epi(int l, int t) {
     GemmEpi e{};
     if (!has(t)) return e;
     e.U = du + ucol(t);
     e.ldu = NT * r;
-    e.L = P + offA[l * NT + t];  // L(j, col) = A_t[col, j]
-    e.slj = 1;
-    e.sln = ldA(t);
+    e.L = P + offA[l * NT + t];
+    e.slj = in_dim(t);
+    e.sln = 1;
     e.rank = r;
     e.scale = 1.0f;
     return e;
   }
-  // [dA_1 … dA_G] = xᵀ·[du_1 … du_G]
+  // [dA_1 … dA_G]ᵀ = ([du_1 … du_G])ᵀ·x, written straight into the stacked At layout
   void lora_grad_a(int l, int g, const float* x, long long ldx, int M) {
     const int n = gcount(g);
     if (n == 0) return;
-    int first = group_first(g);
-    while (!has(first)) first++;
-    int in, o;
-    dims(first, &in, &o);
-    g32(in, (long long)n * r, M, 1.0f, x, 1, ldx, du + ucol(first), NT * r, 1, 0.0f, G + offA[l * NT + first],
-        (long long)n * r);
+    const int first = first_adapted(g), in = in_dim(first);
+    ColsSeg cs;
+    cs.nseg = 1;
+    cs.len[0] = in;
+    lora_cols("lora_da", M, n * r, 1.0f, du + ucol(first), NT * r, x, ldx, cs, G + offAg[l * 4 + g], in, 1);
   }
 
   void check_ready() {
@@ -354,15 +413,14 @@ struct hos_peft {
       LayerW& w = lw[l];
       // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA) ----
       to16(dx, d, M, d);
-      if (has(TD)) lora_grad_b(l, TD, dx, d, M);
+      lora_grad_b(l, 3, dx, d, d, M);
       qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD));
       lora_grad_a(l, 3, a.h, F, M);
       {
         Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (dgu ? 8.0 * M * F : 0));
         launch_swiglu_bwd(a.gu, dh, M, F, (has(TG) || has(TU)) ? dgu : nullptr, hs, st);
       }
-      if (has(TG)) lora_grad_b(l, TG, dgu, 2LL * F, M);
-      if (has(TU)) lora_grad_b(l, TU, dgu + F, 2LL * F, M);
+      if (dgu) lora_grad_b(l, 2, dgu, 2LL * F, 2LL * F, M);
       H16 hu = h16_offset(hs, F);
       qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG));
       qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU));
@@ -373,7 +431,7 @@ struct hos_peft {
       }
       // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
       to16(dx, d, M, d);
-      if (has(TO)) lora_grad_b(l, TO, dx, d, M);
+      lora_grad_b(l, 1, dx, d, d, M);
       qdx(w.w[TO], hs, d, M, dout, qd, 0, down_epi(l, TO));
       lora_grad_a(l, 1, a.o, qd, M);
       {
@@ -387,9 +445,7 @@ struct hos_peft {
         launch_rope(dqkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
         launch_rope(dqkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
       }
-      const int qcol[3] = {0, qd, qd + kvd};
-      for (int t = TQ; t <= TV; t++)
-        if (has(t)) lora_grad_b(l, t, dqkv + qcol[t], W3, M);
+      lora_grad_b(l, 0, dqkv, W3, W3, M);
       to16(dqkv, W3, M, W3);
       H16 hk = h16_offset(hs, qd), hv = h16_offset(hs, qd + kvd);
       qdx(w.w[TQ], hs, W3, M, dxn, d, 0, down_epi(l, TQ));
@@ -456,22 +512,24 @@ struct hos_peft {
     // LoRA arena
     offA.assign((size_t)L * NT, -1);
     offB.assign((size_t)L * NT, -1);
+    offAg.assign((size_t)L * 4, -1);
+    offBg.assign((size_t)L * 4, -1);
     HOS_REQUIRE(r <= 32, HOS_E_INVALID, "peft: LoRA rank must be <= 32");
     long long off = 0;
+    auto pad = [](long long v) { return (v + 63) & ~63LL; };  // 256-byte aligned blocks
     for (int l = 0; l < L; l++)
       for (int g = 0; g < 4; g++) {
         const int n = gcount(g);
         if (n == 0) continue;
-        int in, o;
-        dims(group_first(g), &in, &o);
-        const long long abase = off;  // the group's A factors: one [in, n·r] matrix
-        off += (long long)in * n * r;
+        const int in = in_dim(group_first(g));
+        offAg[l * 4 + g] = off;
+        off = pad(off + (long long)n * r * in);
+        offBg[l * 4 + g] = off;
+        off = pad(off + (long long)r * bw(g));
         for (int t = group_first(g); t <= group_last(g); t++)
           if (has(t)) {
-            dims(t, &in, &o);
-            offA[l * NT + t] = abase + (long long)slot(t) * r;
-            offB[l * NT + t] = off;
-            off += (long long)r * o;
+            offA[l * NT + t] = offAg[l * 4 + g] + (long long)slot(t) * r * in;
+            offB[l * NT + t] = offBg[l * 4 + g] + bcol(t);
           }
       }
     nparams = off;
@@ -681,10 +739,13 @@ int hos_peft_set_lora(hos_peft* p, int layer, int target, const float* A, const 
     HOS_REQUIRE(A && B, HOS_E_INVALID, "null factor");
     int i = lora_index(p, layer, target), in, o;
     p->dims(target, &in, &o);
-    const size_t rb = (size_t)p->r * 4;
-    HOS_HIP_CHECK(hipMemcpy2DAsync(p->P + p->offA[i], (size_t)p->ldA(target) * 4, A, rb, rb, (size_t)in,
-                                   hipMemcpyHostToDevice, p->st));
-    HOS_HIP_CHECK(hipMemcpyAsync(p->P + p->offB[i], B, (size_t)p->r * o * 4, hipMemcpyHostToDevice, p->st));
+    const int r = p->r;
+    std::vector<float> at((size_t)r * in);  // device keeps A_tᵀ [r][in]
+    for (int k = 0; k < in; k++)
+      for (int j = 0; j < r; j++) at[(size_t)j * in + k] = A[(size_t)k * r + j];
+    HOS_HIP_CHECK(hipMemcpyAsync(p->P + p->offA[i], at.data(), at.size() * 4, hipMemcpyHostToDevice, p->st));
+    HOS_HIP_CHECK(hipMemcpy2DAsync(p->P + p->offB[i], (size_t)p->bw(p->group_of(target)) * 4, B, (size_t)o * 4,
+                                   (size_t)o * 4, (size_t)r, hipMemcpyHostToDevice, p->st));
     HOS_HIP_CHECK(hipStreamSynchronize(p->st));
   });
 }
@@ -693,11 +754,17 @@ static int get_pair(hos_peft* p, const float* base, int layer, int target, float
   return pguard(p, [&] {
     int i = lora_index(p, layer, target), in, o;
     p->dims(target, &in, &o);
-    const size_t rb = (size_t)p->r * 4;
-    if (A)
-      HOS_HIP_CHECK(hipMemcpy2DAsync(A, rb, base + p->offA[i], (size_t)p->ldA(target) * 4, rb, (size_t)in,
-                                     hipMemcpyDeviceToHost, p->st));
-    if (B) HOS_HIP_CHECK(hipMemcpyAsync(B, base + p->offB[i], (size_t)p->r * o * 4, hipMemcpyDeviceToHost, p->st));
+    const int r = p->r;
+    if (A) {
+      std::vector<float> at((size_t)r * in);
+      HOS_HIP_CHECK(hipMemcpyAsync(at.data(), base + p->offA[i], at.size() * 4, hipMemcpyDeviceToHost, p->st));
+      HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+      for (int k = 0; k < in; k++)
+        for (int j = 0; j < r; j++) A[(size_t)k * r + j] = at[(size_t)j * in + k];
+    }
+    if (B)
+      HOS_HIP_CHECK(hipMemcpy2DAsync(B, (size_t)o * 4, base + p->offB[i], (size_t)p->bw(p->group_of(target)) * 4,
+                                     (size_t)o * 4, (size_t)r, hipMemcpyDeviceToHost, p->st));
     HOS_HIP_CHECK(hipStreamSynchronize(p->st));
   });
 }

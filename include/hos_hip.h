@@ -165,7 +165,7 @@ int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out);
 /* Per-kernel-class timing with HIP events around every launch (off by default). */
 int hos_peft_profile(hos_peft* p, int enable);
 /* Accumulated stats of one kernel class since profiling was enabled: launches, total ms,
- * algorithmic flops and HBM bytes. Classes: "qgemm_fwd", "qgemm_dx", "lora", "attn_fwd",
+ * algorithmic flops and HBM bytes. Classes: "qgemm_fwd", "qgemm_dx", "lora_down", "lora_db", "lora_du", "lora_da", "attn_fwd",
  * "attn_bwd", "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert". */
 int hos_peft_kernel_stats(hos_peft* p, const char* cls, long long* launches, double* total_ms, double* flops,
                           double* bytes);
