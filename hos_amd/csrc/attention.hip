@@ -13,85 +13,87 @@
 // rows i = 8·(r/4) + 4·(lane/32) + r%4 in register r. Read back as an A operand, register r of that
 // layout supplies row (lane%32) of Xᵀ at contraction index κ(r, lane/32) = 8·(r/4) + 4·(lane/32) + r%4,
 // so a score tile feeds the next MFMA straight from registers provided the other operand is gathered
-// in the same κ order. Per wave: 32 queries (or keys) × 64 head dims; one wave per workgroup.
+// in the same κ order. Per wave: 32 queries (or keys) × 64 head dims; 4 waves per workgroup split the
+// other sequence axis and merge in LDS, so there is no workgroup barrier inside the main loops.
 #include "fused.hpp"
 
 namespace hos {
 namespace {
 
-constexpr int HD = 64, TB = 32, LP = HD + 1;  // tile rows, padded LDS row (floats)
+constexpr int HD = 64, TB = 32, KW = 4, LP = HD + 1;  // head dim, tile rows, waves per workgroup, LDS row
 
 __device__ __forceinline__ int kap(int s, int h) { return 8 * (s >> 2) + 4 * h + (s & 3); }
 
-// Load rows [r0, r0+32) × 64 cols (row stride ld, col offset col) into LDS [32][LP], clamping rows ≥ T
-// to T-1 (masked later); scaled by `mul`.
-__device__ __forceinline__ void load_tile(float (*dst)[LP], const float* __restrict__ src, long long base_row, int r0,
-                                          int T, long long ld, int col, float mul) {
-  const int lane = threadIdx.x;
-  for (int e = lane; e < TB * HD / 4; e += 64) {
-    int r = e / (HD / 4), c4 = e % (HD / 4);
-    int t = r0 + r;
-    long long row = base_row + (t < T ? t : T - 1);
-    float4 v = *(const float4*)(src + row * ld + col + 4 * c4);
-    dst[r][4 * c4] = v.x * mul;
-    dst[r][4 * c4 + 1] = v.y * mul;
-    dst[r][4 * c4 + 2] = v.z * mul;
-    dst[r][4 * c4 + 3] = v.w * mul;
+// Fragment of one row for a contraction over the 64 head dims: frag[4j + e] = row[8j + 4·hl + e]·mul.
+// Any bijection of the contraction index works as long as both MFMA operands use it; this one lets a
+// lane fetch its 32 values as 8 float4.
+__device__ __forceinline__ void load_rowfrag(float* frag, const float* __restrict__ row, int hl, float mul) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const float4 v = *reinterpret_cast<const float4*>(row + 8 * j + 4 * hl);
+    frag[4 * j] = v.x * mul;
+    frag[4 * j + 1] = v.y * mul;
+    frag[4 * j + 2] = v.z * mul;
+    frag[4 * j + 3] = v.w * mul;
   }
 }
 
-// B-operand fragment of a [32 rows][64] matrix held in registers: frag[s] = X[row0 + lane%32][2s + lane/32].
-__device__ __forceinline__ void load_frag(float* frag, const float* __restrict__ src, long long base_row, int r0,
-                                          int T, long long ld, int col, float mul) {
-  const int lane = threadIdx.x;
-  int t = r0 + (lane & 31);
-  long long row = base_row + (t < T ? t : T - 1);
-  const float* p = src + row * ld + col + (lane >> 5);
+// B operand over 32 rows indexed in κ order: col[s] = X[r0 + κ(s, hl)][c], col[16 + s] = …[32 + c].
+__device__ __forceinline__ void load_kapcols(float* col, const float* __restrict__ src, long long base_row, int r0,
+                                             int T, long long ld, int off, int hl, int c, float mul) {
 #pragma unroll
-  for (int s = 0; s < 32; s++) frag[s] = p[2 * s] * mul;
+  for (int s = 0; s < 16; s++) {
+    const int t = r0 + kap(s, hl);
+    const float* row = src + (base_row + (t < T ? t : T - 1)) * ld + off;
+    col[s] = row[c] * mul;
+    col[16 + s] = row[32 + c] * mul;
+  }
 }
 
-__global__ void __launch_bounds__(64) attn_fwd_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
-                                                      int T, int nh, int group, float* __restrict__ o, long long ldo,
-                                                      float* __restrict__ lse) {
-  __shared__ float Ks[TB][LP];
-  __shared__ float Vs[TB][LP];
-  __shared__ float xch[TB];
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
-  const int lane = threadIdx.x, hl = lane >> 5, q0 = qb * TB;
-  const int myq = q0 + (lane & 31);  // this lane's query in the Sᵀ layout
+__device__ __forceinline__ f16v mfma32(float a, float b, f16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Forward. Workgroup = (32 queries, head, sequence); its 4 waves take key blocks w, w+4, … up to the
+// diagonal, each keeping its own online-softmax state (m, l, O); the states are merged in LDS at the end.
+__global__ void __launch_bounds__(256) attn_fwd_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+                                                       int T, int nh, int group, float* __restrict__ o, long long ldo,
+                                                       float* __restrict__ lse) {
+  __shared__ float Os[KW][TB][LP];
+  __shared__ float Ms[KW][TB], Ls[KW][TB];
+  const int nqb = (T + TB - 1) / TB;
+  const int qb = nqb - 1 - (int)blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;  // long rows first
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31, q0 = qb * TB;
+  const int myq = q0 + c;  // this lane's query in the Sᵀ layout
   const long long base = (long long)b * T;
   float qf[32];
-  load_frag(qf, qkv, base, q0, T, ld, h * HD, 0.125f);
+  load_rowfrag(qf, qkv + (base + (myq < T ? myq : T - 1)) * ld + h * HD, hl, 0.125f);
   f16v O0, O1;
 #pragma unroll
   for (int r = 0; r < 16; r++) O0[r] = O1[r] = 0.0f;
   float m = -INFINITY, l = 0.0f;
-  const int nkb = min(qb + 1, (T + TB - 1) / TB);
-  for (int kb = 0; kb < nkb; kb++) {
-    const int k0 = kb * TB;
-    __syncthreads();
-    load_tile(Ks, qkv, base, k0, T, ld, kcol + g * HD, 1.0f);
-    load_tile(Vs, qkv, base, k0, T, ld, vcol + g * HD, 1.0f);
-    __syncthreads();
+  for (int kb = w; kb <= qb; kb += KW) {
+    const int k0 = kb * TB, kr = k0 + c;
+    float kf[32], vv[32];
+    load_rowfrag(kf, qkv + (base + (kr < T ? kr : T - 1)) * ld + kcol + g * HD, hl, 1.0f);
+    load_kapcols(vv, qkv, base, k0, T, ld, vcol + g * HD, hl, c, 1.0f);
     f16v S;
 #pragma unroll
     for (int r = 0; r < 16; r++) S[r] = 0.0f;
 #pragma unroll
-    for (int s = 0; s < 32; s++) S = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[lane & 31][2 * s + hl], qf[s], S, 0, 0, 0);
-    // S[r] = score(key k0 + kap(r, hl), query myq)
+    for (int s = 0; s < 32; s++) S = mfma32(kf[s], qf[s], S);
+    // S[r] = score(key k0 + κ(r, hl), query myq)
     float mb = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      int key = k0 + kap(r, hl);
+      const int key = k0 + kap(r, hl);
       if (key > myq || key >= T) S[r] = -INFINITY;
       mb = fmaxf(mb, S[r]);
     }
     mb = fmaxf(mb, __shfl_xor(mb, 32));
     const float mn = fmaxf(m, mb);
     const float alpha = (m == -INFINITY) ? 0.0f : expf(m - mn);
-    float ps = 0.0f;
-    float p[16];
+    float ps = 0.0f, p[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       p[r] = (S[r] == -INFINITY) ? 0.0f : expf(S[r] - mn);
@@ -100,35 +102,51 @@ __global__ void __launch_bounds__(64) attn_fwd_kernel(const float* __restrict__ 
     ps += __shfl_xor(ps, 32);
     l = l * alpha + ps;
     m = mn;
-    // rescale O rows (queries q0 + kap(r, hl) in the O layout) by their alpha
-    if (lane < 32) xch[lane] = alpha;
-    __syncthreads();
+    // O rows are queries q0 + κ(r, hl): fetch their alpha from the lane that owns that query
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      float a = xch[kap(r, hl)];
+      const float a = __shfl(alpha, kap(r, hl));
       O0[r] *= a;
       O1[r] *= a;
     }
 #pragma unroll
     for (int s = 0; s < 16; s++) {
-      const float* vr = Vs[kap(s, hl)];
-      O0 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], vr[lane & 31], O0, 0, 0, 0);
-      O1 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], vr[32 + (lane & 31)], O1, 0, 0, 0);
+      O0 = mfma32(p[s], vv[s], O0);
+      O1 = mfma32(p[s], vv[16 + s], O1);
     }
   }
-  __syncthreads();
-  if (lane < 32) xch[lane] = l;
-  __syncthreads();
-  if (lane < 32 && myq < T) lse[((long long)b * nh + h) * T + myq] = m + logf(l);
+  if (hl == 0) {
+    Ms[w][c] = m;
+    Ls[w][c] = l;
+  }
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    int q = q0 + kap(r, hl);
-    if (q >= T) continue;
-    float inv = 1.0f / xch[kap(r, hl)];
-    float* orow = o + (base + q) * ldo + h * HD;
-    orow[lane & 31] = O0[r] * inv;
-    orow[32 + (lane & 31)] = O1[r] * inv;
+    Os[w][kap(r, hl)][c] = O0[r];
+    Os[w][kap(r, hl)][32 + c] = O1[r];
   }
+  __syncthreads();
+  // merge the four states: thread → (query tid/8, dims 8·(tid%8) .. +8)
+  const int qi = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 8, t = q0 + qi;
+  if (t >= T) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < KW; v++) mx = fmaxf(mx, Ms[v][qi]);
+  float e[KW], den = 0.0f;
+#pragma unroll
+  for (int v = 0; v < KW; v++) {
+    e[v] = Ms[v][qi] == -INFINITY ? 0.0f : expf(Ms[v][qi] - mx);
+    den += Ls[v][qi] * e[v];
+  }
+  const float inv = 1.0f / den;
+  float* orow = o + (base + t) * ldo + h * HD;
+#pragma unroll
+  for (int d = d0; d < d0 + 8; d++) {
+    float num = 0.0f;
+#pragma unroll
+    for (int v = 0; v < KW; v++) num += Os[v][qi][d] * e[v];
+    orow[d] = num * inv;
+  }
+  if (d0 == 0) lse[((long long)b * nh + h) * T + t] = mx + logf(den);
 }
 
 // Dvec[b,h,t] = Σ_d dO·O over the head's 64 columns.
@@ -146,135 +164,138 @@ __global__ void attn_dvec_kernel(const float* __restrict__ o, const float* __res
   dvec[i] = s;
 }
 
-// dQ for 32 queries of head h: Sᵀ and dPᵀ with lanes on queries, dQ = (dS·K)·2^-3.
-__global__ void __launch_bounds__(64) attn_dq_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
-                                                     const float* __restrict__ dout, long long ldd,
-                                                     const float* __restrict__ lse, const float* __restrict__ dvec,
-                                                     int T, int nh, int group, float* __restrict__ dq,
-                                                     long long ldq) {
-  __shared__ float Ks[TB][LP];
-  __shared__ float Vs[TB][LP];
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
-  const int lane = threadIdx.x, hl = lane >> 5, q0 = qb * TB;
-  const int myq = q0 + (lane & 31);
-  const long long base = (long long)b * T;
+// dQ for 32 queries of head h: Sᵀ and dPᵀ with lanes on queries, dQ = (dS·K)·2^-3. The 4 waves take
+// key blocks w, w+4, …; their partial dQ are summed in wave order.
+__global__ void __launch_bounds__(256) attn_dq_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+                                                      const float* __restrict__ dout, long long ldd,
+                                                      const float* __restrict__ lse, const float* __restrict__ dvec,
+                                                      int T, int nh, int group, float* __restrict__ dq,
+                                                      long long ldq) {
+  __shared__ float As[KW][TB][LP];
+  const int nqb = (T + TB - 1) / TB;
+  const int qb = nqb - 1 - (int)blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31, q0 = qb * TB;
+  const int myq = q0 + c;
+  const long long base = (long long)b * T, qrow = base + (myq < T ? myq : T - 1);
   float qf[32], df[32];
-  load_frag(qf, qkv, base, q0, T, ld, h * HD, 0.125f);
-  load_frag(df, dout, base, q0, T, ldd, h * HD, 1.0f);
+  load_rowfrag(qf, qkv + qrow * ld + h * HD, hl, 0.125f);
+  load_rowfrag(df, dout + qrow * ldd + h * HD, hl, 1.0f);
   const long long si = ((long long)b * nh + h) * T + (myq < T ? myq : T - 1);
   const float L = lse[si], Dv = dvec[si];
   f16v A0, A1;
 #pragma unroll
   for (int r = 0; r < 16; r++) A0[r] = A1[r] = 0.0f;
-  const int nkb = min(qb + 1, (T + TB - 1) / TB);
-  for (int kb = 0; kb < nkb; kb++) {
-    const int k0 = kb * TB;
-    __syncthreads();
-    load_tile(Ks, qkv, base, k0, T, ld, kcol + g * HD, 1.0f);
-    load_tile(Vs, qkv, base, k0, T, ld, vcol + g * HD, 1.0f);
-    __syncthreads();
+  for (int kb = w; kb <= qb; kb += KW) {
+    const int k0 = kb * TB, kr = k0 + c;
+    const long long krow = base + (kr < T ? kr : T - 1);
+    float kf[32], vf[32];
+    load_rowfrag(kf, qkv + krow * ld + kcol + g * HD, hl, 1.0f);
+    load_rowfrag(vf, qkv + krow * ld + vcol + g * HD, hl, 1.0f);
     f16v S, dP;
 #pragma unroll
     for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
 #pragma unroll
     for (int s = 0; s < 32; s++) {
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[lane & 31][2 * s + hl], qf[s], S, 0, 0, 0);
-      dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[lane & 31][2 * s + hl], df[s], dP, 0, 0, 0);
+      S = mfma32(kf[s], qf[s], S);
+      dP = mfma32(vf[s], df[s], dP);
     }
     float ds[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      int key = k0 + kap(r, hl);
-      float pv = (key > myq || key >= T || myq >= T) ? 0.0f : expf(S[r] - L);
+      const int key = k0 + kap(r, hl);
+      const float pv = (key > myq || key >= T || myq >= T) ? 0.0f : expf(S[r] - L);
       ds[r] = pv * (dP[r] - Dv);
     }
+    float kk[32];
+    load_kapcols(kk, qkv, base, k0, T, ld, kcol + g * HD, hl, c, 1.0f);
 #pragma unroll
     for (int s = 0; s < 16; s++) {
-      const float* kr = Ks[kap(s, hl)];
-      A0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], kr[lane & 31], A0, 0, 0, 0);
-      A1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], kr[32 + (lane & 31)], A1, 0, 0, 0);
+      A0 = mfma32(ds[s], kk[s], A0);
+      A1 = mfma32(ds[s], kk[16 + s], A1);
     }
   }
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    int q = q0 + kap(r, hl);
-    if (q >= T) continue;
-    float* out = dq + (base + q) * ldq + h * HD;
-    out[lane & 31] = A0[r] * 0.125f;
-    out[32 + (lane & 31)] = A1[r] * 0.125f;
+    As[w][kap(r, hl)][c] = A0[r];
+    As[w][kap(r, hl)][32 + c] = A1[r];
+  }
+  __syncthreads();
+  const int qi = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 8, t = q0 + qi;
+  if (t >= T) return;
+  float* out = dq + (base + t) * ldq + h * HD;
+#pragma unroll
+  for (int d = d0; d < d0 + 8; d++) {
+    float v = As[0][qi][d];
+#pragma unroll
+    for (int u = 1; u < KW; u++) v += As[u][qi][d];
+    out[d] = v * 0.125f;
   }
 }
 
-// dK, dV for 32 keys against query head h (kv head g = h / group): S and dP with lanes on keys.
-// With group > 1 each head's contribution goes to part[(b·T + key)][h][2·64] and attn_group_sum adds
-// the group in head order; with group == 1 it is written in place.
-__global__ void __launch_bounds__(64) attn_dkdv_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
-                                                       const float* __restrict__ dout, long long ldd,
-                                                       const float* __restrict__ lse,
-                                                       const float* __restrict__ dvec, int T, int nh, int group,
-                                                       float* __restrict__ dkv, long long ldk,
-                                                       float* __restrict__ part) {
-  __shared__ float Qs[TB][LP];
-  __shared__ float Ds[TB][LP];
-  __shared__ float Ls[TB], Dvs[TB];
-  const int kb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
-  const int lane = threadIdx.x, hl = lane >> 5, k0 = kb * TB;
-  const int mykey = k0 + (lane & 31);
-  const long long base = (long long)b * T;
+// dK, dV for 32 keys against query head h (kv head g = h / group): S and dP with lanes on keys. The
+// 4 waves take query blocks kb + w, kb + w + 4, …; partials are summed in wave order. With group > 1
+// each head's result goes to part[(b·T + key)][h][2·64] and attn_group_sum adds the group in head
+// order; with group == 1 it is written in place.
+__global__ void __launch_bounds__(256) attn_dkdv_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+                                                        const float* __restrict__ dout, long long ldd,
+                                                        const float* __restrict__ lse,
+                                                        const float* __restrict__ dvec, int T, int nh, int group,
+                                                        float* __restrict__ dkv, long long ldk,
+                                                        float* __restrict__ part) {
+  __shared__ float Ps[KW][TB][LP];
+  const int nkb = (T + TB - 1) / TB;
+  const int kb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;  // long columns first
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31, k0 = kb * TB;
+  const int mykey = k0 + c;
+  const long long base = (long long)b * T, krow = base + (mykey < T ? mykey : T - 1);
   float kf[32], vf[32];
-  load_frag(kf, qkv, base, k0, T, ld, kcol + g * HD, 1.0f);
-  load_frag(vf, qkv, base, k0, T, ld, vcol + g * HD, 1.0f);
+  load_rowfrag(kf, qkv + krow * ld + kcol + g * HD, hl, 1.0f);
+  load_rowfrag(vf, qkv + krow * ld + vcol + g * HD, hl, 1.0f);
   f16v K0, K1, V0, V1;
 #pragma unroll
   for (int r = 0; r < 16; r++) K0[r] = K1[r] = V0[r] = V1[r] = 0.0f;
-  const int nqb = (T + TB - 1) / TB;
-  {
-    for (int qb = kb; qb < nqb; qb++) {
-      const int q0 = qb * TB;
-      __syncthreads();
-      load_tile(Qs, qkv, base, q0, T, ld, h * HD, 0.125f);
-      load_tile(Ds, dout, base, q0, T, ldd, h * HD, 1.0f);
-      if (lane < TB) {
-        int qt = q0 + lane;
-        long long si = ((long long)b * nh + h) * T + (qt < T ? qt : T - 1);
-        Ls[lane] = lse[si];
-        Dvs[lane] = dvec[si];
-      }
-      __syncthreads();
-      f16v S, dP;
+  for (int qb = kb + w; qb < nkb; qb += KW) {
+    const int q0 = qb * TB, qr = q0 + c;
+    const long long qrow = base + (qr < T ? qr : T - 1);
+    const long long si = ((long long)b * nh + h) * T + (qr < T ? qr : T - 1);
+    const float Lq = lse[si], Dq = dvec[si];
+    float qa[32], da[32];
+    load_rowfrag(qa, qkv + qrow * ld + h * HD, hl, 0.125f);
+    load_rowfrag(da, dout + qrow * ldd + h * HD, hl, 1.0f);
+    f16v S, dP;
 #pragma unroll
-      for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
+    for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
 #pragma unroll
-      for (int s = 0; s < 32; s++) {
-        S = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[lane & 31][2 * s + hl], kf[s], S, 0, 0, 0);
-        dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Ds[lane & 31][2 * s + hl], vf[s], dP, 0, 0, 0);
-      }
-      // S[r] = score(query q0 + kap(r, hl), key mykey)
-      float p[16], ds[16];
+    for (int s = 0; s < 32; s++) {
+      S = mfma32(qa[s], kf[s], S);
+      dP = mfma32(da[s], vf[s], dP);
+    }
+    // S[r] = score(query q0 + κ(r, hl), key mykey)
+    float p[16], ds[16];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        int qi = kap(r, hl), q = q0 + qi;
-        float pv = (mykey > q || q >= T || mykey >= T) ? 0.0f : expf(S[r] - Ls[qi]);
-        p[r] = pv;
-        ds[r] = pv * (dP[r] - Dvs[qi]);
-      }
+    for (int r = 0; r < 16; r++) {
+      const int qi = kap(r, hl), q = q0 + qi;
+      const float Lr = __shfl(Lq, qi), Dr = __shfl(Dq, qi);
+      const float pv = (mykey > q || q >= T || mykey >= T) ? 0.0f : expf(S[r] - Lr);
+      p[r] = pv;
+      ds[r] = pv * (dP[r] - Dr);
+    }
+    float qs[32], dos[32];
+    load_kapcols(qs, qkv, base, q0, T, ld, h * HD, hl, c, 0.125f);
+    load_kapcols(dos, dout, base, q0, T, ldd, h * HD, hl, c, 1.0f);
 #pragma unroll
-      for (int s = 0; s < 16; s++) {
-        const float* dr = Ds[kap(s, hl)];
-        const float* qr = Qs[kap(s, hl)];
-        V0 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], dr[lane & 31], V0, 0, 0, 0);
-        V1 = __builtin_amdgcn_mfma_f32_32x32x2f32(p[s], dr[32 + (lane & 31)], V1, 0, 0, 0);
-        K0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], qr[lane & 31], K0, 0, 0, 0);
-        K1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s], qr[32 + (lane & 31)], K1, 0, 0, 0);
-      }
+    for (int s = 0; s < 16; s++) {
+      V0 = mfma32(p[s], dos[s], V0);
+      V1 = mfma32(p[s], dos[16 + s], V1);
+      K0 = mfma32(ds[s], qs[s], K0);
+      K1 = mfma32(ds[s], qs[16 + s], K1);
     }
   }
-  // Q in LDS carried the 2^-3 scale, so K0/K1 already hold dK = dSᵀ·Q·scale.
-#pragma unroll
-  for (int r = 0; r < 16; r++) {
-    int key = k0 + kap(r, hl);
-    if (key >= T) continue;
-    float *kr, *vr;
+  // Q carried the 2^-3 scale, so K0/K1 already hold dK = dSᵀ·Q·scale. Merge K, then V.
+  const int ki = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 8, key = k0 + ki;
+  float* kr = nullptr;
+  float* vr = nullptr;
+  if (key < T) {
     if (group == 1) {
       kr = dkv + (base + key) * ldk + kcol + g * HD;
       vr = dkv + (base + key) * ldk + vcol + g * HD;
@@ -282,10 +303,28 @@ __global__ void __launch_bounds__(64) attn_dkdv_kernel(const float* __restrict__
       kr = part + ((base + key) * nh + h) * 2 * HD;
       vr = kr + HD;
     }
-    kr[lane & 31] = K0[r];
-    kr[32 + (lane & 31)] = K1[r];
-    vr[lane & 31] = V0[r];
-    vr[32 + (lane & 31)] = V1[r];
+  }
+#pragma unroll
+  for (int pass = 0; pass < 2; pass++) {
+    const f16v& X0 = pass == 0 ? K0 : V0;
+    const f16v& X1 = pass == 0 ? K1 : V1;
+    if (pass) __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      Ps[w][kap(r, hl)][c] = X0[r];
+      Ps[w][kap(r, hl)][32 + c] = X1[r];
+    }
+    __syncthreads();
+    float* dst = pass == 0 ? kr : vr;
+    if (dst) {
+#pragma unroll
+      for (int d = d0; d < d0 + 8; d++) {
+        float v = Ps[0][ki][d];
+#pragma unroll
+        for (int u = 1; u < KW; u++) v += Ps[u][ki][d];
+        dst[d] = v;
+      }
+    }
   }
 }
 
@@ -311,7 +350,7 @@ void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, 
   HOS_REQUIRE(hd == HD, HOS_E_INVALID, "attention: head_dim must be 64");
   HOS_REQUIRE(ld % 4 == 0 && kcol % 4 == 0 && vcol % 4 == 0, HOS_E_INVALID, "attention: unaligned qkv layout");
   dim3 grid(ceil_div(T, TB), nh, B);
-  attn_fwd_kernel<<<grid, 64, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nh / nkv, o, ldo, lse);
+  attn_fwd_kernel<<<grid, 256, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nh / nkv, o, ldo, lse);
   HOS_HIP_CHECK(hipGetLastError());
 }
 
@@ -320,15 +359,15 @@ void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const f
                      long long ldd, float* part, hipStream_t st) {
   HOS_REQUIRE(hd == HD, HOS_E_INVALID, "attention: head_dim must be 64");
   HOS_REQUIRE(nh == nkv || part != nullptr, HOS_E_INVALID, "attention: GQA backward needs a partial buffer");
-  HOS_REQUIRE(ldo % 4 == 0, HOS_E_INVALID, "attention: unaligned dO layout");
+  HOS_REQUIRE(ldo % 4 == 0 && ld % 4 == 0 && kcol % 4 == 0 && vcol % 4 == 0, HOS_E_INVALID, "attention: unaligned layout");
   long long n = (long long)B * nh * T;
   attn_dvec_kernel<<<ceil_div(n, 256), 256, 0, st>>>(o, dout, ldo, T, nh, B, dvec);
   HOS_HIP_CHECK(hipGetLastError());
   dim3 gq(ceil_div(T, TB), nh, B);
-  attn_dq_kernel<<<gq, 64, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd);
+  attn_dq_kernel<<<gq, 256, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd);
   HOS_HIP_CHECK(hipGetLastError());
   dim3 gk(ceil_div(T, TB), nh, B);
-  attn_dkdv_kernel<<<gk, 64, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd, part);
+  attn_dkdv_kernel<<<gk, 256, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd, part);
   HOS_HIP_CHECK(hipGetLastError());
   if (nh != nkv) {
     long long ne = (long long)B * T * nkv * 2 * HD;
