@@ -58,6 +58,7 @@ SIGNATURES = {
     "hos_peft_step_dev": (i32, [vp, vp, vp, i32, i32, ctypes.c_float, ctypes.c_float, vp]),
     "hos_peft_logits": (i32, [vp, vp, i32, vp]),
     "hos_peft_profile": (i32, [vp, i32]),
+    "hos_peft_profile_only": (i32, [vp, ctypes.c_char_p]),
     "hos_peft_kernel_stats": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_longlong),
                                     ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double)]),

@@ -68,6 +68,7 @@ struct hos_peft {
   hos_peft_cfg c{};
   std::string err;
   int d = 0, qd = 0, kvd = 0, W3 = 0, F = 0, V = 0, r = 0, L = 0, Mmax = 0, passes = 3;
+  int pf = 3, pd = 3, phf = 3, phd = 3;  // precision mode per GEMM site: layer fwd / dX, head fwd / dX
   float lscale = 0.0f;
 
   std::vector<LayerW> lw;
@@ -98,6 +99,7 @@ struct hos_peft {
   std::vector<void*> allocs;
 
   bool prof = false;
+  std::string prof_only;  // when set, only this kernel class is timed
   std::vector<ProfRec> recs;
   std::map<std::string, ProfAcc> acc;
 
@@ -129,15 +131,17 @@ struct hos_peft {
     hipEvent_t e0{}, e1{};
     const char* cls;
     double fl, by;
-    Scope(hos_peft* p_, const char* cls_, double fl_, double by_) : p(p_), cls(cls_), fl(fl_), by(by_) {
-      if (p->prof) {
+    bool on;
+    Scope(hos_peft* p_, const char* cls_, double fl_, double by_)
+        : p(p_), cls(cls_), fl(fl_), by(by_), on(p_->prof && (p_->prof_only.empty() || p_->prof_only == cls_)) {
+      if (on) {
         HOS_HIP_CHECK(hipEventCreate(&e0));
         HOS_HIP_CHECK(hipEventCreate(&e1));
         HOS_HIP_CHECK(hipEventRecord(e0, p->st));
       }
     }
     ~Scope() {
-      if (p->prof) {
+      if (on) {
         (void)hipEventRecord(e1, p->st);
         p->recs.push_back(ProfRec{cls, e0, e1, fl, by});
       }
@@ -149,7 +153,7 @@ struct hos_peft {
   // fp16 GEMMs on frozen weights
   // `lo` carries an optional fused LoRA rank-r update (GemmEpi U/L fields).
   void qfwd(const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo, const float* bias,
-            const float* resid, int accumulate, GemmEpi lo = GemmEpi{}) {
+            const float* resid, int accumulate, GemmEpi lo = GemmEpi{}, int np = 0) {
     // algorithmic flops (2·M·N·K), independent of the precision passes
     Scope s(this, "qgemm_fwd", 2.0 * M * w.rows * w.cols,
             2.0 * M * w.cols + wbytes(w) + 4.0 * M * w.rows * (resid || accumulate ? 2 : 1));
@@ -159,10 +163,10 @@ struct hos_peft {
     e.bias = bias;
     e.accumulate = accumulate;
     e.resid = resid;
-    launch_qgemm_fwd(w, a, lda, M, e, ws, ws_bytes, passes, st);
+    launch_qgemm_fwd(w, a, lda, M, e, ws, ws_bytes, np ? np : pf, st);
   }
   void qdx(const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo, int accumulate,
-           GemmEpi lo = GemmEpi{}) {
+           GemmEpi lo = GemmEpi{}, int np = 0) {
     Scope s(this, "qgemm_dx", 2.0 * M * w.rows * w.cols,
             2.0 * M * w.rows + wbytes(w) + 4.0 * M * w.cols * (accumulate ? 2 : 1));
     GemmEpi e = lo;
@@ -171,7 +175,7 @@ struct hos_peft {
     e.bias = nullptr;
     e.accumulate = accumulate;
     e.resid = nullptr;
-    launch_qgemm_dx(w, a, lda, M, e, ws, ws_bytes, passes, st);
+    launch_qgemm_dx(w, a, lda, M, e, ws, ws_bytes, np ? np : pd, st);
   }
   void to16(const float* x, long long ldx, int M, int K) {
     Scope s(this, "convert", 0, 6.0 * M * K);
@@ -388,7 +392,7 @@ struct hos_peft {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d + 2.0 * M * d);
       launch_rmsnorm_fwd(xfinal, out_norm, c.rms_eps, M, d, nullptr, hs, invf, st);
     }
-    qfwd(out_set ? out : tok, hs, d, M, logits, V, nullptr, nullptr, 0);
+    qfwd(out_set ? out : tok, hs, d, M, logits, V, nullptr, nullptr, 0, GemmEpi{}, phf);
     (void)need_logits_only;
   }
 
@@ -402,7 +406,7 @@ struct hos_peft {
       launch_loss_reduce(row_loss, B, T, loss, st);
     }
     const QWeight& head = out_set ? out : tok;
-    qdx(head, dl, V, M, dxn, d, 0);
+    qdx(head, dl, V, M, dxn, d, 0, GemmEpi{}, phd);
     {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d * 3 + 4.0 * M * d);
       launch_fill(dx, (long long)M * d, 0.0f, st);
@@ -506,7 +510,28 @@ struct hos_peft {
     lscale = c.lora_alpha / (float)r;  // src/peft.rs:195
     Mmax = c.max_batch * c.max_seq;
     passes = c.gemm_passes == 0 ? 3 : c.gemm_passes;
-    HOS_REQUIRE(passes >= 1 && passes <= 3, HOS_E_INVALID, "peft: gemm_passes must be 0 (default), 1, 2 or 3");
+    HOS_REQUIRE(passes >= 1 && passes <= 4, HOS_E_INVALID, "peft: gemm_passes must be 0 (default), 1, 2, 3 or 4");
+    // Default precision policy (measured against the f32 path, worst LoRA-gradient rel L2 at the
+    // SmolLM2-135M / Qwen2.5-0.5B configs): the per-layer GEMMs need both operands split (3 passes);
+    // the head's forward is fine in one pass (+2e-5) and its dX needs only the weight split (mode 4).
+    // An explicit gemm_passes applies to every GEMM.
+    if (c.gemm_passes == 0) {
+      pf = pd = 3;
+      phf = 1;
+      phd = 4;
+    } else {
+      pf = pd = phf = phd = passes;
+    }
+    if (const char* e = std::getenv("HOS_PREC_SITES")) {  // diagnostics: "fwd,dx,head_fwd,head_dx"
+      int a = 0, b2 = 0, c2 = 0, d2 = 0;
+      if (std::sscanf(e, "%d,%d,%d,%d", &a, &b2, &c2, &d2) == 4 && a >= 1 && a <= 4 && b2 >= 1 && b2 <= 4 &&
+          c2 >= 1 && c2 <= 4 && d2 >= 1 && d2 <= 4) {
+        pf = a;
+        pd = b2;
+        phf = c2;
+        phd = d2;
+      }
+    }
     const size_t M = (size_t)Mmax;
     lw.resize(L);
     // LoRA arena
@@ -563,11 +588,13 @@ struct hos_peft {
     size_t hcols = std::max<size_t>({(size_t)d, (size_t)W3, (size_t)qd, 2 * (size_t)F});
     hs.data = alloc<half_t>(M * hcols);
     hs.rinv = alloc<float>(M);
-    hs.lo = passes > 1 ? alloc<half_t>(M * hcols) : nullptr;
+    auto alo_mode = [](int m) { return m == 2 || m == 3; };
+    const bool alo = alo_mode(pf) || alo_mode(pd) || alo_mode(phf);
+    hs.lo = alo ? alloc<half_t>(M * hcols) : nullptr;
     logits = alloc<float>(M * V);
     dl.data = alloc<half_t>(M * V);
     dl.rinv = alloc<float>(M);
-    dl.lo = passes > 1 ? alloc<half_t>(M * V) : nullptr;
+    dl.lo = alo_mode(phd) ? alloc<half_t>(M * V) : nullptr;
     row_loss = alloc<float>(M);
     loss = alloc<float>(1);
     dx = alloc<float>(M * d);
@@ -832,6 +859,10 @@ int hos_peft_profile(hos_peft* p, int enable) {
     p->prof = enable != 0;
     if (enable) p->acc.clear();
   });
+}
+
+int hos_peft_profile_only(hos_peft* p, const char* cls) {
+  return pguard(p, [&] { p->prof_only = cls ? cls : ""; });
 }
 
 int hos_peft_kernel_stats(hos_peft* p, const char* cls, long long* launches, double* total_ms, double* flops,

@@ -14,6 +14,7 @@
 //   NP = 1: A·W                            (fp16 × fp16)
 //   NP = 2: A_hi·W + A_lo·W                (activation carried to ~22 bits)
 //   NP = 3: A_hi·W_hi + A_lo·W_hi + A_hi·W_lo  (both operands to ~22 bits; dropped A_lo·W_lo ~2^-22)
+//   NP = 4: A·W_hi + A·W_lo                    (weight to ~22 bits, activation rounded once)
 // where W_hi = fp16(w), W_lo = fp16(w − W_hi) of the f32 dequantized w.
 //
 // Work decomposition: 256 threads = 4 waves (2×2), workgroup tile BM×BN, wave tile (BM/2)×(BN/2)
@@ -73,7 +74,7 @@ __global__ void to_h16_kernel(const float* __restrict__ x, long long ldx, int K,
 void launch_any(bool dx, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws,
                 size_t ws_bytes, int passes, hipStream_t st) {
   if (M <= 0) return;
-  HOS_REQUIRE(passes >= 1 && passes <= 3, HOS_E_INVALID, "qgemm: precision passes must be 1, 2 or 3");
+  HOS_REQUIRE(passes >= 1 && passes <= 4, HOS_E_INVALID, "qgemm: precision mode must be 1, 2, 3 or 4");
   switch (w.type) {
     case GGUF_Q8_0: qgemm_launch_q8(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
     case GGUF_Q4_K: qgemm_launch_q4k(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;

@@ -19,6 +19,7 @@
 //   NP = 1: A·W
 //   NP = 2: A_hi·W + A_lo·W                       (activation carried to ~22 bits)
 //   NP = 3: A_hi·W_hi + A_lo·W_hi + A_hi·W_lo     (both operands to ~22 bits; dropped A_lo·W_lo ~2^-22)
+//   NP = 4: A·W_hi + A·W_lo                       (weight to ~22 bits, activation rounded once)
 // where W_hi = fp16(w), W_lo = fp16(w − W_hi) of the f32 dequantized w.
 //
 // Work decomposition: 256 threads = 4 waves (2×2), workgroup tile BM×BN, wave tile (BM/2)×(BN/2) of
@@ -151,7 +152,7 @@ struct Geo {
   static constexpr int BROW = DX ? BN + 16 : BK + 8;    // B tile row (halves)
   static constexpr int BROWS = DX ? BK : BN;            // B tile rows
   static constexpr int TPR = (DX ? BN : BK) / E;        // threads per B tile row
-  static constexpr int NA = NP >= 2 ? 2 : 1, NB = NP >= 3 ? 2 : 1;
+  static constexpr int NA = (NP == 2 || NP == 3) ? 2 : 1, NB = NP >= 3 ? 2 : 1;
   static constexpr int ATILE = BM * AROW, BTILE = BROWS * BROW;
   static constexpr int BUF = NA * ATILE + NB * BTILE;   // halves per stage
   static constexpr int STAGES = BUF * 2 * 2 <= 65536 ? 2 : 1;
@@ -169,7 +170,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float1
   using G = Geo<BM, BN, BK, DX, NP>;
   static_assert(G::E == 8 || G::E == 16 || G::E == 32, "B run length");
   static_assert(BK % 32 == 0 || (BK == 32), "slab depth");
-  constexpr bool ALO = NP >= 2, BLO = NP >= 3;
+  constexpr bool ALO = NP == 2 || NP == 3, BLO = NP >= 3;
   __shared__ __attribute__((aligned(16))) _Float16 smem[G::SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -394,13 +395,17 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   const int C = DX ? (int)w.rows : (int)w.cols;
   HOS_REQUIRE(C % 32 == 0, HOS_E_INVALID, "qgemm: contraction length must be a multiple of 32");
   HOS_REQUIRE((lda % 8) == 0, HOS_E_INVALID, "qgemm: activation row stride must be a multiple of 8");
-  HOS_REQUIRE(NP == 1 || a.lo != nullptr, HOS_E_INVALID, "qgemm: multi-pass precision needs the operand residual");
+  HOS_REQUIRE((NP != 2 && NP != 3) || a.lo != nullptr, HOS_E_INVALID,
+              "qgemm: activation-split precision needs the operand residual");
   HOS_REQUIRE(epi.rank >= 0 && epi.rank <= 32, HOS_E_INVALID, "qgemm: fused rank-r update supports r <= 32");
   // Tile choice: the largest tile that still gives ~1.25 waves of workgroups over the 256 CUs; only when
   // even 64×64 tiles leave the chip idle is the contraction split (deterministic reduction after).
   auto ntiles = [&](int bm, int bn) { return ceil_div(M, bm) * ceil_div(Nout, bn); };
   int bm = 64, bn = 64, bk = 32;
-  if (ntiles(128, 128) >= 320) {
+  // A very long contraction (the vocabulary-wide head dX) is bound by re-reading the operands once per
+  // tile row / column: take the largest tile and split the contraction instead.
+  const bool longc = C >= 16384;
+  if (ntiles(128, 128) >= 320 || longc) {
     bm = 128;
     bn = 128;
   } else if (ntiles(64, 128) >= 320) {
@@ -410,7 +415,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bm = 128;
     bn = 64;
   }
-  if (C % 64 == 0 && ((bm == 64 && bn == 64) || (NP == 1 && bm == 128 && bn == 128))) bk = 64;
+  if (C % 64 == 0 && ((bm == 64 && bn == 64) || ((NP == 1 || longc) && bm == 128 && bn == 128))) bk = 64;
   if (const char* ov = std::getenv("HOS_QGEMM_TILE")) {  // tuning override: "BMxBNxBK"
     int x = 0, y = 0, z = 0;
     if (std::sscanf(ov, "%dx%dx%d", &x, &y, &z) == 3 && (z == 32 || (z == 64 && C % 64 == 0)) &&

@@ -1,4 +1,4 @@
-// qGEMM instantiations for GGUF_Q4_K (all tile shapes, both directions, 1-3 precision passes).
+// qGEMM instantiations for GGUF_Q4_K (all tile shapes, both directions, precision modes 1-4).
 #include "qgemm_impl.hpp"
 
 namespace hos {
@@ -8,11 +8,13 @@ void qgemm_launch_q4k(bool dx, int passes, const QWeight& w, H16 a, long long ld
   if (dx) {
     if (passes == 1) launch_typed<GGUF_Q4_K, true, 1>(w, a, lda, M, epi, ws, ws_bytes, st);
     else if (passes == 2) launch_typed<GGUF_Q4_K, true, 2>(w, a, lda, M, epi, ws, ws_bytes, st);
-    else launch_typed<GGUF_Q4_K, true, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else if (passes == 3) launch_typed<GGUF_Q4_K, true, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else launch_typed<GGUF_Q4_K, true, 4>(w, a, lda, M, epi, ws, ws_bytes, st);
   } else {
     if (passes == 1) launch_typed<GGUF_Q4_K, false, 1>(w, a, lda, M, epi, ws, ws_bytes, st);
     else if (passes == 2) launch_typed<GGUF_Q4_K, false, 2>(w, a, lda, M, epi, ws, ws_bytes, st);
-    else launch_typed<GGUF_Q4_K, false, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else if (passes == 3) launch_typed<GGUF_Q4_K, false, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else launch_typed<GGUF_Q4_K, false, 4>(w, a, lda, M, epi, ws, ws_bytes, st);
   }
 }
 

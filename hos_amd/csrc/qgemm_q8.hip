@@ -1,4 +1,4 @@
-// qGEMM instantiations for GGUF_Q8_0 (all tile shapes, both directions, 1-3 precision passes).
+// qGEMM instantiations for GGUF_Q8_0 (all tile shapes, both directions, precision modes 1-4).
 #include "qgemm_impl.hpp"
 
 namespace hos {
@@ -8,11 +8,13 @@ void qgemm_launch_q8(bool dx, int passes, const QWeight& w, H16 a, long long lda
   if (dx) {
     if (passes == 1) launch_typed<GGUF_Q8_0, true, 1>(w, a, lda, M, epi, ws, ws_bytes, st);
     else if (passes == 2) launch_typed<GGUF_Q8_0, true, 2>(w, a, lda, M, epi, ws, ws_bytes, st);
-    else launch_typed<GGUF_Q8_0, true, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else if (passes == 3) launch_typed<GGUF_Q8_0, true, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else launch_typed<GGUF_Q8_0, true, 4>(w, a, lda, M, epi, ws, ws_bytes, st);
   } else {
     if (passes == 1) launch_typed<GGUF_Q8_0, false, 1>(w, a, lda, M, epi, ws, ws_bytes, st);
     else if (passes == 2) launch_typed<GGUF_Q8_0, false, 2>(w, a, lda, M, epi, ws, ws_bytes, st);
-    else launch_typed<GGUF_Q8_0, false, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else if (passes == 3) launch_typed<GGUF_Q8_0, false, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+    else launch_typed<GGUF_Q8_0, false, 4>(w, a, lda, M, epi, ws, ws_bytes, st);
   }
 }
 

@@ -134,7 +134,9 @@ class PeftModel:
         self._chk(lib().hos_peft_logits(self.h, ids.ctypes.data, ids.size, out.ctypes.data))
         return out
 
-    def profile(self, on):
+    def profile(self, on, only=None):
+        """Time kernel classes with HIP events (`only`: restrict to one class)."""
+        self._chk(lib().hos_peft_profile_only(self.h, (only or "").encode()))
         self._chk(lib().hos_peft_profile(self.h, int(on)))
 
     def kernel_stats(self, cls):

@@ -96,7 +96,8 @@ int hos_hip_time_qgemm(hos_ctx* ctx, int which, uint64_t key, const float* in_de
  * x: n floats (host), out: bytes_for(type, n) bytes (host). */
 int hos_hip_quantize(hos_ctx* ctx, const float* x, size_t n, uint32_t ggml_type, uint8_t* out);
 /* Precision of this context's qGEMMs: 1 = single fp16 pass (both operands rounded to 11 bits),
- * 2 = activation carried as fp16 hi + lo (2 MFMA passes), 3 = weight split too (3 passes). Default 1.
+ * 2 = activation carried as fp16 hi + lo (2 MFMA passes), 3 = weight split too (3 passes),
+ * 4 = weight carried as fp16 hi + lo, activation rounded once (2 passes). Default 1.
  * (The reference has no counterpart: its GPU GEMMs are f32, src/metal_be.rs:1095-1142.) */
 int hos_hip_set_gemm_passes(hos_ctx* ctx, int passes);
 /* bytes_for (src/gguf.rs:548-561); 0 for an unsupported type. */
@@ -131,7 +132,8 @@ typedef struct {
   float lora_alpha;
   uint32_t lora_targets;
   int max_batch, max_seq; /* sizes the device-resident activation arena */
-  int gemm_passes;        /* qGEMM precision passes, as hos_hip_set_gemm_passes; 0 = default (3) */
+  int gemm_passes;        /* qGEMM precision mode for every GEMM, as hos_hip_set_gemm_passes; 0 = default
+                           * policy: layer GEMMs 3, head forward 1, head dX 4 */
 } hos_peft_cfg;
 
 typedef struct hos_peft hos_peft;
@@ -164,6 +166,8 @@ int hos_peft_step_dev(hos_peft* p, const int32_t* ids_dev, const int32_t* target
 int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out);
 /* Per-kernel-class timing with HIP events around every launch (off by default). */
 int hos_peft_profile(hos_peft* p, int enable);
+/* Restrict the timing to one kernel class (NULL or "" = all classes). */
+int hos_peft_profile_only(hos_peft* p, const char* cls);
 /* Accumulated stats of one kernel class since profiling was enabled: launches, total ms,
  * algorithmic flops and HBM bytes. Classes: "qgemm_fwd", "qgemm_dx", "lora_down", "lora_db", "lora_du", "lora_da", "attn_fwd",
  * "attn_bwd", "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert". */
