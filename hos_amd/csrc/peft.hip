@@ -69,6 +69,7 @@ struct hos_peft {
   std::string err;
   int d = 0, qd = 0, kvd = 0, W3 = 0, F = 0, V = 0, r = 0, L = 0, Mmax = 0, passes = 3;
   int pf = 3, pd = 3, phf = 3, phd = 3;  // precision mode per GEMM site: layer fwd / dX, head fwd / dX
+  int tpf[7] = {0, 0, 0, 0, 0, 0, 0}, tpd[7] = {0, 0, 0, 0, 0, 0, 0};  // per-target overrides (0 = site mode)
   float lscale = 0.0f;
 
   std::vector<LayerW> lw;
@@ -357,9 +358,9 @@ struct hos_peft {
         launch_rmsnorm_fwd(a.x, w.attn_norm, c.rms_eps, M, d, lqkv ? a.xn1 : nullptr, hs, a.inv1, st);
       }
       lora_down(l, 0, a.xn1, d, M);
-      qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0, up_epi(l, TQ));
-      qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0, up_epi(l, TK));
-      qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0, up_epi(l, TV));
+      qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0, up_epi(l, TQ), tpf[TQ]);
+      qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0, up_epi(l, TK), tpf[TK]);
+      qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0, up_epi(l, TV), tpf[TV]);
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
         launch_rope(a.qkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
@@ -372,21 +373,21 @@ struct hos_peft {
       }
       to16(a.o, qd, M, qd);
       lora_down(l, 1, a.o, qd, M);
-      qfwd(w.w[TO], hs, qd, M, a.x2, d, nullptr, a.x, 0, up_epi(l, TO));
+      qfwd(w.w[TO], hs, qd, M, a.x2, d, nullptr, a.x, 0, up_epi(l, TO), tpf[TO]);
       const bool lgu = has(TG) || has(TU);
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lgu ? 2 : 1) + 2.0 * M * d);
         launch_rmsnorm_fwd(a.x2, w.ffn_norm, c.rms_eps, M, d, lgu ? a.xn2 : nullptr, hs, a.inv2, st);
       }
       lora_down(l, 2, a.xn2, d, M);
-      qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, up_epi(l, TG));
-      qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0, up_epi(l, TU));
+      qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, up_epi(l, TG), tpf[TG]);
+      qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0, up_epi(l, TU), tpf[TU]);
       {
         Scope s(this, "swiglu", 0, 8.0 * M * F + 2.0 * M * F + (has(TD) ? 4.0 * M * F : 0));
         launch_swiglu_fwd(a.gu, M, F, has(TD) ? a.h : nullptr, hs, st);
       }
       lora_down(l, 3, a.h, F, M);
-      qfwd(w.w[TD], hs, F, M, xnext, d, nullptr, a.x2, 0, up_epi(l, TD));
+      qfwd(w.w[TD], hs, F, M, xnext, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
     }
     {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d + 2.0 * M * d);
@@ -418,7 +419,7 @@ struct hos_peft {
       // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA) ----
       to16(dx, d, M, d);
       lora_grad_b(l, 3, dx, d, d, M);
-      qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD));
+      qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD), tpd[TD]);
       lora_grad_a(l, 3, a.h, F, M);
       {
         Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (dgu ? 8.0 * M * F : 0));
@@ -426,8 +427,8 @@ struct hos_peft {
       }
       if (dgu) lora_grad_b(l, 2, dgu, 2LL * F, 2LL * F, M);
       H16 hu = h16_offset(hs, F);
-      qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG));
-      qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU));
+      qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG), tpd[TG]);
+      qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU), tpd[TU]);
       lora_grad_a(l, 2, a.xn2, d, M);
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
@@ -436,7 +437,7 @@ struct hos_peft {
       // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
       to16(dx, d, M, d);
       lora_grad_b(l, 1, dx, d, d, M);
-      qdx(w.w[TO], hs, d, M, dout, qd, 0, down_epi(l, TO));
+      qdx(w.w[TO], hs, d, M, dout, qd, 0, down_epi(l, TO), tpd[TO]);
       lora_grad_a(l, 1, a.o, qd, M);
       {
         Scope s(this, "attn_bwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 5,
@@ -452,9 +453,9 @@ struct hos_peft {
       lora_grad_b(l, 0, dqkv, W3, W3, M);
       to16(dqkv, W3, M, W3);
       H16 hk = h16_offset(hs, qd), hv = h16_offset(hs, qd + kvd);
-      qdx(w.w[TQ], hs, W3, M, dxn, d, 0, down_epi(l, TQ));
-      qdx(w.w[TK], hk, W3, M, dxn, d, 1, down_epi(l, TK));
-      qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV));
+      qdx(w.w[TQ], hs, W3, M, dxn, d, 0, down_epi(l, TQ), tpd[TQ]);
+      qdx(w.w[TK], hk, W3, M, dxn, d, 1, down_epi(l, TK), tpd[TK]);
+      qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV), tpd[TV]);
       lora_grad_a(l, 0, a.xn1, d, M);
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
@@ -521,6 +522,15 @@ struct hos_peft {
       phd = 4;
     } else {
       pf = pd = phf = phd = passes;
+    }
+    if (const char* e = std::getenv("HOS_PREC_TARGETS")) {  // diagnostics: 7 fwd modes then 7 dX modes
+      int v[14];
+      if (std::sscanf(e, "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d", v, v + 1, v + 2, v + 3, v + 4, v + 5, v + 6,
+                      v + 7, v + 8, v + 9, v + 10, v + 11, v + 12, v + 13) == 14)
+        for (int t = 0; t < 7; t++) {
+          tpf[t] = v[t];
+          tpd[t] = v[7 + t];
+        }
     }
     if (const char* e = std::getenv("HOS_PREC_SITES")) {  // diagnostics: "fwd,dx,head_fwd,head_dx"
       int a = 0, b2 = 0, c2 = 0, d2 = 0;

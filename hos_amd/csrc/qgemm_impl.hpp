@@ -22,7 +22,7 @@
 //   NP = 4: A·W_hi + A·W_lo                       (weight to ~22 bits, activation rounded once)
 // where W_hi = fp16(w), W_lo = fp16(w − W_hi) of the f32 dequantized w.
 //
-// Work decomposition: 256 threads = 4 waves (2×2), workgroup tile BM×BN, wave tile (BM/2)×(BN/2) of
+// Work decomposition: 4 waves (2×2), or 8 (4×2) for 256-row tiles; workgroup tile BM×BN, wave tile 64×(BN/2) of
 // 32×32 MFMA tiles, LDS double-buffered when both stages fit in 64 KB, register prefetch of the next slab,
 // optional split-K reduced deterministically by splitk_reduce.
 #pragma once
@@ -145,10 +145,12 @@ __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, in
 
 template <int BM, int BN, int BK, bool DX, int NP>
 struct Geo {
-  static constexpr int TM = BM / 64, TN = BN / 64;      // 32×32 tiles per wave
+  static constexpr int NT = BM >= 256 ? 512 : 256;      // threads: 8 waves for 256-row tiles, else 4
+  static constexpr int WGM = NT / 128;                  // waves along M (2 along N)
+  static constexpr int TM = BM / (32 * WGM), TN = BN / 64;  // 32×32 tiles per wave
   static constexpr int AROW = BK + 8;                   // A tile row (halves)
-  static constexpr int A_H8 = BM * BK / 8 / 256;        // A h8 vectors per thread
-  static constexpr int E = BN * BK / 256;               // B values per thread
+  static constexpr int A_H8 = BM * BK / 8 / NT;         // A h8 vectors per thread
+  static constexpr int E = BN * BK / NT;                // B values per thread
   static constexpr int BROW = DX ? BN + 16 : BK + 8;    // B tile row (halves)
   static constexpr int BROWS = DX ? BK : BN;            // B tile rows
   static constexpr int TPR = (DX ? BN : BK) / E;        // threads per B tile row
@@ -163,7 +165,7 @@ struct Geo {
 // ---- the GEMM ----
 // out[m][n] (over n < Nout) = Σ_c A[m][c] · B(n, c); contraction C split over gridDim.z.
 template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
-__global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float16* __restrict__ A,
+__global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightView w, const _Float16* __restrict__ A,
                                                     const _Float16* __restrict__ Alo, const float* __restrict__ rinv,
                                                     long long lda, int M, int Nout, int C, int c_per_split,
                                                     GemmEpi epi, float* __restrict__ ws) {
@@ -201,7 +203,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float1
   auto load = [&](Regs& R, int c0) {
 #pragma unroll
     for (int v = 0; v < G::A_H8; v++) {
-      int idx = tid + 256 * v;  // h8 index within the BM×BK tile
+      int idx = tid + G::NT * v;  // h8 index within the BM×BK tile
       int row = idx / (BK / 8), cv = idx % (BK / 8);
       int m = m0 + row;
       long long off = (long long)m * lda + c0 + 8 * cv;
@@ -219,7 +221,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float1
   auto store = [&](const Regs& R, _Float16* buf) {
 #pragma unroll
     for (int v = 0; v < G::A_H8; v++) {
-      int idx = tid + 256 * v;
+      int idx = tid + G::NT * v;
       int row = idx / (BK / 8), cv = idx % (BK / 8);
       *(h8*)(buf + row * G::AROW + 8 * cv) = R.a[v];
       if constexpr (ALO) *(h8*)(buf + G::ATILE + row * G::AROW + 8 * cv) = R.al[v];
@@ -246,7 +248,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float1
       const int koff = kk + 8 * (lane >> 5);
 #pragma unroll
       for (int i = 0; i < G::TM; i++) {
-        int ro = (wm * (BM / 2) + 32 * i + (lane & 31)) * G::AROW + koff;
+        int ro = (wm * (BM / G::WGM) + 32 * i + (lane & 31)) * G::AROW + koff;
         af[i] = *(const h8*)(as + ro);
         if constexpr (ALO) afl[i] = *(const h8*)(as + G::ATILE + ro);
       }
@@ -298,11 +300,11 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float1
   float* Ls = Us + BM * 32;
   const int rank = split ? 0 : epi.rank;
   if (rank > 0) {
-    for (int e = tid; e < BM * rank; e += 256) {
+    for (int e = tid; e < BM * rank; e += G::NT) {
       int rr = e / rank, jj = e % rank, row = m0 + rr;
       Us[rr * 32 + jj] = row < M ? epi.U[(long long)row * epi.ldu + jj] : 0.0f;
     }
-    for (int e = tid; e < rank * BN; e += 256) {
+    for (int e = tid; e < rank * BN; e += G::NT) {
       int jj = e / BN, cc = e % BN, col = n0 + cc;
       Ls[jj * BN + cc] = col < Nout ? epi.L[(long long)jj * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
     }
@@ -317,7 +319,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QWeightView w, const _Float1
       if (col >= Nout) continue;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int rr = wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int rr = wm * (BM / G::WGM) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int row = m0 + rr;
         if (row >= M) continue;
         float v = acc[i][j][r];
@@ -385,7 +387,7 @@ void launch_shape(const QWeight& w, H16 a, long long lda, long long M, int Nout,
                   GemmEpi epi, float* ws, hipStream_t st) {
   dim3 grid(ceil_div(Nout, BN), ceil_div(M, BM), splits);
   qgemm_kernel<QT, DX, BM, BN, BK, NP>
-      <<<grid, 256, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, (int)M, Nout, C, per, epi, ws);
+      <<<grid, Geo<BM, BN, BK, DX, NP>::NT, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, (int)M, Nout, C, per, epi, ws);
 }
 
 template <uint32_t QT, bool DX, int NP>
@@ -416,10 +418,18 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bn = 64;
   }
   if (C % 64 == 0 && ((bm == 64 && bn == 64) || ((NP == 1 || longc) && bm == 128 && bn == 128))) bk = 64;
+  // Single-pass GEMMs are bound by the weight dequantization (VALU) as much as by MFMA: 8 waves on a
+  // 256-row tile dequantize each B slab once for twice the MFMA work.
+  if (NP == 1 && !longc && C >= 2048 && ntiles(256, 128) >= 256) {
+    bm = 256;
+    bn = 128;
+    bk = 32;
+  }
   if (const char* ov = std::getenv("HOS_QGEMM_TILE")) {  // tuning override: "BMxBNxBK"
     int x = 0, y = 0, z = 0;
     if (std::sscanf(ov, "%dx%dx%d", &x, &y, &z) == 3 && (z == 32 || (z == 64 && C % 64 == 0)) &&
-        ((x == 128 && y == 128) || (x == 64 && y == 128) || (x == 128 && y == 64) || (x == 64 && y == 64))) {
+        ((x == 128 && y == 128) || (x == 64 && y == 128) || (x == 128 && y == 64) || (x == 64 && y == 64) ||
+         (z == 32 && x == 256 && y == 128))) {
       bm = x;
       bn = y;
       bk = z;
@@ -443,6 +453,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   else HOS_QG(64, 128, 64);
   else HOS_QG(128, 64, 64);
   else HOS_QG(64, 64, 64);
+  else HOS_QG(256, 128, 32);
 #undef HOS_QG
   HOS_HIP_CHECK(hipGetLastError());
   if (splits > 1) {
