@@ -35,7 +35,36 @@ def parse():
     ap.add_argument("--config", default="qwen2.5-0.5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline sample")
     ap.add_argument("--cpu-seq", type=int, default=256, help="tokens in the CPU baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of known size (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
+
+
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """A plain device-to-device copy of COPY_BYTES, three times: under rocprofv3 --pmc its FETCH_SIZE and
+    WRITE_SIZE per dispatch against COPY_BYTES give the factor that turns those counters into HBM bytes."""
+    import torch
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": COPY_BYTES, "dispatches": 3}), flush=True)
+
+
+def traffic_per_launch(kernel_class):
+    """HBM bytes per launch of `kernel_class` measured by rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated
+    against a plain copy), read from the committed profile summary when one exists; else None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_class}_traffic_qwen2.5-0.5b_b4x512.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def dx_gemm_probe(gpu):
@@ -89,6 +118,9 @@ def cpu_baseline(cfg, tensors, seq):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the path shards as data parallel over sequences, described in DESIGN.md)", file=sys.stderr)
@@ -149,12 +181,12 @@ def main():
     if ds["flops"] > 0:
         achieved = ds["flops"] / max(ds["launches"], 1) / avg_launch_s / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": None, "kernel": dom,
+                "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": traffic_per_launch(dom), "kernel": dom,
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"] // args.steps}
     else:
         achieved = ds["bytes"] / max(ds["launches"], 1) / avg_launch_s / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom,
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_per_launch(dom), "kernel": dom,
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"] // args.steps}
 
     dx = dx_gemm_probe(gpu)

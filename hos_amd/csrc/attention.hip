@@ -55,13 +55,6 @@ __device__ __forceinline__ void load_kapcols(float* col, const float* __restrict
 // a·b ≈ a_hi·b_hi + a_hi·b_lo + a_lo·b_hi on v_mfma_f32_32x32x16_bf16 — relative error ~2^-16 per product
 // (the dropped a_lo·b_lo and the rounding of lo), fp32 accumulation, f32 exponent range (no scaling of
 // tiny gradients), at 5.3× the throughput of fp32 MFMA per contraction element.
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ void split_bf(float x, bf8& H, bf8& L, int i) {
-  const __bf16 h = (__bf16)x;
-  H[i] = h;
-  L[i] = (__bf16)(x - (float)h);
-}
 // A 64-dim row fragment (rowfrag order) as 4 contraction steps of 8 values per lane.
 struct DFrag {
   bf8 h[4], l[4];
@@ -83,9 +76,7 @@ __device__ __forceinline__ void to_kfrag(const float* f, KFrag& F) {
     for (int i = 0; i < 8; i++) split_bf(f[8 * t + i], F.h[t], F.l[t], i);
 }
 __device__ __forceinline__ f16v mma3(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, f16v c) {
-  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, c, 0, 0, 0);
+  return mma3_bf16(ah, al, bh, bl, c);
 }
 // Σ over the 64 head dims: D[i][j] += A_row_i · B_row_j (both in rowfrag order)
 __device__ __forceinline__ f16v mma_d(const DFrag& a, const DFrag& b, f16v c) {

@@ -17,6 +17,20 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+// bf16 hi/lo split: x = hi + lo with hi = bf16(x) and lo = bf16(x − hi) (x − hi is exact in f32).
+__device__ __forceinline__ void split_bf(float x, bf8& H, bf8& L, int i) {
+  const __bf16 h = (__bf16)x;
+  H[i] = h;
+  L[i] = (__bf16)(x - (float)h);
+}
+// a·b ≈ a_hi·b_hi + a_hi·b_lo + a_lo·b_hi on v_mfma_f32_32x32x16_bf16: ~2^-16 relative, fp32 range.
+__device__ __forceinline__ f16v mma3_bf16(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, f16v c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, c, 0, 0, 0);
+}
 
 // Host-side error carrying a HOS_E_* status code across the C ABI.
 struct Error : std::runtime_error {

@@ -121,6 +121,37 @@ __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, in
     h8 hv, lv;
     if (!r.ok) {
       hv = lv = zero_h8();
+    } else if constexpr (QT == GGUF_Q8_0) {
+      // q is an exact fp16 integer and d came from an fp16 field, so in packed fp16 arithmetic
+      // hi = q·d rounds the exact product once (= fp16 of the exact f32 dequantized value) and
+      // lo = fma(q, d, −hi) is the exact remainder: the same hi/lo as the f32 route, in ~2 ops/element.
+      const _Float16 dh = (_Float16)r.s[0].x;
+      const h2 d2 = {dh, dh};
+      const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+      for (int wv = 0; wv < 2; wv++) {
+        const uint32_t u = r.q[2 * v + wv] ^ 0x80808080u;  // bytes q + 128
+        // 0x6400 | b is the fp16 1024 + b; minus 1152 gives q exactly
+        const uint32_t p0 = (u & 0xFFu) | ((u & 0xFF00u) << 8) | 0x64006400u;
+        const uint32_t p1 = ((u >> 16) & 0xFFu) | ((u >> 8) & 0xFF0000u) | 0x64006400u;
+        h2 x0, x1;
+        __builtin_memcpy(&x0, &p0, 4);
+        __builtin_memcpy(&x1, &p1, 4);
+        x0 -= bias;
+        x1 -= bias;
+        const h2 h0 = x0 * d2, h1 = x1 * d2;
+        hv[4 * wv] = h0[0];
+        hv[4 * wv + 1] = h0[1];
+        hv[4 * wv + 2] = h1[0];
+        hv[4 * wv + 3] = h1[1];
+        if constexpr (SPLIT) {
+          const h2 l0 = __builtin_elementwise_fma(x0, d2, -h0), l1 = __builtin_elementwise_fma(x1, d2, -h1);
+          lv[4 * wv] = l0[0];
+          lv[4 * wv + 1] = l0[1];
+          lv[4 * wv + 2] = l1[0];
+          lv[4 * wv + 3] = l1[1];
+        }
+      }
     } else {
       float f[8];
       const float2 sc = (QT == GGUF_Q6_K && v >= 2) ? r.s[1] : r.s[0];
@@ -177,7 +208,12 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // Workgroup ids are dispatched round-robin over the 8 XCDs, each with its own L2. Give every XCD a
+  // contiguous run of tiles (columns fastest), so the tiles that share an A row block share one L2.
+  int wid = blockIdx.x + gridDim.x * blockIdx.y;
+  const int nwg = gridDim.x * gridDim.y, full = nwg & ~7;
+  if (wid < full) wid = (wid & 7) * (full >> 3) + (wid >> 3);
+  const int m0 = (wid / gridDim.x) * BM, n0 = (wid % gridDim.x) * BN;
   const int cbeg = blockIdx.z * c_per_split;
   const int cend = min(C, cbeg + c_per_split);
   const int nslab = (cend - cbeg) / BK;
