@@ -57,6 +57,18 @@ SIGNATURES = {
     "hos_peft_adamw": (i32, [vp, ctypes.c_float, ctypes.c_float]),
     "hos_peft_step_dev": (i32, [vp, vp, vp, i32, i32, ctypes.c_float, ctypes.c_float, vp]),
     "hos_peft_logits": (i32, [vp, vp, i32, vp]),
+    "hos_hip_embedding": (i32, [vp, u64, vp, sz, vp]),
+    "hos_hip_rmsnorm_fwd": (i32, [vp, vp, vp, sz, sz, ctypes.c_float, vp, vp]),
+    "hos_hip_rmsnorm_bwd": (i32, [vp, vp, vp, vp, vp, sz, sz, vp]),
+    "hos_hip_rope": (i32, [vp, vp, sz, sz, sz, i32, i32, i32, ctypes.c_float, i32, i32]),
+    "hos_hip_swiglu_fwd": (i32, [vp, vp, sz, sz, vp]),
+    "hos_hip_swiglu_bwd": (i32, [vp, vp, vp, sz, sz, vp]),
+    "hos_hip_attention_fwd": (i32, [vp, vp, sz, sz, sz, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "hos_hip_attention_bwd": (i32, [vp, vp, sz, sz, sz, vp, vp, sz, vp, i32, i32, i32, i32, i32, vp, sz]),
+    "hos_hip_cross_entropy": (i32, [vp, vp, sz, sz, vp, ctypes.c_float, vp, vp]),
+    "hos_hip_adamw": (i32, [vp, vp, vp, vp, vp, sz, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                            ctypes.c_float, ctypes.c_float, i32, i32]),
+    "hos_hip_lora": (i32, [vp, vp, vp, sz, sz, sz, i32, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp]),
     "hos_peft_profile": (i32, [vp, i32]),
     "hos_peft_profile_only": (i32, [vp, ctypes.c_char_p]),
     "hos_peft_kernel_stats": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_longlong),

@@ -21,13 +21,19 @@ FLAGS = [
 ]
 
 
+# Files whose f32 arithmetic must round once per operation (byte-exact GGUF codec): no fusion of a·b + c
+# anywhere, including inside inlined header intrinsics.
+NO_CONTRACT = {"quant.hip"}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+    extra = ["-ffp-contract=off"] if os.path.basename(src) in NO_CONTRACT else []
+    cmd = [HIPCC] + FLAGS + extra + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

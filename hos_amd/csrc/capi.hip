@@ -68,6 +68,7 @@ struct hos_ctx {
   std::unordered_map<uint64_t, QWeight> qw;
   std::unordered_map<uint64_t, DevMem> f32cache;
   DevMem ws, t0, t1, t2, t3, t4, t5;
+  DevMem ops[8];  // scratch of the op-level entry points (ops.hip)
   int passes = 1;
   static constexpr size_t kWs = 256ull << 20;
 };
@@ -397,3 +398,13 @@ hipStream_t hos_internal_stream(hos_ctx* c) { return c->stream; }
 int hos_internal_device(hos_ctx* c) { return c->device; }
 
 }  // extern "C"
+
+namespace hos {
+DevMem& internal_scratch(hos_ctx* c, int slot) { return c->ops[slot]; }
+DevMem& internal_ws(hos_ctx* c) {
+  c->ws.ensure(hos_ctx::kWs);
+  return c->ws;
+}
+const QWeight& internal_qweight(hos_ctx* c, uint64_t key) { return get_qw(c, key); }
+void internal_set_error(hos_ctx* c, const std::string& e) { c->err = e; }
+}  // namespace hos

@@ -127,12 +127,14 @@ __global__ void rope_kernel(float* __restrict__ buf, long long ld, int col0, int
   float* base = buf + (long long)m * ld + col0 + h * hd;
   int ia = neox ? p : 2 * p, ib = neox ? p + half : 2 * p + 1;
   float a = base[ia], b = base[ib];
+  // plain operators under this function's contract(off): each product and sum rounds separately, as in
+  // the reference (intrinsics inlined from headers would keep the headers' contraction setting)
   if (!inverse) {
-    base[ia] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    base[ib] = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+    base[ia] = a * c - b * s;
+    base[ib] = a * s + b * c;
   } else {
-    base[ia] = __fadd_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    base[ib] = __fadd_rn(__fmul_rn(-a, s), __fmul_rn(b, c));
+    base[ia] = a * c + b * s;
+    base[ib] = -a * s + b * c;
   }
 }
 
@@ -195,45 +197,101 @@ __global__ void __launch_bounds__(RB) swiglu_bwd_kernel(const float* __restrict_
 }
 
 // Softmax cross-entropy of one row + its gradient (p − onehot)·gscale as an fp16 operand.
+// Online softmax state: (m, s) with s = Σ exp(x − m); merging two states keeps the larger max.
+__device__ __forceinline__ void sm_add(float& m, float& s, float x) {
+  if (x > m) {
+    s = s * expf(m - x) + 1.0f;
+    m = x;
+  } else {
+    s += expf(x - m);
+  }
+}
+__device__ __forceinline__ void sm_merge(float& m, float& s, float m2, float s2) {
+  if (m2 > m) {
+    s = s * expf(m - m2) + s2;
+    m = m2;
+  } else if (m2 > -INFINITY) {
+    s += s2 * expf(m2 - m);
+  }
+}
+
+// Softmax cross-entropy forward + backward of one row (src/tensor.rs:2709-2743): one read of the logits
+// for the row max and exp-sum together (online softmax), one more to write the gradient
+// (p − onehot)·gscale as the fp16 row-scaled operand of the head's dX GEMM.
 __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits, int V,
                                                  const int32_t* __restrict__ targets, float gscale,
                                                  float* __restrict__ row_loss, _Float16* __restrict__ dl,
-                                                 _Float16* __restrict__ dll, float* __restrict__ rinv) {
-  __shared__ float red[8];
+                                                 _Float16* __restrict__ dll, float* __restrict__ rinv,
+                                                 float* __restrict__ dl32) {
+  __shared__ float rm[RB / 64], rs[RB / 64];
   const int row = blockIdx.x;
   const float* lr = logits + (long long)row * V;
-  float mx = -INFINITY;
-  for (int c = threadIdx.x; c < V; c += RB) mx = fmaxf(mx, lr[c]);
-  mx = block_max(mx, red);
-  float sum = 0.0f;
-  for (int c = threadIdx.x; c < V; c += RB) sum += expf(lr[c] - mx);
-  sum = block_sum(sum, red);
+  float m = -INFINITY, sum = 0.0f;
+  const bool vec = (V & 3) == 0;
+  if (vec) {
+    const float4* l4 = reinterpret_cast<const float4*>(lr);
+    for (int c = threadIdx.x; c < V / 4; c += RB) {
+      const float4 x = l4[c];
+      sm_add(m, sum, x.x);
+      sm_add(m, sum, x.y);
+      sm_add(m, sum, x.z);
+      sm_add(m, sum, x.w);
+    }
+  } else {
+    for (int c = threadIdx.x; c < V; c += RB) sm_add(m, sum, lr[c]);
+  }
+  for (int o = 32; o > 0; o >>= 1) sm_merge(m, sum, __shfl_xor(m, o), __shfl_xor(sum, o));
+  if ((threadIdx.x & 63) == 0) {
+    rm[threadIdx.x >> 6] = m;
+    rs[threadIdx.x >> 6] = sum;
+  }
+  __syncthreads();
+  m = rm[0];
+  sum = rs[0];
+#pragma unroll
+  for (int w = 1; w < RB / 64; w++) sm_merge(m, sum, rm[w], rs[w]);
   const int t = targets[row];
-  float pt = expf(lr[t] - mx) / sum;
+  const float pt = expf(lr[t] - m) / sum;
   if (threadIdx.x == 0) row_loss[row] = -logf(fmaxf(pt, 1e-12f));
   // max |p − onehot| = max(1/sum, 1 − p_t) (the row max has p = 1/sum)
-  float amax = fmaxf(1.0f / sum, 1.0f - pt) * fabsf(gscale);
-  int e = row_exp(amax);
-  float sc = ldexpf(1.0f, e);
+  const float amax = fmaxf(1.0f / sum, 1.0f - pt) * fabsf(gscale);
+  const int e = row_exp(amax);
+  const float sc = ldexpf(1.0f, e), inv = 1.0f / sum;
+  if (dl32) {  // plain f32 gradient (the op-level entry point)
+    for (int c = threadIdx.x; c < V; c += RB) {
+      float p = expf(lr[c] - m) * inv;
+      if (c == t) p -= 1.0f;
+      dl32[(long long)row * V + c] = p * gscale;
+    }
+    return;
+  }
   for (int c = threadIdx.x; c < V; c += RB) {
-    float p = expf(lr[c] - mx) / sum;
+    float p = expf(lr[c] - m) * inv;
     if (c == t) p -= 1.0f;
     put_h16(p * gscale * sc, dl, dll, (long long)row * V + c);
   }
   if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
 }
 
-// loss = Σ_b (Σ_t term[b,t] / T) · (1/B), in sequence order (src/main.rs:2588-2596).
-__global__ void loss_reduce_kernel(const float* __restrict__ row_loss, int B, int T, float* __restrict__ loss) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// loss = Σ_b (Σ_t term[b,t] / T) · (1/B), in sequence order (src/main.rs:2588-2596). Each sequence is
+// staged in LDS by the whole workgroup and summed in order by one thread.
+__global__ void __launch_bounds__(256) loss_reduce_kernel(const float* __restrict__ row_loss, int B, int T,
+                                                          float* __restrict__ loss) {
+  __shared__ float buf[2048];
   float mean = 0.0f;
   for (int b = 0; b < B; b++) {
     float s = 0.0f;
-    for (int t = 0; t < T; t++) s += row_loss[b * T + t];
-    s = s / (float)T;
-    mean += s * (1.0f / (float)B);
+    for (int t0 = 0; t0 < T; t0 += 2048) {
+      const int n = min(2048, T - t0);
+      __syncthreads();
+      for (int i = threadIdx.x; i < n; i += 256) buf[i] = row_loss[(long long)b * T + t0 + i];
+      __syncthreads();
+      if (threadIdx.x == 0)
+        for (int i = 0; i < n; i++) s += buf[i];
+    }
+    if (threadIdx.x == 0) mean += (s / (float)T) * (1.0f / (float)B);
   }
-  *loss = mean;
+  if (threadIdx.x == 0) *loss = mean;
 }
 
 __global__ void adamw_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
@@ -242,15 +300,16 @@ __global__ void adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
 #pragma clang fp contract(off)
   long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  float gi = g[i];
-  float mi = __fadd_rn(__fmul_rn(b1, m[i]), __fmul_rn(__fsub_rn(1.0f, b1), gi));
-  float vi = __fadd_rn(__fmul_rn(b2, v[i]), __fmul_rn(__fmul_rn(__fsub_rn(1.0f, b2), gi), gi));
+  // plain operators under contract(off) (see rope_kernel); correctly rounded division and sqrt
+  const float gi = g[i];
+  const float mi = b1 * m[i] + (1.0f - b1) * gi;
+  const float vi = b2 * v[i] + (1.0f - b2) * gi * gi;
   m[i] = mi;
   v[i] = vi;
-  float mh = __fdiv_rn(mi, bc1), vh = __fdiv_rn(vi, bc2);
-  float u = __fdiv_rn(__fmul_rn(lr, mh), __fadd_rn(__fsqrt_rn(vh), eps));
-  if (decay) u = __fadd_rn(u, __fmul_rn(__fmul_rn(lr, wd), p[i]));
-  p[i] = __fsub_rn(p[i], u);
+  const float mh = div_rn(mi, bc1), vh = div_rn(vi, bc2);
+  float u = div_rn(lr * mh, sqrt_rn(vh) + eps);
+  if (decay) u = u + lr * wd * p[i];
+  p[i] = p[i] - u;
 }
 
 __global__ void fill_kernel(float* __restrict__ p, long long n, float v) {
@@ -299,12 +358,12 @@ void launch_swiglu_bwd(const float* gu, const float* dh, int M, int F, float* dg
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_ce(const float* logits, int M, int V, const int32_t* targets, float gscale, float* row_loss, H16 dl,
-               hipStream_t st) {
-  ce_kernel<<<M, RB, 0, st>>>(logits, V, targets, gscale, row_loss, dl.data, dl.lo, dl.rinv);
+               hipStream_t st, float* dl32) {
+  ce_kernel<<<M, RB, 0, st>>>(logits, V, targets, gscale, row_loss, dl.data, dl.lo, dl.rinv, dl32);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_loss_reduce(const float* row_loss, int B, int T, float* loss, hipStream_t st) {
-  loss_reduce_kernel<<<1, 64, 0, st>>>(row_loss, B, T, loss);
+  loss_reduce_kernel<<<1, 256, 0, st>>>(row_loss, B, T, loss);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_adamw(float* p, const float* g, float* m, float* v, long long n, float lr, float b1, float b2, float eps,

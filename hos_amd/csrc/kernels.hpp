@@ -15,6 +15,12 @@ struct QWeightView {
 };
 inline QWeightView view(const QWeight& w) { return QWeightView{w.type, w.rows, w.cols, w.q, w.s}; }
 
+// Correctly rounded f32 division and square root (what Rust's f32 `/` and sqrt give): the f64 operation is
+// correctly rounded, and rounding its result once more to f32 is exact-safe because 53 >= 2·24 + 2. (HIP's
+// __fsqrt_rn is the approximate hardware square root unless OCML rounding mode is enabled.)
+__device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
+__device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt((double)a); }
+
 // One dequantized element, bit-identical to Gguf::dequant_into (src/gguf.rs):
 //   Q8_0  q·d                 (:354-367)
 //   Q4_K  (d·sc)·q − dmin·m   (:385-413; d·sc and dmin·m are precomputed in f32 at repack)

@@ -1,0 +1,240 @@
+// Op-level C ABI: one entry point per fused kernel of the training path, on device pointers, enqueued on
+// the context's stream (hos_hip_synchronize waits). These are the reference's autograd ops
+// (src/tensor.rs) with their VJPs, so each can be checked against the CPU path on its own, as the
+// reference's tests/autograd.rs checks the ops; the training step (peft.hip) schedules the same kernels.
+#include <cmath>
+#include <vector>
+
+#include "ctx.hpp"
+#include "fused.hpp"
+#include "lora.hpp"
+
+using namespace hos;
+
+namespace {
+
+template <class F>
+int op_guard(hos_ctx* c, F&& f) {
+  if (!c) return HOS_E_INVALID;
+  try {
+    HOS_HIP_CHECK(hipSetDevice(hos_internal_device(c)));
+    f(hos_internal_stream(c));
+    internal_set_error(c, "");
+    return HOS_OK;
+  } catch (const Error& e) {
+    internal_set_error(c, e.what());
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    internal_set_error(c, "host allocation failed");
+    return HOS_E_OOM;
+  } catch (const std::exception& e) {
+    internal_set_error(c, e.what());
+    return HOS_E_DEVICE;
+  }
+}
+
+// fp16 operand scratch the fused kernels also write (rows × cols, no residual plane)
+H16 op_h16(hos_ctx* c, size_t rows, size_t cols) {
+  DevMem& d = internal_scratch(c, 0);
+  DevMem& r = internal_scratch(c, 1);
+  d.ensure(rows * cols * 2);
+  r.ensure(rows * 4 + 4);
+  return H16{(half_t*)d.p, (float*)r.p, nullptr};
+}
+
+__global__ void transpose_kernel(const float* __restrict__ src, int rows, int cols, float* __restrict__ dst) {
+  __shared__ float t[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int r = r0 + i, c = c0 + threadIdx.x;
+    if (r < rows && c < cols) t[i][threadIdx.x] = src[(long long)r * cols + c];
+  }
+  __syncthreads();
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int c = c0 + i, r = r0 + threadIdx.x;
+    if (r < rows && c < cols) dst[(long long)c * rows + r] = t[threadIdx.x][i];
+  }
+}
+// dst [cols][rows] = src [rows][cols]ᵀ
+void transpose(const float* src, int rows, int cols, float* dst, hipStream_t st) {
+  dim3 g(ceil_div(cols, 32), ceil_div(rows, 32));
+  transpose_kernel<<<g, dim3(32, 8), 0, st>>>(src, rows, cols, dst);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+// embedding (src/tensor.rs:2438-2457): out[r] = deq(table)[ids[r]] with the table uploaded under `key`.
+int hos_hip_embedding(hos_ctx* c, uint64_t key, const int32_t* ids_dev, size_t rows, float* out_dev) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(ids_dev && out_dev, HOS_E_INVALID, "null pointer");
+    const QWeight& w = internal_qweight(c, key);
+    launch_embed(w, ids_dev, out_dev, (int)rows, (int)w.cols, st);
+  });
+}
+
+// rmsnorm_eps forward (src/tensor.rs:2500-2520): y = x·inv·w, inv = 1/sqrt(mean(x²) + eps) per row.
+int hos_hip_rmsnorm_fwd(hos_ctx* c, const float* x, const float* w, size_t rows, size_t d, float eps, float* y,
+                        float* inv) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(x && w && y && inv, HOS_E_INVALID, "null pointer");
+    launch_rmsnorm_fwd(x, w, eps, (int)rows, (int)d, y, op_h16(c, rows, d), inv, st);
+  });
+}
+
+// rmsnorm_eps backward (src/tensor.rs:2521-2544), input gradient: gx = g·w·inv − inv³·x/d·Σ(g·w·x).
+// (The weight gradient is not formed: the norm weights are frozen in PEFT.)
+int hos_hip_rmsnorm_bwd(hos_ctx* c, const float* g, const float* x, const float* inv, const float* w, size_t rows,
+                        size_t d, float* gx) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(g && x && inv && w && gx, HOS_E_INVALID, "null pointer");
+    launch_fill(gx, (long long)(rows * d), 0.0f, st);
+    launch_rmsnorm_bwd(g, x, inv, w, (int)rows, (int)d, gx, st);
+  });
+}
+
+// rope (src/tensor.rs:2750-2814) in place on the heads of rows [rows, ld] starting at column col0;
+// position = row % seq_len; inverse != 0 applies Rᵀ (the backward).
+int hos_hip_rope(hos_ctx* c, float* x, size_t rows, size_t ld, size_t col0, int n_heads, int head_dim, int seq_len,
+                 float base, int neox, int inverse) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(x && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && seq_len > 0, HOS_E_INVALID,
+                "rope: bad arguments");
+    const int half = head_dim / 2;
+    std::vector<float2> tab((size_t)seq_len * half);
+    for (int p = 0; p < seq_len; p++)
+      for (int i = 0; i < half; i++) {
+        const float freq = 1.0f / powf(base, 2.0f * (float)i / (float)head_dim);
+        const float ang = (float)p * freq;
+        tab[(size_t)p * half + i] = make_float2(sinf(ang), cosf(ang));
+      }
+    DevMem& t = internal_scratch(c, 2);
+    t.ensure(tab.size() * sizeof(float2));
+    HOS_HIP_CHECK(hipMemcpyAsync(t.p, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice, st));
+    launch_rope(x, (long long)ld, (int)col0, n_heads, head_dim, seq_len, (const float2*)t.p, neox != 0, inverse != 0,
+                (int)rows, st);
+    HOS_HIP_CHECK(hipStreamSynchronize(st));  // the host table must outlive the copy
+  });
+}
+
+// SwiGLU silu(gate)·up (src/tensor.rs:2082-2100, 458-480); gu rows = [gate (F) | up (F)], h [rows, F].
+int hos_hip_swiglu_fwd(hos_ctx* c, const float* gu, size_t rows, size_t F, float* h) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(gu && h, HOS_E_INVALID, "null pointer");
+    launch_swiglu_fwd(gu, (int)rows, (int)F, h, op_h16(c, rows, F), st);
+  });
+}
+// Its backward: dgu rows = [d gate | d up].
+int hos_hip_swiglu_bwd(hos_ctx* c, const float* gu, const float* dh, size_t rows, size_t F, float* dgu) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(gu && dh && dgu, HOS_E_INVALID, "null pointer");
+    launch_swiglu_bwd(gu, dh, (int)rows, (int)F, dgu, op_h16(c, rows, 2 * F), st);
+  });
+}
+
+// Causal GQA attention of PeftModel::forward (src/peft.rs:530-553; bmm/softmax src/tensor.rs:2207-2280,
+// 2460-2491) over B sequences of T rows. qkv rows [B·T, ld]: q heads at column 0, k at kcol, v at vcol.
+// o [B·T, ldo]; lse [B, n_heads, T] (saved for the backward).
+int hos_hip_attention_fwd(hos_ctx* c, const float* qkv, size_t ld, size_t kcol, size_t vcol, int B, int T,
+                          int n_heads, int n_kv_heads, int head_dim, float* o, size_t ldo, float* lse) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(qkv && o && lse && B > 0 && T > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, HOS_E_INVALID,
+                "attention: bad arguments");
+    launch_attn_fwd(qkv, (long long)ld, (int)kcol, (int)vcol, B, T, n_heads, n_kv_heads, head_dim, o, (long long)ldo,
+                    lse, st);
+  });
+}
+// Its backward: dqkv (same layout as qkv, row stride ldd) receives dq, dk, dv.
+int hos_hip_attention_bwd(hos_ctx* c, const float* qkv, size_t ld, size_t kcol, size_t vcol, const float* o,
+                          const float* dout, size_t ldo, const float* lse, int B, int T, int n_heads, int n_kv_heads,
+                          int head_dim, float* dqkv, size_t ldd) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(qkv && o && dout && lse && dqkv && B > 0 && T > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                HOS_E_INVALID, "attention: bad arguments");
+    const size_t M = (size_t)B * T;
+    DevMem& dv = internal_scratch(c, 3);
+    dv.ensure(M * n_heads * 4);
+    float* part = nullptr;
+    if (n_heads != n_kv_heads) {
+      DevMem& pm = internal_scratch(c, 4);
+      pm.ensure(M * n_heads * 2 * head_dim * 4);
+      part = (float*)pm.p;
+    }
+    launch_attn_bwd(qkv, (long long)ld, (int)kcol, (int)vcol, o, dout, (long long)ldo, lse, (float*)dv.p, B, T,
+                    n_heads, n_kv_heads, head_dim, dqkv, (long long)ldd, part, st);
+  });
+}
+
+// cross_entropy (src/tensor.rs:2709-2743) per row: row_loss[r] = −ln max(p_target, 1e−12) and
+// dlogits = (p − onehot)·gscale (the reference's g/n is gscale = 1/rows).
+int hos_hip_cross_entropy(hos_ctx* c, const float* logits, size_t rows, size_t V, const int32_t* targets,
+                          float gscale, float* row_loss, float* dlogits) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(logits && targets && row_loss && dlogits, HOS_E_INVALID, "null pointer");
+    launch_ce(logits, (int)rows, (int)V, targets, gscale, row_loss, H16{nullptr, nullptr, nullptr}, st, dlogits);
+  });
+}
+
+// AdamW::step (src/tensor.rs:2952-2975) on n parameters; `step` is the 1-based step count t that the
+// bias corrections 1 − β^t use (f32 powi, as the reference).
+int hos_hip_adamw(hos_ctx* c, float* p, const float* g, float* m, float* v, size_t n, float lr, float beta1,
+                  float beta2, float eps, float wd, int step, int decay) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(p && g && m && v && step >= 1, HOS_E_INVALID, "adamw: bad arguments");
+    const float bc1 = 1.0f - powi_f32(beta1, step), bc2 = 1.0f - powi_f32(beta2, step);
+    launch_adamw(p, g, m, v, (long long)n, lr, beta1, beta2, eps, wd, bc1, bc2, decay != 0, st);
+  });
+}
+
+// One LoRA branch y += s·(x·A)·B (src/peft.rs:508-512) and its backward through the matmul VJPs
+// (src/tensor.rs:340-391), reference layouts A [in, r], B [r, out]:
+//   u = x·A [rows, r];  y += s·u·B (y optional);  dB = s·uᵀ·dy;  du = s·dy·Bᵀ;  dA = xᵀ·du;
+//   dx += du·Aᵀ (dx optional). x [rows, in] and dy [rows, out] row-major, r ≤ 96.
+int hos_hip_lora(hos_ctx* c, const float* x, const float* dy, size_t rows, size_t in, size_t out, int r,
+                 const float* A, const float* B, float scale, float* y, float* u, float* dA, float* dB, float* dx) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(x && dy && A && B && u && dA && dB && r > 0 && r <= 96, HOS_E_INVALID, "lora: bad arguments");
+    HOS_REQUIRE(in % 4 == 0 && out % 4 == 0, HOS_E_INVALID, "lora: in and out must be multiples of 4");
+    DevMem& wsm = internal_ws(c);
+    float* ws = (float*)wsm.p;
+    const size_t wsb = wsm.n;
+    DevMem& at = internal_scratch(c, 5);  // Aᵀ [r, in], then dAᵀ
+    at.ensure((size_t)r * in * 4);
+    DevMem& dub = internal_scratch(c, 6);  // du [rows, r]
+    dub.ensure(rows * r * 4 + 4);
+    float* du = (float*)dub.p;
+    transpose(A, (int)in, r, (float*)at.p, st);
+    RowsSeg down;
+    down.nt = 1;
+    down.r = r;
+    down.kend[0] = (int)in;
+    launch_lora_rows((long long)rows, (long long)in, 1.0f, x, (long long)in, (const float*)at.p, (long long)in, down, u,
+                     r, ws, wsb, st);
+    if (y)
+      launch_gemm_f32((long long)rows, (long long)out, r, scale, u, r, 1, B, (long long)out, 1, 1.0f, y,
+                      (long long)out, ws, wsb, st);
+    ColsSeg cb;
+    cb.nseg = 1;
+    cb.len[0] = (int)out;
+    launch_lora_cols((long long)rows, r, scale, u, r, dy, (long long)out, cb, dB, (long long)out, 1, ws, wsb, st);
+    RowsSeg up;
+    up.nt = 1;
+    up.r = r;
+    up.kend[0] = (int)out;
+    launch_lora_rows((long long)rows, (long long)out, scale, dy, (long long)out, B, (long long)out, up, du, r, ws, wsb,
+                     st);
+    ColsSeg ca;
+    ca.nseg = 1;
+    ca.len[0] = (int)in;
+    launch_lora_cols((long long)rows, r, 1.0f, du, r, x, (long long)in, ca, (float*)at.p, (long long)in, 1, ws, wsb,
+                     st);
+    transpose((const float*)at.p, r, (int)in, dA, st);
+    if (dx)
+      launch_gemm_f32((long long)rows, (long long)in, r, 1.0f, du, r, 1, A, 1, r, 1.0f, dx, (long long)in, ws, wsb,
+                      st);
+  });
+}
+
+}  // extern "C"

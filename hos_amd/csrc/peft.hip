@@ -47,19 +47,6 @@ struct ProfAcc {
   double ms = 0, flops = 0, bytes = 0;
 };
 
-// compiler-rt __powisf2 (Rust f32::powi): square-and-multiply, as the reference's bias corrections use.
-float powi_f32(float a, int b) {
-  bool recip = b < 0;
-  float r = 1.0f;
-  while (true) {
-    if (b & 1) r *= a;
-    b /= 2;
-    if (b == 0) break;
-    a *= a;
-  }
-  return recip ? 1.0f / r : r;
-}
-
 }  // namespace
 
 struct hos_peft {

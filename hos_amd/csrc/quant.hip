@@ -4,7 +4,8 @@
 //
 // Bit-exactness: the reference decodes in f32 with one rounding per operation
 // (src/gguf.rs:354-367 Q8_0, :385-413 Q4_K, :449-477 Q6_K) and never fuses a*b-c. All
-// arithmetic here uses __fmul_rn/__fsub_rn (no contraction) in the same order.
+// arithmetic here keeps the reference's order, and this file is compiled with -ffp-contract=off so no
+// product is fused into a following add (header intrinsics included).
 #include "kernels.hpp"
 
 namespace hos {
@@ -121,8 +122,8 @@ __global__ void quantize_q8_0_kernel(const float* __restrict__ x, uint8_t* __res
   const float* v = x + b * 32;
   float amax = 0.0f;
   for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
-  float d = __fdiv_rn(amax, 127.0f);
-  float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  float d = div_rn(amax, 127.0f);
+  float id = d != 0.0f ? div_rn(1.0f, d) : 0.0f;
   uint8_t* o = out + b * 34;
   uint16_t hd = f32_to_f16bits(d);
   o[0] = (uint8_t)(hd & 0xff);
@@ -149,9 +150,9 @@ __device__ void qkx_scale_min(const float* x, int nmax, float* out_s, float* out
     return;
   }
   float nf = 32.0f, span = __fsub_rn(mx, mn), nm = (float)nmax;
-  float best_s = __fdiv_rn(span, nm), best_m = -mn, best_err = 3.40282347e+38f;
+  float best_s = div_rn(span, nm), best_m = -mn, best_err = 3.40282347e+38f;
   for (int it = 0; it <= 18; it++) {
-    float iscale = __fdiv_rn(__fadd_rn(__fsub_rn(nm, 1.0f), __fmul_rn(0.1f, (float)it)), span);
+    float iscale = div_rn(__fadd_rn(__fsub_rn(nm, 1.0f), __fmul_rn(0.1f, (float)it)), span);
     if (iscale <= 0.0f) continue;
     float sl = 0.0f, sl2 = 0.0f, sx = 0.0f, slx = 0.0f;
     for (int k = 0; k < 32; k++) {
@@ -165,20 +166,20 @@ __device__ void qkx_scale_min(const float* x, int nmax, float* out_s, float* out
     float denom = __fsub_rn(__fmul_rn(nf, sl2), __fmul_rn(sl, sl));
     float scale, min;
     if (denom > 0.0f) {
-      float s = __fdiv_rn(__fsub_rn(__fmul_rn(nf, slx), __fmul_rn(sl, sx)), denom);
-      float b = __fdiv_rn(__fsub_rn(sx, __fmul_rn(s, sl)), nf);
+      float s = div_rn(__fsub_rn(__fmul_rn(nf, slx), __fmul_rn(sl, sx)), denom);
+      float b = div_rn(__fsub_rn(sx, __fmul_rn(s, sl)), nf);
       if (s > 0.0f) {
         scale = s;
         min = fmaxf(-b, 0.0f);
       } else {
-        scale = __fdiv_rn(span, nm);
+        scale = div_rn(span, nm);
         min = -mn;
       }
     } else {
-      scale = __fdiv_rn(span, nm);
+      scale = div_rn(span, nm);
       min = -mn;
     }
-    float inv = __fdiv_rn(1.0f, scale);
+    float inv = div_rn(1.0f, scale);
     float err = 0.0f;
     for (int k = 0; k < 32; k++) {
       float v = x[k];
@@ -207,9 +208,9 @@ __global__ void quantize_q4_k_kernel(const float* __restrict__ x, uint8_t* __res
   float max_scale = 0.0f, max_min = 0.0f;
   for (int j = 0; j < 8; j++) max_scale = fmaxf(max_scale, scales[j]);
   for (int j = 0; j < 8; j++) max_min = fmaxf(max_min, mins[j]);
-  float d = __fdiv_rn(max_scale, 63.0f), dmin = __fdiv_rn(max_min, 63.0f);
-  float id = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-  float idm = dmin > 0.0f ? __fdiv_rn(1.0f, dmin) : 0.0f;
+  float d = div_rn(max_scale, 63.0f), dmin = div_rn(max_min, 63.0f);
+  float id = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+  float idm = dmin > 0.0f ? div_rn(1.0f, dmin) : 0.0f;
   uint32_t ls[8], lm[8];
   for (int j = 0; j < 8; j++) {
     ls[j] = (uint32_t)clampi(sat_i32(roundf(__fmul_rn(scales[j], id))), 0, 63);
@@ -238,8 +239,8 @@ __global__ void quantize_q4_k_kernel(const float* __restrict__ x, uint8_t* __res
     float dq1 = __fmul_rn(d, (float)ls[2 * g + 1]), mq1 = __fmul_rn(dmin, (float)lm[2 * g + 1]);
     for (int l = 0; l < 32; l++) {
       float v0 = sb[g * 64 + l], v1 = sb[g * 64 + 32 + l];
-      uint32_t q0 = dq0 > 0.0f ? (uint32_t)clampi(sat_i32(roundf(__fdiv_rn(__fadd_rn(v0, mq0), dq0))), 0, 15) : 0u;
-      uint32_t q1 = dq1 > 0.0f ? (uint32_t)clampi(sat_i32(roundf(__fdiv_rn(__fadd_rn(v1, mq1), dq1))), 0, 15) : 0u;
+      uint32_t q0 = dq0 > 0.0f ? (uint32_t)clampi(sat_i32(roundf(div_rn(__fadd_rn(v0, mq0), dq0))), 0, 15) : 0u;
+      uint32_t q1 = dq1 > 0.0f ? (uint32_t)clampi(sat_i32(roundf(div_rn(__fadd_rn(v1, mq1), dq1))), 0, 15) : 0u;
       o[16 + g * 32 + l] = (uint8_t)((q0 & 15u) | ((q1 & 15u) << 4));
     }
   }
@@ -261,15 +262,15 @@ __global__ void quantize_q6_k_kernel(const float* __restrict__ x, uint8_t* __res
         mx = v;
       }
     }
-    subscale[s] = amax > 0.0f ? __fdiv_rn(mx, -32.0f) : 0.0f;
+    subscale[s] = amax > 0.0f ? div_rn(mx, -32.0f) : 0.0f;
   }
   float max_scale = 0.0f;
   for (int s = 0; s < 16; s++)
     if (fabsf(subscale[s]) > fabsf(max_scale)) max_scale = subscale[s];
   float d = 0.0f, idd = 0.0f;
   if (max_scale != 0.0f) {
-    d = __fdiv_rn(max_scale, -128.0f);
-    idd = __fdiv_rn(-128.0f, max_scale);
+    d = div_rn(max_scale, -128.0f);
+    idd = div_rn(-128.0f, max_scale);
   }
   int sc[16];
   for (int s = 0; s < 16; s++) sc[s] = clampi(sat_i32(roundf(__fmul_rn(subscale[s], idd))), -128, 127);
@@ -277,7 +278,7 @@ __global__ void quantize_q6_k_kernel(const float* __restrict__ x, uint8_t* __res
   for (int i = 0; i < 128 + 64; i++) o[i] = 0;
   for (int e = 0; e < 256; e++) {
     float scale = __fmul_rn(d, (float)sc[e >> 4]);
-    int q = scale != 0.0f ? clampi(sat_i32(roundf(__fdiv_rn(sb[e], scale))), -32, 31) : 0;
+    int q = scale != 0.0f ? clampi(sat_i32(roundf(div_rn(sb[e], scale))), -32, 31) : 0;
     uint32_t u = (uint32_t)(q + 32) & 63u;
     int n128 = e >> 7, r = e & 127, qq = r >> 5, l = r & 31;
     o[64 * n128 + l + 32 * (qq & 1)] |= (uint8_t)((u & 15u) << (4 * (qq >> 1)));

@@ -151,3 +151,40 @@ class Gpu:
         ms = ctypes.c_float()
         self._chk(lib().hos_hip_time_qgemm(self.h, which, key, in_dev, t, out_dev, iters, ctypes.byref(ms)))
         return ms.value
+
+    # ---- op-level entry points (device pointers) ----
+    def to_dev(self, arr):
+        """Upload an array; returns a DevArray that frees itself with .free()."""
+        arr = np.ascontiguousarray(arr)
+        d = DevArray(self, arr.shape, arr.dtype)
+        self.h2d(d.ptr, arr)
+        return d
+
+    def empty_dev(self, shape, dtype=np.float32, fill=None):
+        d = DevArray(self, shape, dtype)
+        if fill is not None:
+            self.h2d(d.ptr, np.full(shape, fill, dtype))
+        return d
+
+    def op(self, name, *args):
+        """Call hos_hip_<name>(ctx, *args) (DevArray arguments pass their pointers), then synchronize."""
+        conv = [a.ptr if isinstance(a, DevArray) else a for a in args]
+        self._chk(getattr(lib(), "hos_hip_" + name)(self.h, *conv))
+        self.synchronize()
+
+
+class DevArray:
+    """A device allocation of a given shape/dtype owned through a Gpu context."""
+
+    def __init__(self, gpu, shape, dtype):
+        self.gpu, self.shape, self.dtype = gpu, tuple(shape), np.dtype(dtype)
+        nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.ptr = gpu.alloc(max(nbytes, 4))
+
+    def get(self):
+        return self.gpu.d2h(self.ptr, self.shape, self.dtype)
+
+    def free(self):
+        if self.ptr is not None:
+            self.gpu.free(self.ptr)
+            self.ptr = None

@@ -103,6 +103,46 @@ int hos_hip_set_gemm_passes(hos_ctx* ctx, int passes);
 /* bytes_for (src/gguf.rs:548-561); 0 for an unsupported type. */
 size_t hos_hip_bytes_for(uint32_t ggml_type, size_t n);
 
+/* ---- op-level entry points: one per fused kernel of the training path, device pointers, enqueued on
+ * the context stream (hos_hip_synchronize waits). Each is one of the reference's autograd ops
+ * (src/tensor.rs) with its VJP; the training step below schedules the same kernels. ---- */
+/* embedding (src/tensor.rs:2438-2457): out[r] = deq(table)[ids[r]], table uploaded under `key`. */
+int hos_hip_embedding(hos_ctx* ctx, uint64_t key, const int32_t* ids_dev, size_t rows, float* out_dev);
+/* rmsnorm_eps (src/tensor.rs:2500-2544): y = x·inv·w with inv = 1/sqrt(mean(x²)+eps) per row, and the
+ * input gradient gx = g·w·inv − inv³·x/d·Σ(g·w·x) (norm weights are frozen in PEFT: no weight gradient). */
+int hos_hip_rmsnorm_fwd(hos_ctx* ctx, const float* x, const float* w, size_t rows, size_t d, float eps, float* y,
+                        float* inv);
+int hos_hip_rmsnorm_bwd(hos_ctx* ctx, const float* g, const float* x, const float* inv, const float* w, size_t rows,
+                        size_t d, float* gx);
+/* rope (src/tensor.rs:2750-2814), in place on n_heads heads of head_dim at column col0 of rows [rows, ld];
+ * position = row % seq_len; inverse != 0 applies the transpose rotation (the backward). */
+int hos_hip_rope(hos_ctx* ctx, float* x, size_t rows, size_t ld, size_t col0, int n_heads, int head_dim, int seq_len,
+                 float base, int neox, int inverse);
+/* SwiGLU silu(gate)·up (src/tensor.rs:2082-2100, 458-480): gu rows [gate F | up F], h [rows, F]; backward
+ * dgu rows [d gate | d up]. */
+int hos_hip_swiglu_fwd(hos_ctx* ctx, const float* gu, size_t rows, size_t F, float* h);
+int hos_hip_swiglu_bwd(hos_ctx* ctx, const float* gu, const float* dh, size_t rows, size_t F, float* dgu);
+/* Causal GQA attention of PeftModel::forward (src/peft.rs:530-553; src/tensor.rs:2207-2280, 2460-2491) over
+ * B sequences of T rows, head_dim 64: qkv rows [B·T, ld] with q heads at column 0, k at kcol, v at vcol;
+ * o [B·T, ldo]; lse [B, n_heads, T] kept for the backward, which writes dq, dk, dv into dqkv (same layout). */
+int hos_hip_attention_fwd(hos_ctx* ctx, const float* qkv, size_t ld, size_t kcol, size_t vcol, int B, int T,
+                          int n_heads, int n_kv_heads, int head_dim, float* o, size_t ldo, float* lse);
+int hos_hip_attention_bwd(hos_ctx* ctx, const float* qkv, size_t ld, size_t kcol, size_t vcol, const float* o,
+                          const float* dout, size_t ldo, const float* lse, int B, int T, int n_heads, int n_kv_heads,
+                          int head_dim, float* dqkv, size_t ldd);
+/* cross_entropy (src/tensor.rs:2709-2743) per row: row_loss = −ln max(p_target, 1e−12),
+ * dlogits = (p − onehot)·gscale (the reference's g/n: gscale = 1/rows). */
+int hos_hip_cross_entropy(hos_ctx* ctx, const float* logits, size_t rows, size_t V, const int32_t* targets,
+                          float gscale, float* row_loss, float* dlogits);
+/* AdamW::step (src/tensor.rs:2952-2975) on n parameters at 1-based step t (bias corrections by f32 powi). */
+int hos_hip_adamw(hos_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, float lr, float beta1,
+                  float beta2, float eps, float wd, int step, int decay);
+/* One LoRA branch y += s·(x·A)·B (src/peft.rs:508-512) and its backward (matmul VJPs, src/tensor.rs:340-391),
+ * A [in, r], B [r, out] row-major, r <= 96: u = x·A, y += s·u·B (y may be NULL), dB = s·uᵀ·dy,
+ * du = s·dy·Bᵀ, dA = xᵀ·du, dx += du·Aᵀ (dx may be NULL). */
+int hos_hip_lora(hos_ctx* ctx, const float* x, const float* dy, size_t rows, size_t in, size_t out, int r,
+                 const float* A, const float* B, float scale, float* y, float* u, float* dA, float* dB, float* dx);
+
 /* ---- device memory (GpuBuf / download_buf analogue, src/metal_be_stub.rs:13-20) ---- */
 int hos_hip_dev_alloc(hos_ctx* ctx, size_t nbytes, void** dptr);
 int hos_hip_dev_free(hos_ctx* ctx, void* dptr);

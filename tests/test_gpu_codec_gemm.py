@@ -36,8 +36,12 @@ def weights(rows, cols, seed, std=0.02):
 @pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K])
 def test_quantize_bytes_identical(gpu, t):
     print(f"quantize type {t}", flush=True)
-    x = weights(64, 512, 10 + t)
+    x = weights(256, 1024, 10 + t)
     x[3, :32] = 0.0  # an all-zero block exercises the d == 0 paths
+    x[5] *= 1e-6  # tiny and large magnitudes, one-signed rows
+    x[6] *= 1e3
+    x[7] = np.abs(x[7])
+    x[8] = -np.abs(x[8])
     assert np.array_equal(gpu.quantize(x, t), o.quantize(x, t))
 
 
