@@ -168,3 +168,76 @@ def test_smollm2_135m_one_step(gpu):
     assert abs(lg - lo) / abs(lo) <= TOL
     worst = compare_grads(pm, om, cfg, lora, TARGETS)
     print(f"smollm2 loss gpu {lg:.6f} cpu {lo:.6f} worst grad rel L2 {worst:.2e}")
+
+
+def test_qwen25_05b_config_parity():
+    """configs[2] (the benchmark model: Qwen2.5-0.5B architecture, Q4_K with the Q8_0 fallback for 896-wide
+    rows, QKV bias, NEOX RoPE 1e6, LoRA r=16 on all seven projections) against the oracle, B=2 x T=48."""
+    from hos_amd import Gpu
+    from hos_amd.synth import CONFIGS
+    g = Gpu(0)
+    cfg = CONFIGS["qwen2.5-0.5b"]
+    print("peft qwen2.5-0.5b B=2 T=48", flush=True)
+    pm, om, ids, tg, lora, TARGETS = run_pair(g, cfg, B=2, T=48, seed=21)
+    lg = pm.loss_grad(ids, tg)
+    lo = om.loss_grad(ids, tg)
+    assert abs(lg - lo) / abs(lo) <= TOL
+    worst = compare_grads(pm, om, cfg, lora, TARGETS)
+    print(f"qwen loss gpu {lg:.6f} cpu {lo:.6f} worst grad rel L2 {worst:.2e}")
+    pm.close()
+    g.close()
+
+
+def test_llama32_1b_config_parity():
+    """configs[3] architecture (Llama-3.2-1B: 16 layers, d 2048, 32/8 heads, SwiGLU 8192, vocab 128256,
+    tied Q4_K embeddings, interleaved RoPE 5e5) with LoRA r=32 on all projections, B=1 x T=40."""
+    from hos_amd import Gpu
+    from hos_amd.synth import CONFIGS
+    g = Gpu(0)
+    cfg = CONFIGS["llama3.2-1b"]
+    print("peft llama3.2-1b B=1 T=40", flush=True)
+    pm, om, ids, tg, lora, TARGETS = run_pair(g, cfg, B=1, T=40, seed=31)
+    lg = pm.loss_grad(ids, tg)
+    lo = om.loss_grad(ids, tg)
+    assert abs(lg - lo) / abs(lo) <= TOL
+    worst = compare_grads(pm, om, cfg, lora, TARGETS)
+    print(f"llama loss gpu {lg:.6f} cpu {lo:.6f} worst grad rel L2 {worst:.2e}")
+    pm.close()
+    g.close()
+
+
+@pytest.mark.parametrize("name", ["qwen2.5-0.5b", "llama3.2-1b"])
+def test_full_size_step_properties(name):
+    """The benchmark shapes themselves (B4 x T512 for Qwen2.5-0.5B, B8 x T1024 for Llama-3.2-1B), where the
+    oracle would take hours: the step is deterministic (bit-identical loss and gradients on a repeat), every
+    gradient is finite, the initial loss of near-uniform logits is close to ln(vocab), B = 0 makes every dA
+    exactly zero, and a few AdamW steps on one batch lower its loss."""
+    from hos_amd import Gpu, synth
+    from hos_amd.peft import PeftModel
+    g = Gpu(0)
+    cfg = synth.CONFIGS[name]
+    B, T = cfg.batch, cfg.seq
+    print(f"peft full-size properties {name} B={B} T={T}", flush=True)
+    tensors = synth.build_tensors(g, cfg, seed=1)
+    lora = synth.lora_init(cfg, seed=2, b_std=0.0)
+    ids, tg = synth.tokens(cfg, B, T, seed=3)
+    pm = PeftModel(g, cfg, max_batch=B, max_seq=T)
+    pm.load(tensors)
+    for (l, t), (A, Bm) in lora.items():
+        pm.set_lora(l, t, A, Bm)
+    l1 = pm.loss_grad(ids, tg)
+    grads1 = {k: pm.get_lora_grad(*k) for k in list(lora)[:6]}
+    l2 = pm.loss_grad(ids, tg)
+    grads2 = {k: pm.get_lora_grad(*k) for k in grads1}
+    assert l1 == l2
+    for k in grads1:
+        dA, dB = grads1[k]
+        assert np.array_equal(dA, grads2[k][0]) and np.array_equal(dB, grads2[k][1])
+        assert np.isfinite(dB).all() and np.abs(dB).sum() > 0
+        assert not dA.any()  # B = 0: the gradient reaching A is exactly zero
+    assert abs(l1 - np.log(cfg.vocab)) < 0.5
+    losses = [pm.step(ids, tg, lr=1e-3) for _ in range(4)]
+    print(f"{name} losses {losses}", flush=True)
+    assert losses[-1] < losses[0]
+    pm.close()
+    g.close()
