@@ -6,7 +6,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libhos_hip.so")
+LIB_PATH = os.environ.get("HOS_HIP_LIB") or os.path.join(HERE, "libhos_hip.so")
 
 vp, sz, u32, u64, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
 

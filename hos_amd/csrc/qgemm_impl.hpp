@@ -31,6 +31,10 @@
 
 #include "kernels.hpp"
 
+#ifndef HOS_QG_ABLATE
+#define HOS_QG_ABLATE 0  // diagnostics only: 1 no B loads/dequant, 2 no A loads, 4 no LDS fragment reads, 8 no MFMA
+#endif
+
 namespace hos {
 namespace {
 
@@ -118,10 +122,9 @@ template <uint32_t QT, int E, bool SPLIT>
 __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, int lo_off) {
 #pragma unroll
   for (int v = 0; v < E / 8; v++) {
+    // (a run clamped past the last output column only feeds columns that are never stored)
     h8 hv, lv;
-    if (!r.ok) {
-      hv = lv = zero_h8();
-    } else if constexpr (QT == GGUF_Q8_0) {
+    if constexpr (QT == GGUF_Q8_0) {
       // q is an exact fp16 integer and d came from an fp16 field, so in packed fp16 arithmetic
       // hi = q·d rounds the exact product once (= fp16 of the exact f32 dequantized value) and
       // lo = fma(q, d, −hi) is the exact remainder: the same hi/lo as the f32 route, in ~2 ops/element.
@@ -218,21 +221,29 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   const int cend = min(C, cbeg + c_per_split);
   const int nslab = (cend - cbeg) / BK;
 
-  f16v acc[G::TM][G::TN];
+  // A wave with fewer than four 32×32 tiles gets several accumulator sets: the passes and k-steps rotate
+  // over them, so the MFMA pipe always has independent chains instead of one chain that waits for each
+  // previous MFMA's result. They are summed in a fixed order before the epilogue.
+  constexpr int NACC = G::TM * G::TN >= 4 ? 1 : (G::TM * G::TN == 2 ? 2 : 4);
+  constexpr int NPASS = 1 + (ALO ? 1 : 0) + (BLO ? 1 : 0);
+  f16v accs[NACC][G::TM][G::TN];
 #pragma unroll
-  for (int i = 0; i < G::TM; i++)
+  for (int a = 0; a < NACC; a++)
 #pragma unroll
-    for (int j = 0; j < G::TN; j++)
+    for (int i = 0; i < G::TM; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+      for (int j = 0; j < G::TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) accs[a][i][j][r] = 0.0f;
 
-  // Raw (still quantized / still in registers) data of the next slab, in flight from HBM while the
-  // current slab is multiplied.
+  // Raw (still quantized / still in registers) data of the slabs ahead, in flight from HBM while the
+  // current slab is multiplied: R0 = slab s+1 (issued one slab ago), R1 = slab s+2 (issued now). Two
+  // slabs of lead cover the global-memory latency that one slab's MFMA work cannot.
   struct Regs {
     h8 a[G::A_H8], al[G::A_H8];
     Run<QT, G::E> b;
   };
-  Regs R0;
+  Regs R0, R1;
   // this thread's B run: tile row br, first column bc
   const int br = tid / G::TPR, bc = G::E * (tid % G::TPR);
 
@@ -243,8 +254,20 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
       int row = idx / (BK / 8), cv = idx % (BK / 8);
       int m = m0 + row;
       long long off = (long long)m * lda + c0 + 8 * cv;
-      R.a[v] = m < M ? *(const h8*)(A + off) : zero_h8();
-      if constexpr (ALO) R.al[v] = m < M ? *(const h8*)(Alo + off) : zero_h8();
+      if constexpr (HOS_QG_ABLATE & 2) {
+        R.a[v] = zero_h8();
+        R.al[v] = zero_h8();
+        continue;
+      }
+      // Rows past M re-read row M-1: they only feed output rows past M, which are never stored. No
+      // branch, so the compiler counts the loads in flight exactly and waits only for the slab it needs.
+      const long long offc = m < M ? off : (long long)(M - 1) * lda + c0 + 8 * cv;
+      R.a[v] = *(const h8*)(A + offc);
+      if constexpr (ALO) R.al[v] = *(const h8*)(Alo + offc);
+    }
+    if constexpr (HOS_QG_ABLATE & 1) {
+      R.b.ok = false;
+      return;
     }
     if constexpr (DX) {
       const int col = n0 + bc;  // output column run; rows are the contraction
@@ -269,13 +292,14 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   if (nslab > 0) {
     load(R0, cbeg);
     store(R0, smem);
+    load(R0, cbeg + min(1, nslab - 1) * BK);
   }
   __syncthreads();
 
   for (int s = 0; s < nslab; s++) {
     const int buf = G::STAGES == 2 ? (s & 1) : 0;
     const bool more = s + 1 < nslab;
-    if (more) load(R0, cbeg + (s + 1) * BK);
+    load(R1, cbeg + min(s + 2, nslab - 1) * BK);  // past the end: a harmless re-read of the last slab
     const _Float16* as = smem + buf * G::BUF;
     const _Float16* bs = as + G::NA * G::ATILE;
 #pragma unroll
@@ -313,21 +337,46 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
           if constexpr (BLO) bfl[j] = *(const h8*)(bs + G::BTILE + ro);
         }
       }
+      if constexpr (HOS_QG_ABLATE & 4) {
+#pragma unroll
+        for (int i = 0; i < G::TM; i++) af[i] = afl[i] = zero_h8();
+#pragma unroll
+        for (int j = 0; j < G::TN; j++) bf[j] = bfl[j] = zero_h8();
+      }
+      if constexpr (HOS_QG_ABLATE & 8) continue;
 #pragma unroll
       for (int i = 0; i < G::TM; i++)
 #pragma unroll
         for (int j = 0; j < G::TN; j++) {
-          if constexpr (BLO) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], acc[i][j], 0, 0, 0);
-          if constexpr (ALO) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          constexpr int c0 = 0;  // chain index of this k-step's first pass
+          const int cb = c0 + NPASS * (kk / 16);
+          if constexpr (BLO) {
+            f16v& t = accs[(cb + 2) % NACC][i][j];
+            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], t, 0, 0, 0);
+          }
+          if constexpr (ALO) {
+            f16v& t = accs[(cb + 1) % NACC][i][j];
+            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], t, 0, 0, 0);
+          }
+          f16v& t = accs[cb % NACC][i][j];
+          t = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], t, 0, 0, 0);
         }
     }
     if (more) {
       if constexpr (G::STAGES == 1) __syncthreads();  // everyone is done reading the single stage
       store(R0, smem + (G::STAGES == 2 ? (buf ^ 1) : 0) * G::BUF);
     }
+    R0 = R1;
     __syncthreads();
   }
+
+  f16v(&acc)[G::TM][G::TN] = accs[0];
+#pragma unroll
+  for (int a = 1; a < NACC; a++)
+#pragma unroll
+    for (int i = 0; i < G::TM; i++)
+#pragma unroll
+      for (int j = 0; j < G::TN; j++) acc[i][j] += accs[a][i][j];
 
   // epilogue: D[i][j] of a 32×32 tile lives at lane j + 32·((i/4)&1), register (i&3) + 4·(i/8)
   const bool split = gridDim.z > 1;
