@@ -70,6 +70,7 @@ SIGNATURES = {
                             ctypes.c_float, ctypes.c_float, i32, i32]),
     "hos_hip_lora": (i32, [vp, vp, vp, sz, sz, sz, i32, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp]),
     "hos_peft_profile": (i32, [vp, i32]),
+    "hos_peft_use_graph": (i32, [vp, i32]),
     "hos_peft_profile_only": (i32, [vp, ctypes.c_char_p]),
     "hos_peft_kernel_stats": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_longlong),
                                     ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),

@@ -312,6 +312,42 @@ __global__ void adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
   p[i] = p[i] - u;
 }
 
+// The same update with lr, wd and the step count read from device memory (hyper = {lr, wd, t}), so a
+// captured step graph replays with the current values; adam_tick advances t first (one thread).
+__global__ void adam_tick_kernel(AdamHyper* h) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) h->t += 1;
+}
+__device__ float powi_dev(float a, int b) {
+#pragma clang fp contract(off)
+  const bool recip = b < 0;
+  float r = 1.0f;
+  while (true) {
+    if (b & 1) r = r * a;
+    b /= 2;
+    if (b == 0) break;
+    a = a * a;
+  }
+  return recip ? div_rn(1.0f, r) : r;
+}
+__global__ void adamw_dev_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+                                 float* __restrict__ v, long long n, float b1, float b2, float eps,
+                                 const AdamHyper* __restrict__ h, int decay) {
+#pragma clang fp contract(off)
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float lr = h->lr, wd = h->wd;
+  const float bc1 = 1.0f - powi_dev(b1, h->t), bc2 = 1.0f - powi_dev(b2, h->t);
+  const float gi = g[i];
+  const float mi = b1 * m[i] + (1.0f - b1) * gi;
+  const float vi = b2 * v[i] + (1.0f - b2) * gi * gi;
+  m[i] = mi;
+  v[i] = vi;
+  const float mh = div_rn(mi, bc1), vh = div_rn(vi, bc2);
+  float u = div_rn(lr * mh, sqrt_rn(vh) + eps);
+  if (decay) u = u + lr * wd * p[i];
+  p[i] = p[i] - u;
+}
+
 __global__ void fill_kernel(float* __restrict__ p, long long n, float v) {
   long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -369,6 +405,15 @@ void launch_loss_reduce(const float* row_loss, int B, int T, float* loss, hipStr
 void launch_adamw(float* p, const float* g, float* m, float* v, long long n, float lr, float b1, float b2, float eps,
                   float wd, float bc1, float bc2, bool decay, hipStream_t st) {
   adamw_kernel<<<ceil_div(n, 256), 256, 0, st>>>(p, g, m, v, n, lr, b1, b2, eps, wd, bc1, bc2, decay);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_adam_tick(AdamHyper* h, hipStream_t st) {
+  adam_tick_kernel<<<1, 64, 0, st>>>(h);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_adamw_dev(float* p, const float* g, float* m, float* v, long long n, float b1, float b2, float eps,
+                      const AdamHyper* h, bool decay, hipStream_t st) {
+  adamw_dev_kernel<<<ceil_div(n, 256), 256, 0, st>>>(p, g, m, v, n, b1, b2, eps, h, decay);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_fill(float* p, long long n, float v, hipStream_t st) {

@@ -18,6 +18,14 @@ void launch_ce(const float* logits, int M, int V, const int32_t* targets, float 
 void launch_loss_reduce(const float* row_loss, int B, int T, float* loss, hipStream_t st);
 void launch_adamw(float* p, const float* g, float* m, float* v, long long n, float lr, float b1, float b2, float eps,
                   float wd, float bc1, float bc2, bool decay, hipStream_t st);
+// AdamW hyper-parameters in device memory: lr, decoupled weight decay, 1-based step count.
+struct AdamHyper {
+  float lr, wd;
+  int t, pad;
+};
+void launch_adam_tick(AdamHyper* h, hipStream_t st);
+void launch_adamw_dev(float* p, const float* g, float* m, float* v, long long n, float b1, float b2, float eps,
+                      const AdamHyper* h, bool decay, hipStream_t st);
 void launch_fill(float* p, long long n, float v, hipStream_t st);
 void launch_copy_rows(const float* src, long long lds, float* dst, long long ldd, int rows, int cols,
                       hipStream_t st);

@@ -86,6 +86,12 @@ struct hos_peft {
   int32_t *ids = nullptr, *tgts = nullptr;
   std::vector<void*> allocs;
 
+  // AdamW hyper-parameters in device memory (lr, wd written before each step; t advanced on the device)
+  AdamHyper* hyp = nullptr;
+  AdamHyper hyp_host{};
+  // Captured optimizer steps, keyed by (B, T, ids, targets, loss) device pointers.
+  bool use_graph = true;
+  std::map<std::vector<uintptr_t>, hipGraphExec_t> graphs;
   bool prof = false;
   std::string prof_only;  // when set, only this kernel class is timed
   std::vector<ProfRec> recs;
@@ -451,13 +457,63 @@ struct hos_peft {
     }
   }
 
-  void adamw(float lr, float wd) {
+  void set_hyper(float lr, float wd) {
+    hyp_host.lr = lr;
+    hyp_host.wd = wd;
+    HOS_HIP_CHECK(hipMemcpyAsync(hyp, &hyp_host, 2 * sizeof(float), hipMemcpyHostToDevice, st));
+  }
+  // AdamW over the arena with lr/wd/t from device memory (set_hyper first); bias corrections by f32 powi
+  // of the device step count, exactly as the host's powi would give.
+  void adamw_enqueue() {
     adam_t += 1;
-    float bc1 = 1.0f - powi_f32(0.9f, (int)adam_t);
-    float bc2 = 1.0f - powi_f32(0.95f, (int)adam_t);
     Scope s(this, "adamw", 0, 4.0 * nparams * 7);
+    launch_adam_tick(hyp, st);
     // every LoRA factor is 2-D, so decay applies to all (src/main.rs:2571)
-    launch_adamw(P, G, M1, V1, nparams, lr, 0.9f, 0.95f, 1e-8f, wd, bc1, bc2, true, st);
+    launch_adamw_dev(P, G, M1, V1, nparams, 0.9f, 0.95f, 1e-8f, hyp, true, st);
+  }
+  void adamw(float lr, float wd) {
+    set_hyper(lr, wd);
+    adamw_enqueue();
+  }
+  // One optimizer step on device-resident ids/targets: zero-grad is implicit (every gradient buffer is
+  // overwritten), forward, backward, AdamW, loss copy. Replayed from a captured graph after its first use.
+  void step_body(const int32_t* ids_dev, const int32_t* targets_dev, int B, int T, float* loss_dev) {
+    HOS_HIP_CHECK(hipMemcpyAsync(ids, ids_dev, (size_t)B * T * 4, hipMemcpyDeviceToDevice, st));
+    HOS_HIP_CHECK(hipMemcpyAsync(tgts, targets_dev, (size_t)B * T * 4, hipMemcpyDeviceToDevice, st));
+    forward(B, T, false);
+    loss_backward(B, T);
+    adamw_enqueue();
+    if (loss_dev) HOS_HIP_CHECK(hipMemcpyAsync(loss_dev, loss, 4, hipMemcpyDeviceToDevice, st));
+  }
+  void step(const int32_t* ids_dev, const int32_t* targets_dev, int B, int T, float lr, float wd, float* loss_dev) {
+    set_hyper(lr, wd);
+    if (!use_graph || prof) {
+      step_body(ids_dev, targets_dev, B, T, loss_dev);
+      return;
+    }
+    const std::vector<uintptr_t> key = {(uintptr_t)B, (uintptr_t)T, (uintptr_t)ids_dev, (uintptr_t)targets_dev,
+                                        (uintptr_t)loss_dev};
+    auto it = graphs.find(key);
+    if (it == graphs.end()) {
+      hipGraph_t g = nullptr;
+      HOS_HIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+      try {
+        step_body(ids_dev, targets_dev, B, T, loss_dev);
+      } catch (...) {
+        (void)hipStreamEndCapture(st, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      HOS_HIP_CHECK(hipStreamEndCapture(st, &g));
+      adam_t -= 1;  // the capture enqueued nothing; the launch below runs the step
+      hipGraphExec_t ex = nullptr;
+      hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      HOS_HIP_CHECK(e);
+      it = graphs.emplace(key, ex).first;
+    }
+    adam_t += 1;
+    HOS_HIP_CHECK(hipGraphLaunch(it->second, st));
   }
 
   void collect_prof() {
@@ -605,6 +661,8 @@ struct hos_peft {
     if (c.n_heads != c.n_kv_heads) attn_part = alloc<float>(M * c.n_heads * 2 * c.head_dim);
     ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(d, F) * 4 * 8, 1ull << 30));
     ws = alloc<float>(ws_bytes / 4);
+    hyp = alloc<AdamHyper>(1);
+    launch_fill((float*)hyp, sizeof(AdamHyper) / 4, 0.0f, st);  // lr = wd = 0, t = 0 (all-zero bits)
     ids = alloc<int32_t>(M);
     tgts = alloc<int32_t>(M);
     // RoPE (sin, cos) table with the reference's f32 powf/sinf/cosf (src/tensor.rs:2769-2778)
@@ -623,6 +681,8 @@ struct hos_peft {
 
   void release() {
     (void)hipStreamSynchronize(st);
+    for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+    graphs.clear();
     for (auto& rc : recs) {
       (void)hipEventDestroy(rc.e0);
       (void)hipEventDestroy(rc.e1);
@@ -828,13 +888,12 @@ int hos_peft_step_dev(hos_peft* p, const int32_t* ids_dev, const int32_t* target
     HOS_REQUIRE(ids_dev && targets_dev, HOS_E_INVALID, "null pointer");
     p->check_ready();
     p->check_bt(B, T);
-    HOS_HIP_CHECK(hipMemcpyAsync(p->ids, ids_dev, (size_t)B * T * 4, hipMemcpyDeviceToDevice, p->st));
-    HOS_HIP_CHECK(hipMemcpyAsync(p->tgts, targets_dev, (size_t)B * T * 4, hipMemcpyDeviceToDevice, p->st));
-    p->forward(B, T, false);
-    p->loss_backward(B, T);
-    p->adamw(lr, wd);
-    if (loss_dev) HOS_HIP_CHECK(hipMemcpyAsync(loss_dev, p->loss, 4, hipMemcpyDeviceToDevice, p->st));
+    p->step(ids_dev, targets_dev, B, T, lr, wd, loss_dev);
   });
+}
+
+int hos_peft_use_graph(hos_peft* p, int enable) {
+  return pguard(p, [&] { p->use_graph = enable != 0; });
 }
 
 int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out) {

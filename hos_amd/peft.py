@@ -128,6 +128,10 @@ class PeftModel:
     def step_dev(self, ids_dev, tgt_dev, B, T, lr, wd=0.0, loss_dev=None):
         self._chk(lib().hos_peft_step_dev(self.h, ids_dev, tgt_dev, B, T, lr, wd, loss_dev))
 
+    def use_graph(self, on):
+        """Replay a captured graph of the whole step in step_dev (default on)."""
+        self._chk(lib().hos_peft_use_graph(self.h, int(on)))
+
     def logits(self, ids):
         ids = np.ascontiguousarray(ids, np.int32).ravel()
         out = np.empty((ids.size, self.cfg.vocab), np.float32)

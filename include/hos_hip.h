@@ -202,6 +202,10 @@ int hos_peft_adamw(hos_peft* p, float lr, float wd);
  * loss_dev receives the step's loss (one float, device). */
 int hos_peft_step_dev(hos_peft* p, const int32_t* ids_dev, const int32_t* targets_dev, int B, int T, float lr,
                       float wd, float* loss_dev);
+/* hos_peft_step_dev replays a captured HIP graph of the whole step after its first call for a given
+ * (B, T, ids, targets, loss) pointer set (default on; off = enqueue kernel by kernel). Profiling
+ * (hos_peft_profile) always runs the step kernel by kernel. */
+int hos_peft_use_graph(hos_peft* p, int enable);
 /* Logits [T, vocab] of one sequence (PeftModel::logits, src/peft.rs:462-464). */
 int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out);
 /* Per-kernel-class timing with HIP events around every launch (off by default). */

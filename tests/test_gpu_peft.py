@@ -241,3 +241,39 @@ def test_full_size_step_properties(name):
     assert losses[-1] < losses[0]
     pm.close()
     g.close()
+
+
+def test_graph_replay_matches_eager(gpu):
+    """hos_peft_step_dev replays a captured graph of the step after its first call. Two identical models,
+    one eager and one replaying: after every step (with host synchronisation and eager reads in between)
+    the loss and every LoRA factor are bit-identical, including after an lr change between replays."""
+    from hos_amd import synth
+    from hos_amd.peft import PeftModel
+    cfg = tiny(12, n_layers=2)
+    print("peft graph replay vs eager", flush=True)
+    tensors = synth.build_tensors(gpu, cfg, seed=4)
+    lora = synth.lora_init(cfg, seed=5, b_std=0.02)
+    ids, tg = synth.tokens(cfg, 2, 64, seed=6)
+    models = []
+    for graph in (False, True):
+        pm = PeftModel(gpu, cfg, max_batch=2, max_seq=64)
+        pm.load(tensors)
+        for (l, t), (A, Bm) in lora.items():
+            pm.set_lora(l, t, A, Bm)
+        pm.use_graph(graph)
+        models.append(pm)
+    I, TG, L = gpu.to_dev(ids), gpu.to_dev(tg), gpu.empty_dev((1,))
+    for step, lr in enumerate((1e-3, 1e-3, 3e-3, 1e-3, 1e-3)):
+        out = []
+        for pm in models:
+            pm.step_dev(I.ptr, TG.ptr, 2, 64, lr, 0.01, L.ptr)
+            gpu.synchronize()
+            out.append((L.get()[0], [pm.get_lora(l, t) for (l, t) in lora]))
+        (la, fa), (lb, fb) = out
+        assert la == lb, f"step {step}: loss {la} vs {lb}"
+        for (A1, B1), (A2, B2) in zip(fa, fb):
+            assert np.array_equal(A1, A2) and np.array_equal(B1, B2), f"step {step}"
+    for a in (I, TG, L):
+        a.free()
+    for pm in models:
+        pm.close()
