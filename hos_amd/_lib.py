@@ -48,6 +48,9 @@ SIGNATURES = {
     "hos_hip_d2h": (i32, [vp, vp, vp, sz]),
     "hos_peft_create": (i32, [vp, ctypes.POINTER(PeftCfg), ctypes.POINTER(vp)]),
     "hos_peft_destroy": (None, [vp]),
+    "hos_gguf_config": (i32, [ctypes.c_char_p, ctypes.POINTER(PeftCfg), ctypes.c_char_p, sz]),
+    "hos_peft_create_from_gguf": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(PeftCfg), ctypes.POINTER(vp),
+                                        ctypes.POINTER(PeftCfg)]),
     "hos_peft_last_error": (ctypes.c_char_p, [vp]),
     "hos_peft_set_tensor": (i32, [vp, ctypes.c_char_p, vp, sz, u32, sz, sz]),
     "hos_peft_set_lora": (i32, [vp, i32, i32, vp, vp]),

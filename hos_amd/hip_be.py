@@ -7,6 +7,7 @@ n, a_key)`` returns ``Aᵀ·B``; ``b_key=None`` means "no caching". Where the re
 ``HosError`` carrying the C status code.
 """
 import ctypes
+import weakref
 
 import numpy as np
 
@@ -47,9 +48,15 @@ class Gpu:
         if rc:
             raise HosError(rc, f"hos_hip_create(device={device}) failed (no usable HIP device?)")
         self.h = h
+        self._children = weakref.WeakSet()  # objects that live on this context; closed before it
+
+    def adopt(self, obj):
+        self._children.add(obj)
 
     def close(self):
         if getattr(self, "h", None):
+            for c in list(getattr(self, "_children", ())):
+                c.close()
             lib().hos_hip_destroy(self.h)
             self.h = None
 

@@ -57,17 +57,59 @@ class ModelConfig:
                 "down": (f, d)}[t]
 
 
+def _cstruct(cfg, max_batch=None, max_seq=None):
+    return PeftCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
+                   cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank,
+                   cfg.lora_alpha, cfg.target_mask, max_batch or cfg.batch, max_seq or cfg.seq, cfg.gemm_passes)
+
+
+def _from_cstruct(c, name, **train):
+    return ModelConfig(name=name, n_layers=c.n_layers, dim=c.dim, n_heads=c.n_heads, n_kv_heads=c.n_kv_heads,
+                       head_dim=c.head_dim, ffn_dim=c.ffn_dim, vocab=c.vocab, rms_eps=c.rms_eps,
+                       rope_base=c.rope_base, rope_neox=bool(c.rope_neox), attn_bias=bool(c.attn_bias), **train)
+
+
+def gguf_config(path, **train):
+    """The model config a GGUF file declares (Model::load's metadata mapping, src/model.rs:713-771),
+    parsed by the library (no device work). ``train`` sets the ModelConfig training fields."""
+    tmp = ModelConfig(name="gguf", n_layers=0, dim=0, n_heads=0, n_kv_heads=0, head_dim=0, ffn_dim=0, vocab=0,
+                      **train)
+    c = _cstruct(tmp)
+    err = ctypes.create_string_buffer(512)
+    rc = lib().hos_gguf_config(str(path).encode(), ctypes.byref(c), err, len(err))
+    if rc:
+        raise HosError(rc, err.value.decode())
+    return _from_cstruct(c, str(path), **train)
+
+
 class PeftModel:
-    def __init__(self, gpu: Gpu, cfg: ModelConfig, max_batch=None, max_seq=None):
+    def __init__(self, gpu: Gpu, cfg: ModelConfig, max_batch=None, max_seq=None, _handle=None):
         self.gpu, self.cfg = gpu, cfg
-        c = PeftCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
-                    cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank,
-                    cfg.lora_alpha, cfg.target_mask, max_batch or cfg.batch, max_seq or cfg.seq, cfg.gemm_passes)
+        if _handle is not None:
+            self.h = _handle
+            gpu.adopt(self)
+            return
+        c = _cstruct(cfg, max_batch, max_seq)
         h = ctypes.c_void_p()
         rc = lib().hos_peft_create(gpu.h, ctypes.byref(c), ctypes.byref(h))
         if rc:
             raise HosError(rc, "hos_peft_create failed (see stderr)")
         self.h = h
+        gpu.adopt(self)
+
+    @classmethod
+    def from_gguf(cls, gpu: Gpu, path, max_batch=1, max_seq=128, **train):
+        """Load a GGUF base model (Model::load, src/model.rs:713-921) and wrap it with LoRA adapters as
+        ``train`` (lora_rank, lora_alpha, lora_targets, gemm_passes, lr, ...) describes."""
+        tmp = ModelConfig(name="gguf", n_layers=0, dim=0, n_heads=0, n_kv_heads=0, head_dim=0, ffn_dim=0,
+                          vocab=0, batch=max_batch, seq=max_seq, **train)
+        c, out = _cstruct(tmp), PeftCfg()
+        h = ctypes.c_void_p()
+        rc = lib().hos_peft_create_from_gguf(gpu.h, str(path).encode(), ctypes.byref(c), ctypes.byref(h),
+                                             ctypes.byref(out))
+        if rc:
+            raise HosError(rc, f"hos_peft_create_from_gguf({path}) failed (see stderr)")
+        return cls(gpu, _from_cstruct(out, str(path), batch=max_batch, seq=max_seq, **train), _handle=h)
 
     def close(self):
         if getattr(self, "h", None):

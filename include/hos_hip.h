@@ -188,6 +188,18 @@ const char* hos_peft_last_error(const hos_peft* p);
  * Norm weights and biases: F32. Linear weights: Q8_0, Q4_K or Q6_K. */
 int hos_peft_set_tensor(hos_peft* p, const char* name, const uint8_t* bytes, size_t nbytes, uint32_t ggml_type,
                         size_t rows, size_t cols);
+/* Model::load (src/model.rs:713-921) over the GGUF reader (src/gguf.rs:225-286): parses the file at path,
+ * maps {arch}.embedding_length / block_count / attention.head_count[_kv] / feed_forward_length /
+ * attention.layer_norm_rms_epsilon / rope.freq_base / attention.key_length | rope.dimension_count to the
+ * model fields of *cfg (vocab from token_embd, attn_bias from blk.0.attn_q.bias, NEOX RoPE for qwen2),
+ * keeping cfg's LoRA / arena fields as given. No device work; err (may be NULL) receives the message. */
+int hos_gguf_config(const char* path, hos_peft_cfg* cfg, char* err, size_t err_len);
+/* hos_gguf_config + hos_peft_create + hos_peft_set_tensor for every model tensor in the file. train
+ * supplies the LoRA / arena fields; out_cfg (may be NULL) receives the mapped config. Architectures:
+ * llama, qwen2, mistral; linear weights Q8_0 / Q4_K / Q6_K (else HOS_E_UNSUPPORTED_QUANT); 1-D F16 / BF16
+ * tensors are widened to F32. */
+int hos_peft_create_from_gguf(hos_ctx* ctx, const char* path, const hos_peft_cfg* train, hos_peft** out,
+                              hos_peft_cfg* out_cfg);
 /* LoRA factors of one (layer, target index 0..6 = q,k,v,o,gate,up,down), reference layout:
  * A [in, r], B [r, out] row-major (src/peft.rs:187-199). */
 int hos_peft_set_lora(hos_peft* p, int layer, int target, const float* A, const float* B);
