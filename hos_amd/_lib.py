@@ -48,6 +48,11 @@ SIGNATURES = {
     "hos_hip_d2h": (i32, [vp, vp, vp, sz]),
     "hos_peft_create": (i32, [vp, ctypes.POINTER(PeftCfg), ctypes.POINTER(vp)]),
     "hos_peft_destroy": (None, [vp]),
+    "hos_peft_save_hos": (i32, [vp, ctypes.c_char_p, ctypes.c_char_p, i32]),
+    "hos_peft_load_hos": (i32, [vp, ctypes.c_char_p, i32]),
+    "hos_peft_adapter_id": (i32, [vp, ctypes.c_char_p]),
+    "hos_peft_base_id": (i32, [vp, ctypes.c_char_p]),
+    "hos_format_card": (i32, [ctypes.c_char_p, ctypes.c_char_p, sz, ctypes.POINTER(sz)]),
     "hos_gguf_config": (i32, [ctypes.c_char_p, ctypes.POINTER(PeftCfg), ctypes.c_char_p, sz]),
     "hos_peft_create_from_gguf": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(PeftCfg), ctypes.POINTER(vp),
                                         ctypes.POINTER(PeftCfg)]),

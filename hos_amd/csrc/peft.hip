@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "ctx.hpp"
+#include "peft_internal.hpp"
 #include "fused.hpp"
 #include "lora.hpp"
 
@@ -782,6 +783,83 @@ void check_ids(hos_peft* p, const int32_t* ids, int n) {
 }
 }  // namespace
 
+namespace hos {
+
+// One (layer, target) factor pair of an arena buffer in the reference layout (A [in, r], B [r, out]
+// row-major); the device keeps A_tᵀ [r][in] inside its group's At block and B_t as columns of Bcat.
+void peft_factor_io(hos_peft* p, PeftBuf which, int layer, int target, float* A, float* B, bool upload) {
+  float* base = which == PEFT_PARAM ? p->P : which == PEFT_GRAD ? p->G : which == PEFT_ADAM_M ? p->M1 : p->V1;
+  const int i = lora_index(p, layer, target);
+  int in, o;
+  p->dims(target, &in, &o);
+  const int r = p->r;
+  const size_t bpitch = (size_t)p->bw(p->group_of(target)) * 4;
+  std::vector<float> at;
+  if (A) at.resize((size_t)r * in);
+  if (upload) {
+    if (A) {
+      for (int k = 0; k < in; k++)
+        for (int j = 0; j < r; j++) at[(size_t)j * in + k] = A[(size_t)k * r + j];
+      HOS_HIP_CHECK(hipMemcpyAsync(base + p->offA[i], at.data(), at.size() * 4, hipMemcpyHostToDevice, p->st));
+    }
+    if (B)
+      HOS_HIP_CHECK(hipMemcpy2DAsync(base + p->offB[i], bpitch, B, (size_t)o * 4, (size_t)o * 4, (size_t)r,
+                                     hipMemcpyHostToDevice, p->st));
+    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+    return;
+  }
+  if (A) HOS_HIP_CHECK(hipMemcpyAsync(at.data(), base + p->offA[i], at.size() * 4, hipMemcpyDeviceToHost, p->st));
+  if (B)
+    HOS_HIP_CHECK(hipMemcpy2DAsync(B, (size_t)o * 4, base + p->offB[i], bpitch, (size_t)o * 4, (size_t)r,
+                                   hipMemcpyDeviceToHost, p->st));
+  HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+  if (A)
+    for (int k = 0; k < in; k++)
+      for (int j = 0; j < r; j++) A[(size_t)k * r + j] = at[(size_t)j * in + k];
+}
+
+PeftShape peft_shape(const hos_peft* p) {
+  PeftShape s{};
+  s.L = p->L;
+  s.r = p->r;
+  s.targets = p->c.lora_targets;
+  for (int t = 0; t < NT; t++) p->dims(t, &s.in[t], &s.out[t]);
+  s.step = p->adam_t;
+  s.lr = p->hyp_host.lr;
+  s.wd = p->hyp_host.wd;
+  s.vocab = p->V;
+  s.dim = p->d;
+  return s;
+}
+
+void peft_set_adam_state(hos_peft* p, uint64_t step, float lr, float wd) {
+  HOS_REQUIRE(step <= 0x7fffffffull, HOS_E_FORMAT, "optimizer step count out of range");
+  p->adam_t = step;
+  p->hyp_host.t = (int)step;
+  p->hyp_host.lr = lr;
+  p->hyp_host.wd = wd;
+  HOS_HIP_CHECK(hipMemcpyAsync(p->hyp, &p->hyp_host, sizeof(AdamHyper), hipMemcpyHostToDevice, p->st));
+  HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+}
+
+// The token embedding dequantized to f32 [vocab, dim] on the host (Model::load's tok_embd).
+void peft_token_embedding(hos_peft* p, std::vector<float>& out) {
+  HOS_REQUIRE(p->tok.q != nullptr, HOS_E_MISSING_TENSOR, "missing tensor 'token_embd.weight'");
+  const size_t n = (size_t)p->V * p->d;
+  float* dev = nullptr;
+  HOS_HIP_CHECK(hipMalloc(&dev, n * 4));
+  out.resize(n);
+  launch_dequant(p->tok, dev, p->st);
+  hipError_t e = hipMemcpyAsync(out.data(), dev, n * 4, hipMemcpyDeviceToHost, p->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->st);
+  (void)hipFree(dev);
+  HOS_HIP_CHECK(e);
+}
+
+int peft_call(hos_peft* p, const std::function<void()>& f) { return pguard(p, f); }
+
+}  // namespace hos
+
 extern "C" {
 
 int hos_peft_create(hos_ctx* ctx, const hos_peft_cfg* cfg, hos_peft** out) {
@@ -821,42 +899,14 @@ int hos_peft_set_tensor(hos_peft* p, const char* name, const uint8_t* bytes, siz
 int hos_peft_set_lora(hos_peft* p, int layer, int target, const float* A, const float* B) {
   return pguard(p, [&] {
     HOS_REQUIRE(A && B, HOS_E_INVALID, "null factor");
-    int i = lora_index(p, layer, target), in, o;
-    p->dims(target, &in, &o);
-    const int r = p->r;
-    std::vector<float> at((size_t)r * in);  // device keeps A_tᵀ [r][in]
-    for (int k = 0; k < in; k++)
-      for (int j = 0; j < r; j++) at[(size_t)j * in + k] = A[(size_t)k * r + j];
-    HOS_HIP_CHECK(hipMemcpyAsync(p->P + p->offA[i], at.data(), at.size() * 4, hipMemcpyHostToDevice, p->st));
-    HOS_HIP_CHECK(hipMemcpy2DAsync(p->P + p->offB[i], (size_t)p->bw(p->group_of(target)) * 4, B, (size_t)o * 4,
-                                   (size_t)o * 4, (size_t)r, hipMemcpyHostToDevice, p->st));
-    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
-  });
-}
-
-static int get_pair(hos_peft* p, const float* base, int layer, int target, float* A, float* B) {
-  return pguard(p, [&] {
-    int i = lora_index(p, layer, target), in, o;
-    p->dims(target, &in, &o);
-    const int r = p->r;
-    if (A) {
-      std::vector<float> at((size_t)r * in);
-      HOS_HIP_CHECK(hipMemcpyAsync(at.data(), base + p->offA[i], at.size() * 4, hipMemcpyDeviceToHost, p->st));
-      HOS_HIP_CHECK(hipStreamSynchronize(p->st));
-      for (int k = 0; k < in; k++)
-        for (int j = 0; j < r; j++) A[(size_t)k * r + j] = at[(size_t)j * in + k];
-    }
-    if (B)
-      HOS_HIP_CHECK(hipMemcpy2DAsync(B, (size_t)o * 4, base + p->offB[i], (size_t)p->bw(p->group_of(target)) * 4,
-                                     (size_t)o * 4, (size_t)r, hipMemcpyDeviceToHost, p->st));
-    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+    hos::peft_factor_io(p, hos::PEFT_PARAM, layer, target, const_cast<float*>(A), const_cast<float*>(B), true);
   });
 }
 int hos_peft_get_lora(hos_peft* p, int layer, int target, float* A, float* B) {
-  return p ? get_pair(p, p->P, layer, target, A, B) : HOS_E_INVALID;
+  return pguard(p, [&] { hos::peft_factor_io(p, hos::PEFT_PARAM, layer, target, A, B, false); });
 }
 int hos_peft_get_lora_grad(hos_peft* p, int layer, int target, float* dA, float* dB) {
-  return p ? get_pair(p, p->G, layer, target, dA, dB) : HOS_E_INVALID;
+  return pguard(p, [&] { hos::peft_factor_io(p, hos::PEFT_GRAD, layer, target, dA, dB, false); });
 }
 
 int hos_peft_loss_grad(hos_peft* p, const int32_t* ids, const int32_t* targets, int B, int T, float* loss) {

@@ -5,6 +5,7 @@
 The model lives on one device; the host only enqueues.
 """
 import ctypes
+import json
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -191,3 +192,59 @@ class PeftModel:
         self._chk(lib().hos_peft_kernel_stats(self.h, cls.encode(), ctypes.byref(n), ctypes.byref(ms),
                                               ctypes.byref(fl), ctypes.byref(by)))
         return {"launches": n.value, "ms": ms.value, "flops": fl.value, "bytes": by.value}
+
+    # ---------------- checkpoints (.hos capsule) ----------------
+    def adapter_id(self):
+        """model_id of the adapter tensors (src/format.rs:100-111)."""
+        buf = ctypes.create_string_buffer(17)
+        self._chk(lib().hos_peft_adapter_id(self.h, buf))
+        return buf.value.decode()
+
+    def base_id(self):
+        """The base model's id as save_adapter records it (src/main.rs:2641-2646)."""
+        buf = ctypes.create_string_buffer(17)
+        self._chk(lib().hos_peft_base_id(self.h, buf))
+        return buf.value.decode()
+
+    def adapter_card(self, name, base_path="", end_loss=0.0, steps=0, lr=0.0, method="lora",
+                     base_arch="Llama"):
+        """The card save_adapter writes (src/main.rs:2614-2688), as JSON text with serde's field order."""
+        f32 = lambda x: float(str(np.float32(x)))  # noqa: E731  shortest f32 digits
+        base = self.base_id()
+        card = {
+            "format": "hos", "spec": 1, "name": name, "id": self.adapter_id(), "mode": "adapter",
+            "arch": {"base_architecture": base_arch, "block_count": self.cfg.n_layers, "method": method,
+                     "source_format": "hos-peft"},
+            "provenance": {"created": "", "engine": "hos-peft", "dataset": f"{method} adapter on {base_path}",
+                           "dataset_hash": base},
+            "resume": {"seed": 0, "step": 0, "rng_state": 0},
+            "history": [{"steps": int(steps), "final_loss": f32(end_loss), "optimizer": "adamw", "lr": f32(lr)}],
+            "lineage": [base],
+        }
+        return json.dumps(card, separators=(",", ":"))
+
+    def save_hos(self, path, card=None, optimizer=True):
+        """Write the adapters (and AdamW state) as a .hos capsule; card: JSON text or dict (None = default)."""
+        if isinstance(card, dict):
+            card = json.dumps(card, separators=(",", ":"))
+        self._chk(lib().hos_peft_save_hos(self.h, str(path).encode(), card.encode() if card else None,
+                                          int(optimizer)))
+
+    def load_hos(self, path, optimizer=True):
+        """Restore adapters (and AdamW state) from a .hos capsule."""
+        self._chk(lib().hos_peft_load_hos(self.h, str(path).encode(), int(optimizer)))
+
+
+def read_card(path):
+    """The card of a .hos file as a dict (read_card, src/format.rs:270-285)."""
+    need = ctypes.c_size_t()
+    buf = ctypes.create_string_buffer(4096)
+    rc = lib().hos_format_card(str(path).encode(), buf, len(buf), ctypes.byref(need))
+    if rc:
+        raise HosError(rc, buf.value.decode(errors="replace"))
+    if need.value > len(buf):
+        buf = ctypes.create_string_buffer(need.value)
+        rc = lib().hos_format_card(str(path).encode(), buf, len(buf), ctypes.byref(need))
+        if rc:
+            raise HosError(rc, buf.value.decode(errors="replace"))
+    return json.loads(buf.value.decode())

@@ -218,6 +218,29 @@ int hos_peft_step_dev(hos_peft* p, const int32_t* ids_dev, const int32_t* target
  * (B, T, ids, targets, loss) pointer set (default on; off = enqueue kernel by kernel). Profiling
  * (hos_peft_profile) always runs the step kernel by kernel. */
 int hos_peft_use_graph(hos_peft* p, int enable);
+/* Adapter / optimizer checkpoint in the .hos capsule layout (src/format.rs:1-26, writer :287-346,
+ * reader :401-485; version 2, every tensor F32 with its FNV-1a 64 checksum, file checksum last).
+ * Tensors: lora.{l}.a{t} [in, r] and lora.{l}.b{t} [r, out] (ROLE_WEIGHT) for every adapted target t in
+ * q,k,v,o,gate,up,down order (PeftModel::adapter_tensors, src/peft.rs:731-740, whose q|v model writes
+ * lora.{l}.{aq,bq,av,bv}); with_optimizer adds opt.m.{k} / opt.v.{k} (ROLE_OPT_STATE, the k-th parameter
+ * in that order) and the scalars opt.step, opt.lr, opt.beta1, opt.beta2, opt.wd (ROLE_SCALAR), as the
+ * lifecycle checkpoint of src/main.rs:6276-6307. card_json is stored verbatim; NULL writes a default
+ * adapter card (Card::new + mode "adapter", id = hos_peft_adapter_id, resume.step = AdamW steps). */
+int hos_peft_save_hos(hos_peft* p, const char* path, const char* card_json, int with_optimizer);
+/* Inverse of hos_peft_save_hos (v1 and v2 files). Every adapted target's factors must be present with the
+ * model's shapes (else HOS_E_MISSING_TENSOR / HOS_E_FORMAT); other tensors are ignored. Checksums are
+ * verified; a failing file leaves the model unchanged. with_optimizer also restores m, v, the step count,
+ * lr and wd (without it the optimizer state is left as it is). */
+int hos_peft_load_hos(hos_peft* p, const char* path, int with_optimizer);
+/* model_id (src/format.rs:100-111) of the adapter tensors: FNV-1a 64 over their f32 bytes, 16 hex digits
+ * plus NUL into out17. */
+int hos_peft_adapter_id(hos_peft* p, char* out17);
+/* The base model's id as save_adapter records it (src/main.rs:2641-2646): FNV-1a 64 of the dequantized
+ * f32 token embedding. */
+int hos_peft_base_id(hos_peft* p, char* out17);
+/* read_card (src/format.rs:270-285): the card JSON of a .hos file into out (NUL-terminated, truncated to
+ * len); *needed (may be NULL) = its length + 1. On error out receives the message. No device work. */
+int hos_format_card(const char* path, char* out, size_t len, size_t* needed);
 /* Logits [T, vocab] of one sequence (PeftModel::logits, src/peft.rs:462-464). */
 int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out);
 /* Per-kernel-class timing with HIP events around every launch (off by default). */
