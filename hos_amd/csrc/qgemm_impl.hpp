@@ -185,7 +185,9 @@ struct Geo {
   static constexpr int AROW = BK + 8;                   // A tile row (halves)
   static constexpr int A_H8 = BM * BK / 8 / NT;         // A h8 vectors per thread
   static constexpr int E = BN * BK / NT;                // B values per thread
-  static constexpr int BROW = DX ? BN + 16 : BK + 8;    // B tile row (halves)
+  // B tile row (halves). DX: 32 halves of padding put the 16-lane groups of a transposed fragment read on
+  // disjoint banks (16 halves left half of those reads two-way conflicted).
+  static constexpr int BROW = DX ? BN + 32 : BK + 8;
   static constexpr int BROWS = DX ? BK : BN;            // B tile rows
   static constexpr int TPR = (DX ? BN : BK) / E;        // threads per B tile row
   static constexpr int NA = (NP == 2 || NP == 3) ? 2 : 1, NB = NP >= 3 ? 2 : 1;

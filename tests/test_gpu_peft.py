@@ -188,15 +188,16 @@ def test_qwen25_05b_config_parity():
     g.close()
 
 
+@pytest.mark.timeout(600)  # the CPU oracle of a 1.2 B-parameter model takes minutes on a loaded host
 def test_llama32_1b_config_parity():
     """configs[3] architecture (Llama-3.2-1B: 16 layers, d 2048, 32/8 heads, SwiGLU 8192, vocab 128256,
-    tied Q4_K embeddings, interleaved RoPE 5e5) with LoRA r=32 on all projections, B=1 x T=40."""
+    tied Q4_K embeddings, interleaved RoPE 5e5) with LoRA r=32 on all projections, B=1 x T=24."""
     from hos_amd import Gpu
     from hos_amd.synth import CONFIGS
     g = Gpu(0)
     cfg = CONFIGS["llama3.2-1b"]
-    print("peft llama3.2-1b B=1 T=40", flush=True)
-    pm, om, ids, tg, lora, TARGETS = run_pair(g, cfg, B=1, T=40, seed=31)
+    print("peft llama3.2-1b B=1 T=24", flush=True)
+    pm, om, ids, tg, lora, TARGETS = run_pair(g, cfg, B=1, T=24, seed=31)
     lg = pm.loss_grad(ids, tg)
     lo = om.loss_grad(ids, tg)
     assert abs(lg - lo) / abs(lo) <= TOL
