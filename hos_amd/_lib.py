@@ -17,6 +17,7 @@ class PeftCfg(ctypes.Structure):
         ("ffn_dim", i32), ("vocab", i32), ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float),
         ("rope_neox", i32), ("attn_bias", i32), ("lora_rank", i32), ("lora_alpha", ctypes.c_float),
         ("lora_targets", u32), ("max_batch", i32), ("max_seq", i32), ("gemm_passes", i32),
+        ("n_experts", i32), ("n_experts_used", i32), ("qk_norm", i32),
     ]
 
 
@@ -41,6 +42,8 @@ SIGNATURES = {
     "hos_hip_time_qgemm": (i32, [vp, i32, u64, vp, sz, vp, i32, ctypes.POINTER(ctypes.c_float)]),
     "hos_hip_quantize": (i32, [vp, vp, sz, u32, vp]),
     "hos_hip_bytes_for": (sz, [u32, sz]),
+    "hos_hip_quantize_dev": (i32, [vp, vp, sz, u32, vp]),
+    "hos_hip_randn_dev": (i32, [vp, vp, sz, u64, ctypes.c_float]),
     "hos_hip_set_gemm_passes": (i32, [vp, i32]),
     "hos_hip_dev_alloc": (i32, [vp, sz, ctypes.POINTER(vp)]),
     "hos_hip_dev_free": (i32, [vp, vp]),

@@ -358,6 +358,25 @@ int hos_hip_quantize(hos_ctx* c, const float* x, size_t n, uint32_t type, uint8_
   });
 }
 
+int hos_hip_quantize_dev(hos_ctx* c, const float* x_dev, size_t n, uint32_t type, uint8_t* out_dev) {
+  return guard(c, [&] {
+    HOS_REQUIRE(x_dev && out_dev, HOS_E_INVALID, "null pointer");
+    size_t be = block_elems(type);
+    HOS_REQUIRE(be != 0, HOS_E_UNSUPPORTED_QUANT, "quantize: unsupported type " + std::to_string(type));
+    HOS_REQUIRE(n % be == 0, HOS_E_INVALID, "quantize: length must be a multiple of the block size");
+    launch_quantize(x_dev, n, type, out_dev, c->stream);
+    HOS_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int hos_hip_randn_dev(hos_ctx* c, float* out_dev, size_t n, uint64_t seed, float stddev) {
+  return guard(c, [&] {
+    HOS_REQUIRE(out_dev != nullptr, HOS_E_INVALID, "null pointer");
+    launch_randn(out_dev, n, seed, stddev, c->stream);
+    HOS_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
 size_t hos_hip_bytes_for(uint32_t type, size_t n) { return gguf_bytes_for(type, n); }
 
 int hos_hip_set_gemm_passes(hos_ctx* c, int passes) {

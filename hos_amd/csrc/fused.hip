@@ -362,7 +362,29 @@ __global__ void copy_rows_kernel(const float* __restrict__ src, long long lds, f
   dst[r * ldd + c] = src[r * lds + c];
 }
 
+// splitmix64 finaliser as the counter-based generator; Box–Muller on two 24-bit uniforms in (0, 1)
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__global__ void randn_kernel(float* __restrict__ out, long long n, uint64_t seed, float stddev) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t h = mix64(seed ^ mix64((uint64_t)i));
+  const float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+  const float u2 = ((float)((h >> 16) & 0xFFFFFF) + 0.5f) * (1.0f / 16777216.0f);
+  out[i] = stddev * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307f * u2);
+}
+
 }  // namespace
+
+void launch_randn(float* out, size_t n, uint64_t seed, float stddev, hipStream_t st) {
+  if (n == 0) return;
+  randn_kernel<<<ceil_div((long long)n, 256), 256, 0, st>>>(out, (long long)n, seed, stddev);
+  HOS_HIP_CHECK(hipGetLastError());
+}
 
 void launch_embed(const QWeight& table, const int32_t* ids, float* x, int M, int d, hipStream_t st) {
   long long n = (long long)M * d;

@@ -192,9 +192,8 @@ float half_to_f32(uint16_t h) {
 hos_peft_cfg map_config(const GgufFile& g, const hos_peft_cfg* train) {
   const std::string arch = g.meta_str("general.architecture", "llama");
   if (g.has("blk.0.ssm_a")) throw Error(HOS_E_UNSUPPORTED_ARCH, "hybrid SSM models are not trainable here");
-  HOS_REQUIRE(arch == "llama" || arch == "qwen2" || arch == "mistral", HOS_E_UNSUPPORTED_ARCH,
-              "architecture '" + arch + "' is not supported by the training step (llama, qwen2, mistral)");
-  HOS_REQUIRE(!g.has("blk.0.ffn_gate_exps.weight"), HOS_E_UNSUPPORTED_ARCH, "mixture-of-experts layers");
+  HOS_REQUIRE(arch == "llama" || arch == "qwen2" || arch == "mistral" || arch == "olmoe", HOS_E_UNSUPPORTED_ARCH,
+              "architecture '" + arch + "' is not supported by the training step (llama, qwen2, mistral, olmoe)");
   auto need = [&](const std::string& key) {
     uint64_t v = 0;
     HOS_REQUIRE(g.meta_u64(arch + "." + key, &v), HOS_E_MISSING_META, "missing metadata '" + arch + "." + key + "'");
@@ -220,7 +219,15 @@ hos_peft_cfg map_config(const GgufFile& g, const hos_peft_cfg* train) {
   HOS_REQUIRE(c.dim > 0, HOS_E_FORMAT, "embedding_length is 0");
   c.vocab = (int)(n_elements(it->second) / (uint64_t)c.dim);
   c.attn_bias = g.has("blk.0.attn_q.bias") ? 1 : 0;
-  c.rope_neox = arch == "qwen2" ? 1 : 0;
+  c.rope_neox = (arch == "qwen2" || arch == "olmoe") ? 1 : 0;  // Arch::rope_neox, src/model.rs:80-82
+  // mixture of experts (src/model.rs:792-795): expert_count > 0 and the stacked expert tensors present
+  uint64_t ne = 0, nu = 0;
+  (void)g.meta_u64(arch + ".expert_count", &ne);
+  (void)g.meta_u64(arch + ".expert_used_count", &nu);
+  const bool moe = ne > 0 && g.has("blk.0.ffn_gate_exps.weight");
+  c.n_experts = moe ? (int)ne : 0;
+  c.n_experts_used = moe ? (int)nu : 0;
+  c.qk_norm = g.has("blk.0.attn_q_norm.weight") ? 1 : 0;
   return c;
 }
 
@@ -283,7 +290,8 @@ int hos_peft_create_from_gguf(hos_ctx* ctx, const char* path, const hos_peft_cfg
     const size_t cols = t.dims.empty() ? 1 : (size_t)t.dims[0];
     const size_t rows = t.dims.size() > 1 ? (size_t)(n_elements(t) / (t.dims[0] ? t.dims[0] : 1)) : 1;
     uint32_t type = t.type;
-    if ((t.type == T_F16 || t.type == T_BF16) && t.dims.size() == 1) {  // norms / biases: widen to F32
+    const bool router = name.size() > 19 && name.compare(name.size() - 19, 19, "ffn_gate_inp.weight") == 0;
+    if ((t.type == T_F16 || t.type == T_BF16) && (t.dims.size() == 1 || router)) {  // norms, biases, router: F32
       const size_t n = nb / 2;
       widened.resize(n);
       for (size_t k = 0; k < n; k++) {

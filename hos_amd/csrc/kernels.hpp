@@ -69,6 +69,19 @@ struct GemmEpi {
   int rank = 0;
   float scale = 0.0f;
 };
+// Grouped (mixture-of-experts) GEMM schedule: W holds n_experts stacked [rows, cols] blocks; workgroup row
+// y of the launch computes rows tiles[3y+1] .. +tiles[3y+2] of the operand against expert tiles[3y]
+// (−1: nothing to do). Built on the device by the router, so the launch needs no host round trip.
+struct GroupSched {
+  const int* tiles = nullptr;
+  int max_tiles = 0;
+  int n_experts = 0;
+};
+// Row tile height of the grouped GEMMs (the router's schedule is built for it).
+constexpr int GROUP_BM = 128;
+// out[r] (+)= A[r]·deq(W_e)ᵀ (fwd) or A[r]·deq(W_e) (dx) for the rows r the schedule gives expert e.
+void launch_qgemm_grouped(bool dx, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi, int passes,
+                          hipStream_t st);
 // Y[M, W.rows] = A[M, W.cols] · deq(W)ᵀ, A an fp16 row-scaled operand with row stride lda.
 void launch_qgemm_fwd(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
                       int passes, hipStream_t st);
@@ -77,6 +90,8 @@ void launch_qgemm_dx(const QWeight& w, H16 a, long long lda, long long M, GemmEp
                      int passes, hipStream_t st);
 // f32 [M, K] (row stride ldx) -> fp16 row-scaled operand (row stride K); residual too when out.lo is set.
 void launch_to_h16(const float* x, long long ldx, long long M, long long K, H16 out, hipStream_t st);
+// n samples of N(0, stddev²) from a counter-based hash of (seed, index) (synthetic weights on the device)
+void launch_randn(float* out, size_t n, uint64_t seed, float stddev, hipStream_t st);
 
 // ---- gemm_f32.hip ----
 // C[M,N] = alpha·Σ_k A(m,k)·B(k,n) + beta·C, A(m,k) = A[m·sam + k·sak], B(k,n) = B[k·sbk + n·sbn].

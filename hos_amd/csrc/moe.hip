@@ -1,0 +1,276 @@
+// Mixture-of-experts FFN plumbing (OLMoE) and QK-norm for the LoRA training step.
+//
+// Forward semantics follow src/forward.rs:542-572 (router logits → softmax over all experts → the top
+// n_experts_used by probability → Σ p_e·SwiGLU_e(x) with the raw probabilities, OLMoE's
+// norm_topk_prob = false) and :487-493 (RMSNorm of the full q / k projections before RoPE). The
+// reference's PEFT model has no MoE backward; the backward here is the chain rule of that forward: the
+// routing choice is piecewise constant, so gradients reach x through the experts and the probabilities.
+//
+// Layout: the M·K (token, expert) selections are grouped by expert into P = M·K contiguous rows (expert e
+// at offsets[e] .. offsets[e] + counts[e]); a selection's row is pos[t][s]. The expert GEMMs run over those
+// rows against the stacked quantized weights (launch_qgemm_grouped), and the combine / its backward go
+// back to token order with fixed (selection-order) summation, so results do not depend on the order in
+// which the router's atomics handed out rows.
+#include "moe.hpp"
+
+namespace hos {
+namespace {
+
+constexpr int NB = 256;
+
+__device__ __forceinline__ float wsum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float bsum(float v, float* red) {
+  v = wsum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.0f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += red[i];
+  __syncthreads();
+  return s;
+}
+
+// ---- QK-norm (the autograd rmsnorm_eps of src/tensor.rs:2500-2544 on a column block) ----
+__global__ void __launch_bounds__(NB) qknorm_fwd_kernel(float* __restrict__ buf, long long ld, int col0, int n,
+                                                         const float* __restrict__ w, float eps,
+                                                         float* __restrict__ pre, float* __restrict__ inv) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  float* xr = buf + (long long)row * ld + col0;
+  float* pr = pre + (long long)row * n;
+  float ss = 0.0f;
+  for (int c = threadIdx.x; c < n; c += NB) {
+    const float v = xr[c];
+    pr[c] = v;
+    ss += v * v;
+  }
+  ss = bsum(ss, red) / (float)n;
+  const float iv = 1.0f / sqrtf(ss + eps);
+  for (int c = threadIdx.x; c < n; c += NB) xr[c] = pr[c] * iv * w[c];
+  if (threadIdx.x == 0) inv[row] = iv;
+}
+
+// g ← g·w·inv − inv³·x/n·Σ(g·w·x)
+__global__ void __launch_bounds__(NB) qknorm_bwd_kernel(float* __restrict__ g, long long ld, int col0, int n,
+                                                         const float* __restrict__ w, const float* __restrict__ pre,
+                                                         const float* __restrict__ inv) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  float* gr = g + (long long)row * ld + col0;
+  const float* xr = pre + (long long)row * n;
+  float s = 0.0f;
+  for (int c = threadIdx.x; c < n; c += NB) s += gr[c] * w[c] * xr[c];
+  s = bsum(s, red);
+  const float iv = inv[row];
+  const float k = iv * iv * iv / (float)n * s;
+  for (int c = threadIdx.x; c < n; c += NB) gr[c] = gr[c] * w[c] * iv - xr[c] * k;
+}
+
+// ---- router: one wave per token, lane j = expert j (E ≤ 64) ----
+__global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict__ logits, int M, int E, int K,
+                                                        float* __restrict__ pfull, int* __restrict__ sel_e,
+                                                        float* __restrict__ sel_p, int* __restrict__ slot,
+                                                        int* __restrict__ counts) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
+  if (t >= M) return;
+  const bool on = j < E;
+  const float l = on ? logits[(long long)t * E + j] : -INFINITY;
+  float mx = l;
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  const float ex = on ? expf(l - mx) : 0.0f;
+  const float p = ex / wsum(ex);
+  if (on) pfull[(long long)t * E + j] = p;
+  // top K: repeated arg-max, ties to the lower expert (the stable descending sort of the reference)
+  bool taken = !on;
+  for (int s = 0; s < K; s++) {
+    float bv = taken ? -1.0f : p;
+    int bi = taken ? 64 : j;
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (j == bi) {
+      taken = true;
+      const long long q = (long long)t * K + s;
+      sel_e[q] = j;
+      sel_p[q] = p;
+      slot[q] = atomicAdd(&counts[j], 1);
+    }
+  }
+}
+
+__global__ void moe_plan_kernel(const int* __restrict__ counts, int E, int* __restrict__ offsets,
+                                int* __restrict__ tiles, int max_tiles) {
+  if (threadIdx.x != 0) return;
+  int off = 0, nt = 0;
+  for (int e = 0; e < E; e++) {
+    offsets[e] = off;
+    const int n = counts[e];
+    for (int r = 0; r < n; r += GROUP_BM) {
+      if (nt < max_tiles) {
+        tiles[3 * nt] = e;
+        tiles[3 * nt + 1] = off + r;
+        tiles[3 * nt + 2] = min(GROUP_BM, n - r);
+      }
+      nt++;
+    }
+    off += n;
+  }
+  offsets[E] = off;
+  for (int i = nt; i < max_tiles; i++) tiles[3 * i] = -1;
+}
+
+// one workgroup per selection: copy the token's operand row (hi, lo, row scale) to its expert-order row
+__global__ void __launch_bounds__(NB) moe_gather_kernel(H16 src, long long lds, const int* __restrict__ sel_e,
+                                                         const int* __restrict__ slot, const int* __restrict__ offsets,
+                                                         int K, int d, int* __restrict__ pos, H16 dst, long long ldd) {
+  const long long q = blockIdx.x;
+  const int t = (int)(q / K);
+  const int p = offsets[sel_e[q]] + slot[q];
+  if (threadIdx.x == 0) {
+    pos[q] = p;
+    dst.rinv[p] = src.rinv[t];
+  }
+  const _Float16* sh = src.data + (long long)t * lds;
+  _Float16* dh = dst.data + (long long)p * ldd;
+  for (int c = threadIdx.x; c < d; c += NB) dh[c] = sh[c];
+  if (dst.lo) {
+    const _Float16* sl = src.lo + (long long)t * lds;
+    _Float16* dl = dst.lo + (long long)p * ldd;
+    for (int c = threadIdx.x; c < d; c += NB) dl[c] = sl[c];
+  }
+}
+
+__global__ void moe_combine_kernel(const float* __restrict__ Y, const int* __restrict__ pos,
+                                   const float* __restrict__ sel_p, const float* __restrict__ resid, int M, int K,
+                                   int d, float* __restrict__ out) {
+#pragma clang fp contract(off)
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * d) return;
+  const int t = (int)(i / d), c = (int)(i % d);
+  float acc = 0.0f;
+  for (int s = 0; s < K; s++) acc += sel_p[t * K + s] * Y[(long long)pos[t * K + s] * d + c];
+  out[i] = resid[i] + acc;
+}
+
+// one workgroup per selection
+__global__ void __launch_bounds__(NB) moe_combine_bwd_kernel(const float* __restrict__ g, const float* __restrict__ Y,
+                                                              const int* __restrict__ pos,
+                                                              const float* __restrict__ sel_p, int K, int d,
+                                                              float* __restrict__ dY, float* __restrict__ dp) {
+  __shared__ float red[4];
+  const long long q = blockIdx.x;
+  const int t = (int)(q / K);
+  const long long p = pos[q];
+  const float w = sel_p[q];
+  const float* gr = g + (long long)t * d;
+  const float* yr = Y + p * d;
+  float* dr = dY + p * d;
+  float s = 0.0f;
+  for (int c = threadIdx.x; c < d; c += NB) {
+    dr[c] = w * gr[c];
+    s += yr[c] * gr[c];
+  }
+  s = bsum(s, red);
+  if (threadIdx.x == 0) dp[q] = s;
+}
+
+__global__ void __launch_bounds__(256) moe_router_bwd_kernel(const float* __restrict__ pfull,
+                                                             const float* __restrict__ dp,
+                                                             const int* __restrict__ sel_e, int M, int E, int K,
+                                                             float* __restrict__ dlogits) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
+  if (t >= M) return;
+  float dpj = 0.0f;
+  for (int s = 0; s < K; s++)
+    if (sel_e[t * K + s] == j) dpj = dp[t * K + s];
+  const float p = j < E ? pfull[(long long)t * E + j] : 0.0f;
+  const float S = wsum(p * dpj);
+  if (j < E) dlogits[(long long)t * E + j] = p * (dpj - S);
+}
+
+__global__ void moe_gather_sum_kernel(const float* __restrict__ dX, const int* __restrict__ pos, int M, int K, int d,
+                                      float* __restrict__ dxn) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * d) return;
+  const int t = (int)(i / d), c = (int)(i % d);
+  float acc = 0.0f;
+  for (int s = 0; s < K; s++) acc += dX[(long long)pos[t * K + s] * d + c];
+  dxn[i] = acc;
+}
+
+__global__ void fill_i32_kernel(int* p, long long n, int v) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+}  // namespace
+
+void launch_qknorm_fwd(float* buf, long long ld, int col0, int n, const float* w, float eps, int M, float* pre,
+                       float* inv, hipStream_t st) {
+  if (M <= 0) return;
+  qknorm_fwd_kernel<<<M, NB, 0, st>>>(buf, ld, col0, n, w, eps, pre, inv);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_qknorm_bwd(float* g, long long ld, int col0, int n, const float* w, const float* pre, const float* inv,
+                       int M, hipStream_t st) {
+  if (M <= 0) return;
+  qknorm_bwd_kernel<<<M, NB, 0, st>>>(g, ld, col0, n, w, pre, inv);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_moe_route(const float* logits, int M, int E, int K, float* pfull, int* sel_e, float* sel_p, int* slot,
+                      int* counts, hipStream_t st) {
+  HOS_REQUIRE(E >= 1 && E <= 64 && K >= 1 && K <= E, HOS_E_INVALID, "moe: need 1 <= experts used <= experts <= 64");
+  if (M <= 0) return;
+  moe_route_kernel<<<ceil_div(M, 4), 256, 0, st>>>(logits, M, E, K, pfull, sel_e, sel_p, slot, counts);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_moe_plan(const int* counts, int E, int* offsets, int* tiles, int max_tiles, hipStream_t st) {
+  moe_plan_kernel<<<1, 64, 0, st>>>(counts, E, offsets, tiles, max_tiles);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_moe_gather(H16 src, long long lds, const int* sel_e, const int* slot, const int* offsets, int M, int K,
+                       int d, int* pos, H16 dst, long long ldd, hipStream_t st) {
+  if (M <= 0) return;
+  moe_gather_kernel<<<(unsigned)((long long)M * K), NB, 0, st>>>(src, lds, sel_e, slot, offsets, K, d, pos, dst, ldd);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_moe_combine(const float* Y, const int* pos, const float* sel_p, const float* resid, int M, int K, int d,
+                        float* out, hipStream_t st) {
+  const long long n = (long long)M * d;
+  if (n <= 0) return;
+  moe_combine_kernel<<<ceil_div(n, 256), 256, 0, st>>>(Y, pos, sel_p, resid, M, K, d, out);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_moe_combine_bwd(const float* g, const float* Y, const int* pos, const float* sel_p, int M, int K, int d,
+                            float* dY, float* dp, hipStream_t st) {
+  if (M <= 0) return;
+  moe_combine_bwd_kernel<<<(unsigned)((long long)M * K), NB, 0, st>>>(g, Y, pos, sel_p, K, d, dY, dp);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_moe_router_bwd(const float* pfull, const float* dp, const int* sel_e, int M, int E, int K, float* dlogits,
+                           hipStream_t st) {
+  if (M <= 0) return;
+  moe_router_bwd_kernel<<<ceil_div(M, 4), 256, 0, st>>>(pfull, dp, sel_e, M, E, K, dlogits);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_moe_gather_sum(const float* dX, const int* pos, int M, int K, int d, float* dxn, hipStream_t st) {
+  const long long n = (long long)M * d;
+  if (n <= 0) return;
+  moe_gather_sum_kernel<<<ceil_div(n, 256), 256, 0, st>>>(dX, pos, M, K, d, dxn);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_fill_i32(int* p, long long n, int v, hipStream_t st) {
+  if (n <= 0) return;
+  fill_i32_kernel<<<ceil_div(n, 256), 256, 0, st>>>(p, n, v);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace hos

@@ -19,6 +19,7 @@
 #include "peft_internal.hpp"
 #include "fused.hpp"
 #include "lora.hpp"
+#include "moe.hpp"
 
 using namespace hos;
 
@@ -32,10 +33,18 @@ struct LayerW {
   float* attn_norm = nullptr;   // [d]
   float* ffn_norm = nullptr;    // [d]
   float* bias[3] = {nullptr, nullptr, nullptr};  // q k v
+  float *q_norm = nullptr, *k_norm = nullptr;     // OLMoE QK-norm weights [qd], [kvd]
+  float* router = nullptr;                        // MoE router [E][d] (f32, ffn_gate_inp.weight)
+  QWeight xg, xu, xd;                             // MoE experts, stacked [E·F][d], [E·F][d], [E·d][F]
 };
 
 struct LayerAct {
   float *x, *xn1, *inv1, *qkv, *o, *lse, *x2, *xn2, *inv2, *gu, *h, *u;
+  float *qk_pre = nullptr, *qk_inv = nullptr;  // QK-norm: pre-norm q|k [M][qd+kvd], 1/rms [2][M]
+  // MoE: softmax [M][E], selections [M][K] (expert, probability, slot, expert-order row), per-expert
+  // counts / offsets, grouped-GEMM schedule, expert pre-activations [P][2F] and outputs [P][d] (P = M·K)
+  float *pfull = nullptr, *sel_p = nullptr, *gug = nullptr, *yg = nullptr;
+  int *sel_e = nullptr, *slot = nullptr, *pos = nullptr, *counts = nullptr, *offsets = nullptr, *tiles = nullptr;
 };
 
 struct ProfRec {
@@ -61,6 +70,9 @@ struct hos_peft {
   float lscale = 0.0f;
 
   std::vector<LayerW> lw;
+  int E = 0, K = 0, max_tiles = 0;  // MoE: experts, experts per token, grouped-GEMM schedule length
+  H16 hx{};                         // MoE operand scratch [M·K][max(d, 2F)]
+  float *mlogits = nullptr, *mdY = nullptr, *mdH = nullptr, *mdX = nullptr, *mdp = nullptr, *mdl = nullptr;
   QWeight tok, out;
   bool out_set = false;
   float* out_norm = nullptr;
@@ -324,14 +336,86 @@ struct hos_peft {
     HOS_REQUIRE(out_norm != nullptr, HOS_E_MISSING_TENSOR, "missing tensor 'output_norm.weight'");
     for (int l = 0; l < L; l++) {
       const char* names[NT] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
-      for (int t = 0; t < NT; t++)
+      for (int t = 0; t < (E ? TG : NT); t++)
         HOS_REQUIRE(lw[l].w[t].q != nullptr, HOS_E_MISSING_TENSOR,
                     "missing tensor 'blk." + std::to_string(l) + "." + names[t] + ".weight'");
+      if (E)
+        HOS_REQUIRE(lw[l].router && lw[l].xg.q && lw[l].xu.q && lw[l].xd.q, HOS_E_MISSING_TENSOR,
+                    "missing mixture-of-experts tensors of blk." + std::to_string(l));
+      if (c.qk_norm)
+        HOS_REQUIRE(lw[l].q_norm && lw[l].k_norm, HOS_E_MISSING_TENSOR,
+                    "missing QK-norm weights of blk." + std::to_string(l));
       HOS_REQUIRE(lw[l].attn_norm && lw[l].ffn_norm, HOS_E_MISSING_TENSOR,
                   "missing norm weights of blk." + std::to_string(l));
       if (c.attn_bias)
         HOS_REQUIRE(lw[l].bias[0] && lw[l].bias[1] && lw[l].bias[2], HOS_E_MISSING_TENSOR,
                     "missing attention biases of blk." + std::to_string(l));
+    }
+  }
+
+  // ---------------- mixture of experts (OLMoE) ----------------
+  void grouped(bool dxdir, const QWeight& w, H16 a, long long lda, const int* tiles, float* out, long long ldo,
+               int accumulate, int M, int np) {
+    const double er = (double)w.rows / E;  // W rows of one expert
+    Scope s(this, dxdir ? "qgemm_dx" : "qgemm_fwd", 2.0 * M * K * er * w.cols,
+            2.0 * M * K * (dxdir ? er : w.cols) + wbytes(w) + 4.0 * M * K * (dxdir ? w.cols : er));
+    GemmEpi e{};
+    e.out = out;
+    e.ldo = ldo;
+    e.accumulate = accumulate;
+    launch_qgemm_grouped(dxdir, w, GroupSched{tiles, max_tiles, E}, a, lda, e, np, st);
+  }
+  // x_next = x2 + Σ_top-K p_e·SwiGLU_e(xn2) (src/forward.rs:542-572); xn2 (f32) and its fp16 operand in hs
+  // come from the FFN RMSNorm.
+  void moe_forward(int l, int M, float* xnext) {
+    LayerAct& a = act[l];
+    LayerW& w = lw[l];
+    const long long P = (long long)M * K;
+    {
+      Scope s(this, "moe_route", 2.0 * M * d * E, 4.0 * ((double)M * d + (double)E * d + 4.0 * M * E) + 4.0 * P * d);
+      launch_gemm_f32(M, E, d, 1.0f, a.xn2, d, 1, w.router, 1, d, 0.0f, mlogits, E, ws, ws_bytes, st);
+      launch_fill_i32(a.counts, E, 0, st);
+      launch_moe_route(mlogits, M, E, K, a.pfull, a.sel_e, a.sel_p, a.slot, a.counts, st);
+      launch_moe_plan(a.counts, E, a.offsets, a.tiles, max_tiles, st);
+      launch_moe_gather(hs, d, a.sel_e, a.slot, a.offsets, M, K, d, a.pos, hx, d, st);
+    }
+    grouped(false, w.xg, hx, d, a.tiles, a.gug, 2LL * F, 0, M, pf);
+    grouped(false, w.xu, hx, d, a.tiles, a.gug + F, 2LL * F, 0, M, pf);
+    {
+      Scope s(this, "swiglu", 0, 8.0 * P * F + 2.0 * P * F);
+      launch_swiglu_fwd(a.gug, (int)P, F, nullptr, hx, st);
+    }
+    grouped(false, w.xd, hx, F, a.tiles, a.yg, d, 0, M, pf);
+    {
+      Scope s(this, "moe_combine", 0, 4.0 * (2.0 * M * d + P * d));
+      launch_moe_combine(a.yg, a.pos, a.sel_p, a.x2, M, K, d, xnext, st);
+    }
+  }
+  // dx: gradient at x_next on entry; leaves dxn = gradient at xn2 (experts + router)
+  void moe_backward(int l, int M) {
+    LayerAct& a = act[l];
+    LayerW& w = lw[l];
+    const long long P = (long long)M * K;
+    {
+      Scope s(this, "moe_combine", 0, 4.0 * (M * d + 2.0 * P * d));
+      launch_moe_combine_bwd(dx, a.yg, a.pos, a.sel_p, M, K, d, mdY, mdp, st);
+    }
+    {
+      Scope s(this, "convert", 0, 6.0 * P * d);
+      launch_to_h16(mdY, d, P, d, hx, st);
+    }
+    grouped(true, w.xd, hx, d, a.tiles, mdH, F, 0, M, pd);
+    {
+      Scope s(this, "swiglu", 0, 4.0 * P * F * 3 + 4.0 * P * F);
+      launch_swiglu_bwd(a.gug, mdH, (int)P, F, nullptr, hx, st);
+    }
+    grouped(true, w.xg, hx, 2LL * F, a.tiles, mdX, d, 0, M, pd);
+    grouped(true, w.xu, h16_offset(hx, F), 2LL * F, a.tiles, mdX, d, 1, M, pd);
+    {
+      Scope s(this, "moe_route", 2.0 * M * d * E, 4.0 * (P * d + 2.0 * M * d + (double)E * d + 3.0 * M * E));
+      launch_moe_router_bwd(a.pfull, mdp, a.sel_e, M, E, K, mdl, st);
+      launch_moe_gather_sum(mdX, a.pos, M, K, d, dxn, st);
+      launch_gemm_f32(M, d, E, 1.0f, mdl, E, 1, w.router, d, 1, 1.0f, dxn, d, ws, ws_bytes, st);
     }
   }
 
@@ -355,6 +439,11 @@ struct hos_peft {
       qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0, up_epi(l, TQ), tpf[TQ]);
       qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0, up_epi(l, TK), tpf[TK]);
       qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0, up_epi(l, TV), tpf[TV]);
+      if (c.qk_norm) {
+        Scope s(this, "rmsnorm", 0, 4.0 * M * (qd + kvd) * 3);
+        launch_qknorm_fwd(a.qkv, W3, 0, qd, w.q_norm, c.rms_eps, M, a.qk_pre, a.qk_inv, st);
+        launch_qknorm_fwd(a.qkv, W3, qd, kvd, w.k_norm, c.rms_eps, M, a.qk_pre + (size_t)M * qd, a.qk_inv + M, st);
+      }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
         launch_rope(a.qkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
@@ -368,10 +457,14 @@ struct hos_peft {
       to16(a.o, qd, M, qd);
       lora_down(l, 1, a.o, qd, M);
       qfwd(w.w[TO], hs, qd, M, a.x2, d, nullptr, a.x, 0, up_epi(l, TO), tpf[TO]);
-      const bool lgu = has(TG) || has(TU);
+      const bool lgu = has(TG) || has(TU) || E;
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lgu ? 2 : 1) + 2.0 * M * d);
         launch_rmsnorm_fwd(a.x2, w.ffn_norm, c.rms_eps, M, d, lgu ? a.xn2 : nullptr, hs, a.inv2, st);
+      }
+      if (E) {
+        moe_forward(l, M, xnext);
+        continue;
       }
       lora_down(l, 2, a.xn2, d, M);
       qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, up_epi(l, TG), tpf[TG]);
@@ -410,7 +503,10 @@ struct hos_peft {
     for (int l = L - 1; l >= 0; l--) {
       LayerAct& a = act[l];
       LayerW& w = lw[l];
-      // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA) ----
+      // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA), or the mixture of experts ----
+      if (E) {
+        moe_backward(l, M);
+      } else {
       to16(dx, d, M, d);
       lora_grad_b(l, 3, dx, d, d, M);
       qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD), tpd[TD]);
@@ -424,6 +520,7 @@ struct hos_peft {
       qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG), tpd[TG]);
       qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU), tpd[TU]);
       lora_grad_a(l, 2, a.xn2, d, M);
+      }
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
         launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st);
@@ -443,6 +540,11 @@ struct hos_peft {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
         launch_rope(dqkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
         launch_rope(dqkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+      }
+      if (c.qk_norm) {
+        Scope s(this, "rmsnorm", 0, 4.0 * M * (qd + kvd) * 4);
+        launch_qknorm_bwd(dqkv, W3, 0, qd, w.q_norm, a.qk_pre, a.qk_inv, M, st);
+        launch_qknorm_bwd(dqkv, W3, qd, kvd, w.k_norm, a.qk_pre + (size_t)M * qd, a.qk_inv + M, M, st);
       }
       lora_grad_b(l, 0, dqkv, W3, W3, M);
       to16(dqkv, W3, M, W3);
@@ -541,7 +643,13 @@ struct hos_peft {
     HOS_REQUIRE(c.n_layers > 0 && c.dim > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.ffn_dim > 0 && c.vocab > 0,
                 HOS_E_INVALID, "peft: bad model dimensions");
     HOS_REQUIRE(c.n_heads % c.n_kv_heads == 0, HOS_E_INVALID, "peft: n_heads must be a multiple of n_kv_heads");
-    HOS_REQUIRE(c.head_dim == 64, HOS_E_UNSUPPORTED_ARCH, "peft: head_dim must be 64");
+    HOS_REQUIRE(c.head_dim == 64 || c.head_dim == 128, HOS_E_UNSUPPORTED_ARCH, "peft: head_dim must be 64 or 128");
+    E = c.n_experts;
+    K = c.n_experts_used;
+    HOS_REQUIRE(E == 0 || (E <= 64 && K >= 1 && K <= E), HOS_E_INVALID,
+                "peft: mixture of experts needs 1 <= n_experts_used <= n_experts <= 64");
+    HOS_REQUIRE(E == 0 || !(c.lora_targets & (HOS_T_GATE | HOS_T_UP | HOS_T_DOWN)), HOS_E_INVALID,
+                "peft: a mixture-of-experts FFN takes no LoRA on gate/up/down");
     HOS_REQUIRE(c.lora_rank > 0 && c.max_batch > 0 && c.max_seq > 0, HOS_E_INVALID, "peft: bad rank/batch/seq");
     HOS_REQUIRE(c.dim % 32 == 0 && c.ffn_dim % 32 == 0, HOS_E_INVALID, "peft: dim and ffn_dim must be multiples of 32");
     L = c.n_layers;
@@ -631,11 +739,41 @@ struct hos_peft {
       a.o = alloc<float>(M * qd);
       a.lse = alloc<float>(M * c.n_heads);
       a.x2 = alloc<float>(M * d);
-      a.xn2 = (has(TG) || has(TU)) ? alloc<float>(M * d) : nullptr;
+      a.xn2 = (has(TG) || has(TU) || E) ? alloc<float>(M * d) : nullptr;
       a.inv2 = alloc<float>(M);
-      a.gu = alloc<float>(M * 2 * F);
+      a.gu = E ? nullptr : alloc<float>(M * 2 * F);
       a.h = has(TD) ? alloc<float>(M * F) : nullptr;
       a.u = alloc<float>(M * NT * r);
+      if (c.qk_norm) {
+        a.qk_pre = alloc<float>(M * (qd + kvd));
+        a.qk_inv = alloc<float>(2 * M);
+      }
+      if (E) {
+        const size_t P = M * K;
+        max_tiles = (int)((P + GROUP_BM - 1) / GROUP_BM) + E;
+        a.pfull = alloc<float>(M * E);
+        a.sel_p = alloc<float>(P);
+        a.sel_e = alloc<int>(P);
+        a.slot = alloc<int>(P);
+        a.pos = alloc<int>(P);
+        a.counts = alloc<int>(E);
+        a.offsets = alloc<int>(E + 1);
+        a.tiles = alloc<int>(3 * (size_t)max_tiles);
+        a.gug = alloc<float>(P * 2 * F);
+        a.yg = alloc<float>(P * d);
+      }
+    }
+    if (E) {
+      const size_t P = M * K, xc = std::max<size_t>((size_t)d, 2 * (size_t)F);
+      hx.data = alloc<half_t>(P * xc);
+      hx.rinv = alloc<float>(P);
+      hx.lo = (pf == 2 || pf == 3 || pd == 2 || pd == 3) ? alloc<half_t>(P * xc) : nullptr;
+      mlogits = alloc<float>(M * E);
+      mdY = alloc<float>(P * d);
+      mdH = alloc<float>(P * F);
+      mdX = alloc<float>(P * d);
+      mdp = alloc<float>(P);
+      mdl = alloc<float>(M * E);
     }
     xfinal = alloc<float>(M * d);
     invf = alloc<float>(M);
@@ -655,7 +793,7 @@ struct hos_peft {
     dxn = alloc<float>(M * d);
     dqkv = alloc<float>(M * W3);
     dout = alloc<float>(M * qd);
-    dh = alloc<float>(M * F);
+    dh = E ? nullptr : alloc<float>(M * F);
     dgu = (has(TG) || has(TU)) ? alloc<float>(M * 2 * F) : nullptr;
     du = alloc<float>(M * NT * r);
     dvec = alloc<float>(M * c.n_heads);
@@ -689,8 +827,12 @@ struct hos_peft {
       (void)hipEventDestroy(rc.e1);
     }
     recs.clear();
-    for (auto& l : lw)
+    for (auto& l : lw) {
       for (auto& w : l.w) free_qweight(w);
+      free_qweight(l.xg);
+      free_qweight(l.xu);
+      free_qweight(l.xd);
+    }
     free_qweight(tok);
     free_qweight(out);
     for (void* p : allocs) (void)hipFree(p);
@@ -735,6 +877,14 @@ struct hos_peft {
     if (leaf == "attn_q.bias") return set_f32(&w.bias[0], bytes, nbytes, type, (size_t)qd, name);
     if (leaf == "attn_k.bias") return set_f32(&w.bias[1], bytes, nbytes, type, (size_t)kvd, name);
     if (leaf == "attn_v.bias") return set_f32(&w.bias[2], bytes, nbytes, type, (size_t)kvd, name);
+    if (leaf == "attn_q_norm.weight") return set_f32(&w.q_norm, bytes, nbytes, type, (size_t)qd, name);
+    if (leaf == "attn_k_norm.weight") return set_f32(&w.k_norm, bytes, nbytes, type, (size_t)kvd, name);
+    if (E) {
+      if (leaf == "ffn_gate_inp.weight") return set_f32(&w.router, bytes, nbytes, type, (size_t)E * d, name);
+      if (leaf == "ffn_gate_exps.weight") return set_q(w.xg, bytes, nbytes, type, rows, cols, (size_t)E * F, d, name);
+      if (leaf == "ffn_up_exps.weight") return set_q(w.xu, bytes, nbytes, type, rows, cols, (size_t)E * F, d, name);
+      if (leaf == "ffn_down_exps.weight") return set_q(w.xd, bytes, nbytes, type, rows, cols, (size_t)E * d, F, name);
+    }
     const char* names[NT] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
                              "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
     for (int t = 0; t < NT; t++)

@@ -30,6 +30,12 @@ void qgemm_launch_q4k(bool dx, int passes, const QWeight& w, H16 a, long long ld
                       float* ws, size_t ws_bytes, hipStream_t st);
 void qgemm_launch_q6k(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
                       float* ws, size_t ws_bytes, hipStream_t st);
+void qgemm_grouped_q8(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                      hipStream_t st);
+void qgemm_grouped_q4k(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                       hipStream_t st);
+void qgemm_grouped_q6k(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                       hipStream_t st);
 
 namespace {
 
@@ -92,6 +98,17 @@ void launch_qgemm_fwd(const QWeight& w, H16 a, long long lda, long long M, GemmE
 void launch_qgemm_dx(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
                      int passes, hipStream_t st) {
   launch_any(true, w, a, lda, M, epi, ws, ws_bytes, passes, st);
+}
+void launch_qgemm_grouped(bool dx, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi, int passes,
+                          hipStream_t st) {
+  HOS_REQUIRE(passes >= 1 && passes <= 4, HOS_E_INVALID, "qgemm: precision mode must be 1, 2, 3 or 4");
+  if (gs.max_tiles <= 0) return;
+  switch (w.type) {
+    case GGUF_Q8_0: qgemm_grouped_q8(dx, passes, w, gs, a, lda, epi, st); break;
+    case GGUF_Q4_K: qgemm_grouped_q4k(dx, passes, w, gs, a, lda, epi, st); break;
+    case GGUF_Q6_K: qgemm_grouped_q6k(dx, passes, w, gs, a, lda, epi, st); break;
+    default: throw Error(HOS_E_UNSUPPORTED_QUANT, "qgemm: unsupported quant type");
+  }
 }
 void launch_to_h16(const float* x, long long ldx, long long M, long long K, H16 out, hipStream_t st) {
   if (M <= 0) return;

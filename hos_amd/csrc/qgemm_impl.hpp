@@ -177,6 +177,13 @@ __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, in
   }
 }
 
+// Device-side view of a GroupSched: per-expert strides of the repacked weight (bytes of q, floats of s) and
+// the W rows of one expert.
+struct GroupKernelArgs {
+  const int* tiles = nullptr;
+  long long q_stride = 0, s_stride = 0, rows = 0;
+};
+
 template <int BM, int BN, int BK, bool DX, int NP>
 struct Geo {
   static constexpr int NT = BM >= 256 ? 512 : 256;      // threads: 8 waves for 256-row tiles, else 4
@@ -204,8 +211,23 @@ template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
 __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightView w, const _Float16* __restrict__ A,
                                                     const _Float16* __restrict__ Alo, const float* __restrict__ rinv,
                                                     long long lda, int M, int Nout, int C, int c_per_split,
-                                                    GemmEpi epi, float* __restrict__ ws) {
+                                                    GemmEpi epi, float* __restrict__ ws, GroupKernelArgs gk) {
   using G = Geo<BM, BN, BK, DX, NP>;
+  if (gk.tiles) {  // grouped: this workgroup row is one row tile of one expert
+    const int* tl = gk.tiles + 3 * blockIdx.y;
+    const int e = tl[0];
+    if (e < 0) return;
+    const long long r0 = tl[1];
+    M = tl[2];
+    A += r0 * lda;
+    if (Alo) Alo += r0 * lda;
+    rinv += r0;
+    epi.out += r0 * epi.ldo;
+    if (epi.resid) epi.resid += r0 * epi.ldo;
+    w.q = (const uint8_t*)w.q + e * gk.q_stride;
+    w.s += e * gk.s_stride;
+    w.rows = gk.rows;
+  }
   static_assert(G::E == 8 || G::E == 16 || G::E == 32, "B run length");
   static_assert(BK % 32 == 0 || (BK == 32), "slab depth");
   constexpr bool ALO = NP == 2 || NP == 3, BLO = NP >= 3;
@@ -218,6 +240,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   int wid = blockIdx.x + gridDim.x * blockIdx.y;
   const int nwg = gridDim.x * gridDim.y, full = nwg & ~7;
   if (wid < full) wid = (wid & 7) * (full >> 3) + (wid >> 3);
+  if (gk.tiles) wid = blockIdx.x;  // grouped: row tile fixed above, no remap
   const int m0 = (wid / gridDim.x) * BM, n0 = (wid % gridDim.x) * BN;
   const int cbeg = blockIdx.z * c_per_split;
   const int cend = min(C, cbeg + c_per_split);
@@ -474,7 +497,8 @@ void launch_shape(const QWeight& w, H16 a, long long lda, long long M, int Nout,
                   GemmEpi epi, float* ws, hipStream_t st) {
   dim3 grid(ceil_div(Nout, BN), ceil_div(M, BM), splits);
   qgemm_kernel<QT, DX, BM, BN, BK, NP>
-      <<<grid, Geo<BM, BN, BK, DX, NP>::NT, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, (int)M, Nout, C, per, epi, ws);
+      <<<grid, Geo<BM, BN, BK, DX, NP>::NT, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, (int)M, Nout, C, per, epi, ws,
+                                                     GroupKernelArgs{});
 }
 
 template <uint32_t QT, bool DX, int NP>
@@ -548,6 +572,32 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     splitk_reduce<<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
     HOS_HIP_CHECK(hipGetLastError());
   }
+}
+
+// Grouped launch (mixture-of-experts): W = n_experts stacked blocks, 128×128 tiles, no split.
+template <uint32_t QT, bool DX, int NP>
+void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi, hipStream_t st) {
+  HOS_REQUIRE(gs.n_experts > 0 && w.rows % gs.n_experts == 0, HOS_E_INVALID, "grouped qgemm: bad expert count");
+  const long long er = w.rows / gs.n_experts;  // W rows of one expert
+  const int Nout = DX ? (int)w.cols : (int)er;
+  const int C = DX ? (int)er : (int)w.cols;
+  HOS_REQUIRE(C % 32 == 0 && lda % 8 == 0, HOS_E_INVALID, "grouped qgemm: contraction must be a multiple of 32");
+  HOS_REQUIRE((NP != 2 && NP != 3) || a.lo != nullptr, HOS_E_INVALID, "grouped qgemm: needs the operand residual");
+  HOS_REQUIRE(epi.rank == 0, HOS_E_INVALID, "grouped qgemm: no fused rank-r term");
+  GroupKernelArgs gk;
+  gk.tiles = gs.tiles;
+  gk.rows = er;
+  const long long n = er * w.cols;  // elements of one expert
+  gk.q_stride = QT == GGUF_Q4_K ? n / 2 : n;
+  gk.s_stride = QT == GGUF_Q4_K ? n / 16 : (QT == GGUF_Q8_0 ? n / 32 : n / 16);
+  dim3 grid(ceil_div(Nout, 128), gs.max_tiles, 1);
+  if (C % 64 == 0)
+    qgemm_kernel<QT, DX, 128, 128, 64, NP><<<grid, 256, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, 0, Nout, C, C,
+                                                                 epi, nullptr, gk);
+  else
+    qgemm_kernel<QT, DX, 128, 128, 32, NP><<<grid, 256, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, 0, Nout, C, C,
+                                                                 epi, nullptr, gk);
+  HOS_HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace

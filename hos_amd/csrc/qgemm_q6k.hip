@@ -19,3 +19,20 @@ void qgemm_launch_q6k(bool dx, int passes, const QWeight& w, H16 a, long long ld
 }
 
 }  // namespace hos
+
+namespace hos {
+void qgemm_grouped_q6k(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                      hipStream_t st) {
+  if (dx) {
+    if (passes == 1) launch_typed_grouped<GGUF_Q6_K, true, 1>(w, gs, a, lda, epi, st);
+    else if (passes == 2) launch_typed_grouped<GGUF_Q6_K, true, 2>(w, gs, a, lda, epi, st);
+    else if (passes == 3) launch_typed_grouped<GGUF_Q6_K, true, 3>(w, gs, a, lda, epi, st);
+    else launch_typed_grouped<GGUF_Q6_K, true, 4>(w, gs, a, lda, epi, st);
+  } else {
+    if (passes == 1) launch_typed_grouped<GGUF_Q6_K, false, 1>(w, gs, a, lda, epi, st);
+    else if (passes == 2) launch_typed_grouped<GGUF_Q6_K, false, 2>(w, gs, a, lda, epi, st);
+    else if (passes == 3) launch_typed_grouped<GGUF_Q6_K, false, 3>(w, gs, a, lda, epi, st);
+    else launch_typed_grouped<GGUF_Q6_K, false, 4>(w, gs, a, lda, epi, st);
+  }
+}
+}  // namespace hos

@@ -136,6 +136,26 @@ class Gpu:
         self._chk(lib().hos_hip_quantize(self.h, _p(x), x.size, ggml_type, _p(out)))
         return out
 
+    def random_quantized(self, rows, cols, ggml_type, seed, stddev=0.02):
+        """Quantized bytes of a [rows, cols] ~N(0, stddev²) matrix drawn and quantized on the device (fast
+        synthetic weights for very large tensors), in chunks of whole rows."""
+        out = np.empty(bytes_for(ggml_type, rows * cols), np.uint8)
+        chunk = max(1, (64 << 20) // cols)
+        x, q = self.alloc(chunk * cols * 4), self.alloc(bytes_for(ggml_type, chunk * cols))
+        try:
+            done = 0
+            for r0 in range(0, rows, chunk):
+                n = min(chunk, rows - r0) * cols
+                self._chk(lib().hos_hip_randn_dev(self.h, x, n, (seed << 20) + r0 // chunk, stddev))
+                self._chk(lib().hos_hip_quantize_dev(self.h, x, n, ggml_type, q))
+                nb = bytes_for(ggml_type, n)
+                self._chk(lib().hos_hip_d2h(self.h, _p(out[done:done + nb]), q, nb))
+                done += nb
+        finally:
+            self.free(x)
+            self.free(q)
+        return out
+
     # ---- device memory ----
     def alloc(self, nbytes):
         p = ctypes.c_void_p()

@@ -42,6 +42,9 @@ class ModelConfig:
     seq: int = 128
     lr: float = 1e-3
     gemm_passes: int = 0      # qGEMM precision passes (0 = library default)
+    n_experts: int = 0        # mixture-of-experts FFN (0 = dense), src/model.rs:642-643
+    n_experts_used: int = 0
+    qk_norm: bool = False     # OLMoE RMSNorm of the q / k projections before RoPE
     extra: dict = field(default_factory=dict)
 
     @property
@@ -61,13 +64,15 @@ class ModelConfig:
 def _cstruct(cfg, max_batch=None, max_seq=None):
     return PeftCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
                    cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank,
-                   cfg.lora_alpha, cfg.target_mask, max_batch or cfg.batch, max_seq or cfg.seq, cfg.gemm_passes)
+                   cfg.lora_alpha, cfg.target_mask, max_batch or cfg.batch, max_seq or cfg.seq, cfg.gemm_passes,
+                   cfg.n_experts, cfg.n_experts_used, int(cfg.qk_norm))
 
 
 def _from_cstruct(c, name, **train):
     return ModelConfig(name=name, n_layers=c.n_layers, dim=c.dim, n_heads=c.n_heads, n_kv_heads=c.n_kv_heads,
                        head_dim=c.head_dim, ffn_dim=c.ffn_dim, vocab=c.vocab, rms_eps=c.rms_eps,
-                       rope_base=c.rope_base, rope_neox=bool(c.rope_neox), attn_bias=bool(c.attn_bias), **train)
+                       rope_base=c.rope_base, rope_neox=bool(c.rope_neox), attn_bias=bool(c.attn_bias),
+                       n_experts=c.n_experts, n_experts_used=c.n_experts_used, qk_norm=bool(c.qk_norm), **train)
 
 
 def gguf_config(path, **train):

@@ -29,6 +29,13 @@ CONFIGS = {
                                ffn_dim=8192, vocab=128256, rms_eps=1e-5, rope_base=5e5, rope_neox=False,
                                lora_rank=32, lora_alpha=16.0, lora_targets=ALL, quant=GGML_Q4_K,
                                head_quant=GGML_Q4_K, batch=8, seq=1024, lr=1e-4),
+    # OLMoE architecture, 64 experts top-8 (SwiGLU 1024) kept in Q8_0, QK-norm, head_dim 128,
+    # LoRA r=16 on the attention projections, 4 x 512
+    "olmoe": ModelConfig("olmoe", n_layers=16, dim=2048, n_heads=16, n_kv_heads=16, head_dim=128, ffn_dim=1024,
+                         vocab=50304, rms_eps=1e-5, rope_base=10000.0, rope_neox=True, lora_rank=16,
+                         lora_alpha=16.0, lora_targets=("q", "k", "v", "o"), quant=GGML_Q8_0,
+                         head_quant=GGML_Q8_0, batch=4, seq=512, lr=1e-4, n_experts=64, n_experts_used=8,
+                         qk_norm=True),
 }
 
 
@@ -44,33 +51,53 @@ def tensor_list(cfg):
     if not cfg.tied:
         out.append(("output.weight", cfg.vocab, d, "head"))
     out.append(("output_norm.weight", 1, d, "norm"))
+    E = cfg.n_experts
     for l in range(cfg.n_layers):
         p = f"blk.{l}."
         out += [(p + "attn_norm.weight", 1, d, "norm"), (p + "attn_q.weight", qd, d, "lin"),
                 (p + "attn_k.weight", kvd, d, "lin"), (p + "attn_v.weight", kvd, d, "lin"),
-                (p + "attn_output.weight", d, qd, "lin"), (p + "ffn_norm.weight", 1, d, "norm"),
-                (p + "ffn_gate.weight", f, d, "lin"), (p + "ffn_up.weight", f, d, "lin"),
-                (p + "ffn_down.weight", d, f, "lin")]
+                (p + "attn_output.weight", d, qd, "lin"), (p + "ffn_norm.weight", 1, d, "norm")]
+        if E:  # MoE (src/model.rs:815-838): f32 router [E, d], stacked experts [E·rows, cols]
+            out += [(p + "ffn_gate_inp.weight", E, d, "router"), (p + "ffn_gate_exps.weight", E * f, d, "lin"),
+                    (p + "ffn_up_exps.weight", E * f, d, "lin"), (p + "ffn_down_exps.weight", E * d, f, "lin")]
+        else:
+            out += [(p + "ffn_gate.weight", f, d, "lin"), (p + "ffn_up.weight", f, d, "lin"),
+                    (p + "ffn_down.weight", d, f, "lin")]
+        if cfg.qk_norm:
+            out += [(p + "attn_q_norm.weight", 1, qd, "norm"), (p + "attn_k_norm.weight", 1, kvd, "norm")]
         if cfg.attn_bias:
             out += [(p + "attn_q.bias", 1, qd, "bias"), (p + "attn_k.bias", 1, kvd, "bias"),
                     (p + "attn_v.bias", 1, kvd, "bias")]
     return out
 
 
-def build_tensors(gpu, cfg, seed=1234):
-    """name -> (raw bytes, ggml_type, rows, cols), quantized on the device."""
+def build_tensors(gpu, cfg, seed=1234, quantize=None, norm_jitter=0.0):
+    """name -> (raw bytes, ggml_type, rows, cols), quantized on the device (or with `quantize(w, type)`).
+    Norm weights are 1.0 (+ U(-norm_jitter, norm_jitter)); the MoE router is f32 ~N(0, 0.02) like the other
+    weights (cfg.extra["router_std"] overrides)."""
+    device = quantize is None
+    quantize = quantize or gpu.quantize
     rng = np.random.default_rng(seed)
     tensors = {}
-    for name, rows, cols, kind in tensor_list(cfg):
-        if kind == "norm":
-            tensors[name] = (np.ones(cols, np.float32).view(np.uint8), GGML_F32, 1, cols)
+    for idx, (name, rows, cols, kind) in enumerate(tensor_list(cfg)):
+        if device and "_exps" in name:
+            # MoE expert stacks (billions of values at OLMoE size): drawn and quantized on the device
+            t = storage_type(cfg.quant, cols)
+            tensors[name] = (gpu.random_quantized(rows, cols, t, seed=seed * 4096 + idx), t, rows, cols)
             continue
-        w = (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-        if kind == "bias":
-            tensors[name] = (w.ravel().view(np.uint8), GGML_F32, 1, cols)
+        if kind == "norm":
+            v = np.ones(cols, np.float32)
+            if norm_jitter:
+                v += rng.uniform(-norm_jitter, norm_jitter, cols).astype(np.float32)
+            tensors[name] = (v.view(np.uint8), GGML_F32, 1, cols)
+            continue
+        std = np.float32(cfg.extra.get("router_std", 0.02) if kind == "router" else 0.02)
+        w = (rng.standard_normal((rows, cols), dtype=np.float32) * std).astype(np.float32)
+        if kind in ("bias", "router"):
+            tensors[name] = (w.ravel().view(np.uint8), GGML_F32, rows, cols)
             continue
         t = storage_type(cfg.head_quant if kind == "head" else cfg.quant, cols)
-        tensors[name] = (gpu.quantize(w, t), t, rows, cols)
+        tensors[name] = (quantize(w, t), t, rows, cols)
     return tensors
 
 
@@ -98,6 +125,8 @@ def algorithmic_flops_per_token(cfg, seq):
     """F_tok = 4·P_base + 6·P_lora + 6·L·T·q_dim, causal attention counted once (the reference's
     baseline formula)."""
     d, qd, kvd, f, v = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.ffn_dim, cfg.vocab
-    p_base = cfg.n_layers * (d * qd + 2 * d * kvd + qd * d + 3 * d * f) + d * v
+    # a mixture of experts counts the active parameters: the K routed experts and the router
+    ffn = (cfg.n_experts_used * 3 * d * f + d * cfg.n_experts) if cfg.n_experts else 3 * d * f
+    p_base = cfg.n_layers * (d * qd + 2 * d * kvd + qd * d + ffn) + d * v
     p_lora = cfg.n_layers * sum(cfg.lora_rank * sum(cfg.target_dims(t)) for t in cfg.lora_targets)
     return 4 * p_base + 6 * p_lora + 6 * cfg.n_layers * seq * qd

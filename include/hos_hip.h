@@ -95,6 +95,11 @@ int hos_hip_time_qgemm(hos_ctx* ctx, int which, uint64_t key, const float* in_de
  * Q6_K :426-495), run on the device; byte-identical to the reference encoders.
  * x: n floats (host), out: bytes_for(type, n) bytes (host). */
 int hos_hip_quantize(hos_ctx* ctx, const float* x, size_t n, uint32_t ggml_type, uint8_t* out);
+/* hos_hip_quantize on device buffers (x_dev f32 [n] -> out_dev, hos_hip_bytes_for(type, n) bytes). */
+int hos_hip_quantize_dev(hos_ctx* ctx, const float* x_dev, size_t n, uint32_t ggml_type, uint8_t* out_dev);
+/* Synthetic data: n samples of N(0, stddev^2) into out_dev from a counter-based hash of (seed, index);
+ * no counterpart in the reference (its Tensor::randn is a host xorshift). */
+int hos_hip_randn_dev(hos_ctx* ctx, float* out_dev, size_t n, uint64_t seed, float stddev);
 /* Precision of this context's qGEMMs: 1 = single fp16 pass (both operands rounded to 11 bits),
  * 2 = activation carried as fp16 hi + lo (2 MFMA passes), 3 = weight split too (3 passes),
  * 4 = weight carried as fp16 hi + lo, activation rounded once (2 passes). Default 1.
@@ -174,6 +179,13 @@ typedef struct {
   int max_batch, max_seq; /* sizes the device-resident activation arena */
   int gemm_passes;        /* qGEMM precision mode for every GEMM, as hos_hip_set_gemm_passes; 0 = default
                            * policy: layer GEMMs 3, head forward 1, head dX 4 */
+  /* Mixture-of-experts FFN (src/model.rs:642-643; OLMoE): n_experts stacked SwiGLU experts
+   * (blk.N.ffn_{gate,up,down}_exps.weight) behind an f32 router (blk.N.ffn_gate_inp.weight), top
+   * n_experts_used by softmax probability, raw probabilities as weights (src/forward.rs:542-572).
+   * 0 = dense FFN. LoRA targets gate/up/down are not allowed with experts. */
+  int n_experts, n_experts_used;
+  /* RMSNorm of the full q / k projections before RoPE (blk.N.attn_{q,k}_norm.weight, src/forward.rs:487-493) */
+  int qk_norm;
 } hos_peft_cfg;
 
 typedef struct hos_peft hos_peft;
@@ -185,7 +197,9 @@ const char* hos_peft_last_error(const hos_peft* p);
 /* One GGUF tensor by its GGUF name (src/model.rs:713-921): token_embd.weight, output.weight
  * (absent = tied to token_embd), output_norm.weight, blk.N.{attn_norm, attn_q, attn_k, attn_v,
  * attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight, blk.N.attn_{q,k,v}.bias.
- * Norm weights and biases: F32. Linear weights: Q8_0, Q4_K or Q6_K. */
+ * Norm weights and biases: F32. Linear weights: Q8_0, Q4_K or Q6_K. With n_experts > 0 the FFN tensors are
+ * blk.N.ffn_gate_inp.weight (F32 [E, dim]) and blk.N.ffn_{gate,up,down}_exps.weight ([E·ffn, dim],
+ * [E·ffn, dim], [E·dim, ffn]); with qk_norm, blk.N.attn_q_norm.weight / attn_k_norm.weight (F32). */
 int hos_peft_set_tensor(hos_peft* p, const char* name, const uint8_t* bytes, size_t nbytes, uint32_t ggml_type,
                         size_t rows, size_t cols);
 /* Model::load (src/model.rs:713-921) over the GGUF reader (src/gguf.rs:225-286): parses the file at path,

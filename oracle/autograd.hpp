@@ -380,6 +380,66 @@ inline Tensor softmax_rows(const Tensor& A) {
   });
 }
 
+// Rows of X in the order `rows` gives (a row may repeat); backward scatter-adds into the source rows.
+// Used by the mixture-of-experts FFN to run each expert only on the tokens routed to it.
+inline Tensor gather_rows(const Tensor& X, const std::vector<size_t>& rows) {
+  size_t d = X->shape[1], n = rows.size();
+  std::vector<float> out(n * d);
+  for (size_t i = 0; i < n; i++) std::memcpy(&out[i * d], &X->data[rows[i] * d], d * sizeof(float));
+  return build(std::move(out), {n, d}, {X}, [rows, d](const std::vector<float>& g, const std::vector<Tensor>& par) {
+    std::vector<float> gx(par[0]->data.size(), 0.0f);
+    for (size_t i = 0; i < rows.size(); i++)
+      for (size_t j = 0; j < d; j++) gx[rows[i] * d + j] += g[i * d + j];
+    par[0]->add_grad(gx);
+  });
+}
+
+// Mixture-of-experts combine, src/forward.rs:542-572: for each token t, over its selected experts in
+// selection order (descending probability), ffn[t] += p[t, e]·y_e[row of t]; the probabilities are the raw
+// softmax values (no renormalisation, OLMoE's norm_topk_prob = false). ys[e] holds expert e's outputs for
+// the tokens routed to it (null when none); sel[t][s] = (expert, row in ys[e]). Backward: dy_e[row] =
+// p[t, e]·g[t]; dp[t, e] = y_e[row]·g[t] for the selected experts (0 for the others).
+inline Tensor moe_mix(const std::vector<Tensor>& ys, const Tensor& P,
+                      const std::vector<std::vector<std::pair<size_t, size_t>>>& sel, size_t d) {
+  size_t T = sel.size(), E = P->shape[1];
+  std::vector<float> out(T * d, 0.0f);
+  for (size_t t = 0; t < T; t++)
+    for (auto [e, row] : sel[t]) {
+      const float w = P->data[t * E + e];
+      const float* y = &ys[e]->data[row * d];
+      for (size_t j = 0; j < d; j++) out[t * d + j] += w * y[j];
+    }
+  std::vector<Tensor> parents{P};
+  std::vector<int> slot(E, -1);
+  for (size_t e = 0; e < E; e++)
+    if (ys[e]) {
+      slot[e] = (int)parents.size();
+      parents.push_back(ys[e]);
+    }
+  return build(std::move(out), {T, d}, parents,
+               [sel, slot, T, E, d](const std::vector<float>& g, const std::vector<Tensor>& par) {
+                 const Tensor& Pt = par[0];
+                 std::vector<float> gp(T * E, 0.0f);
+                 std::vector<std::vector<float>> gy(par.size());
+                 for (size_t i = 1; i < par.size(); i++) gy[i].assign(par[i]->data.size(), 0.0f);
+                 for (size_t t = 0; t < T; t++)
+                   for (auto [e, row] : sel[t]) {
+                     const int k = slot[e];
+                     const float w = Pt->data[t * E + e];
+                     const float* y = &par[k]->data[row * d];
+                     float dp = 0.0f;
+                     for (size_t j = 0; j < d; j++) {
+                       gy[k][row * d + j] += w * g[t * d + j];
+                       dp += y[j] * g[t * d + j];
+                     }
+                     gp[t * E + e] = dp;
+                   }
+                 Pt->add_grad(gp);
+                 for (size_t i = 1; i < par.size(); i++)
+                   if (par[i]->requires_grad) par[i]->add_grad(gy[i]);
+               });
+}
+
 // src/tensor.rs:2500-2544: y = x·inv·w, inv = 1/sqrt(mean(x²)+eps).
 inline Tensor rmsnorm_eps(const Tensor& X, const Tensor& W, float eps) {
   size_t r = X->shape[0], d = X->shape[1];

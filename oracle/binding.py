@@ -28,6 +28,7 @@ class OrcCfg(ctypes.Structure):
         ("vocab", ctypes.c_int), ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float),
         ("rope_neox", ctypes.c_int), ("attn_bias", ctypes.c_int), ("lora_rank", ctypes.c_int),
         ("lora_alpha", ctypes.c_float), ("lora_targets", ctypes.c_uint32),
+        ("n_experts", ctypes.c_int), ("n_experts_used", ctypes.c_int), ("qk_norm", ctypes.c_int),
     ]
 
 
@@ -233,7 +234,8 @@ class OracleModel:
         self.cfg = cfg
         c = OrcCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
                    cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank,
-                   cfg.lora_alpha, cfg.lora_targets)
+                   cfg.lora_alpha, cfg.lora_targets, int(getattr(cfg, "n_experts", 0)),
+                   int(getattr(cfg, "n_experts_used", 0)), int(getattr(cfg, "qk_norm", 0)))
         self._c = c
         self.h = lib().orc_model_create(ctypes.byref(c))
 

@@ -53,4 +53,7 @@ typedef struct {
   int lora_rank;
   float lora_alpha;
   uint32_t lora_targets;
+  // Mixture-of-experts FFN (src/model.rs:642-643, 792-795; 0 = dense) and OLMoE's QK-norm
+  // (src/model.rs:698-699, 872-873).
+  int n_experts, n_experts_used, qk_norm;
 } orc_cfg;

@@ -12,6 +12,7 @@
 //     targets = q|v reproduces src/peft.rs:508-512 exactly.
 //   * LoRA A/B supplied by the caller (the reference draws A with Tensor::randn,
 //     src/tensor.rs:241-256, and B = 0; randn_uniform restates that draw).
+#include <algorithm>
 #include <map>
 #include <string>
 
@@ -24,8 +25,22 @@ struct Lora {
   Tensor A, B;  // A [in, r], B [r, out]
 };
 
+// Experts of one MoE projection, kept in their GGUF bytes and dequantized per forward (QExperts,
+// src/model.rs:659-671): expert e is the e-th [rows, cols] block.
+struct Experts {
+  std::vector<uint8_t> bytes;
+  uint32_t type = 0;
+  size_t rows = 0, cols = 0, expert_bytes = 0;
+  explicit operator bool() const { return !bytes.empty(); }
+  // expert e as a frozen [cols, rows] constant (t_const of its [rows, cols] matrix)
+  Tensor expert(size_t e) const;
+};
+
 struct BaseLayer {
   Tensor attn_norm, wq, wk, wv, wo, bq, bk, bv, ffn_norm, w_gate, w_up, w_down;
+  Tensor q_norm, k_norm;  // OLMoE QK-norm weights (absent for other models)
+  Tensor router;          // MoE router as [dim, n_experts] (ffn_gate_inp.weight [n_experts, dim])
+  Experts gate_x, up_x, down_x;
   Lora lora[7];  // q k v o gate up down
 };
 
@@ -88,9 +103,37 @@ static Tensor t_const(const std::vector<float>& d, size_t out, size_t inn) {
   return constant(std::move(t), {inn, out});
 }
 
+Tensor Experts::expert(size_t e) const {
+  std::vector<float> f(rows * cols);
+  dequant_into(bytes.data() + e * expert_bytes, type, rows * cols, f.data());
+  return t_const(f, rows, cols);
+}
+
 // Tensor names follow GGUF (src/model.rs:760-880). Bytes are dequantized with the
 // restated dequant_into, as Weight::to_f32 does (src/model.rs:251-273).
 int model_set_tensor(Model* m, const std::string& name, const uint8_t* bytes, uint32_t type, size_t rows, size_t cols) {
+  {
+    // MoE expert stacks stay quantized (src/model.rs:815-833): rows = n_experts · per-expert rows.
+    const char* stacks[3] = {"ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight"};
+    for (int k = 0; k < 3; k++) {
+      const std::string sfx = std::string(".") + stacks[k];
+      if (name.size() > sfx.size() && name.compare(name.size() - sfx.size(), sfx.size(), sfx) == 0) {
+        const orc_cfg& c = m->c;
+        size_t dot = name.find('.', 4);
+        int li = std::stoi(name.substr(4, dot - 4));
+        if (li < 0 || li >= c.n_layers || c.n_experts <= 0 || rows % (size_t)c.n_experts) return ORC_E_INVALID;
+        BaseLayer& l = m->layers[li];
+        Experts& x = k == 0 ? l.gate_x : (k == 1 ? l.up_x : l.down_x);
+        x.type = type;
+        x.rows = rows / c.n_experts;
+        x.cols = cols;
+        x.expert_bytes = bytes_for(type, x.rows * cols);
+        if (!x.expert_bytes) return ORC_E_UNSUPPORTED_QUANT;
+        x.bytes.assign(bytes, bytes + x.expert_bytes * c.n_experts);
+        return 0;
+      }
+    }
+  }
   std::vector<float> f(rows * cols);
   int rc = dequant_into(bytes, type, rows * cols, f.data());
   if (rc) return rc;
@@ -120,6 +163,9 @@ int model_set_tensor(Model* m, const std::string& name, const uint8_t* bytes, ui
   else if (leaf == "attn_q.bias") l.bq = constant(f, {rows * cols});
   else if (leaf == "attn_k.bias") l.bk = constant(f, {rows * cols});
   else if (leaf == "attn_v.bias") l.bv = constant(f, {rows * cols});
+  else if (leaf == "attn_q_norm.weight") l.q_norm = constant(f, {rows * cols});
+  else if (leaf == "attn_k_norm.weight") l.k_norm = constant(f, {rows * cols});
+  else if (leaf == "ffn_gate_inp.weight") l.router = t_const(f, rows, cols);
   else return ORC_E_INVALID;
   return 0;
 }
@@ -127,6 +173,38 @@ int model_set_tensor(Model* m, const std::string& name, const uint8_t* bytes, ui
 static Tensor lora_apply(const Model* m, const Lora& lo, const Tensor& y, const Tensor& x) {
   if (!lo.A) return y;
   return add(y, scale(matmul(matmul(x, lo.A), lo.B), m->lora_scale()));
+}
+
+// Mixture-of-experts FFN, src/forward.rs:542-572 over a batch of rows: router logits, softmax over all
+// experts, the top n_experts_used by probability (a stable descending sort, ties in expert order), and
+// Σ p·expert_e(xn) over the selected experts with the raw probabilities; each expert is a SwiGLU FFN
+// (silu(x·gate_e)·(x·up_e))·down_e on its dequantized weights, run on the rows routed to it. The
+// routing is piecewise constant: gradients flow through the probabilities and the experts only.
+static Tensor moe_ffn(const Model* m, const BaseLayer& bl, const Tensor& xn) {
+  const orc_cfg& c = m->c;
+  const size_t T = xn->shape[0], d = xn->shape[1], E = c.n_experts, K = c.n_experts_used;
+  Tensor p = softmax_rows(matmul(xn, bl.router));
+  std::vector<std::vector<size_t>> rows(E);
+  std::vector<std::vector<std::pair<size_t, size_t>>> sel(T);
+  for (size_t t = 0; t < T; t++) {
+    std::vector<size_t> idx(E);
+    for (size_t e = 0; e < E; e++) idx[e] = e;
+    const float* pr = &p->data[t * E];
+    std::stable_sort(idx.begin(), idx.end(), [pr](size_t a, size_t b) { return pr[a] > pr[b]; });
+    for (size_t s = 0; s < K; s++) {
+      const size_t e = idx[s];
+      sel[t].push_back({e, rows[e].size()});
+      rows[e].push_back(t);
+    }
+  }
+  std::vector<Tensor> ys(E);
+  for (size_t e = 0; e < E; e++) {
+    if (rows[e].empty()) continue;
+    Tensor xe = gather_rows(xn, rows[e]);
+    Tensor h = mul(silu(matmul(xe, bl.gate_x.expert(e))), matmul(xe, bl.up_x.expert(e)));
+    ys[e] = matmul(h, bl.down_x.expert(e));
+  }
+  return moe_mix(ys, p, sel, d);
 }
 
 // PeftModel::forward (LoRA path), src/peft.rs:474-604.
@@ -155,6 +233,12 @@ Tensor model_forward(const Model* m, const std::vector<size_t>& ids) {
     if (bl.bq) q = add(q, bl.bq);
     if (bl.bk) k = add(k, bl.bk);
     if (bl.bv) v = add(v, bl.bv);
+    // OLMoE QK-norm: RMSNorm over the full q / k projections before RoPE (src/forward.rs:487-493), as the
+    // autograd rmsnorm_eps
+    if (c.qk_norm) {
+      q = rmsnorm_eps(q, bl.q_norm, c.rms_eps);
+      k = rmsnorm_eps(k, bl.k_norm, c.rms_eps);
+    }
     q = rope(q, nh, hd, c.rope_base, c.rope_neox != 0, pos);
     k = rope(k, nkv, hd, c.rope_base, c.rope_neox != 0, pos);
     Tensor qh = reshape(transpose12_4d(reshape(q, {1, t, nh, hd})), {nh, t, hd});
@@ -168,6 +252,10 @@ Tensor model_forward(const Model* m, const std::vector<size_t>& ids) {
     Tensor o = lora_apply(m, bl.lora[3], matmul(ctx, bl.wo), ctx);
     x = add(x, o);
     Tensor xn2 = rmsnorm_eps(x, bl.ffn_norm, c.rms_eps);
+    if (c.n_experts > 0) {
+      x = add(x, moe_ffn(m, bl, xn2));
+      continue;
+    }
     Tensor gt = lora_apply(m, bl.lora[4], matmul(xn2, bl.w_gate), xn2);
     Tensor up = lora_apply(m, bl.lora[5], matmul(xn2, bl.w_up), xn2);
     Tensor hmid = mul(silu(gt), up);

@@ -129,9 +129,6 @@ def test_errors(tmp_path):
     assert rc == HOS_E_MISSING_TENSOR and "token_embd" in err
     rc, _, err = _config(_write(tmp_path, gguf_bytes(model_meta(cfg, "mamba"), _tensors(cfg)), "arch.gguf"))
     assert rc == HOS_E_UNSUPPORTED_ARCH and "mamba" in err
-    t = _tensors(cfg)
-    t["blk.0.ffn_gate_exps.weight"] = (np.zeros(34, np.uint8), 8, [32, 1])
-    assert _config(_write(tmp_path, gguf_bytes(model_meta(cfg, "qwen2"), t), "moe.gguf"))[0] == HOS_E_UNSUPPORTED_ARCH
     bad = gguf_bytes({"general.architecture": (STR, "qwen2"), "x": (U32, 1)}, {})
     i = bad.index(b"x") + 1
     bad = bad[:i] + struct.pack("<I", 99) + bad[i + 4:]
@@ -180,3 +177,19 @@ def test_fuzz_never_crashes(tmp_path):
             b[r.next() % len(b)] ^= r.byte()
         p.write_bytes(bytes(b))
         _config(p)
+
+
+def test_olmoe_mapping(tmp_path):
+    """OLMoE (src/model.rs:792-795, 872-873): expert_count / expert_used_count with the stacked expert
+    tensors present make a mixture-of-experts FFN; attn_q_norm turns on QK-norm; NEOX RoPE."""
+    cfg = Cfg()
+    meta = model_meta(cfg, "olmoe", extra={"olmoe.expert_count": (U32, 8), "olmoe.expert_used_count": (U32, 2)})
+    t = _tensors(cfg, bias=False)
+    t["blk.0.ffn_gate_exps.weight"] = (np.zeros(8 * 256 * 128 // 32 * 34, np.uint8), 8, [128, 256, 8])
+    t["blk.0.attn_q_norm.weight"] = (np.ones(128, np.float32), 0, [128])
+    rc, c, err = _config(_write(tmp_path, gguf_bytes(meta, t)))
+    assert rc == 0, err
+    assert (c.n_experts, c.n_experts_used, c.qk_norm, c.rope_neox) == (8, 2, 1, 1)
+    del t["blk.0.ffn_gate_exps.weight"]  # expert_count without expert tensors: dense (src/model.rs:795)
+    rc, c, err = _config(_write(tmp_path, gguf_bytes(meta, t), "dense.gguf"))
+    assert rc == 0 and c.n_experts == 0

@@ -89,10 +89,11 @@ def test_swiglu_fwd_bwd(gpu):
         a.free()
 
 
-@pytest.mark.parametrize("B,T,nh,nkv", [(1, 128, 9, 3), (2, 77, 14, 2), (1, 64, 4, 4)])
-def test_attention_fwd_bwd(gpu, B, T, nh, nkv):
-    hd = 64
-    print(f"attention B={B} T={T} heads={nh}/{nkv}", flush=True)
+@pytest.mark.parametrize("B,T,nh,nkv,hd", [(1, 128, 9, 3, 64), (2, 77, 14, 2, 64), (1, 64, 4, 4, 64),
+                                           # OLMoE's head dim (16 heads of 128, no GQA) and a GQA case
+                                           (2, 70, 4, 4, 128), (1, 97, 6, 2, 128)])
+def test_attention_fwd_bwd(gpu, B, T, nh, nkv, hd):
+    print(f"attention B={B} T={T} heads={nh}/{nkv} hd={hd}", flush=True)
     rng = np.random.default_rng(B * T + nh)
     q = rng.standard_normal((B, T, nh * hd)).astype(np.float32)
     k = rng.standard_normal((B, T, nkv * hd)).astype(np.float32)

@@ -34,7 +34,7 @@ def gpu():
 def oracle_model(cfg, tensors, lora):
     oc = types.SimpleNamespace(**{k: getattr(cfg, k) for k in (
         "n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "rms_eps", "rope_base",
-        "rope_neox", "attn_bias", "lora_rank", "lora_alpha")})
+        "rope_neox", "attn_bias", "lora_rank", "lora_alpha", "n_experts", "n_experts_used", "qk_norm")})
     oc.lora_targets = cfg.target_mask
     m = o.OracleModel(oc)
     for name, (raw, t, rows, cols) in tensors.items():
