@@ -55,10 +55,10 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_per_dispatch": COPY_BYTES, "dispatches": 3}), flush=True)
 
 
-def traffic_per_launch(kernel_class):
+def traffic_per_launch(kernel_class, cfg):
     """HBM bytes per launch of `kernel_class` measured by rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated
-    against a plain copy), read from the committed profile summary when one exists; else None."""
-    path = os.path.join(ROOT, "profiles", f"{kernel_class}_traffic_qwen2.5-0.5b_b4x512.md")
+    against a plain copy), read from the committed profile summary of this workload when one exists."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_class}_traffic_{cfg.name}_b{cfg.batch}x{cfg.seq}.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -89,6 +89,19 @@ def dx_gemm_probe(gpu):
     gpu.free(dout)
     gpu.evict(0xD0)
     return out
+
+
+QNAME = {8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}
+
+
+def workload(cfg):
+    base = QNAME[cfg.quant] + " base"
+    if cfg.quant != 8 and cfg.dim % 256:
+        base += f" (Q8_0 for {cfg.dim}-wide rows)"
+    if cfg.n_experts:
+        base += f"; {cfg.n_experts} experts top-{cfg.n_experts_used}, QK-norm" if cfg.qk_norm else \
+            f"; {cfg.n_experts} experts top-{cfg.n_experts_used}"
+    return f"{cfg.name} LoRA r{cfg.lora_rank} on {','.join(cfg.lora_targets)}; {base}; AdamW"
 
 
 def cpu_baseline(cfg, tensors, seq):
@@ -149,7 +162,7 @@ def main():
     gpu.synchronize()
 
     classes = ["qgemm_fwd", "qgemm_dx", "lora_down", "lora_db", "lora_du", "lora_da", "attn_fwd", "attn_bwd",
-               "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert"]
+               "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert", "moe_route", "moe_combine"]
     # Breakdown pass (every kernel class timed with HIP events; not the timed region): finds the
     # dominant class and gives the per-class split.
     pm.profile(True)
@@ -183,12 +196,12 @@ def main():
     if ds["flops"] > 0:
         achieved = ds["flops"] / max(ds["launches"], 1) / avg_launch_s / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": traffic_per_launch(dom), "kernel": dom,
+                "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": traffic_per_launch(dom, cfg), "kernel": dom,
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"]}
     else:
         achieved = ds["bytes"] / max(ds["launches"], 1) / avg_launch_s / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_per_launch(dom), "kernel": dom,
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_per_launch(dom, cfg), "kernel": dom,
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"]}
 
     dx = dx_gemm_probe(gpu)
@@ -199,8 +212,7 @@ def main():
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16 MFMA (hi/lo split: 3 passes per layer GEMM, 1-2 on the head) + f32", "data": "synthetic",
-        "config": {"workload": f"{cfg.name} LoRA r{cfg.lora_rank} on q,k,v,o,gate,up,down; Q4_K base "
-                               "(Q8_0 for 896-wide rows); AdamW", "global_batch": B, "seq_len": T,
+        "config": {"workload": workload(cfg), "global_batch": B, "seq_len": T,
                    "parallelism": "dp1", "precision": "layer GEMMs 3-pass, head fwd 1-pass, head dX weight-split"},
         "roofline": roof,
         "mfma_roofline_frac_step": round(value * f_tok / 1e12 / PEAK_MFMA_TFLOPS, 4),
