@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--config", default="qwen2.5-0.5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline sample")
     ap.add_argument("--cpu-seq", type=int, default=256, help="tokens in the CPU baseline sample")
+    ap.add_argument("--finetune", action="store_true",
+                    help="time the full-parameter finetune step (FtModel: every weight trainable in f32) instead")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -129,10 +131,51 @@ def cpu_baseline(cfg, tensors, seq):
             "sample": f"1 sequence x {seq} tokens (fwd+bwd+AdamW), {dt:.1f} s"}
 
 
+def finetune_bench(args):
+    """Full-parameter finetune (src/finetune.rs FtModel) tokens/s on the same synthetic workload: every
+    weight dequantized once to trainable f32, f32 weight GEMMs, dW for every matrix, AdamW over all."""
+    from hos_amd import Gpu, synth
+    from hos_amd.finetune import FtModel
+    cfg = synth.CONFIGS[args.config]
+    gpu = Gpu(0)
+    ft = FtModel(gpu, cfg)
+    ft.load(synth.build_tensors(gpu, cfg, seed=1234))
+    B, T = cfg.batch, cfg.seq
+    ids, tg = synth.tokens(cfg, B, T, seed=8)
+    ids_dev, tg_dev, loss_dev = gpu.alloc(ids.nbytes), gpu.alloc(tg.nbytes), gpu.alloc(4)
+    gpu.h2d(ids_dev, ids)
+    gpu.h2d(tg_dev, tg)
+    for _ in range(args.warmup):
+        ft.step_dev(ids_dev, tg_dev, B, T, 1e-5, 0.0, loss_dev)
+    gpu.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ft.step_dev(ids_dev, tg_dev, B, T, 1e-5, 0.0, loss_dev)
+    gpu.synchronize()
+    dt = time.perf_counter() - t0
+    value = B * T * args.steps / dt
+    # every weight trains: 6 flops per parameter per token plus attention
+    d, qd, kvd, f, v = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.ffn_dim, cfg.vocab
+    p_mat = cfg.n_layers * (d * qd + 2 * d * kvd + qd * d + 3 * d * f) + d * v
+    f_tok = 6 * p_mat + 6 * cfg.n_layers * T * qd
+    line = {"metric": "full-finetune tokens/sec (fwd+bwd+AdamW, every weight trainable f32)",
+            "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(dt / args.steps * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32 (fp32 MFMA weight GEMMs)", "data": "synthetic",
+            "config": {"workload": f"{cfg.name} full finetune", "global_batch": B, "seq_len": T,
+                       "parallelism": "dp1"},
+            "fp32_mfma_frac_step": round(value * f_tok / 1e12 / 157.3, 4),
+            "loss": round(float(gpu.d2h(loss_dev, (1,), np.float32)[0]), 5)}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.finetune:
+        finetune_bench(args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "

@@ -51,6 +51,14 @@ SIGNATURES = {
     "hos_hip_d2h": (i32, [vp, vp, vp, sz]),
     "hos_peft_create": (i32, [vp, ctypes.POINTER(PeftCfg), ctypes.POINTER(vp)]),
     "hos_peft_destroy": (None, [vp]),
+    "hos_ft_create": (i32, [vp, ctypes.POINTER(PeftCfg), ctypes.POINTER(vp)]),
+    "hos_ft_destroy": (None, [vp]),
+    "hos_ft_last_error": (ctypes.c_char_p, [vp]),
+    "hos_ft_set_tensor": (i32, [vp, ctypes.c_char_p, vp, sz, u32, sz, sz]),
+    "hos_ft_get": (i32, [vp, ctypes.c_char_p, vp, vp]),
+    "hos_ft_loss_grad": (i32, [vp, vp, vp, i32, i32, ctypes.POINTER(ctypes.c_float)]),
+    "hos_ft_adamw": (i32, [vp, ctypes.c_float, ctypes.c_float]),
+    "hos_ft_step_dev": (i32, [vp, vp, vp, i32, i32, ctypes.c_float, ctypes.c_float, vp]),
     "hos_peft_save_hos": (i32, [vp, ctypes.c_char_p, ctypes.c_char_p, i32]),
     "hos_peft_load_hos": (i32, [vp, ctypes.c_char_p, i32]),
     "hos_peft_adapter_id": (i32, [vp, ctypes.c_char_p]),

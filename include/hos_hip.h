@@ -255,6 +255,28 @@ int hos_peft_base_id(hos_peft* p, char* out17);
 /* read_card (src/format.rs:270-285): the card JSON of a .hos file into out (NUL-terminated, truncated to
  * len); *needed (may be NULL) = its length + 1. On error out receives the message. No device work. */
 int hos_format_card(const char* path, char* out, size_t len, size_t* needed);
+/* ---- full-parameter finetune (FtModel, src/finetune.rs) ----
+ * Every weight a trainable f32 parameter on the device: quantized tensors are dequantized once at load
+ * (Weight::to_f32); a tied head becomes an untied copy of the embedding (src/finetune.rs:101-107). Dense
+ * Llama family only (n_experts = 0, qk_norm = 0; the LoRA fields of the config are ignored). Weight GEMMs
+ * in f32 (fp32 MFMA), weight gradients dW = dYᵀ·X (the matmul_atb of src/metal_be.rs:1212-1234). */
+typedef struct hos_ft hos_ft;
+int hos_ft_create(hos_ctx* ctx, const hos_peft_cfg* cfg, hos_ft** out);
+void hos_ft_destroy(hos_ft* p);
+const char* hos_ft_last_error(const hos_ft* p);
+/* Same GGUF names as hos_peft_set_tensor; F32 or Q8_0 / Q4_K / Q6_K. */
+int hos_ft_set_tensor(hos_ft* p, const char* name, const uint8_t* bytes, size_t nbytes, uint32_t ggml_type,
+                      size_t rows, size_t cols);
+/* Current value and gradient of one parameter by GGUF name, GGUF layout ([out, in] row-major); either
+ * pointer may be NULL. */
+int hos_ft_get(hos_ft* p, const char* name, float* value, float* grad);
+/* zero_grad + B sequences, loss·(1/B) each (the accumulation of src/main.rs:2834-2855). */
+int hos_ft_loss_grad(hos_ft* p, const int32_t* ids, const int32_t* targets, int B, int T, float* loss);
+/* AdamW::step over FtModel::params (β 0.9/0.95, eps 1e-8, decay on 2-D tensors, src/main.rs:2803-2804). */
+int hos_ft_adamw(hos_ft* p, float lr, float wd);
+/* loss_grad + adamw on device-resident ids/targets; enqueues only. */
+int hos_ft_step_dev(hos_ft* p, const int32_t* ids_dev, const int32_t* targets_dev, int B, int T, float lr, float wd,
+                    float* loss_dev);
 /* Logits [T, vocab] of one sequence (PeftModel::logits, src/peft.rs:462-464). */
 int hos_peft_logits(hos_peft* p, const int32_t* ids, int T, float* out);
 /* Per-kernel-class timing with HIP events around every launch (off by default). */

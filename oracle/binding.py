@@ -77,6 +77,9 @@ def lib():
         L.orc_model_loss_grad.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int]
         L.orc_model_adamw.argtypes = [vp, ctypes.c_float, ctypes.c_float]
         L.orc_model_logits.argtypes = [vp, vp, ctypes.c_int, vp]
+        L.orc_ft_create.restype = vp
+        L.orc_ft_create.argtypes = [ctypes.POINTER(OrcCfg)]
+        L.orc_ft_get.argtypes = [vp, ctypes.c_char_p, vp, vp]
         _lib = L
     return _lib
 
@@ -282,3 +285,23 @@ class OracleModel:
         out = np.empty((ids.size, self.cfg.vocab), np.float32)
         lib().orc_model_logits(self.h, _p(ids), ids.size, _p(out))
         return out
+
+
+class OracleFt(OracleModel):
+    """FtModel (src/finetune.rs) restatement: every weight trainable; same set_tensor / loss_grad / adamw."""
+
+    def __init__(self, cfg):
+        c = OrcCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
+                   cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank or 1,
+                   cfg.lora_alpha, 0, 0, 0, 0)
+        self.cfg = cfg
+        self._c = c
+        self.h = lib().orc_ft_create(ctypes.byref(c))
+
+    def get(self, name, shape):
+        """(value, gradient) of a parameter by GGUF name, GGUF layout."""
+        v = np.empty(shape, np.float32)
+        g = np.empty(shape, np.float32)
+        if lib().orc_ft_get(self.h, name.encode(), _p(v), _p(g)):
+            raise ValueError(name)
+        return v, g

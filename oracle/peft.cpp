@@ -49,9 +49,21 @@ struct Model {
   Tensor tok_embd, out_norm, out;
   std::vector<BaseLayer> layers;
   std::unique_ptr<AdamW> opt;
+  // Full-parameter finetune (FtModel, src/finetune.rs:62-108): every weight a trainable f32 parameter,
+  // the head an untied copy when the file ties it; no LoRA.
+  bool full = false;
   float lora_scale() const { return c.lora_alpha / (float)c.lora_rank; }
 
   std::vector<Tensor> params() const {
+    if (full) {  // FtModel::params order, src/finetune.rs:181-200
+      std::vector<Tensor> p{tok_embd, out_norm, out};
+      for (auto& l : layers) {
+        for (const Tensor& t : {l.attn_norm, l.wq, l.wk, l.wv, l.wo, l.ffn_norm, l.w_gate, l.w_up, l.w_down}) p.push_back(t);
+        for (const Tensor& b : {l.bq, l.bk, l.bv})
+          if (b) p.push_back(b);
+      }
+      return p;
+    }
     // LoRA factors per layer, in target order (src/peft.rs:295-302 lists aq,bq,av,bv).
     std::vector<Tensor> p;
     for (auto& l : layers)
@@ -95,12 +107,13 @@ Model* model_create(const orc_cfg* cfg) {
   return m;
 }
 
-// t_const, src/peft.rs:24-33: W [out,in] row-major (GGUF) -> constant [in,out].
-static Tensor t_const(const std::vector<float>& d, size_t out, size_t inn) {
+// t_const, src/peft.rs:24-33: W [out,in] row-major (GGUF) -> constant [in,out]; transposed_param
+// (src/finetune.rs:26-35) is the same transpose as a trainable parameter.
+static Tensor t_const(const std::vector<float>& d, size_t out, size_t inn, bool trainable = false) {
   std::vector<float> t(out * inn);
   for (size_t o = 0; o < out; o++)
     for (size_t i = 0; i < inn; i++) t[i * out + o] = d[o * inn + i];
-  return constant(std::move(t), {inn, out});
+  return tnew(std::move(t), {inn, out}, trainable);
 }
 
 Tensor Experts::expert(size_t e) const {
@@ -138,31 +151,33 @@ int model_set_tensor(Model* m, const std::string& name, const uint8_t* bytes, ui
   int rc = dequant_into(bytes, type, rows * cols, f.data());
   if (rc) return rc;
   const orc_cfg& c = m->c;
+  const bool tr = m->full;
+  auto vec1 = [&](std::vector<float> v) { return tnew(std::move(v), {rows * cols}, tr); };
   if (name == "token_embd.weight") {
-    m->tok_embd = constant(f, {rows, cols});
-    if (!m->out) m->out = t_const(f, rows, cols);  // tied head until output.weight arrives
+    m->tok_embd = tnew(f, {rows, cols}, tr);
+    if (!m->out) m->out = t_const(f, rows, cols, tr);  // tied head until output.weight arrives
     return 0;
   }
-  if (name == "output.weight") { m->out = t_const(f, rows, cols); return 0; }
-  if (name == "output_norm.weight") { m->out_norm = constant(f, {rows * cols}); return 0; }
+  if (name == "output.weight") { m->out = t_const(f, rows, cols, tr); return 0; }
+  if (name == "output_norm.weight") { m->out_norm = vec1(f); return 0; }
   if (name.rfind("blk.", 0) != 0) return ORC_E_INVALID;
   size_t dot = name.find('.', 4);
   int li = std::stoi(name.substr(4, dot - 4));
   if (li < 0 || li >= c.n_layers) return ORC_E_INVALID;
   std::string leaf = name.substr(dot + 1);
   BaseLayer& l = m->layers[li];
-  if (leaf == "attn_norm.weight") l.attn_norm = constant(f, {rows * cols});
-  else if (leaf == "ffn_norm.weight") l.ffn_norm = constant(f, {rows * cols});
-  else if (leaf == "attn_q.weight") l.wq = t_const(f, rows, cols);
-  else if (leaf == "attn_k.weight") l.wk = t_const(f, rows, cols);
-  else if (leaf == "attn_v.weight") l.wv = t_const(f, rows, cols);
-  else if (leaf == "attn_output.weight") l.wo = t_const(f, rows, cols);
-  else if (leaf == "ffn_gate.weight") l.w_gate = t_const(f, rows, cols);
-  else if (leaf == "ffn_up.weight") l.w_up = t_const(f, rows, cols);
-  else if (leaf == "ffn_down.weight") l.w_down = t_const(f, rows, cols);
-  else if (leaf == "attn_q.bias") l.bq = constant(f, {rows * cols});
-  else if (leaf == "attn_k.bias") l.bk = constant(f, {rows * cols});
-  else if (leaf == "attn_v.bias") l.bv = constant(f, {rows * cols});
+  if (leaf == "attn_norm.weight") l.attn_norm = vec1(f);
+  else if (leaf == "ffn_norm.weight") l.ffn_norm = vec1(f);
+  else if (leaf == "attn_q.weight") l.wq = t_const(f, rows, cols, tr);
+  else if (leaf == "attn_k.weight") l.wk = t_const(f, rows, cols, tr);
+  else if (leaf == "attn_v.weight") l.wv = t_const(f, rows, cols, tr);
+  else if (leaf == "attn_output.weight") l.wo = t_const(f, rows, cols, tr);
+  else if (leaf == "ffn_gate.weight") l.w_gate = t_const(f, rows, cols, tr);
+  else if (leaf == "ffn_up.weight") l.w_up = t_const(f, rows, cols, tr);
+  else if (leaf == "ffn_down.weight") l.w_down = t_const(f, rows, cols, tr);
+  else if (leaf == "attn_q.bias") l.bq = vec1(f);
+  else if (leaf == "attn_k.bias") l.bk = vec1(f);
+  else if (leaf == "attn_v.bias") l.bv = vec1(f);
   else if (leaf == "attn_q_norm.weight") l.q_norm = constant(f, {rows * cols});
   else if (leaf == "attn_k_norm.weight") l.k_norm = constant(f, {rows * cols});
   else if (leaf == "ffn_gate_inp.weight") l.router = t_const(f, rows, cols);
@@ -300,6 +315,58 @@ void model_adamw(Model* m, float lr, float wd) {
 
 // ---- LoRA factor access for the extern "C" surface ----
 extern "C" {
+// Full-parameter finetune model (FtModel): set tensors, loss_grad and adamw as for the LoRA model.
+void* orc_ft_create(const orc_cfg* cfg) {
+  orc_cfg c = *cfg;
+  c.lora_targets = 0;
+  auto* m = orc::model_create(&c);
+  m->full = true;
+  return m;
+}
+// Value (and gradient) of one parameter by its GGUF tensor name, in the GGUF layout ([out, in] row-major
+// for matrices; the model keeps them transposed as FtModel does).
+int orc_ft_get(void* mh, const char* cname, float* value, float* grad) {
+  auto* m = (orc::Model*)mh;
+  std::string name(cname);
+  orc::Tensor t;
+  bool transposed = true;
+  if (name == "token_embd.weight") { t = m->tok_embd; transposed = false; }
+  else if (name == "output.weight") t = m->out;
+  else if (name == "output_norm.weight") { t = m->out_norm; transposed = false; }
+  else if (name.rfind("blk.", 0) == 0) {
+    size_t dot = name.find('.', 4);
+    int li = std::stoi(name.substr(4, dot - 4));
+    if (li < 0 || li >= m->c.n_layers) return ORC_E_INVALID;
+    auto& l = m->layers[li];
+    std::string leaf = name.substr(dot + 1);
+    if (leaf == "attn_norm.weight") { t = l.attn_norm; transposed = false; }
+    else if (leaf == "ffn_norm.weight") { t = l.ffn_norm; transposed = false; }
+    else if (leaf == "attn_q.bias") { t = l.bq; transposed = false; }
+    else if (leaf == "attn_k.bias") { t = l.bk; transposed = false; }
+    else if (leaf == "attn_v.bias") { t = l.bv; transposed = false; }
+    else if (leaf == "attn_q.weight") t = l.wq;
+    else if (leaf == "attn_k.weight") t = l.wk;
+    else if (leaf == "attn_v.weight") t = l.wv;
+    else if (leaf == "attn_output.weight") t = l.wo;
+    else if (leaf == "ffn_gate.weight") t = l.w_gate;
+    else if (leaf == "ffn_up.weight") t = l.w_up;
+    else if (leaf == "ffn_down.weight") t = l.w_down;
+  }
+  if (!t) return ORC_E_INVALID;
+  auto put = [&](const std::vector<float>& src, float* dst) {
+    if (!dst) return;
+    if (!transposed) {
+      std::memcpy(dst, src.data(), src.size() * 4);
+      return;
+    }
+    const size_t inn = t->shape[0], out = t->shape[1];
+    for (size_t o = 0; o < out; o++)
+      for (size_t i = 0; i < inn; i++) dst[o * inn + i] = src[i * out + o];
+  };
+  put(t->data, value);
+  put(t->grad, grad);
+  return 0;
+}
 void orc_model_destroy(void* mh) { delete (orc::Model*)mh; }
 int orc_model_set_lora(void* mh, int layer, int target, const float* A, const float* B) {
   auto* m = (orc::Model*)mh;

@@ -14,7 +14,7 @@ LIB = os.path.join(ROOT, "hos_amd", "libhos_hip.so")
 def declared():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(hos_(?:hip|peft|gguf|format)_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(hos_(?:hip|peft|gguf|format|ft)_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_boundary():
