@@ -18,6 +18,7 @@ class PeftCfg(ctypes.Structure):
         ("rope_neox", i32), ("attn_bias", i32), ("lora_rank", i32), ("lora_alpha", ctypes.c_float),
         ("lora_targets", u32), ("max_batch", i32), ("max_seq", i32), ("gemm_passes", i32),
         ("n_experts", i32), ("n_experts_used", i32), ("qk_norm", i32),
+        ("rga_genes", i32), ("rga_bottleneck", i32), ("rga_lambda", ctypes.c_float),
     ]
 
 
@@ -72,6 +73,8 @@ SIGNATURES = {
     "hos_peft_set_lora": (i32, [vp, i32, i32, vp, vp]),
     "hos_peft_get_lora": (i32, [vp, i32, i32, vp, vp]),
     "hos_peft_get_lora_grad": (i32, [vp, i32, i32, vp, vp]),
+    "hos_peft_set_adapter": (i32, [vp, ctypes.c_char_p, vp, ctypes.c_size_t]),
+    "hos_peft_get_adapter": (i32, [vp, ctypes.c_char_p, vp, vp, ctypes.c_size_t]),
     "hos_peft_loss_grad": (i32, [vp, vp, vp, i32, i32, ctypes.POINTER(ctypes.c_float)]),
     "hos_peft_adamw": (i32, [vp, ctypes.c_float, ctypes.c_float]),
     "hos_peft_step_dev": (i32, [vp, vp, vp, i32, i32, ctypes.c_float, ctypes.c_float, vp]),

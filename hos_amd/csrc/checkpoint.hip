@@ -52,6 +52,19 @@ struct Tensor {
 void adapter_tensors(hos_peft* p, const PeftShape& s, PeftBuf which, const char* prefix, std::vector<Tensor>& out,
                      bool flat) {
   int k = 0;
+  if (s.rga) {  // named tensors; the optimizer state follows the parameter order
+    for (auto& [name, shape] : peft_rga_tensors(p, flat)) {
+      Tensor t;
+      t.data.resize((size_t)shape[0] * shape[1]);
+      peft_rga_io(p, which, name, t.data.data(), t.data.size(), false);
+      t.nfloats = t.data.size();
+      t.role = flat ? ROLE_OPT_STATE : ROLE_WEIGHT;
+      t.name = flat ? std::string(prefix) + std::to_string(k++) : name;
+      t.shape = flat ? std::vector<uint32_t>{(uint32_t)t.nfloats} : shape;
+      out.push_back(std::move(t));
+    }
+    return;
+  }
   for (int l = 0; l < s.L; l++)
     for (int t = 0; t < 7; t++) {
       if (!((s.targets >> t) & 1u)) continue;
@@ -239,12 +252,13 @@ std::string default_card(const PeftShape& s, const std::string& id) {
   // Card::new + the adapter fields of save_adapter (src/format.rs:79-97, src/main.rs:2646-2676); keys in
   // serde's order, the arch object's keys sorted as serde_json's map keeps them.
   char buf[640];
+  const char* method = s.rga ? "rga" : "lora";
   std::snprintf(buf, sizeof(buf),
-                "{\"format\":\"hos\",\"spec\":1,\"name\":\"hos-peft-lora\",\"id\":\"%s\",\"mode\":\"adapter\","
-                "\"arch\":{\"block_count\":%d,\"method\":\"lora\",\"source_format\":\"hos-peft\"},"
+                "{\"format\":\"hos\",\"spec\":1,\"name\":\"hos-peft-%s\",\"id\":\"%s\",\"mode\":\"adapter\","
+                "\"arch\":{\"block_count\":%d,\"method\":\"%s\",\"source_format\":\"hos-peft\"},"
                 "\"provenance\":{\"created\":\"\",\"engine\":\"hos-peft\",\"dataset\":\"\",\"dataset_hash\":\"\"},"
                 "\"resume\":{\"seed\":0,\"step\":%llu,\"rng_state\":0},\"history\":[],\"lineage\":[]}",
-                id.c_str(), s.L, (unsigned long long)s.step);
+                method, id.c_str(), s.L, method, (unsigned long long)s.step);
   return buf;
 }
 
@@ -317,8 +331,39 @@ int hos_peft_load_hos(hos_peft* p, const char* path, int with_optimizer) {
       std::vector<float> a, b, ma, mb, va, vb;
     };
     std::vector<Pair> pairs;
+    // RGA: every adapter tensor by name (+ its moments by parameter index)
+    struct Named {
+      std::string name;
+      std::vector<float> v, m, vv;
+    };
+    std::vector<Named> rn;
+    if (s.rga) {
+      for (auto& [name, shape] : peft_rga_tensors(p, false)) {
+        Named q{name};
+        const Tensor& t = need(c, name);
+        need_shape(t, shape);
+        decode_f32(t, q.v);
+        rn.push_back(std::move(q));
+      }
+      if (with_optimizer) {
+        int kk = 0;
+        for (auto& [name, shape] : peft_rga_tensors(p, true)) {
+          Named* q = nullptr;
+          for (auto& x : rn)
+            if (x.name == name) q = &x;
+          const uint32_t n = shape[0] * shape[1];
+          const Tensor& tm = need(c, "opt.m." + std::to_string(kk));
+          const Tensor& tv = need(c, "opt.v." + std::to_string(kk));
+          need_shape(tm, {n});
+          need_shape(tv, {n});
+          decode_f32(tm, q->m);
+          decode_f32(tv, q->vv);
+          kk++;
+        }
+      }
+    }
     int k = 0;
-    for (int l = 0; l < s.L; l++)
+    for (int l = 0; l < (s.rga ? 0 : s.L); l++)
       for (int t = 0; t < 7; t++) {
         if (!((s.targets >> t) & 1u)) continue;
         Pair q{l, t};
@@ -357,6 +402,13 @@ int hos_peft_load_hos(hos_peft* p, const char* path, int with_optimizer) {
       }
       HOS_REQUIRE(step >= 0 && step <= 2147483647.0f && step == (float)(uint64_t)step, HOS_E_FORMAT,
                   "opt.step is not a step count");
+    }
+    for (Named& q : rn) {
+      peft_rga_io(p, PEFT_PARAM, q.name, q.v.data(), q.v.size(), true);
+      if (with_optimizer) {
+        peft_rga_io(p, PEFT_ADAM_M, q.name, q.m.data(), q.m.size(), true);
+        peft_rga_io(p, PEFT_ADAM_V, q.name, q.vv.data(), q.vv.size(), true);
+      }
     }
     for (Pair& q : pairs) {
       peft_factor_io(p, PEFT_PARAM, q.l, q.t, q.a.data(), q.b.data(), true);

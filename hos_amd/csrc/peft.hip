@@ -20,6 +20,7 @@
 #include "fused.hpp"
 #include "lora.hpp"
 #include "moe.hpp"
+#include "rga.hpp"
 
 using namespace hos;
 
@@ -41,6 +42,8 @@ struct LayerW {
 struct LayerAct {
   float *x, *xn1, *inv1, *qkv, *o, *lse, *x2, *xn2, *inv2, *gu, *h, *u;
   float *qk_pre = nullptr, *qk_inv = nullptr;  // QK-norm: pre-norm q|k [M][qd+kvd], 1/rms [2][M]
+  // RGA: residual before the adapter [M][d], gates | relu'd bottlenecks [M][Rp], H ⊙ gate [M][Kbp]
+  float *xr = nullptr, *ra = nullptr, *hg = nullptr;
   // MoE: softmax [M][E], selections [M][K] (expert, probability, slot, expert-order row), per-expert
   // counts / offsets, grouped-GEMM schedule, expert pre-activations [P][2F] and outputs [P][d] (P = M·K)
   float *pfull = nullptr, *sel_p = nullptr, *gug = nullptr, *yg = nullptr;
@@ -81,6 +84,14 @@ struct hos_peft {
   // the first row of A_tᵀ in At and the first column of B_t in Bcat; -1 when not adapted
   std::vector<long long> offAg, offBg, offA, offB;
   long long nparams = 0;
+  // RGA (rga_genes > 0): Kg genes of bottleneck bn per layer; stacked factors RT [Rp][d] (W_rᵀ rows, then each
+  // down_kᵀ) and Up [Kbp][d] (each up_k) per layer, wg [8][Kg] and the genome [8]; widths padded to 4.
+  bool rga = false;
+  int Kg = 0, bn = 0, Rp = 0, Kbp = 0;
+  float rlambda = 0.0f;
+  long long offWg = -1, offGen = -1;
+  std::vector<long long> offRT, offUp;
+  float *rz = nullptr, *rdg = nullptr, *rgb = nullptr, *rdgb = nullptr, *rgsum = nullptr;
   float *P = nullptr, *G = nullptr, *M1 = nullptr, *V1 = nullptr;
   uint64_t adam_t = 0;
 
@@ -426,6 +437,10 @@ struct hos_peft {
       Scope s(this, "embed", 0, 4.0 * M * d + (double)M * d);
       launch_embed(tok, ids, act[0].x, M, d, st);
     }
+    if (rga) {
+      Scope s(this, "rga", 0, 4.0 * (16.0 * Kg + Kg));
+      launch_rga_bias(P + offGen, P + offWg, Kg, rgb, st);
+    }
     for (int l = 0; l < L; l++) {
       LayerAct& a = act[l];
       LayerW& w = lw[l];
@@ -474,7 +489,8 @@ struct hos_peft {
         launch_swiglu_fwd(a.gu, M, F, has(TD) ? a.h : nullptr, hs, st);
       }
       lora_down(l, 3, a.h, F, M);
-      qfwd(w.w[TD], hs, F, M, xnext, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
+      qfwd(w.w[TD], hs, F, M, rga ? a.xr : xnext, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
+      if (rga) rga_forward(l, M, xnext);
     }
     {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d + 2.0 * M * d);
@@ -493,6 +509,10 @@ struct hos_peft {
       launch_ce(logits, M, V, tgts, gscale, row_loss, dl, st);
       launch_loss_reduce(row_loss, B, T, loss, st);
     }
+    if (rga && rlambda > 0.0f) {
+      Scope s(this, "rga", 0, 4.0 * L * M);
+      launch_rga_loss(rgsum, Mmax, L, B, T, Kg, rlambda, loss, st);
+    }
     const QWeight& head = out_set ? out : tok;
     qdx(head, dl, V, M, dxn, d, 0, GemmEpi{}, phd);
     {
@@ -503,6 +523,7 @@ struct hos_peft {
     for (int l = L - 1; l >= 0; l--) {
       LayerAct& a = act[l];
       LayerW& w = lw[l];
+      if (rga) rga_backward(l, B, T);  // dx: gradient at x_{l+1} -> at the FFN output
       // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA), or the mixture of experts ----
       if (E) {
         moe_backward(l, M);
@@ -557,6 +578,58 @@ struct hos_peft {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
         launch_rmsnorm_bwd(dxn, a.x, a.inv1, w.attn_norm, M, d, dx, st);
       }
+    }
+    if (rga) {
+      Scope s(this, "rga", 0, 4.0 * (L * Kg + 32.0 * Kg));
+      launch_rga_genome_grad(P + offGen, P + offWg, rdgb, L, Kg, G + offWg, G + offGen, st);
+    }
+  }
+
+  // ---------------- RGA adapter (src/peft.rs:565-584) ----------------
+  // x_next = xr + (H ⊙ gate)·Up with [gate logits | bottleneck] = xr·RTᵀ
+  void rga_forward(int l, int M, float* xnext) {
+    LayerAct& a = act[l];
+    RowsSeg rs;
+    rs.nt = 1;
+    rs.r = Rp;
+    rs.kend[0] = d;
+    lora_rows("rga", M, d, 1.0f, a.xr, d, P + offRT[l], d, rs, rz, Rp);
+    {
+      Scope s(this, "rga", 0, 4.0 * M * (3.0 * Rp + Kbp + 1));
+      launch_rga_act_fwd(rz, Rp, M, Kg, bn, rgb, a.ra, a.hg, Kbp, rgsum + (long long)l * Mmax, st);
+    }
+    {
+      Scope s(this, "rga", 2.0 * M * d * Kbp, 4.0 * ((double)M * d * 3 + (double)M * Kbp + (double)Kbp * d));
+      HOS_HIP_CHECK(hipMemcpyAsync(xnext, a.xr, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
+      launch_gemm_f32(M, d, Kbp, 1.0f, a.hg, Kbp, 1, P + offUp[l], d, 1, 1.0f, xnext, d, ws, ws_bytes, st);
+    }
+  }
+  // dx: gradient at x_next on entry, at xr on exit (identity + the adapter's input gradient); fills the
+  // layer's RT and Up gradients and its gate-bias gradient.
+  void rga_backward(int l, int B, int T) {
+    const int M = B * T;
+    LayerAct& a = act[l];
+    ColsSeg cs;
+    cs.nseg = 1;
+    cs.len[0] = d;
+    lora_cols("rga", M, Kbp, 1.0f, a.hg, Kbp, dx, d, cs, G + offUp[l], d, 1);  // dUp = (H ⊙ gate)ᵀ·dx
+    RowsSeg rs;
+    rs.nt = 1;
+    rs.r = Kbp;
+    rs.kend[0] = d;
+    lora_rows("rga", M, d, 1.0f, dx, d, P + offUp[l], d, rs, rdg, Kbp);  // dG = dx·Upᵀ
+    {
+      // the sparsity term: (1/B)·(λ/L)·mean over a sequence's T·K gates
+      const float pc = rlambda > 0.0f ? rlambda / ((float)B * (float)L * (float)T * (float)Kg) : 0.0f;
+      Scope s(this, "rga", 0, 4.0 * M * (3.0 * Rp + Kbp) + 4.0 * M * Kg);
+      launch_rga_act_bwd(a.ra, Rp, rdg, Kbp, M, Kg, bn, pc, rz, st);
+      launch_rga_colsum(rz, Rp, M, Kg, rdgb + (long long)l * Kg, st);
+    }
+    cs.len[0] = d;
+    lora_cols("rga", M, Rp, 1.0f, rz, Rp, a.xr, d, cs, G + offRT[l], d, 1);  // dRT = dZᵀ·xr
+    {
+      Scope s(this, "rga", 2.0 * M * d * Rp, 4.0 * ((double)M * d * 2 + (double)M * Rp + (double)Rp * d));
+      launch_gemm_f32(M, d, Rp, 1.0f, rz, Rp, 1, P + offRT[l], d, 1, 1.0f, dx, d, ws, ws_bytes, st);  // dx += dZ·RT
     }
   }
 
@@ -651,6 +724,18 @@ struct hos_peft {
     HOS_REQUIRE(E == 0 || !(c.lora_targets & (HOS_T_GATE | HOS_T_UP | HOS_T_DOWN)), HOS_E_INVALID,
                 "peft: a mixture-of-experts FFN takes no LoRA on gate/up/down");
     HOS_REQUIRE(c.lora_rank > 0 && c.max_batch > 0 && c.max_seq > 0, HOS_E_INVALID, "peft: bad rank/batch/seq");
+    rga = c.rga_genes > 0;
+    if (rga) {
+      HOS_REQUIRE(c.lora_targets == 0, HOS_E_INVALID, "peft: RGA adapters replace LoRA (lora_targets must be 0)");
+      HOS_REQUIRE(E == 0, HOS_E_UNSUPPORTED_ARCH, "peft: RGA on a mixture-of-experts model is not supported");
+      HOS_REQUIRE(c.rga_genes <= RGA_MAX_GENES && c.rga_bottleneck > 0, HOS_E_INVALID, "peft: bad RGA genes/bottleneck");
+      Kg = c.rga_genes;
+      bn = c.rga_bottleneck;
+      Rp = (Kg + Kg * bn + 3) & ~3;
+      Kbp = (Kg * bn + 3) & ~3;
+      HOS_REQUIRE(Rp <= 96, HOS_E_INVALID, "peft: RGA genes·(1 + bottleneck) must be <= 96");
+      rlambda = c.rga_lambda;
+    }
     HOS_REQUIRE(c.dim % 32 == 0 && c.ffn_dim % 32 == 0, HOS_E_INVALID, "peft: dim and ffn_dim must be multiples of 32");
     L = c.n_layers;
     d = c.dim;
@@ -719,6 +804,20 @@ struct hos_peft {
             offB[l * NT + t] = offBg[l * 4 + g] + bcol(t);
           }
       }
+    if (rga) {  // RGA arena, in PeftModel::params order: wg, per layer the bank, the genome
+      offWg = off;
+      off = pad(off + (long long)RGA_GLEN * Kg);
+      offRT.assign(L, -1);
+      offUp.assign(L, -1);
+      for (int l = 0; l < L; l++) {
+        offRT[l] = off;
+        off = pad(off + (long long)Rp * d);
+        offUp[l] = off;
+        off = pad(off + (long long)Kbp * d);
+      }
+      offGen = off;
+      off = pad(off + RGA_GLEN);
+    }
     nparams = off;
     P = alloc<float>(nparams);
     G = alloc<float>(nparams);
@@ -744,6 +843,11 @@ struct hos_peft {
       a.gu = E ? nullptr : alloc<float>(M * 2 * F);
       a.h = has(TD) ? alloc<float>(M * F) : nullptr;
       a.u = alloc<float>(M * NT * r);
+      if (rga) {
+        a.xr = alloc<float>(M * d);
+        a.ra = alloc<float>(M * Rp);
+        a.hg = alloc<float>(M * Kbp);
+      }
       if (c.qk_norm) {
         a.qk_pre = alloc<float>(M * (qd + kvd));
         a.qk_inv = alloc<float>(2 * M);
@@ -774,6 +878,13 @@ struct hos_peft {
       mdX = alloc<float>(P * d);
       mdp = alloc<float>(P);
       mdl = alloc<float>(M * E);
+    }
+    if (rga) {
+      rz = alloc<float>(M * Rp);
+      rdg = alloc<float>(M * Kbp);
+      rgb = alloc<float>(Kg);
+      rdgb = alloc<float>((size_t)L * Kg);
+      rgsum = alloc<float>((size_t)L * M);
     }
     xfinal = alloc<float>(M * d);
     invf = alloc<float>(M);
@@ -968,6 +1079,74 @@ void peft_factor_io(hos_peft* p, PeftBuf which, int layer, int target, float* A,
       for (int j = 0; j < r; j++) A[(size_t)k * r + j] = at[(size_t)j * in + k];
 }
 
+// An RGA parameter by adapter tensor name (src/peft.rs:741-760), reference layout, from / to an arena buffer.
+// genome.0 and wg are stored as they are; rga.{l}.wr [d, K] and rga.{l}.down.{k} [d, b] are rows of the
+// stacked transpose RT (rows 0..K-1 and K + k·b .. +b-1); rga.{l}.up.{k} [b, d] is a block of Up's rows.
+void peft_rga_io(hos_peft* p, PeftBuf which, const std::string& name, float* data, size_t n, bool upload) {
+  HOS_REQUIRE(p->rga, HOS_E_INVALID, "not an RGA model");
+  float* base = which == PEFT_PARAM ? p->P : which == PEFT_GRAD ? p->G : which == PEFT_ADAM_M ? p->M1 : p->V1;
+  const int d = p->d, K = p->Kg, b = p->bn;
+  long long off = -1;
+  size_t rows = 0, cols = 0;
+  bool trans = false;  // stored transposed: element (i, j) of the [rows, cols] tensor at off + j·d + i
+  if (name == "genome.0") {
+    off = p->offGen;
+    rows = 1;
+    cols = RGA_GLEN;
+  } else if (name == "wg") {
+    off = p->offWg;
+    rows = RGA_GLEN;
+    cols = K;
+  } else if (name.rfind("rga.", 0) == 0) {
+    const size_t d1 = name.find('.', 4);
+    HOS_REQUIRE(d1 != std::string::npos, HOS_E_INVALID, "unknown adapter tensor '" + name + "'");
+    const int l = std::atoi(name.substr(4, d1 - 4).c_str());
+    HOS_REQUIRE(l >= 0 && l < p->L, HOS_E_INVALID, "layer out of range in '" + name + "'");
+    const std::string leaf = name.substr(d1 + 1);
+    if (leaf == "wr") {
+      off = p->offRT[l];
+      rows = d;
+      cols = K;
+      trans = true;
+    } else if (leaf.rfind("down.", 0) == 0 || leaf.rfind("up.", 0) == 0) {
+      const bool dn = leaf[0] == 'd';
+      const int k = std::atoi(leaf.substr(dn ? 5 : 3).c_str());
+      HOS_REQUIRE(k >= 0 && k < K, HOS_E_INVALID, "gene out of range in '" + name + "'");
+      if (dn) {
+        off = p->offRT[l] + (long long)(K + k * b) * d;
+        rows = d;
+        cols = b;
+        trans = true;
+      } else {
+        off = p->offUp[l] + (long long)k * b * d;
+        rows = b;
+        cols = d;
+      }
+    }
+  }
+  HOS_REQUIRE(off >= 0, HOS_E_INVALID, "unknown adapter tensor '" + name + "'");
+  HOS_REQUIRE(n == rows * cols, HOS_E_INVALID,
+              "adapter tensor '" + name + "' has " + std::to_string(rows * cols) + " elements, got " + std::to_string(n));
+  std::vector<float> dev(n);
+  if (upload) {
+    if (trans)
+      for (size_t i = 0; i < rows; i++)
+        for (size_t j = 0; j < cols; j++) dev[j * rows + i] = data[i * cols + j];
+    else
+      std::memcpy(dev.data(), data, n * 4);
+    HOS_HIP_CHECK(hipMemcpyAsync(base + off, dev.data(), n * 4, hipMemcpyHostToDevice, p->st));
+    HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+    return;
+  }
+  HOS_HIP_CHECK(hipMemcpyAsync(dev.data(), base + off, n * 4, hipMemcpyDeviceToHost, p->st));
+  HOS_HIP_CHECK(hipStreamSynchronize(p->st));
+  if (trans)
+    for (size_t i = 0; i < rows; i++)
+      for (size_t j = 0; j < cols; j++) data[i * cols + j] = dev[j * rows + i];
+  else
+    std::memcpy(data, dev.data(), n * 4);
+}
+
 PeftShape peft_shape(const hos_peft* p) {
   PeftShape s{};
   s.L = p->L;
@@ -979,7 +1158,36 @@ PeftShape peft_shape(const hos_peft* p) {
   s.wd = p->hyp_host.wd;
   s.vocab = p->V;
   s.dim = p->d;
+  s.rga = p->rga;
   return s;
+}
+
+std::vector<std::pair<std::string, std::vector<uint32_t>>> peft_rga_tensors(const hos_peft* p, bool param_order) {
+  std::vector<std::pair<std::string, std::vector<uint32_t>>> v;
+  const uint32_t d = p->d, K = p->Kg, b = p->bn;
+  auto rga = [&](int l, const std::string& leaf, uint32_t r, uint32_t c) {
+    v.push_back({"rga." + std::to_string(l) + "." + leaf, {r, c}});
+  };
+  if (!param_order) {
+    v.push_back({"genome.0", {1, (uint32_t)RGA_GLEN}});
+    v.push_back({"wg", {(uint32_t)RGA_GLEN, K}});
+  } else {
+    v.push_back({"wg", {(uint32_t)RGA_GLEN, K}});
+  }
+  for (int l = 0; l < p->L; l++) {
+    rga(l, "wr", d, K);
+    if (param_order) {
+      for (uint32_t k = 0; k < K; k++) rga(l, "down." + std::to_string(k), d, b);
+      for (uint32_t k = 0; k < K; k++) rga(l, "up." + std::to_string(k), b, d);
+    } else {
+      for (uint32_t k = 0; k < K; k++) {
+        rga(l, "down." + std::to_string(k), d, b);
+        rga(l, "up." + std::to_string(k), b, d);
+      }
+    }
+  }
+  if (param_order) v.push_back({"genome.0", {1, (uint32_t)RGA_GLEN}});
+  return v;
 }
 
 void peft_set_adam_state(hos_peft* p, uint64_t step, float lr, float wd) {
@@ -1057,6 +1265,20 @@ int hos_peft_get_lora(hos_peft* p, int layer, int target, float* A, float* B) {
 }
 int hos_peft_get_lora_grad(hos_peft* p, int layer, int target, float* dA, float* dB) {
   return pguard(p, [&] { hos::peft_factor_io(p, hos::PEFT_GRAD, layer, target, dA, dB, false); });
+}
+
+int hos_peft_set_adapter(hos_peft* p, const char* name, const float* data, size_t n) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(name && data, HOS_E_INVALID, "null pointer");
+    hos::peft_rga_io(p, hos::PEFT_PARAM, name, const_cast<float*>(data), n, true);
+  });
+}
+int hos_peft_get_adapter(hos_peft* p, const char* name, float* value, float* grad, size_t n) {
+  return pguard(p, [&] {
+    HOS_REQUIRE(name != nullptr, HOS_E_INVALID, "null name");
+    if (value) hos::peft_rga_io(p, hos::PEFT_PARAM, name, value, n, false);
+    if (grad) hos::peft_rga_io(p, hos::PEFT_GRAD, name, grad, n, false);
+  });
 }
 
 int hos_peft_loss_grad(hos_peft* p, const int32_t* ids, const int32_t* targets, int B, int T, float* loss) {

@@ -2,6 +2,8 @@
 #pragma once
 #include <cstdint>
 #include <functional>
+#include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/hos_hip.h"
@@ -17,7 +19,15 @@ struct PeftShape {
   uint64_t step;         // AdamW steps taken
   float lr, wd;          // last AdamW hyper-parameters
   int vocab, dim;
+  bool rga;              // RGA adapters instead of LoRA
 };
+
+// RGA adapter tensors as (name, shape): PeftModel::adapter_tensors order (genome, wg, then per layer wr and
+// each gene's down, up; src/peft.rs:741-760), or with param_order PeftModel::params order (wg, per layer wr,
+// downs, ups, then the genome; src/peft.rs:283-311), which the optimizer state follows.
+std::vector<std::pair<std::string, std::vector<uint32_t>>> peft_rga_tensors(const hos_peft* p, bool param_order);
+// Copy one RGA tensor of `which` by name between the device and a host buffer (reference layout, n floats).
+void peft_rga_io(hos_peft* p, PeftBuf which, const std::string& name, float* data, size_t n, bool upload);
 
 // Copy one (layer, target) factor pair of `which` between the device and host buffers in the reference
 // layout (A [in, r], B [r, out] row-major). Either pointer may be null.

@@ -45,7 +45,28 @@ class ModelConfig:
     n_experts: int = 0        # mixture-of-experts FFN (0 = dense), src/model.rs:642-643
     n_experts_used: int = 0
     qk_norm: bool = False     # OLMoE RMSNorm of the q / k projections before RoPE
+    # RGA adapters instead of LoRA (src/peft.rs:61-96): genes per layer, gene bottleneck, gate sparsity weight
+    rga_genes: int = 0
+    rga_bottleneck: int = 4
+    rga_lambda: float = 1e-3
     extra: dict = field(default_factory=dict)
+
+    @property
+    def is_rga(self):
+        return self.rga_genes > 0
+
+    def rga_shapes(self):
+        """Adapter tensor name -> shape, in PeftModel::params order (src/peft.rs:283-311; genome last)."""
+        k, b, d = self.rga_genes, self.rga_bottleneck, self.dim
+        out = {"wg": (8, k)}
+        for l in range(self.n_layers):
+            out[f"rga.{l}.wr"] = (d, k)
+            for kk in range(k):
+                out[f"rga.{l}.down.{kk}"] = (d, b)
+            for kk in range(k):
+                out[f"rga.{l}.up.{kk}"] = (b, d)
+        out["genome.0"] = (1, 8)
+        return out
 
     @property
     def target_mask(self):
@@ -65,7 +86,8 @@ def _cstruct(cfg, max_batch=None, max_seq=None):
     return PeftCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
                    cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank,
                    cfg.lora_alpha, cfg.target_mask, max_batch or cfg.batch, max_seq or cfg.seq, cfg.gemm_passes,
-                   cfg.n_experts, cfg.n_experts_used, int(cfg.qk_norm))
+                   cfg.n_experts, cfg.n_experts_used, int(cfg.qk_norm), cfg.rga_genes, cfg.rga_bottleneck,
+                   cfg.rga_lambda)
 
 
 def _from_cstruct(c, name, **train):
@@ -156,6 +178,20 @@ class PeftModel:
 
     def get_lora_grad(self, layer, target):
         return self._pair(lib().hos_peft_get_lora_grad, layer, target)
+
+    def set_rga(self, name, value):
+        """An RGA parameter by its adapter tensor name (genome.0, wg, rga.{l}.wr / down.{k} / up.{k}),
+        reference layout (PeftModel::adapter_tensors, src/peft.rs:741-760)."""
+        v = np.ascontiguousarray(value, np.float32)
+        self._chk(lib().hos_peft_set_adapter(self.h, name.encode(), v.ctypes.data, v.size))
+
+    def get_rga(self, name):
+        """(value, gradient) of an RGA parameter, reference layout."""
+        shape = self.cfg.rga_shapes()[name]
+        v = np.empty(shape, np.float32)
+        g = np.empty(shape, np.float32)
+        self._chk(lib().hos_peft_get_adapter(self.h, name.encode(), v.ctypes.data, g.ctypes.data, v.size))
+        return v, g
 
     def loss_grad(self, ids, targets):
         ids = np.ascontiguousarray(ids, np.int32)

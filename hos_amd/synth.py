@@ -114,6 +114,17 @@ def lora_init(cfg, seed=99, b_std=0.0):
     return out
 
 
+def rga_init(cfg, seed=99, std=0.02, up_std=0.0):
+    """RGA parameters by adapter tensor name: genome, wg, wr and the gene downs ~N(0, std), ups = 0 as the
+    reference initializes them (src/peft.rs:200-215), or ~N(0, up_std) for gradient checks."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in cfg.rga_shapes().items():
+        s = up_std if ".up." in name else std
+        out[name] = (rng.standard_normal(shape, dtype=np.float32) * np.float32(s)).astype(np.float32)
+    return out
+
+
 def tokens(cfg, batch, seq, seed=7):
     """Uniform token ids over the vocab; targets are the next-token shift."""
     rng = np.random.default_rng(seed)

@@ -186,6 +186,13 @@ typedef struct {
   int n_experts, n_experts_used;
   /* RMSNorm of the full q / k projections before RoPE (blk.N.attn_{q,k}_norm.weight, src/forward.rs:487-493) */
   int qk_norm;
+  /* RGA adapters instead of LoRA (PeftModel "rga", src/peft.rs:61-96, 200-215, 565-584) when rga_genes > 0:
+   * per layer, after the FFN, x += Σ_k sigmoid(x·W_r + genome·W_g)[:, k] ⊙ relu(x·down_k)·up_k, with
+   * rga_genes genes of bottleneck rga_bottleneck and one genome; the loss adds (rga_lambda / L)·Σ_l mean(gate_l)
+   * per sequence (loss_g, src/peft.rs:447-459). lora_targets must be 0 and n_experts 0 (the reference's PEFT
+   * refuses mixture-of-experts models). Parameters are set and read by name (hos_peft_set_adapter). */
+  int rga_genes, rga_bottleneck;
+  float rga_lambda;
 } hos_peft_cfg;
 
 typedef struct hos_peft hos_peft;
@@ -219,6 +226,12 @@ int hos_peft_create_from_gguf(hos_ctx* ctx, const char* path, const hos_peft_cfg
 int hos_peft_set_lora(hos_peft* p, int layer, int target, const float* A, const float* B);
 int hos_peft_get_lora(hos_peft* p, int layer, int target, float* A, float* B);
 int hos_peft_get_lora_grad(hos_peft* p, int layer, int target, float* dA, float* dB);
+/* An RGA parameter by its adapter tensor name and reference layout (PeftModel::adapter_tensors,
+ * src/peft.rs:741-760): genome.0 [1, 8], wg [8, genes], rga.{l}.wr [dim, genes], rga.{l}.down.{k}
+ * [dim, bottleneck], rga.{l}.up.{k} [bottleneck, dim]; n = the tensor's element count (else HOS_E_INVALID).
+ * get: value and/or grad (either may be NULL). */
+int hos_peft_set_adapter(hos_peft* p, const char* name, const float* data, size_t n);
+int hos_peft_get_adapter(hos_peft* p, const char* name, float* value, float* grad, size_t n);
 /* zero_grad + for each of B sequences: loss(seq)·(1/B), backward (src/main.rs:2583-2596,
  * src/train.rs:33-52). ids/targets: [B, T] int32 (host). *loss = Σ_b loss_b / B. */
 int hos_peft_loss_grad(hos_peft* p, const int32_t* ids, const int32_t* targets, int B, int T, float* loss);

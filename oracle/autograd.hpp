@@ -234,6 +234,38 @@ inline Tensor mean(const Tensor& A) {
 
 inline Tensor square(const Tensor& A) { return mul(A, A); }  // src/tensor.rs:2131-2133
 
+// src/tensor.rs:2387-2399: column j of a [n, c] matrix as [n, 1]; bwd scatters into that column.
+inline Tensor col(const Tensor& A, size_t j) {
+  const size_t n = A->shape[0], c = A->shape[1];
+  std::vector<float> out(n);
+  for (size_t i = 0; i < n; i++) out[i] = A->data[i * c + j];
+  return build(std::move(out), {n, 1}, {A}, [n, c, j](const std::vector<float>& g, const std::vector<Tensor>& par) {
+    std::vector<float> gi(n * c, 0.0f);
+    for (size_t i = 0; i < n; i++) gi[i * c + j] = g[i];
+    par[0]->add_grad(gi);
+  });
+}
+
+// src/tensor.rs:2402-2436: a[n, c] * b[n, 1] row-broadcast; db[i] = Σ_j g[i, j]·a[i, j] in j order.
+inline Tensor mul_broadcast(const Tensor& A, const Tensor& B) {
+  const size_t n = A->shape[0], c = A->shape[1];
+  std::vector<float> out(n * c);
+  for (size_t i = 0; i < n; i++)
+    for (size_t j = 0; j < c; j++) out[i * c + j] = A->data[i * c + j] * B->data[i];
+  return build(std::move(out), {n, c}, {A, B}, [n, c](const std::vector<float>& g, const std::vector<Tensor>& par) {
+    const auto& a = par[0]->data;
+    const auto& b = par[1]->data;
+    std::vector<float> da(n * c), db(n, 0.0f);
+    for (size_t i = 0; i < n; i++)
+      for (size_t j = 0; j < c; j++) {
+        da[i * c + j] = g[i * c + j] * b[i];
+        db[i] += g[i * c + j] * a[i * c + j];
+      }
+    par[0]->add_grad(da);
+    par[1]->add_grad(db);
+  });
+}
+
 // src/tensor.rs:2136-2145
 inline Tensor scale(const Tensor& A, float c) {
   std::vector<float> out(A->data.size());

@@ -29,6 +29,7 @@ class OrcCfg(ctypes.Structure):
         ("rope_neox", ctypes.c_int), ("attn_bias", ctypes.c_int), ("lora_rank", ctypes.c_int),
         ("lora_alpha", ctypes.c_float), ("lora_targets", ctypes.c_uint32),
         ("n_experts", ctypes.c_int), ("n_experts_used", ctypes.c_int), ("qk_norm", ctypes.c_int),
+        ("rga_genes", ctypes.c_int), ("rga_bottleneck", ctypes.c_int), ("rga_lambda", ctypes.c_float),
     ]
 
 
@@ -73,6 +74,7 @@ def lib():
         L.orc_model_set_lora.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
         L.orc_model_get_lora.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
         L.orc_model_get_lora_grad.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
+        L.orc_model_rga_tensor.argtypes = [vp, ctypes.c_char_p, vp, vp, sz, ctypes.c_int]
         L.orc_model_loss_grad.restype = ctypes.c_float
         L.orc_model_loss_grad.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int]
         L.orc_model_adamw.argtypes = [vp, ctypes.c_float, ctypes.c_float]
@@ -238,7 +240,9 @@ class OracleModel:
         c = OrcCfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab,
                    cfg.rms_eps, cfg.rope_base, int(cfg.rope_neox), int(cfg.attn_bias), cfg.lora_rank,
                    cfg.lora_alpha, cfg.lora_targets, int(getattr(cfg, "n_experts", 0)),
-                   int(getattr(cfg, "n_experts_used", 0)), int(getattr(cfg, "qk_norm", 0)))
+                   int(getattr(cfg, "n_experts_used", 0)), int(getattr(cfg, "qk_norm", 0)),
+                   int(getattr(cfg, "rga_genes", 0)), int(getattr(cfg, "rga_bottleneck", 0)),
+                   float(getattr(cfg, "rga_lambda", 0.0)))
         self._c = c
         self.h = lib().orc_model_create(ctypes.byref(c))
 
@@ -270,6 +274,20 @@ class OracleModel:
         B = np.empty(shapes[1], np.float32)
         lib().orc_model_get_lora_grad(self.h, layer, target, _p(A), _p(B))
         return A, B
+
+    def set_rga(self, name, value):
+        """Set an RGA parameter by its adapter tensor name (genome.0, wg, rga.{l}.wr / down.{k} / up.{k})."""
+        v = _f32(value)
+        if lib().orc_model_rga_tensor(self.h, name.encode(), _p(v), None, v.size, 1):
+            raise ValueError(f"set_rga {name}")
+
+    def get_rga(self, name, shape):
+        """(value, gradient) of an RGA parameter in the reference layout."""
+        v = np.empty(shape, np.float32)
+        g = np.empty(shape, np.float32)
+        if lib().orc_model_rga_tensor(self.h, name.encode(), _p(v), _p(g), v.size, 0):
+            raise ValueError(f"get_rga {name}")
+        return v, g
 
     def loss_grad(self, ids, targets):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

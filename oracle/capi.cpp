@@ -9,7 +9,7 @@ namespace orc {
 struct Model;
 Model* model_create(const orc_cfg* cfg);
 int model_set_tensor(Model* m, const std::string& name, const uint8_t* bytes, uint32_t type, size_t rows, size_t cols);
-Tensor model_forward(const Model* m, const std::vector<size_t>& ids);
+Tensor model_forward(const Model* m, const std::vector<size_t>& ids, std::vector<Tensor>* gate_means);
 float model_loss_grad(Model* m, const int32_t* ids, const int32_t* tgts, int B, int T);
 void model_adamw(Model* m, float lr, float wd);
 void target_dims(const orc_cfg& c, int t, size_t* in, size_t* out);
@@ -247,7 +247,7 @@ void orc_model_adamw(orc_model* m, float lr, float wd) { model_adamw((Model*)m, 
 int orc_model_logits(orc_model* m, const int32_t* ids, int T, float* out) {
   std::vector<size_t> id(T);
   for (int i = 0; i < T; i++) id[i] = (size_t)ids[i];
-  Tensor y = model_forward((Model*)m, id);
+  Tensor y = model_forward((Model*)m, id, nullptr);
   put(y->data, out);
   return 0;
 }

@@ -56,4 +56,9 @@ typedef struct {
   // Mixture-of-experts FFN (src/model.rs:642-643, 792-795; 0 = dense) and OLMoE's QK-norm
   // (src/model.rs:698-699, 872-873).
   int n_experts, n_experts_used, qk_norm;
+  // RGA adapters instead of LoRA (src/peft.rs:61-96, 200-215; PeftCfg genes / bottleneck, src/peft.rs:121-126)
+  // when rga_genes > 0 (lora_targets must then be 0); rga_lambda is the gate sparsity weight of loss_g
+  // (src/peft.rs:447-459; cmd_peft's PEFT_LAMBDA, src/main.rs:2559-2562).
+  int rga_genes, rga_bottleneck;
+  float rga_lambda;
 } orc_cfg;

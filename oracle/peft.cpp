@@ -5,6 +5,8 @@
 //   PeftModel::loss_g / forward                       src/peft.rs:447-604
 //   cmd_peft step loop (zero_grad, accumulate, AdamW) src/main.rs:2583-2601
 //   train_minibatch                                   src/train.rs:33-52
+//   RGA adapters (PeftModel "rga": genome-regulated gene bank) src/peft.rs:61-96, 200-215, 491-499, 565-584,
+//     params order :283-311, loss_g's gate sparsity term :447-459 (one genome; no clones, no grown FFN)
 // Extensions the benchmark configs need, each reducing exactly to the reference when
 // switched to the reference's setting:
 //   * LoRA targets beyond q/v (k, o, gate, up, down), applied as `y += (x·A·B)·(α/r)`
@@ -44,10 +46,20 @@ struct BaseLayer {
   Lora lora[7];  // q k v o gate up down
 };
 
+// RgaLayer (src/peft.rs:61-66): gate weights and the gene bank of one layer.
+struct RgaLayer {
+  Tensor wr;                     // [dim, K]
+  std::vector<Tensor> down, up;  // K x [dim, b], K x [b, dim]
+};
+
 struct Model {
   orc_cfg c;
   Tensor tok_embd, out_norm, out;
   std::vector<BaseLayer> layers;
+  // RGA (src/peft.rs:77-83): genome [1, GLEN], wg [GLEN, K], per-layer banks
+  Tensor genome, wg;
+  std::vector<RgaLayer> rga;
+  bool is_rga() const { return c.rga_genes > 0; }
   std::unique_ptr<AdamW> opt;
   // Full-parameter finetune (FtModel, src/finetune.rs:62-108): every weight a trainable f32 parameter,
   // the head an untied copy when the file ties it; no LoRA.
@@ -62,6 +74,17 @@ struct Model {
         for (const Tensor& b : {l.bq, l.bk, l.bv})
           if (b) p.push_back(b);
       }
+      return p;
+    }
+    // RGA: params_bank (wg, then per layer wr, down..., up...) then the genome (src/peft.rs:283-311)
+    if (is_rga()) {
+      std::vector<Tensor> p{wg};
+      for (auto& l : rga) {
+        p.push_back(l.wr);
+        for (auto& t : l.down) p.push_back(t);
+        for (auto& t : l.up) p.push_back(t);
+      }
+      p.push_back(genome);
       return p;
     }
     // LoRA factors per layer, in target order (src/peft.rs:295-302 lists aq,bq,av,bv).
@@ -104,6 +127,19 @@ Model* model_create(const orc_cfg* cfg) {
         l.lora[t].A = param(std::vector<float>(in * r, 0.0f), {in, r});
         l.lora[t].B = param(std::vector<float>(r * out, 0.0f), {r, out});
       }
+  if (cfg->rga_genes > 0) {  // shapes of src/peft.rs:200-215 (GLEN = 8); values come from the caller
+    const size_t k = cfg->rga_genes, b = cfg->rga_bottleneck, d = cfg->dim, glen = 8;
+    m->genome = param(std::vector<float>(glen, 0.0f), {1, glen});
+    m->wg = param(std::vector<float>(glen * k, 0.0f), {glen, k});
+    m->rga.resize(cfg->n_layers);
+    for (auto& l : m->rga) {
+      l.wr = param(std::vector<float>(d * k, 0.0f), {d, k});
+      for (size_t kk = 0; kk < k; kk++) {
+        l.down.push_back(param(std::vector<float>(d * b, 0.0f), {d, b}));
+        l.up.push_back(param(std::vector<float>(b * d, 0.0f), {b, d}));
+      }
+    }
+  }
   return m;
 }
 
@@ -222,8 +258,8 @@ static Tensor moe_ffn(const Model* m, const BaseLayer& bl, const Tensor& xn) {
   return moe_mix(ys, p, sel, d);
 }
 
-// PeftModel::forward (LoRA path), src/peft.rs:474-604.
-Tensor model_forward(const Model* m, const std::vector<size_t>& ids) {
+// PeftModel::forward, src/peft.rs:474-604 -> logits; gate_means receives the per-layer RGA gate means.
+Tensor model_forward(const Model* m, const std::vector<size_t>& ids, std::vector<Tensor>* gate_means) {
   const orc_cfg& c = m->c;
   size_t t = ids.size(), hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv_heads;
   size_t qd = nh * hd, group = nh / nkv;
@@ -236,8 +272,13 @@ Tensor model_forward(const Model* m, const std::vector<size_t>& ids) {
       for (size_t j = i + 1; j < t; j++) mk[(h * t + i) * t + j] = -1e9f;
   Tensor mask = constant(std::move(mk), {nh * t, t});
 
+  // the genome's per-gene gate bias [K] (src/peft.rs:491-499)
+  Tensor g_bias;
+  if (m->is_rga()) g_bias = reshape(matmul(m->genome, m->wg), {(size_t)c.rga_genes});
+
   Tensor x = embedding(m->tok_embd, ids);
-  for (const BaseLayer& bl : m->layers) {
+  for (size_t li = 0; li < m->layers.size(); li++) {
+    const BaseLayer& bl = m->layers[li];
     Tensor xn = rmsnorm_eps(x, bl.attn_norm, c.rms_eps);
     Tensor q = matmul(xn, bl.wq);
     Tensor k = matmul(xn, bl.wk);
@@ -276,6 +317,19 @@ Tensor model_forward(const Model* m, const std::vector<size_t>& ids) {
     Tensor hmid = mul(silu(gt), up);
     Tensor dn = lora_apply(m, bl.lora[6], matmul(hmid, bl.w_down), hmid);
     x = add(x, dn);
+    // RGA: genome-regulated sparse gene expression on the residual (src/peft.rs:565-584)
+    if (m->is_rga()) {
+      const RgaLayer& rl = m->rga[li];
+      Tensor gate = sigmoid(add(matmul(x, rl.wr), g_bias));  // [t, K]
+      Tensor upd;
+      for (int kk = 0; kk < c.rga_genes; kk++) {
+        Tensor gene = matmul(relu(matmul(x, rl.down[kk])), rl.up[kk]);  // [t, dim]
+        Tensor gated = mul_broadcast(gene, col(gate, (size_t)kk));
+        upd = upd ? add(upd, gated) : gated;
+      }
+      x = add(x, upd);
+      if (gate_means) gate_means->push_back(mean(gate));
+    }
   }
   return matmul(rmsnorm_eps(x, m->out_norm, c.rms_eps), m->out);
 }
@@ -291,7 +345,16 @@ float model_loss_grad(Model* m, const int32_t* ids, const int32_t* tgts, int B, 
       id[i] = (size_t)ids[b * T + i];
       tg[i] = (size_t)tgts[b * T + i];
     }
-    Tensor loss = scale(cross_entropy(model_forward(m, id), tg), 1.0f / (float)B);
+    // loss_g (src/peft.rs:447-459): cross-entropy + (RGA, lambda > 0) (λ/L)·Σ_l mean(gate_l)
+    std::vector<Tensor> gm;
+    Tensor lossb = cross_entropy(model_forward(m, id, &gm), tg);
+    const float lambda = m->is_rga() ? m->c.rga_lambda : 0.0f;
+    if (lambda > 0.0f && !gm.empty()) {
+      Tensor sgm = gm[0];
+      for (size_t i = 1; i < gm.size(); i++) sgm = add(sgm, gm[i]);
+      lossb = add(lossb, scale(sgm, lambda / (float)gm.size()));
+    }
+    Tensor loss = scale(lossb, 1.0f / (float)B);
     backward(loss);
     mean_loss += loss->data[0];
   }
@@ -368,6 +431,40 @@ int orc_ft_get(void* mh, const char* cname, float* value, float* grad) {
   return 0;
 }
 void orc_model_destroy(void* mh) { delete (orc::Model*)mh; }
+// An RGA parameter by its adapter tensor name (PeftModel::adapter_tensors, src/peft.rs:741-760): genome.0, wg,
+// rga.{l}.wr, rga.{l}.down.{k}, rga.{l}.up.{k}, in the reference layout. set != 0 writes value from the caller;
+// otherwise value and grad (each may be NULL) are read. n must equal the tensor's element count.
+int orc_model_rga_tensor(void* mh, const char* cname, float* value, float* grad, size_t n, int set) {
+  auto* m = (orc::Model*)mh;
+  if (!m->is_rga()) return ORC_E_INVALID;
+  std::string name(cname);
+  orc::Tensor t;
+  if (name == "genome.0") t = m->genome;
+  else if (name == "wg") t = m->wg;
+  else if (name.rfind("rga.", 0) == 0) {
+    size_t d1 = name.find('.', 4);
+    if (d1 == std::string::npos) return ORC_E_INVALID;
+    int li = std::stoi(name.substr(4, d1 - 4));
+    if (li < 0 || li >= m->c.n_layers) return ORC_E_INVALID;
+    std::string leaf = name.substr(d1 + 1);
+    auto& l = m->rga[li];
+    if (leaf == "wr") t = l.wr;
+    else if (leaf.rfind("down.", 0) == 0 || leaf.rfind("up.", 0) == 0) {
+      const bool dn = leaf[0] == 'd';
+      int k = std::stoi(leaf.substr(dn ? 5 : 3));
+      if (k < 0 || k >= m->c.rga_genes) return ORC_E_INVALID;
+      t = dn ? l.down[k] : l.up[k];
+    }
+  }
+  if (!t || t->data.size() != n) return ORC_E_INVALID;
+  if (set) {
+    std::memcpy(t->data.data(), value, n * 4);
+    return 0;
+  }
+  if (value) std::memcpy(value, t->data.data(), n * 4);
+  if (grad) std::memcpy(grad, t->grad.data(), n * 4);
+  return 0;
+}
 int orc_model_set_lora(void* mh, int layer, int target, const float* A, const float* B) {
   auto* m = (orc::Model*)mh;
   if (layer < 0 || layer >= m->c.n_layers || target < 0 || target > 6) return ORC_E_INVALID;
