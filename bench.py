@@ -12,6 +12,7 @@ last step of the timed region), the isolated configs[1] dX GEMM (4096^3, Q4_K) a
 baseline (the oracle's restatement of HOS's CPU training path on this host's cores, a bounded sample).
 """
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -35,6 +36,8 @@ def parse():
     ap.add_argument("--config", default="qwen2.5-0.5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline sample")
     ap.add_argument("--cpu-seq", type=int, default=256, help="tokens in the CPU baseline sample")
+    ap.add_argument("--rga", action="store_true",
+                    help="train RGA adapters (4 genes of bottleneck 4, lambda 1e-3: cmd_peft's defaults) instead of LoRA")
     ap.add_argument("--finetune", action="store_true",
                     help="time the full-parameter finetune step (FtModel: every weight trainable in f32) instead")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -103,6 +106,9 @@ def workload(cfg):
     if cfg.n_experts:
         base += f"; {cfg.n_experts} experts top-{cfg.n_experts_used}, QK-norm" if cfg.qk_norm else \
             f"; {cfg.n_experts} experts top-{cfg.n_experts_used}"
+    if cfg.rga_genes:
+        return (f"{cfg.name} RGA {cfg.rga_genes} genes x bottleneck {cfg.rga_bottleneck}, lambda {cfg.rga_lambda:g}; "
+                f"{base}; AdamW")
     return f"{cfg.name} LoRA r{cfg.lora_rank} on {','.join(cfg.lora_targets)}; {base}; AdamW"
 
 
@@ -114,11 +120,14 @@ def cpu_baseline(cfg, tensors, seq):
     from hos_amd import synth
     oc = types.SimpleNamespace(**{k: getattr(cfg, k) for k in (
         "n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "rms_eps", "rope_base",
-        "rope_neox", "attn_bias", "lora_rank", "lora_alpha")})
+        "rope_neox", "attn_bias", "lora_rank", "lora_alpha", "rga_genes", "rga_bottleneck", "rga_lambda")})
     oc.lora_targets = cfg.target_mask
     m = o.OracleModel(oc)
     for name, (raw, t, rows, cols) in tensors.items():
         m.set_tensor(name, raw, t, rows, cols)
+    if cfg.is_rga:
+        for name, v in synth.rga_init(cfg, seed=5).items():
+            m.set_rga(name, v)
     for (l, t), (A, B) in synth.lora_init(cfg, seed=5).items():
         m.set_lora(l, ("q", "k", "v", "o", "gate", "up", "down").index(t), A, B)
     ids, tg = synth.tokens(cfg, 1, seq, seed=8)
@@ -185,11 +194,16 @@ def main():
     from hos_amd.peft import PeftModel
 
     cfg = synth.CONFIGS[args.config]
+    if args.rga:  # src/main.rs:1017 (PEFT_GENES / PEFT_BOTTLE defaults), :2559-2562 (PEFT_LAMBDA default)
+        cfg = dataclasses.replace(cfg, lora_targets=(), rga_genes=4, rga_bottleneck=4, rga_lambda=1e-3)
     gpu = Gpu(0)
     t_setup = time.perf_counter()
     tensors = synth.build_tensors(gpu, cfg, seed=1234)
     pm = PeftModel(gpu, cfg)
     pm.load(tensors)
+    if cfg.is_rga:
+        for name, v in synth.rga_init(cfg, seed=5).items():
+            pm.set_rga(name, v)
     for (l, t), (A, B) in synth.lora_init(cfg, seed=5).items():
         pm.set_lora(l, t, A, B)
     B, T = cfg.batch, cfg.seq
@@ -205,7 +219,7 @@ def main():
     gpu.synchronize()
 
     classes = ["qgemm_fwd", "qgemm_dx", "lora_down", "lora_db", "lora_du", "lora_da", "attn_fwd", "attn_bwd",
-               "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert", "moe_route", "moe_combine"]
+               "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert", "moe_route", "moe_combine", "rga"]
     # Breakdown pass (every kernel class timed with HIP events; not the timed region): finds the
     # dominant class and gives the per-class split.
     pm.profile(True)
@@ -252,7 +266,7 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, tensors, args.cpu_seq)
     line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC + (" [RGA adapters]" if cfg.is_rga else ""), "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16 MFMA (hi/lo split: 3 passes per layer GEMM, 1-2 on the head) + f32", "data": "synthetic",
         "config": {"workload": workload(cfg), "global_batch": B, "seq_len": T,

@@ -140,4 +140,6 @@ def algorithmic_flops_per_token(cfg, seq):
     ffn = (cfg.n_experts_used * 3 * d * f + d * cfg.n_experts) if cfg.n_experts else 3 * d * f
     p_base = cfg.n_layers * (d * qd + 2 * d * kvd + qd * d + ffn) + d * v
     p_lora = cfg.n_layers * sum(cfg.lora_rank * sum(cfg.target_dims(t)) for t in cfg.lora_targets)
+    if cfg.rga_genes:  # RGA: gate weights + each gene's down and up per layer (the genome terms are per step)
+        p_lora += cfg.n_layers * cfg.rga_genes * d * (1 + 2 * cfg.rga_bottleneck)
     return 4 * p_base + 6 * p_lora + 6 * cfg.n_layers * seq * qd
