@@ -40,6 +40,8 @@ def parse():
                     help="train RGA adapters (4 genes of bottleneck 4, lambda 1e-3: cmd_peft's defaults) instead of LoRA")
     ap.add_argument("--finetune", action="store_true",
                     help="time the full-parameter finetune step (FtModel: every weight trainable in f32) instead")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="enqueue the step kernel by kernel instead of replaying its captured HIP graph (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -206,6 +208,8 @@ def main():
             pm.set_rga(name, v)
     for (l, t), (A, B) in synth.lora_init(cfg, seed=5).items():
         pm.set_lora(l, t, A, B)
+    if args.no_graph:
+        pm.use_graph(False)
     B, T = cfg.batch, cfg.seq
     ids, tg = synth.tokens(cfg, B, T, seed=8)
     ids_dev, tg_dev, loss_dev = gpu.alloc(ids.nbytes), gpu.alloc(tg.nbytes), gpu.alloc(4)

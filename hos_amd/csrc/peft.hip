@@ -91,7 +91,7 @@ struct hos_peft {
   float rlambda = 0.0f;
   long long offWg = -1, offGen = -1;
   std::vector<long long> offRT, offUp;
-  float *rz = nullptr, *rdg = nullptr, *rgb = nullptr, *rdgb = nullptr, *rgsum = nullptr;
+  float *rz = nullptr, *rdg = nullptr, *rgb = nullptr, *rdgb = nullptr, *rgsum = nullptr, *rgm = nullptr;
   float *P = nullptr, *G = nullptr, *M1 = nullptr, *V1 = nullptr;
   uint64_t adam_t = 0;
 
@@ -511,7 +511,7 @@ struct hos_peft {
     }
     if (rga && rlambda > 0.0f) {
       Scope s(this, "rga", 0, 4.0 * L * M);
-      launch_rga_loss(rgsum, Mmax, L, B, T, Kg, rlambda, loss, st);
+      launch_rga_loss(rgsum, Mmax, L, B, T, Kg, rlambda, rgm, loss, st);
     }
     const QWeight& head = out_set ? out : tok;
     qdx(head, dl, V, M, dxn, d, 0, GemmEpi{}, phd);
@@ -885,6 +885,7 @@ struct hos_peft {
       rgb = alloc<float>(Kg);
       rdgb = alloc<float>((size_t)L * Kg);
       rgsum = alloc<float>((size_t)L * M);
+      rgm = alloc<float>((size_t)L * M);  // B <= B·T <= the row capacity
     }
     xfinal = alloc<float>(M * d);
     invf = alloc<float>(M);

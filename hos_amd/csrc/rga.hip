@@ -116,29 +116,33 @@ __global__ void rga_genome_grad_kernel(const float* __restrict__ genome, const f
   }
 }
 
-// loss += Σ_b (1/B)·(λ/L)·Σ_l mean over sequence b of layer l's gates (gsum + l·ldl: row sums of K gates).
-__global__ void __launch_bounds__(256) rga_loss_kernel(const float* __restrict__ gsum, long long ldl, int L, int B,
-                                                       int T, int K, float lambda, float* __restrict__ loss) {
+// gm[l·B + b] = mean over sequence b of layer l's T·K gates (gsum + l·ldl: row sums), one workgroup each with a
+// fixed-order tree.
+__global__ void __launch_bounds__(256) rga_gate_mean_kernel(const float* __restrict__ gsum, long long ldl, int B,
+                                                            int T, int K, float* __restrict__ gm) {
   __shared__ float part[256];
+  const int l = blockIdx.x / B, b = blockIdx.x % B;
+  const float* g = gsum + (long long)l * ldl + (long long)b * T;
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < T; i += 256) s += g[i];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) gm[blockIdx.x] = part[0] / (float)(T * K);
+}
+
+// loss += Σ_b (1/B)·(λ/L)·Σ_l gm[l·B + b] (layers in order, as loss_g adds the gate means)
+__global__ void rga_loss_kernel(const float* __restrict__ gm, int L, int B, float lambda, float* __restrict__ loss) {
   float tot = 0.0f;
   for (int b = 0; b < B; b++) {
-    float sl = 0.0f;  // Σ_l mean_l (layer order)
-    for (int l = 0; l < L; l++) {
-      const float* g = gsum + (long long)l * ldl + (long long)b * T;
-      float s = 0.0f;
-      for (int i = threadIdx.x; i < T; i += 256) s += g[i];
-      part[threadIdx.x] = s;
-      __syncthreads();
-      for (int w = 128; w > 0; w >>= 1) {
-        if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
-        __syncthreads();
-      }
-      sl += part[0] / (float)(T * K);
-      __syncthreads();
-    }
+    float sl = 0.0f;
+    for (int l = 0; l < L; l++) sl += gm[l * B + b];
     tot += sl * (lambda / (float)L) * (1.0f / (float)B);
   }
-  if (threadIdx.x == 0) loss[0] += tot;
+  loss[0] += tot;
 }
 
 }  // namespace
@@ -149,12 +153,12 @@ void launch_rga_bias(const float* genome, const float* wg, int K, float* gb, hip
 }
 void launch_rga_act_fwd(const float* Z, int ldz, int M, int K, int b, const float* gb, float* A, float* Hg, int ldh,
                         float* gsum, hipStream_t st) {
-  rga_act_fwd_kernel<<<ceil_div(M, 256), 256, 0, st>>>(Z, ldz, M, K, b, gb, A, Hg, ldh, gsum);
+  rga_act_fwd_kernel<<<ceil_div(M, 64), 64, 0, st>>>(Z, ldz, M, K, b, gb, A, Hg, ldh, gsum);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rga_act_bwd(const float* A, int ldz, const float* dG, int ldh, int M, int K, int b, float pc, float* dZ,
                         hipStream_t st) {
-  rga_act_bwd_kernel<<<ceil_div(M, 256), 256, 0, st>>>(A, ldz, dG, ldh, M, K, b, pc, dZ);
+  rga_act_bwd_kernel<<<ceil_div(M, 64), 64, 0, st>>>(A, ldz, dG, ldh, M, K, b, pc, dZ);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rga_colsum(const float* dZ, int ldz, int M, int K, float* out, hipStream_t st) {
@@ -166,9 +170,11 @@ void launch_rga_genome_grad(const float* genome, const float* wg, const float* d
   rga_genome_grad_kernel<<<1, 64, 0, st>>>(genome, wg, dgb, L, K, gwg, ggen);
   HOS_HIP_CHECK(hipGetLastError());
 }
-void launch_rga_loss(const float* gsum, long long ldl, int L, int B, int T, int K, float lambda, float* loss,
-                     hipStream_t st) {
-  rga_loss_kernel<<<1, 256, 0, st>>>(gsum, ldl, L, B, T, K, lambda, loss);
+void launch_rga_loss(const float* gsum, long long ldl, int L, int B, int T, int K, float lambda, float* gm,
+                     float* loss, hipStream_t st) {
+  rga_gate_mean_kernel<<<L * B, 256, 0, st>>>(gsum, ldl, B, T, K, gm);
+  HOS_HIP_CHECK(hipGetLastError());
+  rga_loss_kernel<<<1, 1, 0, st>>>(gm, L, B, lambda, loss);
   HOS_HIP_CHECK(hipGetLastError());
 }
 

@@ -21,8 +21,9 @@ void launch_rga_colsum(const float* dZ, int ldz, int M, int K, float* out, hipSt
 // gradients of wg [8][K] and genome [8] from the per-layer gate-bias gradients dgb [L][K]
 void launch_rga_genome_grad(const float* genome, const float* wg, const float* dgb, int L, int K, float* gwg,
                             float* ggen, hipStream_t st);
-// loss += Σ_b (1/B)·(λ/L)·Σ_l mean(gate_l over sequence b); gsum: layer l's row sums at gsum + l·ldl
-void launch_rga_loss(const float* gsum, long long ldl, int L, int B, int T, int K, float lambda, float* loss,
-                     hipStream_t st);
+// loss += Σ_b (1/B)·(λ/L)·Σ_l mean(gate_l over sequence b); gsum: layer l's row sums at gsum + l·ldl;
+// gm: scratch for the L·B means
+void launch_rga_loss(const float* gsum, long long ldl, int L, int B, int T, int K, float lambda, float* gm,
+                     float* loss, hipStream_t st);
 
 }  // namespace hos
