@@ -208,3 +208,40 @@ def test_checkpoint_names_and_resume(gpu, tmp_path):
     assert la == lb
     for name in cfg.rga_shapes():
         assert np.array_equal(pm.get_rga(name)[0], fresh.get_rga(name)[0]), name
+
+
+def test_full_size_step_properties():
+    """The benchmark shapes (Qwen2.5-0.5B architecture, B4 x T512) with RGA at cmd_peft's defaults (4 genes,
+    bottleneck 4, λ 1e-3), where the oracle would take hours: the step is deterministic (bit-identical loss and
+    gradients on a repeat), every gradient is finite, up = 0 makes every down gradient exactly zero (dG = dx·Upᵀ
+    vanishes) while wr still moves through the sparsity term, the initial loss is ln(vocab) plus about
+    λ·mean(gate), and a few AdamW steps on one batch lower the loss."""
+    import dataclasses
+
+    from hos_amd import Gpu, synth
+    g = Gpu(0)
+    cfg = dataclasses.replace(synth.CONFIGS["qwen2.5-0.5b"], lora_targets=(), rga_genes=4, rga_bottleneck=4,
+                              rga_lambda=1e-3)
+    B, T = cfg.batch, cfg.seq
+    print(f"rga full-size properties B={B} T={T}", flush=True)
+    tensors = synth.build_tensors(g, cfg, seed=1)
+    params = synth.rga_init(cfg, seed=2)  # ups = 0
+    ids, tg = synth.tokens(cfg, B, T, seed=3)
+    pm = device_model(g, cfg, tensors, params, B, T)
+    l1 = pm.loss_grad(ids, tg)
+    names = ["genome.0", "wg", "rga.0.wr", "rga.0.down.1", "rga.23.up.3", "rga.11.down.0"]
+    g1 = {n: pm.get_rga(n)[1] for n in names}
+    l2 = pm.loss_grad(ids, tg)
+    g2 = {n: pm.get_rga(n)[1] for n in names}
+    assert l1 == l2
+    for n in names:
+        assert np.array_equal(g1[n], g2[n]), n
+        assert np.isfinite(g1[n]).all(), n
+    assert not g1["rga.0.down.1"].any() and not g1["rga.11.down.0"].any()
+    assert np.abs(g1["rga.0.wr"]).sum() > 0 and np.abs(g1["rga.23.up.3"]).sum() > 0
+    assert abs(l1 - np.log(cfg.vocab)) < 0.5
+    losses = [pm.step(ids, tg, lr=1e-3) for _ in range(4)]
+    print(f"rga losses {losses}", flush=True)
+    assert losses[-1] < losses[0]
+    pm.close()
+    g.close()
