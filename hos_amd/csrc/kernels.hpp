@@ -68,6 +68,9 @@ struct GemmEpi {
   long long slj = 0, sln = 0;
   int rank = 0;
   float scale = 0.0f;
+  // Column segments of a stacked projection (q|k|v, gate|up): output columns n >= ub0 (and >= ub1) take their U
+  // block ustep (2·ustep) columns further on — each target's own rank-r factor. 0 = one U for all columns.
+  int ustep = 0, ub0 = 0, ub1 = 0;
 };
 // Grouped (mixture-of-experts) GEMM schedule: W holds n_experts stacked [rows, cols] blocks; workgroup row
 // y of the launch computes rows tiles[3y+1] .. +tiles[3y+2] of the operand against expert tiles[3y]

@@ -37,6 +37,10 @@ struct LayerW {
   float *q_norm = nullptr, *k_norm = nullptr;     // OLMoE QK-norm weights [qd], [kvd]
   float* router = nullptr;                        // MoE router [E][d] (f32, ffn_gate_inp.weight)
   QWeight xg, xu, xd;                             // MoE experts, stacked [E·F][d], [E·F][d], [E·d][F]
+  // q|k|v and gate|up stacked row-wise (same encoding and width), each group one GEMM; the q|k|v biases
+  // concatenated. Absent when the parts differ in encoding.
+  QWeight qkv, gu;
+  float* bias_qkv = nullptr;
 };
 
 struct LayerAct {
@@ -79,6 +83,7 @@ struct hos_peft {
   QWeight tok, out;
   bool out_set = false;
   float* out_norm = nullptr;
+  bool stacks_dirty = true;  // a projection or bias changed since the stacked copies were built
 
   // LoRA arena offsets (floats): per (layer, group) the stacked At and Bcat blocks; per (layer, target)
   // the first row of A_tᵀ in At and the first column of B_t in Bcat; -1 when not adapted
@@ -293,6 +298,93 @@ struct hos_peft {
     e.scale = lscale;
     return e;
   }
+  // A group's projections as one stacked GEMM: possible when its targets are all adapted or none is (the
+  // stacked output lines up with Bcat / the stacked At only then), the per-target precision overrides agree,
+  // and (dX) the stacked rank fits the fused epilogue.
+  bool group_uniform(int g) const {
+    const int n = gcount(g), all = group_last(g) - group_first(g) + 1;
+    if (n != 0 && n != all) return false;
+    for (int t = group_first(g) + 1; t <= group_last(g); t++)
+      if (tpf[t] != tpf[group_first(g)] || tpd[t] != tpd[group_first(g)]) return false;
+    return true;
+  }
+  // Forward epilogue of a stacked group: each column segment adds its own target's s·u_t·B_t
+  // (u_t at column ucol(first) + slot·r, B_t the matching Bcat columns).
+  GemmEpi stacked_up_epi(int l, int g) {
+    GemmEpi e{};
+    if (gcount(g) == 0) return e;
+    const int t0 = group_first(g);
+    e.U = act[l].u + ucol(t0);
+    e.ldu = NT * r;
+    e.L = P + offBg[l * 4 + g];
+    e.slj = bw(g);
+    e.sln = 1;
+    e.rank = r;
+    e.scale = lscale;
+    e.ustep = r;
+    e.ub0 = out_dim(t0);
+    e.ub1 = g == 0 ? out_dim(TQ) + out_dim(TK) : 1 << 30;
+    return e;
+  }
+  // dX epilogue of a stacked group: dx_in += [du_1 … du_G]·[A_1ᵀ; …; A_Gᵀ], one rank-G·r term (At block).
+  GemmEpi stacked_down_epi(int l, int g) {
+    GemmEpi e{};
+    if (gcount(g) == 0) return e;
+    e.U = du + ucol(group_first(g));
+    e.ldu = NT * r;
+    e.L = P + offAg[l * 4 + g];
+    e.slj = in_dim(group_first(g));
+    e.sln = 1;
+    e.rank = gcount(g) * r;
+    e.scale = 1.0f;
+    return e;
+  }
+  // (Re)build the stacked copies of every layer (host side, before a step; never inside a capture).
+  void build_stacks() {
+    if (!stacks_dirty) return;
+    // captured steps hold the old weight pointers (a re-uploaded tensor has new ones too): capture again
+    for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+    graphs.clear();
+    for (int l = 0; l < L; l++) {
+      LayerW& w = lw[l];
+      free_qweight(w.qkv);
+      free_qweight(w.gu);
+      stack(w.qkv, {&w.w[TQ], &w.w[TK], &w.w[TV]});
+      if (!E) stack(w.gu, {&w.w[TG], &w.w[TU]});
+      if (c.attn_bias && w.bias[0] && w.bias[1] && w.bias[2]) {
+        if (!w.bias_qkv) w.bias_qkv = alloc<float>((size_t)W3);
+        HOS_HIP_CHECK(hipMemcpyAsync(w.bias_qkv, w.bias[0], (size_t)qd * 4, hipMemcpyDeviceToDevice, st));
+        HOS_HIP_CHECK(hipMemcpyAsync(w.bias_qkv + qd, w.bias[1], (size_t)kvd * 4, hipMemcpyDeviceToDevice, st));
+        HOS_HIP_CHECK(hipMemcpyAsync(w.bias_qkv + qd + kvd, w.bias[2], (size_t)kvd * 4, hipMemcpyDeviceToDevice, st));
+      }
+    }
+    HOS_HIP_CHECK(hipStreamSynchronize(st));
+    stacks_dirty = false;
+  }
+  // Row-wise concatenation of repacked weights (their q and s arrays are row-major, so the stack is the
+  // concatenation of each array); left empty unless every part is present with one encoding and width.
+  void stack(QWeight& out, std::initializer_list<const QWeight*> parts) {
+    const QWeight* p0 = *parts.begin();
+    long long rows = 0;
+    for (const QWeight* p : parts) {
+      if (!p->q || p->type != p0->type || p->cols != p0->cols) return;
+      rows += p->rows;
+    }
+    out.type = p0->type;
+    out.rows = rows;
+    out.cols = p0->cols;
+    qweight_sizes(out.type, out.rows, out.cols, &out.q_bytes, &out.s_bytes);
+    HOS_HIP_CHECK(hipMalloc(&out.q, out.q_bytes));
+    HOS_HIP_CHECK(hipMalloc((void**)&out.s, out.s_bytes));
+    size_t qo = 0, so = 0;
+    for (const QWeight* p : parts) {
+      HOS_HIP_CHECK(hipMemcpyAsync((uint8_t*)out.q + qo, p->q, p->q_bytes, hipMemcpyDeviceToDevice, st));
+      HOS_HIP_CHECK(hipMemcpyAsync((uint8_t*)out.s + so, p->s, p->s_bytes, hipMemcpyDeviceToDevice, st));
+      qo += p->q_bytes;
+      so += p->s_bytes;
+    }
+  }
+
   // From dy, the gradient of the group's fused projection output (row stride ldy, target t at column
   // ycol(t)): dB_t = s·u_tᵀ·dy_t for every adapted t (one launch), du_t = s·dy_t·B_tᵀ (one launch).
   void lora_grad_b(int l, int g, const float* dy, long long ldy, long long kspan, int M) {
@@ -343,6 +435,10 @@ struct hos_peft {
   }
 
   void check_ready() {
+    check_tensors();
+    build_stacks();
+  }
+  void check_tensors() {
     HOS_REQUIRE(tok.q != nullptr, HOS_E_MISSING_TENSOR, "missing tensor 'token_embd.weight'");
     HOS_REQUIRE(out_norm != nullptr, HOS_E_MISSING_TENSOR, "missing tensor 'output_norm.weight'");
     for (int l = 0; l < L; l++) {
@@ -451,9 +547,14 @@ struct hos_peft {
         launch_rmsnorm_fwd(a.x, w.attn_norm, c.rms_eps, M, d, lqkv ? a.xn1 : nullptr, hs, a.inv1, st);
       }
       lora_down(l, 0, a.xn1, d, M);
-      qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0, up_epi(l, TQ), tpf[TQ]);
-      qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0, up_epi(l, TK), tpf[TK]);
-      qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0, up_epi(l, TV), tpf[TV]);
+      if (w.qkv.q && group_uniform(0) && (!c.attn_bias || w.bias_qkv)) {
+        qfwd(w.qkv, hs, d, M, a.qkv, W3, c.attn_bias ? w.bias_qkv : nullptr, nullptr, 0, stacked_up_epi(l, 0),
+             tpf[TQ]);
+      } else {
+        qfwd(w.w[TQ], hs, d, M, a.qkv, W3, w.bias[0], nullptr, 0, up_epi(l, TQ), tpf[TQ]);
+        qfwd(w.w[TK], hs, d, M, a.qkv + qd, W3, w.bias[1], nullptr, 0, up_epi(l, TK), tpf[TK]);
+        qfwd(w.w[TV], hs, d, M, a.qkv + qd + kvd, W3, w.bias[2], nullptr, 0, up_epi(l, TV), tpf[TV]);
+      }
       if (c.qk_norm) {
         Scope s(this, "rmsnorm", 0, 4.0 * M * (qd + kvd) * 3);
         launch_qknorm_fwd(a.qkv, W3, 0, qd, w.q_norm, c.rms_eps, M, a.qk_pre, a.qk_inv, st);
@@ -482,8 +583,12 @@ struct hos_peft {
         continue;
       }
       lora_down(l, 2, a.xn2, d, M);
-      qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, up_epi(l, TG), tpf[TG]);
-      qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0, up_epi(l, TU), tpf[TU]);
+      if (w.gu.q && group_uniform(2)) {
+        qfwd(w.gu, hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, stacked_up_epi(l, 2), tpf[TG]);
+      } else {
+        qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, up_epi(l, TG), tpf[TG]);
+        qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0, up_epi(l, TU), tpf[TU]);
+      }
       {
         Scope s(this, "swiglu", 0, 8.0 * M * F + 2.0 * M * F + (has(TD) ? 4.0 * M * F : 0));
         launch_swiglu_fwd(a.gu, M, F, has(TD) ? a.h : nullptr, hs, st);
@@ -537,9 +642,13 @@ struct hos_peft {
         launch_swiglu_bwd(a.gu, dh, M, F, (has(TG) || has(TU)) ? dgu : nullptr, hs, st);
       }
       if (dgu) lora_grad_b(l, 2, dgu, 2LL * F, 2LL * F, M);
-      H16 hu = h16_offset(hs, F);
-      qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG), tpd[TG]);
-      qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU), tpd[TU]);
+      if (w.gu.q && group_uniform(2) && gcount(2) * r <= 32) {
+        qdx(w.gu, hs, 2LL * F, M, dxn, d, 0, stacked_down_epi(l, 2), tpd[TG]);
+      } else {
+        H16 hu = h16_offset(hs, F);
+        qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG), tpd[TG]);
+        qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU), tpd[TU]);
+      }
       lora_grad_a(l, 2, a.xn2, d, M);
       }
       {
@@ -944,6 +1053,8 @@ struct hos_peft {
       free_qweight(l.xg);
       free_qweight(l.xu);
       free_qweight(l.xd);
+      free_qweight(l.qkv);
+      free_qweight(l.gu);
     }
     free_qweight(tok);
     free_qweight(out);
@@ -970,6 +1081,7 @@ struct hos_peft {
   void set_tensor(const std::string& name, const uint8_t* bytes, size_t nbytes, uint32_t type, size_t rows,
                   size_t cols) {
     HOS_REQUIRE(bytes != nullptr, HOS_E_INVALID, "null bytes");
+    stacks_dirty = true;
     if (name == "token_embd.weight") return set_q(tok, bytes, nbytes, type, rows, cols, V, d, name);
     if (name == "output.weight") {
       set_q(out, bytes, nbytes, type, rows, cols, V, d, name);

@@ -410,9 +410,11 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   float* Ls = Us + BM * 32;
   const int rank = split ? 0 : epi.rank;
   if (rank > 0) {
+    // a tile never straddles a column segment (the launcher picks BN to divide the boundaries)
+    const float* Ub = epi.U + (epi.ustep ? epi.ustep * ((n0 >= epi.ub0) + (n0 >= epi.ub1)) : 0);
     for (int e = tid; e < BM * rank; e += G::NT) {
       int rr = e / rank, jj = e % rank, row = m0 + rr;
-      Us[rr * 32 + jj] = row < M ? epi.U[(long long)row * epi.ldu + jj] : 0.0f;
+      Us[rr * 32 + jj] = row < M ? Ub[(long long)row * epi.ldu + jj] : 0.0f;
     }
     for (int e = tid; e < rank * BN; e += G::NT) {
       int jj = e / BN, cc = e % BN, col = n0 + cc;
@@ -546,10 +548,22 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
       bk = z;
     }
   }
+  // Column-segmented U (stacked projections): tiles must not straddle a segment boundary, and the split-K
+  // reduction (which stages one U block for all its columns) is not used.
+  const bool useg = epi.rank > 0 && epi.ustep > 0;
+  if (useg) {
+    auto fits = [&](int b) { return epi.ub0 % b == 0 && (epi.ub1 >= Nout || epi.ub1 % b == 0); };
+    if (!fits(bn)) {
+      bn = 64;
+      if (bm == 256) bm = 128;
+      if (bk == 64 && !(bm == 64 || C % 64 == 0)) bk = 32;
+    }
+    HOS_REQUIRE(fits(bn), HOS_E_INVALID, "qgemm: column segments must be multiples of 64");
+  }
   int tiles = ntiles(bm, bn);
   int nslab = C / bk;
   int splits = 1;
-  while (tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
+  while (!useg && tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
          (size_t)(splits * 2) * M * Nout * sizeof(float) <= ws_bytes)
     splits *= 2;
   int per = ceil_div(nslab, splits) * bk;
@@ -565,6 +579,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   else HOS_QG(128, 64, 64);
   else HOS_QG(64, 64, 64);
   else HOS_QG(256, 128, 32);
+  else throw Error(HOS_E_INVALID, "qgemm: no kernel for the chosen tile");
 #undef HOS_QG
   HOS_HIP_CHECK(hipGetLastError());
   if (splits > 1) {
