@@ -93,9 +93,12 @@ __global__ void __launch_bounds__(RB) rmsnorm_fwd_kernel(const float* __restrict
 }
 
 // dx += g·w·inv − inv³·x/d·Σ(g·w·x)
+// (hd != null: also the fp16 GEMM operand of the updated dx row, as to_h16 makes it)
 __global__ void __launch_bounds__(RB) rmsnorm_bwd_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                           const float* __restrict__ inv_in,
-                                                          const float* __restrict__ w, int d, float* __restrict__ dx) {
+                                                          const float* __restrict__ w, int d, float* __restrict__ dx,
+                                                          _Float16* __restrict__ hd, _Float16* __restrict__ hl,
+                                                          float* __restrict__ hr) {
   __shared__ float red[8];
   const int row = blockIdx.x;
   const float* gr = g + (long long)row * d;
@@ -107,6 +110,7 @@ __global__ void __launch_bounds__(RB) rmsnorm_bwd_kernel(const float* __restrict
   float k = inv * inv * inv / (float)d * s;
   float* dr = dx + (long long)row * d;
   for (int c = threadIdx.x; c < d; c += RB) dr[c] += gr[c] * w[c] * inv - xr[c] * k;
+  if (hd) block_row_h16(dr, d, hd + (long long)row * d, hl ? hl + (long long)row * d : nullptr, hr + row);
 }
 
 // RoPE on [M, ld] rows, heads at column col0 + h·hd. tab: (sin, cos) per (position, i), built on the host
@@ -397,8 +401,8 @@ void launch_rmsnorm_fwd(const float* x, const float* w, float eps, int M, int d,
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
-                        hipStream_t st) {
-  rmsnorm_bwd_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx);
+                        hipStream_t st, H16 out) {
+  rmsnorm_bwd_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,

@@ -6,8 +6,9 @@ namespace hos {
 void launch_embed(const QWeight& table, const int32_t* ids, float* x, int M, int d, hipStream_t st);
 void launch_rmsnorm_fwd(const float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
                         hipStream_t st);
+// out.data != null: also write dx's fp16 GEMM operand (as launch_to_h16 would)
 void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
-                        hipStream_t st);
+                        hipStream_t st, H16 out = H16{nullptr, nullptr, nullptr});
 void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,
                  bool inverse, int M, hipStream_t st);
 void launch_swiglu_fwd(const float* gu, int M, int F, float* h, H16 out, hipStream_t st);

@@ -43,6 +43,40 @@ __device__ __forceinline__ float deq_one(const QWeightView& w, long long r, long
   return deq_q6k(((const int8_t*)w.q)[i], w.s[i >> 4]);
 }
 
+// One row (this workgroup's) of f32 -> the fp16 GEMM operand with an exact power-of-two scale putting the row
+// max-abs in [2^14, 2^15): out = fp16(x·2^e), lo = fp16(x·2^e − out) (lo may be null), rinv = 2^-e. Every thread
+// of the workgroup calls it; it reads only the elements c ≡ threadIdx.x (mod blockDim.x) of xr.
+__device__ inline void block_row_h16(const float* xr, int K, _Float16* orow, _Float16* lrow, float* rinv) {
+  __shared__ float red[32];
+  float amax = 0.0f;
+  for (int c = threadIdx.x; c < K; c += blockDim.x) amax = fmaxf(amax, fabsf(xr[c]));
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float a = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) a = fmaxf(a, red[i]);
+    red[0] = a;
+  }
+  __syncthreads();
+  amax = red[0];
+  int e = 0;
+  if (amax > 0.0f && amax < 3.0e38f) {
+    int ex;
+    frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
+    e = 15 - ex;
+    e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  }
+  const float sc = ldexpf(1.0f, e);
+  if (threadIdx.x == 0) *rinv = ldexpf(1.0f, -e);
+  for (int c = threadIdx.x; c < K; c += blockDim.x) {
+    const float v = xr[c] * sc;
+    const _Float16 h = (_Float16)v;
+    orow[c] = h;
+    if (lrow) lrow[c] = (_Float16)(v - (float)h);
+  }
+}
+
 // ---- quant.hip ----
 size_t gguf_bytes_for(uint32_t t, size_t n);
 size_t block_elems(uint32_t t);

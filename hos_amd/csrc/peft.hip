@@ -620,10 +620,13 @@ struct hos_peft {
     }
     const QWeight& head = out_set ? out : tok;
     qdx(head, dl, V, M, dxn, d, 0, GemmEpi{}, phd);
+    // The RMSNorm backwards also write the fp16 operand of their dx for the GEMMs that follow; not where the
+    // RGA backward changes dx in between or a mixture-of-experts FFN takes no such operand.
+    const bool fuse16 = !rga && !E;
     {
-      Scope s(this, "rmsnorm", 0, 4.0 * M * d * 3 + 4.0 * M * d);
+      Scope s(this, "rmsnorm", 0, 4.0 * M * d * 3 + 4.0 * M * d + (fuse16 ? 6.0 * M * d : 0));
       launch_fill(dx, (long long)M * d, 0.0f, st);
-      launch_rmsnorm_bwd(dxn, xfinal, invf, out_norm, M, d, dx, st);
+      launch_rmsnorm_bwd(dxn, xfinal, invf, out_norm, M, d, dx, st, fuse16 ? hs : H16{nullptr, nullptr, nullptr});
     }
     for (int l = L - 1; l >= 0; l--) {
       LayerAct& a = act[l];
@@ -633,7 +636,7 @@ struct hos_peft {
       if (E) {
         moe_backward(l, M);
       } else {
-      to16(dx, d, M, d);
+      if (!fuse16) to16(dx, d, M, d);
       lora_grad_b(l, 3, dx, d, d, M);
       qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD), tpd[TD]);
       lora_grad_a(l, 3, a.h, F, M);
@@ -652,11 +655,10 @@ struct hos_peft {
       lora_grad_a(l, 2, a.xn2, d, M);
       }
       {
-        Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
-        launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st);
+        Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4 + 6.0 * M * d);
+        launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st, hs);
       }
       // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
-      to16(dx, d, M, d);
       lora_grad_b(l, 1, dx, d, d, M);
       qdx(w.w[TO], hs, d, M, dout, qd, 0, down_epi(l, TO), tpd[TO]);
       lora_grad_a(l, 1, a.o, qd, M);
@@ -684,8 +686,9 @@ struct hos_peft {
       qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV), tpd[TV]);
       lora_grad_a(l, 0, a.xn1, d, M);
       {
-        Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4);
-        launch_rmsnorm_bwd(dxn, a.x, a.inv1, w.attn_norm, M, d, dx, st);
+        const bool emit = fuse16 && l > 0;
+        Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4 + (emit ? 6.0 * M * d : 0));
+        launch_rmsnorm_bwd(dxn, a.x, a.inv1, w.attn_norm, M, d, dx, st, emit ? hs : H16{nullptr, nullptr, nullptr});
       }
     }
     if (rga) {

@@ -43,37 +43,8 @@ namespace {
 __global__ void to_h16_kernel(const float* __restrict__ x, long long ldx, int K, _Float16* __restrict__ out,
                               _Float16* __restrict__ lo, float* __restrict__ rinv) {
   const int row = blockIdx.x;
-  const float* xr = x + (long long)row * ldx;
-  float amax = 0.0f;
-  for (int c = threadIdx.x; c < K; c += blockDim.x) amax = fmaxf(amax, fabsf(xr[c]));
-  __shared__ float red[32];
-  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float a = 0.0f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); i++) a = fmaxf(a, red[i]);
-    red[0] = a;
-  }
-  __syncthreads();
-  amax = red[0];
-  int e = 0;
-  if (amax > 0.0f && amax < 3.0e38f) {
-    int ex;
-    frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
-    e = 15 - ex;
-    e = e > 100 ? 100 : (e < -100 ? -100 : e);
-  }
-  float sc = ldexpf(1.0f, e);
-  if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
-  _Float16* orow = out + (long long)row * K;
-  _Float16* lrow = lo ? lo + (long long)row * K : nullptr;
-  for (int c = threadIdx.x; c < K; c += blockDim.x) {
-    float v = xr[c] * sc;
-    _Float16 h = (_Float16)v;
-    orow[c] = h;
-    if (lrow) lrow[c] = (_Float16)(v - (float)h);
-  }
+  block_row_h16(x + (long long)row * ldx, K, out + (long long)row * K, lo ? lo + (long long)row * K : nullptr,
+                rinv + row);
 }
 
 
