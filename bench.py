@@ -222,7 +222,7 @@ def main():
         pm.step_dev(ids_dev, tg_dev, B, T, cfg.lr, 0.0, loss_dev)
     gpu.synchronize()
 
-    classes = ["qgemm_fwd", "qgemm_dx", "lora_down", "lora_db", "lora_du", "lora_da", "attn_fwd", "attn_bwd",
+    classes = ["qgemm_fwd", "qgemm_dx", "lora_down", "lora_du", "lora_dab", "attn_fwd", "attn_bwd",
                "rmsnorm", "swiglu", "rope", "ce", "adamw", "embed", "convert", "moe_route", "moe_combine", "rga"]
     # Breakdown pass (every kernel class timed with HIP events; not the timed region): finds the
     # dominant class and gives the per-class split.

@@ -166,24 +166,23 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
 // ---------------- cols: C(j, c) = α·Σ_m S[m, j]·G[m, c] ----------------
 // Workgroup: 64 columns of one segment × all j × an m-chunk; wave w takes the chunk's 4-row steps
 // w, w+4, … Lane (q, p): m = step + q, columns c0+4p .. +3 (one float4; component e is MFMA tile e).
+// bx: the workgroup's column block within its job; red: LDS of at least 2·NS·16·64 floats.
 template <int NS>
-__global__ void __launch_bounds__(256) lora_cols_kernel(int M, int ns, int mchunk, float alpha,
-                                                        const float* __restrict__ Sm, long long lds,
-                                                        const float* __restrict__ Gm, long long ldg, ColsSeg sg,
-                                                        float* __restrict__ C, long long scj, long long scc,
-                                                        float* part) {
+__device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, int mchunk, float* red, float* part) {
   constexpr int NJR = NS * 16, E = NJR * 64;
-  __shared__ float red[2 * E];
+  const ColsSeg& sg = jb.sg;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
   int t = 0;
 #pragma unroll
   for (int i = 1; i < 4; i++)
-    if (i < sg.nseg && (int)blockIdx.x >= sg.blk0[i]) t = i;
-  const int c0 = ((int)blockIdx.x - sg.blk0[t]) * 64, len = sg.len[t];
+    if (i < sg.nseg && bx >= sg.blk0[i]) t = i;
+  const int c0 = (bx - sg.blk0[t]) * 64, len = sg.len[t];
   const int mb = blockIdx.y * mchunk, me = min(M, mb + mchunk);
   const bool cv = c0 + 4 * p < len;
-  const float* gcol = Gm + sg.gbeg[t] + c0 + 4 * p;
-  const float* scol = Sm + sg.soff[t];
+  const float* gcol = jb.Gm + sg.gbeg[t] + c0 + 4 * p;
+  const float* scol = jb.Sm + sg.soff[t];
+  const long long lds = jb.lds, ldg = jb.ldg;
+  const int ns = jb.ns;
 
   f4v acc[NS][4];
 #pragma unroll
@@ -224,11 +223,29 @@ __global__ void __launch_bounds__(256) lora_cols_kernel(int M, int ns, int mchun
     const int i = idx & 3, e = (idx >> 2) & 3, js = idx >> 4;
     return (16 * js + 4 * q + i) * 64 + 4 * p + e;
   });
-  const long long ocol = sg.ocol[t];
-  finish_block(red, E, part, [&](int e, float val) {
-    const int j = e / 64, c = c0 + e % 64;
-    if (j < ns && c < len) C[(long long)j * scj + (ocol + c) * scc] = alpha * val;
-  });
+  if (gridDim.y == 1) {
+    const long long ocol = sg.ocol[t];
+    for (int e = threadIdx.x; e < E; e += 256) {
+      const int j = e / 64, c = c0 + e % 64;
+      if (j < ns && c < len) jb.C[(long long)j * jb.scj + (ocol + c) * jb.scc] = jb.alpha * red[e];
+    }
+    return;
+  }
+  // this split's partial of the block: job region, then [split][block][E]
+  float* mine = part + jb.part_off + ((long long)blockIdx.y * jb.gx + bx) * E;
+  for (int e = threadIdx.x; e < E; e += 256) mine[e] = red[e];
+}
+
+// Two independent jobs over the same contraction length in one launch: workgroups [0, b.bx0) run job a with
+// NSA row tiles, the rest job b with NSB. A single job passes b with bx0 = the grid width.
+template <int NSA, int NSB>
+__global__ void __launch_bounds__(256) lora_cols_kernel(int M, int mchunk, ColsJobDev a, ColsJobDev b, float* part) {
+  constexpr int EMAX = (NSA > NSB ? NSA : NSB) * 16 * 64;
+  __shared__ float red[2 * EMAX];
+  if ((int)blockIdx.x < b.bx0)
+    cols_body<NSA>(a, (int)blockIdx.x, M, mchunk, red, part);
+  else
+    cols_body<NSB>(b, (int)blockIdx.x - b.bx0, M, mchunk, red, part);
 }
 
 // Separate-launch reductions of the partials (one thread per output element of every block).
@@ -241,18 +258,26 @@ __global__ void lora_rows_reduce(const float* __restrict__ part, int S, int gx, 
   if (row >= M || c >= n) return;
   C[(long long)row * ldc + c] = alpha * sum_parts(part, S, gx, bx, E, e);
 }
-__global__ void lora_cols_reduce(const float* __restrict__ part, int S, int gx, int NJR, int ns, ColsSeg sg,
-                                 float alpha, float* __restrict__ C, long long scj, long long scc) {
-  const int E = NJR * 64;
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)gx * E) return;
+// One thread per output element of every block of both jobs (job a's elements first).
+__device__ __forceinline__ void cols_reduce_one(const ColsJobDev& jb, const float* part, int S, long long i) {
+  const int E = jb.nsr * 64;
   const int bx = (int)(i / E), e = (int)(i % E);
+  const ColsSeg& sg = jb.sg;
   int t = 0;
   for (int k = 1; k < sg.nseg; k++)
     if (bx >= sg.blk0[k]) t = k;
   const int j = e / 64, c = (bx - sg.blk0[t]) * 64 + e % 64;
-  if (j >= ns || c >= sg.len[t]) return;
-  C[(long long)j * scj + ((long long)sg.ocol[t] + c) * scc] = alpha * sum_parts(part, S, gx, bx, E, e);
+  if (j >= jb.ns || c >= sg.len[t]) return;
+  jb.C[(long long)j * jb.scj + ((long long)sg.ocol[t] + c) * jb.scc] =
+      jb.alpha * sum_parts(part + jb.part_off, S, jb.gx, bx, E, e);
+}
+__global__ void lora_cols_reduce(const float* __restrict__ part, int S, ColsJobDev a, ColsJobDev b) {
+  const long long na = (long long)a.gx * a.nsr * 64, nb = (long long)b.gx * b.nsr * 64;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < na)
+    cols_reduce_one(a, part, S, i);
+  else if (i < na + nb)
+    cols_reduce_one(b, part, S, i - na);
 }
 
 int ceil_div_i(long long a, long long b) { return (int)((a + b - 1) / b); }
@@ -306,41 +331,87 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
   }
 }
 
+namespace {
+// Device form of a job: segment blocks laid out, row tiles (nsr = 16·NS) and partial region assigned.
+ColsJobDev prepare(const ColsJob& j, int bx0) {
+  ColsJobDev d{};
+  HOS_REQUIRE(j.ns > 0 && j.ns <= 96 && j.sg.nseg > 0 && j.sg.nseg <= 4, HOS_E_INVALID,
+              "lora_cols: ns must be in 1..96, 1 to 4 segments");
+  HOS_REQUIRE(j.ldg % 4 == 0 && ((uintptr_t)j.Gm & 15) == 0, HOS_E_INVALID, "lora_cols: G must be 16-byte aligned");
+  d.Sm = j.Sm;
+  d.Gm = j.Gm;
+  d.C = j.C;
+  d.lds = j.lds;
+  d.ldg = j.ldg;
+  d.scj = j.scj;
+  d.scc = j.scc;
+  d.alpha = j.alpha;
+  d.ns = j.ns;
+  d.nsr = (j.ns + 15) / 16 * 16;
+  d.sg = j.sg;
+  int gx = 0;
+  for (int t = 0; t < j.sg.nseg; t++) {
+    HOS_REQUIRE(j.sg.gbeg[t] % 4 == 0 && j.sg.len[t] % 4 == 0 && j.sg.len[t] > 0, HOS_E_INVALID,
+                "lora_cols: segment columns must be multiples of 4");
+    d.sg.blk0[t] = gx;
+    gx += ceil_div_i(j.sg.len[t], 64);
+  }
+  d.gx = gx;
+  d.bx0 = bx0;
+  return d;
+}
+}  // namespace
+
+void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float* ws, size_t ws_bytes, hipStream_t st) {
+  if (M <= 0) return;
+  ColsJobDev a = prepare(ja, 0);
+  ColsJobDev b{};
+  if (jb) {
+    b = prepare(*jb, a.gx);
+  } else {
+    b = a;  // never run: its block range is empty
+    b.bx0 = a.gx;
+    b.gx = 0;
+  }
+  const int gx = a.gx + b.gx;
+  int S = std::max(1, std::min(ceil_div_i(split_target(), gx), ceil_div_i(M, 16)));
+  int mchunk = ceil_div_i(ceil_div_i(M, S), 16) * 16;
+  S = std::max(1, ceil_div_i(M, mchunk));
+  a.part_off = 0;
+  b.part_off = (long long)S * a.gx * a.nsr * 64;
+  const long long need = b.part_off + (long long)S * b.gx * b.nsr * 64;
+  HOS_REQUIRE(S == 1 || (size_t)need * 4 <= ws_bytes, HOS_E_INVALID, "lora_cols: workspace too small");
+  const int NA = a.nsr / 16, NB = jb ? b.nsr / 16 : NA;
+  dim3 grid(gx, S);
+#define COLS(X, Y)                                                                  \
+  if (NA == X && NB == Y) {                                                         \
+    lora_cols_kernel<X, Y><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, ws);         \
+    launched = true;                                                                \
+  }
+  bool launched = false;
+  COLS(1, 1) COLS(2, 2) COLS(3, 3) COLS(4, 4) COLS(5, 5) COLS(6, 6) COLS(1, 2) COLS(1, 3) COLS(2, 4) COLS(2, 6)
+#undef COLS
+  if (!launched) {
+    // width pair without a combined kernel: run the jobs one after the other
+    HOS_REQUIRE(jb != nullptr, HOS_E_INVALID, "lora_cols: bad width");
+    launch_lora_cols2(M, ja, nullptr, ws, ws_bytes, st);
+    launch_lora_cols2(M, *jb, nullptr, ws, ws_bytes, st);
+    return;
+  }
+  HOS_HIP_CHECK(hipGetLastError());
+  if (S > 1) {
+    const long long tot = (long long)a.gx * a.nsr * 64 + (long long)b.gx * b.nsr * 64;
+    lora_cols_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, a, b);
+    HOS_HIP_CHECK(hipGetLastError());
+  }
+}
+
 void launch_lora_cols(long long M, int ns, float alpha, const float* Sm, long long lds, const float* Gm, long long ldg,
                       ColsSeg sg, float* C, long long scj, long long scc, float* ws, size_t ws_bytes,
                       hipStream_t st) {
   if (M <= 0 || ns <= 0 || sg.nseg <= 0) return;
-  HOS_REQUIRE(ns <= 96 && sg.nseg <= 4, HOS_E_INVALID, "lora_cols: ns must be <= 96, at most 4 segments");
-  HOS_REQUIRE(ldg % 4 == 0 && ((uintptr_t)Gm & 15) == 0, HOS_E_INVALID, "lora_cols: G must be 16-byte aligned");
-  int gx = 0;
-  for (int t = 0; t < sg.nseg; t++) {
-    HOS_REQUIRE(sg.gbeg[t] % 4 == 0 && sg.len[t] % 4 == 0 && sg.len[t] > 0, HOS_E_INVALID,
-                "lora_cols: segment columns must be multiples of 4");
-    sg.blk0[t] = gx;
-    gx += ceil_div_i(sg.len[t], 64);
-  }
-  int S = std::max(1, std::min(ceil_div_i(split_target(), gx), ceil_div_i(M, 16)));
-  int mchunk = ceil_div_i(ceil_div_i(M, S), 16) * 16;
-  S = std::max(1, ceil_div_i(M, mchunk));
-  const int NS = (ns + 15) / 16;
-  HOS_REQUIRE(S == 1 || (size_t)S * gx * NS * 16 * 64 * 4 <= ws_bytes, HOS_E_INVALID, "lora_cols: workspace too small");
-  dim3 grid(gx, S);
-#define COLS(NSV)                                                                                            \
-  case NSV:                                                                                                  \
-    lora_cols_kernel<NSV><<<grid, 256, 0, st>>>((int)M, ns, mchunk, alpha, Sm, lds, Gm, ldg, sg, C, scj, scc, \
-                                                ws);                                                \
-    break;
-  switch (NS) {
-    COLS(1) COLS(2) COLS(3) COLS(4) COLS(5) COLS(6)
-    default: throw Error(HOS_E_INVALID, "lora_cols: bad width");
-  }
-#undef COLS
-  HOS_HIP_CHECK(hipGetLastError());
-  if (S > 1) {
-    const long long tot = (long long)gx * NS * 16 * 64;
-    lora_cols_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, NS * 16, ns, sg, alpha, C, scj, scc);
-    HOS_HIP_CHECK(hipGetLastError());
-  }
+  ColsJob j{ns, alpha, Sm, lds, Gm, ldg, sg, C, scj, scc};
+  launch_lora_cols2(M, j, nullptr, ws, ws_bytes, st);
 }
 
 }  // namespace hos

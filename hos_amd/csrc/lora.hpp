@@ -30,4 +30,31 @@ void launch_lora_cols(long long M, int ns, float alpha, const float* Sm, long lo
                       ColsSeg sg, float* C, long long scj, long long scc, float* ws, size_t ws_bytes,
                       hipStream_t st);
 
+// One cols product as a job (the arguments of launch_lora_cols).
+struct ColsJob {
+  int ns = 0;
+  float alpha = 1.0f;
+  const float* Sm = nullptr;
+  long long lds = 0;
+  const float* Gm = nullptr;
+  long long ldg = 0;
+  ColsSeg sg;
+  float* C = nullptr;
+  long long scj = 0, scc = 0;
+};
+// Kernel-side job: the above with its block range and partial-sum region.
+struct ColsJobDev {
+  const float* Sm;
+  const float* Gm;
+  float* C;
+  long long lds, ldg, scj, scc, part_off;
+  float alpha;
+  int ns, nsr, gx, bx0;
+  ColsSeg sg;
+};
+// Two independent cols products over the same M in one launch (and one reduction launch); b may be null.
+// Deterministic: the split of M depends only on M and the combined block count, and every output element sums
+// its split partials in split order.
+void launch_lora_cols2(long long M, const ColsJob& a, const ColsJob* b, float* ws, size_t ws_bytes, hipStream_t st);
+
 }  // namespace hos

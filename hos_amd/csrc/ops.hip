@@ -215,21 +215,22 @@ int hos_hip_lora(hos_ctx* c, const float* x, const float* dy, size_t rows, size_
     if (y)
       launch_gemm_f32((long long)rows, (long long)out, r, scale, u, r, 1, B, (long long)out, 1, 1.0f, y,
                       (long long)out, ws, wsb, st);
-    ColsSeg cb;
-    cb.nseg = 1;
-    cb.len[0] = (int)out;
-    launch_lora_cols((long long)rows, r, scale, u, r, dy, (long long)out, cb, dB, (long long)out, 1, ws, wsb, st);
     RowsSeg up;
     up.nt = 1;
     up.r = r;
     up.kend[0] = (int)out;
     launch_lora_rows((long long)rows, (long long)out, scale, dy, (long long)out, B, (long long)out, up, du, r, ws, wsb,
                      st);
+    // dB = s·uᵀ·dy and dAᵀ = duᵀ·x in one launch
+    ColsSeg cb;
+    cb.nseg = 1;
+    cb.len[0] = (int)out;
     ColsSeg ca;
     ca.nseg = 1;
     ca.len[0] = (int)in;
-    launch_lora_cols((long long)rows, r, 1.0f, du, r, x, (long long)in, ca, (float*)at.p, (long long)in, 1, ws, wsb,
-                     st);
+    const ColsJob jdb{r, scale, u, r, dy, (long long)out, cb, dB, (long long)out, 1};
+    const ColsJob jda{r, 1.0f, du, r, x, (long long)in, ca, (float*)at.p, (long long)in, 1};
+    launch_lora_cols2((long long)rows, jdb, &jda, ws, wsb, st);
     transpose((const float*)at.p, r, (int)in, dA, st);
     if (dx)
       launch_gemm_f32((long long)rows, (long long)in, r, 1.0f, du, r, 1, A, 1, r, 1.0f, dx, (long long)in, ws, wsb,

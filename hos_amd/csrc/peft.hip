@@ -73,6 +73,8 @@ struct hos_peft {
   std::string err;
   int d = 0, qd = 0, kvd = 0, W3 = 0, F = 0, V = 0, r = 0, L = 0, Mmax = 0, passes = 3;
   int pf = 3, pd = 3, phf = 3, phd = 3;  // precision mode per GEMM site: layer fwd / dX, head fwd / dX
+  ColsJob pend_db;       // dB of the group whose backward is in progress, launched with its dA
+  int pend_group = -1;
   int tpf[7] = {0, 0, 0, 0, 0, 0, 0}, tpd[7] = {0, 0, 0, 0, 0, 0, 0};  // per-target overrides (0 = site mode)
   float lscale = 0.0f;
 
@@ -386,7 +388,8 @@ struct hos_peft {
   }
 
   // From dy, the gradient of the group's fused projection output (row stride ldy, target t at column
-  // ycol(t)): dB_t = s·u_tᵀ·dy_t for every adapted t (one launch), du_t = s·dy_t·B_tᵀ (one launch).
+  // ycol(t)): du_t = s·dy_t·B_tᵀ for every adapted t (one launch). dB_t = s·u_tᵀ·dy_t is queued and launched with
+  // the group's dA by lora_grad_a: dy, u, x and du are all unchanged in between.
   void lora_grad_b(int l, int g, const float* dy, long long ldy, long long kspan, int M) {
     const int n = gcount(g);
     if (n == 0) return;
@@ -406,9 +409,10 @@ struct hos_peft {
       rs.boff[i] = bcol(t);
     }
     const int w = bw(g);
-    lora_cols("lora_db", M, r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1);
     lora_rows("lora_du", M, kspan, lscale, dy, ldy, P + offBg[l * 4 + g], w, rs, du + ucol(first_adapted(g)),
               NT * r);
+    pend_db = ColsJob{r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1};
+    pend_group = g;
   }
   // Epilogue term dx_in += du_t·A_tᵀ of the base dX GEMM: L(j, col) = At[(slot·r + j)·in + col]
   GemmEpi down_epi(int l, int t) {
@@ -423,17 +427,26 @@ struct hos_peft {
     e.scale = 1.0f;
     return e;
   }
-  // [dA_1 … dA_G]ᵀ = ([du_1 … du_G])ᵀ·x, written straight into the stacked At layout
+  // [dA_1 … dA_G]ᵀ = ([du_1 … du_G])ᵀ·x, written straight into the stacked At layout, in one launch with the
+  // group's queued dB
   void lora_grad_a(int l, int g, const float* x, long long ldx, int M) {
     const int n = gcount(g);
     if (n == 0) return;
+    HOS_REQUIRE(pend_group == g, HOS_E_INVALID, "peft: dA without the group's dB queued");
+    pend_group = -1;
     const int first = first_adapted(g), in = in_dim(first);
     ColsSeg cs;
     cs.nseg = 1;
     cs.len[0] = in;
-    lora_cols("lora_da", M, n * r, 1.0f, du + ucol(first), NT * r, x, ldx, cs, G + offAg[l * 4 + g], in, 1);
+    const ColsJob da{n * r, 1.0f, du + ucol(first), NT * r, x, ldx, cs, G + offAg[l * 4 + g], in, 1};
+    double fl = 2.0 * M * n * r * in, by = 4.0 * (M * (double)in + (double)M * n * r + (double)n * r * in);
+    for (int t = 0; t < pend_db.sg.nseg; t++) {
+      fl += 2.0 * M * r * pend_db.sg.len[t];
+      by += 4.0 * ((double)M * pend_db.sg.len[t] + (double)M * r + (double)r * pend_db.sg.len[t]);
+    }
+    Scope s(this, "lora_dab", fl, by);
+    launch_lora_cols2(M, pend_db, &da, ws, ws_bytes, st);
   }
-
   void check_ready() {
     check_tensors();
     build_stacks();
