@@ -77,17 +77,23 @@ __device__ __forceinline__ void finish_block(const float* red, int E, float* par
 }
 
 // ---------------- rows: C[M, n] = α·X·Bᵀ ----------------
-// Workgroup: 32 rows × all n columns × a k-chunk; wave w takes the chunk's 16-wide k steps w, w+4, …
+// Workgroup: 16·RT rows × all n columns × a k-chunk; wave w takes the chunk's 16-wide k steps w, w+4, …
 // Lane (q = lane/16, p = lane%16): rows m0+16t+p, k-slot q (k = step + 4q .. +3 as one float4).
-template <int NJ>
+#ifndef HOS_ROWS_UNROLL
+#define HOS_ROWS_UNROLL 2
+#endif
+#ifndef HOS_COLS_UNROLL
+#define HOS_COLS_UNROLL 4
+#endif
+template <int NJ, int RT = 2>
 __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk, float alpha,
                                                         const float* __restrict__ X, long long ldx,
                                                         const float* __restrict__ Bt, long long ldb, RowsSeg sg,
                                                         float* __restrict__ C, long long ldc, float* part) {
-  constexpr int NC = NJ * 16, E = 32 * NC;
+  constexpr int NC = NJ * 16, E = 16 * RT * NC;
   __shared__ float red[2 * E];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
-  const int m0 = blockIdx.x * 32;
+  const int m0 = blockIdx.x * 16 * RT;
   const int kb = blockIdx.y * kchunk, ke = min(K, kb + kchunk);
   const int n = sg.nt * sg.r;
 
@@ -107,48 +113,57 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
       khi[jt] = 0;
     }
   }
-  const float* xr[2];
-  bool rv[2];
+  const float* xr[RT];
+  bool rv[RT];
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
+  for (int t = 0; t < RT; t++) {
     const int row = m0 + 16 * t + p;
     rv[t] = row < M;
     xr[t] = X + (long long)(rv[t] ? row : 0) * ldx;
   }
 
-  f4v acc[2][NJ];
+  f4v acc[RT][NJ];
 #pragma unroll
-  for (int t = 0; t < 2; t++)
+  for (int t = 0; t < RT; t++)
 #pragma unroll
     for (int jt = 0; jt < NJ; jt++) acc[t][jt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll 2
-  for (int k = kb + 16 * wave; k < ke; k += 64) {
-    const int kk = k + 4 * q;
-    const bool kin = kk < ke;
-    float4 xa[2], bv[NJ];
+  // HOS_ROWS_UNROLL k steps per trip, every load issued before the MFMAs that use them (the compiler does not
+  // unroll a loop around convergent MFMA builtins with a runtime trip count). Out-of-range steps load zeros and
+  // add exact zeros: each accumulator sums the same products in the same order as one step per trip.
+  constexpr int U = HOS_ROWS_UNROLL;
+  for (int k0 = kb + 16 * wave; k0 < ke; k0 += 64 * U) {
+    float4 xa[U][RT], bv[U][NJ];
 #pragma unroll
-    for (int t = 0; t < 2; t++)
-      xa[t] = (rv[t] && kin) ? *reinterpret_cast<const float4*>(xr[t] + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < U; u++) {
+      const int kk = k0 + 64 * u + 4 * q;
+      const bool kin = kk < ke;
 #pragma unroll
-    for (int jt = 0; jt < NJ; jt++)
-      bv[jt] = (kin && kk >= klo[jt] && kk < khi[jt]) ? *reinterpret_cast<const float4*>(bp[jt] + kk)
-                                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int t = 0; t < RT; t++)
+        xa[u][t] = (rv[t] && kin) ? *reinterpret_cast<const float4*>(xr[t] + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+      for (int jt = 0; jt < NJ; jt++)
+        bv[u][jt] = (kin && kk >= klo[jt] && kk < khi[jt]) ? *reinterpret_cast<const float4*>(bp[jt] + kk)
+                                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
-      for (int jt = 0; jt < NJ; jt++) {
-        acc[t][jt] = mfma16(xa[t].x, bv[jt].x, acc[t][jt]);
-        acc[t][jt] = mfma16(xa[t].y, bv[jt].y, acc[t][jt]);
-        acc[t][jt] = mfma16(xa[t].z, bv[jt].z, acc[t][jt]);
-        acc[t][jt] = mfma16(xa[t].w, bv[jt].w, acc[t][jt]);
-      }
+    for (int u = 0; u < U; u++)
+      if (k0 + 64 * u < ke)  // wave-uniform
+#pragma unroll
+      for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int jt = 0; jt < NJ; jt++) {
+          acc[t][jt] = mfma16(xa[u][t].x, bv[u][jt].x, acc[t][jt]);
+          acc[t][jt] = mfma16(xa[u][t].y, bv[u][jt].y, acc[t][jt]);
+          acc[t][jt] = mfma16(xa[u][t].z, bv[u][jt].z, acc[t][jt]);
+          acc[t][jt] = mfma16(xa[u][t].w, bv[u][jt].w, acc[t][jt]);
+        }
   }
 
   // flatten: element (row 16t+4q+i, col 16jt+p) of the 32×NC block
-  float v[2 * NJ * 4];
+  float v[RT * NJ * 4];
 #pragma unroll
-  for (int t = 0; t < 2; t++)
+  for (int t = 0; t < RT; t++)
 #pragma unroll
     for (int jt = 0; jt < NJ; jt++)
 #pragma unroll
@@ -190,25 +205,33 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
 #pragma unroll
     for (int e = 0; e < 4; e++) acc[js][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll 4
-  for (int m4 = mb + 4 * wave; m4 < me; m4 += 16) {
-    const int m = m4 + q;
-    const bool mv = m < me;
-    const float4 g = (mv && cv) ? *reinterpret_cast<const float4*>(gcol + (long long)m * ldg)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-    float s[NS];
+  // HOS_COLS_UNROLL 4-row steps per trip, loads first (as in the rows kernel; zero steps past the end add
+  // exact zeros, so the summation order per accumulator is that of one step per trip).
+  constexpr int U = HOS_COLS_UNROLL;
+  for (int m40 = mb + 4 * wave; m40 < me; m40 += 16 * U) {
+    float4 g[U];
+    float s[U][NS];
 #pragma unroll
-    for (int js = 0; js < NS; js++) {
-      const int j = js * 16 + p;
-      s[js] = (mv && j < ns) ? scol[(long long)m * lds + j] : 0.0f;
+    for (int u = 0; u < U; u++) {
+      const int m = m40 + 16 * u + q;
+      const bool mv = m < me;
+      g[u] = (mv && cv) ? *reinterpret_cast<const float4*>(gcol + (long long)m * ldg) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int js = 0; js < NS; js++) {
+        const int j = js * 16 + p;
+        s[u][js] = (mv && j < ns) ? scol[(long long)m * lds + j] : 0.0f;
+      }
     }
 #pragma unroll
-    for (int js = 0; js < NS; js++) {
-      acc[js][0] = mfma16(s[js], g.x, acc[js][0]);
-      acc[js][1] = mfma16(s[js], g.y, acc[js][1]);
-      acc[js][2] = mfma16(s[js], g.z, acc[js][2]);
-      acc[js][3] = mfma16(s[js], g.w, acc[js][3]);
-    }
+    for (int u = 0; u < U; u++)
+      if (m40 + 16 * u < me)  // wave-uniform
+#pragma unroll
+      for (int js = 0; js < NS; js++) {
+        acc[js][0] = mfma16(s[u][js], g[u].x, acc[js][0]);
+        acc[js][1] = mfma16(s[u][js], g[u].y, acc[js][1]);
+        acc[js][2] = mfma16(s[u][js], g[u].z, acc[js][2]);
+        acc[js][3] = mfma16(s[u][js], g[u].w, acc[js][3]);
+      }
   }
 
   // flatten: element (j = 16js+4q+i, column 4p+e) of the NJR×64 block
@@ -249,12 +272,12 @@ __global__ void __launch_bounds__(256) lora_cols_kernel(int M, int mchunk, ColsJ
 }
 
 // Separate-launch reductions of the partials (one thread per output element of every block).
-__global__ void lora_rows_reduce(const float* __restrict__ part, int S, int gx, int NC, int M, int n, float alpha,
-                                 float* __restrict__ C, long long ldc) {
-  const int E = 32 * NC;
+__global__ void lora_rows_reduce(const float* __restrict__ part, int S, int gx, int RB, int NC, int M, int n,
+                                 float alpha, float* __restrict__ C, long long ldc) {
+  const int E = RB * NC;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long long)gx * E) return;
-  const int bx = (int)(i / E), e = (int)(i % E), rr = e / NC, c = e % NC, row = bx * 32 + rr;
+  const int bx = (int)(i / E), e = (int)(i % E), rr = e / NC, c = e % NC, row = bx * RB + rr;
   if (row >= M || c >= n) return;
   C[(long long)row * ldc + c] = alpha * sum_parts(part, S, gx, bx, E, e);
 }
@@ -326,7 +349,7 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
   HOS_HIP_CHECK(hipGetLastError());
   if (S > 1) {
     const long long tot = (long long)gx * 32 * NJ * 16;
-    lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, NJ * 16, (int)M, n, alpha, C, ldc);
+    lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, 32, NJ * 16, (int)M, n, alpha, C, ldc);
     HOS_HIP_CHECK(hipGetLastError());
   }
 }
