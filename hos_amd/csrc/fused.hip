@@ -200,6 +200,243 @@ __global__ void __launch_bounds__(RB) swiglu_bwd_kernel(const float* __restrict_
   if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
 }
 
+// Register-resident variants of the two kernels above for F % 4 == 0, F <= 4·RB·NV: each thread loads its
+// float4 columns once (i = tid + RB·j), so the row is read from HBM once and the fp16 pass works from
+// registers; the same per-element arithmetic and the same row max, hence the same outputs.
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void put_h16x4(float4 v, _Float16* hi, _Float16* lo, long long i) {
+  h16x4 h{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  *reinterpret_cast<h16x4*>(hi + i) = h;
+  if (lo) {
+    h16x4 l{(_Float16)(v.x - (float)h.x), (_Float16)(v.y - (float)h.y), (_Float16)(v.z - (float)h.z),
+            (_Float16)(v.w - (float)h.w)};
+    *reinterpret_cast<h16x4*>(lo + i) = l;
+  }
+}
+__device__ __forceinline__ float4 scale4(float4 v, float s) { return make_float4(v.x * s, v.y * s, v.z * s, v.w * s); }
+__device__ __forceinline__ float amax4(float a, float4 v) {
+  return fmaxf(fmaxf(a, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+constexpr int SWIGLU_NV = 8;
+
+__global__ void __launch_bounds__(RB) swiglu_fwd_reg_kernel(const float* __restrict__ gu, int F,
+                                                             float* __restrict__ h, _Float16* __restrict__ hh,
+                                                             _Float16* __restrict__ hl, float* __restrict__ rinv) {
+  __shared__ float red[8];
+  const int row = blockIdx.x, F4 = F >> 2;
+  const float4* g = reinterpret_cast<const float4*>(gu + (long long)row * 2 * F);
+  const float4* u = g + F4;
+  float4 gv[SWIGLU_NV], uv[SWIGLU_NV];
+#pragma unroll
+  for (int j = 0; j < SWIGLU_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < F4) {
+      gv[j] = g[i];
+      uv[j] = u[i];
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SWIGLU_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < F4) {
+      const float4 v = make_float4(silu_f(gv[j].x) * uv[j].x, silu_f(gv[j].y) * uv[j].y, silu_f(gv[j].z) * uv[j].z,
+                                   silu_f(gv[j].w) * uv[j].w);
+      gv[j] = v;
+      amax = amax4(amax, v);
+      if (h) reinterpret_cast<float4*>(h + (long long)row * F)[i] = v;
+    }
+  }
+  amax = block_max(amax, red);
+  const int e = row_exp(amax);
+  const float sc = ldexpf(1.0f, e);
+#pragma unroll
+  for (int j = 0; j < SWIGLU_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < F4) put_h16x4(scale4(gv[j], sc), hh, hl, (long long)row * F + 4 * i);
+  }
+  if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
+}
+
+__device__ __forceinline__ void swiglu_vjp(float x, float uu, float dd, float& dg, float& du) {
+  float s = 1.0f / (1.0f + expf(-x));
+  dg = dd * uu * (s + x * s * (1.0f - s));
+  du = dd * (x / (1.0f + expf(-x)));
+}
+
+__global__ void __launch_bounds__(RB) swiglu_bwd_reg_kernel(const float* __restrict__ gu,
+                                                             const float* __restrict__ dh, int F,
+                                                             float* __restrict__ dgu, _Float16* __restrict__ dgh,
+                                                             _Float16* __restrict__ dgl, float* __restrict__ rinv) {
+  __shared__ float red[8];
+  const int row = blockIdx.x, F4 = F >> 2;
+  const float4* g = reinterpret_cast<const float4*>(gu + (long long)row * 2 * F);
+  const float4* u = g + F4;
+  const float4* d = reinterpret_cast<const float4*>(dh + (long long)row * F);
+  float4 gv[SWIGLU_NV], uv[SWIGLU_NV];
+  {
+    float4 dv[SWIGLU_NV];
+#pragma unroll
+    for (int j = 0; j < SWIGLU_NV; j++) {
+      const int i = threadIdx.x + RB * j;
+      if (i < F4) {
+        gv[j] = g[i];
+        uv[j] = u[i];
+        dv[j] = d[i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < SWIGLU_NV; j++) {
+      const int i = threadIdx.x + RB * j;
+      if (i < F4) {
+        float4 a, b;
+        swiglu_vjp(gv[j].x, uv[j].x, dv[j].x, a.x, b.x);
+        swiglu_vjp(gv[j].y, uv[j].y, dv[j].y, a.y, b.y);
+        swiglu_vjp(gv[j].z, uv[j].z, dv[j].z, a.z, b.z);
+        swiglu_vjp(gv[j].w, uv[j].w, dv[j].w, a.w, b.w);
+        gv[j] = a;  // d gate
+        uv[j] = b;  // d up
+      }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SWIGLU_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < F4) {
+      amax = amax4(amax4(amax, gv[j]), uv[j]);
+      if (dgu) {
+        float4* o = reinterpret_cast<float4*>(dgu + (long long)row * 2 * F);
+        o[i] = gv[j];
+        o[F4 + i] = uv[j];
+      }
+    }
+  }
+  amax = block_max(amax, red);
+  const int e = row_exp(amax);
+  const float sc = ldexpf(1.0f, e);
+#pragma unroll
+  for (int j = 0; j < SWIGLU_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < F4) {
+      put_h16x4(scale4(gv[j], sc), dgh, dgl, (long long)row * 2 * F + 4 * i);
+      put_h16x4(scale4(uv[j], sc), dgh, dgl, (long long)row * 2 * F + F + 4 * i);
+    }
+  }
+  if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
+}
+
+// Register-resident RMSNorm forward / backward for d % 4 == 0, d <= 4·RB·NORM_NV (same per-element arithmetic as
+// the kernels above; the row sums are taken over each thread's float4 columns, then across the block).
+constexpr int NORM_NV = 4;
+
+__global__ void __launch_bounds__(RB) rmsnorm_fwd_reg_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                              float eps, int d, float* __restrict__ xn,
+                                                              _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                              float* __restrict__ rinv,
+                                                              float* __restrict__ inv_out) {
+  __shared__ float red[8];
+  const int row = blockIdx.x, d4 = d >> 2;
+  const float4* xr = reinterpret_cast<const float4*>(x + (long long)row * d);
+  float4 xv[NORM_NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NORM_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < d4) {
+      xv[j] = xr[i];
+      ss += xv[j].x * xv[j].x;
+      ss += xv[j].y * xv[j].y;
+      ss += xv[j].z * xv[j].z;
+      ss += xv[j].w * xv[j].w;
+    }
+  }
+  ss = block_sum(ss, red) / (float)d;
+  const float inv = 1.0f / sqrtf(ss + eps);
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NORM_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < d4) {
+      const float4 wv = reinterpret_cast<const float4*>(w)[i];
+      const float4 y = make_float4(xv[j].x * inv * wv.x, xv[j].y * inv * wv.y, xv[j].z * inv * wv.z,
+                                   xv[j].w * inv * wv.w);
+      xv[j] = y;
+      amax = amax4(amax, y);
+      if (xn) reinterpret_cast<float4*>(xn + (long long)row * d)[i] = y;
+    }
+  }
+  amax = block_max(amax, red);
+  const int e = row_exp(amax);
+  const float sc = ldexpf(1.0f, e);
+#pragma unroll
+  for (int j = 0; j < NORM_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < d4) put_h16x4(scale4(xv[j], sc), xh, xl, (long long)row * d + 4 * i);
+  }
+  if (threadIdx.x == 0) {
+    rinv[row] = ldexpf(1.0f, -e);
+    inv_out[row] = inv;
+  }
+}
+
+__global__ void __launch_bounds__(RB) rmsnorm_bwd_reg_kernel(const float* __restrict__ g, const float* __restrict__ x,
+                                                              const float* __restrict__ inv_in,
+                                                              const float* __restrict__ w, int d,
+                                                              float* __restrict__ dx, _Float16* __restrict__ hd,
+                                                              _Float16* __restrict__ hl, float* __restrict__ hr) {
+  __shared__ float red[8];
+  const int row = blockIdx.x, d4 = d >> 2;
+  const float4* gr = reinterpret_cast<const float4*>(g + (long long)row * d);
+  const float4* xr = reinterpret_cast<const float4*>(x + (long long)row * d);
+  float4* dr = reinterpret_cast<float4*>(dx + (long long)row * d);
+  float4 gw[NORM_NV], xv[NORM_NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NORM_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < d4) {
+      const float4 wv = reinterpret_cast<const float4*>(w)[i];
+      const float4 gv = gr[i];
+      xv[j] = xr[i];
+      gw[j] = make_float4(gv.x * wv.x, gv.y * wv.y, gv.z * wv.z, gv.w * wv.w);
+      s += gw[j].x * xv[j].x;
+      s += gw[j].y * xv[j].y;
+      s += gw[j].z * xv[j].z;
+      s += gw[j].w * xv[j].w;
+    }
+  }
+  s = block_sum(s, red);
+  const float inv = inv_in[row];
+  const float k = inv * inv * inv / (float)d * s;
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NORM_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < d4) {
+      float4 o = dr[i];
+      o.x += gw[j].x * inv - xv[j].x * k;
+      o.y += gw[j].y * inv - xv[j].y * k;
+      o.z += gw[j].z * inv - xv[j].z * k;
+      o.w += gw[j].w * inv - xv[j].w * k;
+      dr[i] = o;
+      xv[j] = o;
+      amax = amax4(amax, o);
+    }
+  }
+  if (!hd) return;
+  amax = block_max(amax, red);
+  const int e = row_exp(amax);
+  const float sc = ldexpf(1.0f, e);
+#pragma unroll
+  for (int j = 0; j < NORM_NV; j++) {
+    const int i = threadIdx.x + RB * j;
+    if (i < d4) put_h16x4(scale4(xv[j], sc), hd, hl, (long long)row * d + 4 * i);
+  }
+  if (threadIdx.x == 0) hr[row] = ldexpf(1.0f, -e);
+}
+
 // Softmax cross-entropy of one row + its gradient (p − onehot)·gscale as an fp16 operand.
 // Online softmax state: (m, s) with s = Σ exp(x − m); merging two states keeps the larger max.
 __device__ __forceinline__ void sm_add(float& m, float& s, float x) {
@@ -395,14 +632,25 @@ void launch_embed(const QWeight& table, const int32_t* ids, float* x, int M, int
   embed_kernel<<<ceil_div(n, 256), 256, 0, st>>>(view(table), ids, x, M, d);
   HOS_HIP_CHECK(hipGetLastError());
 }
+static bool norm_reg_ok(int d, const void* a, const void* b, const void* c, const void* h, const void* l) {
+  auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
+  return d % 4 == 0 && d <= 4 * RB * NORM_NV && al(a, 16) && al(b, 16) && al(c, 16) && al(h, 8) && al(l, 8);
+}
 void launch_rmsnorm_fwd(const float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
                         hipStream_t st) {
-  rmsnorm_fwd_kernel<<<M, RB, 0, st>>>(x, w, eps, d, xn, out.data, out.lo, out.rinv, inv);
+  if (norm_reg_ok(d, x, w, xn, out.data, out.lo))
+    rmsnorm_fwd_reg_kernel<<<M, RB, 0, st>>>(x, w, eps, d, xn, out.data, out.lo, out.rinv, inv);
+  else
+    rmsnorm_fwd_kernel<<<M, RB, 0, st>>>(x, w, eps, d, xn, out.data, out.lo, out.rinv, inv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
                         hipStream_t st, H16 out) {
-  rmsnorm_bwd_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv);
+  auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
+  if (norm_reg_ok(d, g, x, w, out.data, out.lo) && al(dx, 16))
+    rmsnorm_bwd_reg_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv);
+  else
+    rmsnorm_bwd_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,
@@ -411,12 +659,24 @@ void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T,
   rope_kernel<<<ceil_div(n, 256), 256, 0, st>>>(buf, ld, col0, n_heads, hd, T, tab, neox, inverse, M);
   HOS_HIP_CHECK(hipGetLastError());
 }
+// The register-resident kernels need F % 4 == 0, F <= 4·RB·SWIGLU_NV and 16-byte (f32) / 8-byte (fp16) aligned
+// rows; other shapes take the two-pass kernels.
+static bool swiglu_reg_ok(int F, const void* a, const void* b, const void* c, const void* d, const void* e) {
+  auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
+  return F % 4 == 0 && F <= 4 * RB * SWIGLU_NV && al(a, 16) && al(b, 16) && al(c, 16) && al(d, 8) && al(e, 8);
+}
 void launch_swiglu_fwd(const float* gu, int M, int F, float* h, H16 out, hipStream_t st) {
-  swiglu_fwd_kernel<<<M, RB, 0, st>>>(gu, F, h, out.data, out.lo, out.rinv);
+  if (swiglu_reg_ok(F, gu, h, nullptr, out.data, out.lo))
+    swiglu_fwd_reg_kernel<<<M, RB, 0, st>>>(gu, F, h, out.data, out.lo, out.rinv);
+  else
+    swiglu_fwd_kernel<<<M, RB, 0, st>>>(gu, F, h, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_swiglu_bwd(const float* gu, const float* dh, int M, int F, float* dgu, H16 out, hipStream_t st) {
-  swiglu_bwd_kernel<<<M, RB, 0, st>>>(gu, dh, F, dgu, out.data, out.lo, out.rinv);
+  if (swiglu_reg_ok(F, gu, dh, dgu, out.data, out.lo))
+    swiglu_bwd_reg_kernel<<<M, RB, 0, st>>>(gu, dh, F, dgu, out.data, out.lo, out.rinv);
+  else
+    swiglu_bwd_kernel<<<M, RB, 0, st>>>(gu, dh, F, dgu, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_ce(const float* logits, int M, int V, const int32_t* targets, float gscale, float* row_loss, H16 dl,
