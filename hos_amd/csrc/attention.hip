@@ -231,7 +231,7 @@ __global__ void attn_dvec_kernel(const float* __restrict__ o, const float* __res
 // dQ for 32 queries of head h: Sᵀ and dPᵀ with lanes on queries, dQ = (dS·K)·2^-3. The 4 waves take
 // key blocks w, w+4, …; their partial dQ are summed in wave order.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_dq_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 2 : 1))) attn_dq_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
                                                       const float* __restrict__ dout, long long ldd,
                                                       const float* __restrict__ lse, const float* __restrict__ dvec,
                                                       int T, int nh, int group, float* __restrict__ dq,
@@ -314,7 +314,7 @@ __global__ void __launch_bounds__(256) attn_dq_kernel(const float* __restrict__ 
 // each head's result goes to part[(b·T + key)][h][2·64] and attn_group_sum adds the group in head
 // order; with group == 1 it is written in place.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_dkdv_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 2 : 1))) attn_dkdv_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
                                                         const float* __restrict__ dout, long long ldd,
                                                         const float* __restrict__ lse,
                                                         const float* __restrict__ dvec, int T, int nh, int group,

@@ -342,8 +342,8 @@ struct hos_ft {
         add_bias(a.qkv + qd, W3, M, kvd, Vp(l, BK));
         add_bias(a.qkv + qd + kvd, W3, M, kvd, Vp(l, BV));
       }
-      launch_rope(a.qkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
-      launch_rope(a.qkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
+      // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
+      launch_rope(a.qkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
       launch_attn_fwd(a.qkv, W3, qd, qd + kvd, B, T, c.n_heads, c.n_kv_heads, c.head_dim, a.o, qd, a.lse, st);
       launch_copy_rows(a.x, d, a.x2, d, M, d, st);
       fwd(a.o, qd, W(l, WO), d, qd, M, 1.0f, a.x2, d);
@@ -386,8 +386,8 @@ struct hos_ft {
       bwd_x(dx, d, W(l, WO), d, qd, M, 0.0f, dout, qd);
       launch_attn_bwd(a.qkv, W3, qd, qd + kvd, a.o, dout, qd, a.lse, dvec, B, T, c.n_heads, c.n_kv_heads,
                       c.head_dim, dqkv, W3, part, st);
-      launch_rope(dqkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
-      launch_rope(dqkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+      // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
+      launch_rope(dqkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
       if (c.attn_bias) {
         colsum(dqkv, W3, nullptr, 0, nullptr, M, qd, dV(l, BQ));
         colsum(dqkv + qd, W3, nullptr, 0, nullptr, M, kvd, dV(l, BK));

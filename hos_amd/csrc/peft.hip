@@ -575,8 +575,8 @@ struct hos_peft {
       }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
-        launch_rope(a.qkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
-        launch_rope(a.qkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
+        // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
+        launch_rope(a.qkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
       }
       {
         Scope s(this, "attn_fwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 2,
@@ -683,8 +683,8 @@ struct hos_peft {
       }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
-        launch_rope(dqkv, W3, 0, c.n_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
-        launch_rope(dqkv, W3, qd, c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+        // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
+        launch_rope(dqkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
       }
       if (c.qk_norm) {
         Scope s(this, "rmsnorm", 0, 4.0 * M * (qd + kvd) * 4);
