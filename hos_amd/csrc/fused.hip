@@ -471,13 +471,20 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
   const bool vec = (V & 3) == 0;
   if (vec) {
     const float4* l4 = reinterpret_cast<const float4*>(lr);
-    for (int c = threadIdx.x; c < V / 4; c += RB) {
-      const float4 x = l4[c];
+    auto add4 = [&](float4 x) {
       sm_add(m, sum, x.x);
       sm_add(m, sum, x.y);
       sm_add(m, sum, x.z);
       sm_add(m, sum, x.w);
+    };
+    // two loads in flight, elements folded in the thread's column order
+    int c = threadIdx.x;
+    for (; c + RB < V / 4; c += 2 * RB) {
+      const float4 x0 = l4[c], x1 = l4[c + RB];
+      add4(x0);
+      add4(x1);
     }
+    if (c < V / 4) add4(l4[c]);
   } else {
     for (int c = threadIdx.x; c < V; c += RB) sm_add(m, sum, lr[c]);
   }
@@ -506,10 +513,33 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
     }
     return;
   }
-  for (int c = threadIdx.x; c < V; c += RB) {
-    float p = expf(lr[c] - m) * inv;
-    if (c == t) p -= 1.0f;
-    put_h16(p * gscale * sc, dl, dll, (long long)row * V + c);
+  if (vec && ((uintptr_t)dl & 7) == 0 && ((uintptr_t)dll & 7) == 0) {
+    // float4 loads (two in flight) and 8-byte fp16 stores; the same per-element arithmetic as below
+    const float4* l4 = reinterpret_cast<const float4*>(lr);
+    const int V4 = V >> 2;
+    auto grad4 = [&](float4 x, int c4) {
+      const int c = 4 * c4;
+      float4 p = make_float4(expf(x.x - m) * inv, expf(x.y - m) * inv, expf(x.z - m) * inv, expf(x.w - m) * inv);
+      if (c == t) p.x -= 1.0f;
+      if (c + 1 == t) p.y -= 1.0f;
+      if (c + 2 == t) p.z -= 1.0f;
+      if (c + 3 == t) p.w -= 1.0f;
+      put_h16x4(make_float4(p.x * gscale * sc, p.y * gscale * sc, p.z * gscale * sc, p.w * gscale * sc), dl, dll,
+                (long long)row * V + c);
+    };
+    int c4 = threadIdx.x;
+    for (; c4 + RB < V4; c4 += 2 * RB) {
+      const float4 x0 = l4[c4], x1 = l4[c4 + RB];
+      grad4(x0, c4);
+      grad4(x1, c4 + RB);
+    }
+    if (c4 < V4) grad4(l4[c4], c4);
+  } else {
+    for (int c = threadIdx.x; c < V; c += RB) {
+      float p = expf(lr[c] - m) * inv;
+      if (c == t) p -= 1.0f;
+      put_h16(p * gscale * sc, dl, dll, (long long)row * V + c);
+    }
   }
   if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
 }
