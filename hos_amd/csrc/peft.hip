@@ -737,7 +737,8 @@ struct hos_peft {
     ColsSeg cs;
     cs.nseg = 1;
     cs.len[0] = d;
-    lora_cols("rga", M, Kbp, 1.0f, a.hg, Kbp, dx, d, cs, G + offUp[l], d, 1);  // dUp = (H ⊙ gate)ᵀ·dx
+    // dUp = (H ⊙ gate)ᵀ·dx, launched below with dRT (dx is unchanged until the dZ·RT update)
+    const ColsJob dup{Kbp, 1.0f, a.hg, Kbp, dx, d, cs, G + offUp[l], d, 1};
     RowsSeg rs;
     rs.nt = 1;
     rs.r = Kbp;
@@ -750,8 +751,11 @@ struct hos_peft {
       launch_rga_act_bwd(a.ra, Rp, rdg, Kbp, M, Kg, bn, pc, rz, st);
       launch_rga_colsum(rz, Rp, M, Kg, rdgb + (long long)l * Kg, st);
     }
-    cs.len[0] = d;
-    lora_cols("rga", M, Rp, 1.0f, rz, Rp, a.xr, d, cs, G + offRT[l], d, 1);  // dRT = dZᵀ·xr
+    {
+      const ColsJob drt{Rp, 1.0f, rz, Rp, a.xr, d, cs, G + offRT[l], d, 1};  // dRT = dZᵀ·xr
+      Scope s(this, "rga", 2.0 * M * d * (Kbp + Rp), 4.0 * ((double)M * d * 2 + (double)M * (Kbp + Rp) + (double)(Kbp + Rp) * d));
+      launch_lora_cols2(M, dup, &drt, ws, ws_bytes, st);
+    }
     {
       Scope s(this, "rga", 2.0 * M * d * Rp, 4.0 * ((double)M * d * 2 + (double)M * Rp + (double)Rp * d));
       launch_gemm_f32(M, d, Rp, 1.0f, rz, Rp, 1, P + offRT[l], d, 1, 1.0f, dx, d, ws, ws_bytes, st);  // dx += dZ·RT
