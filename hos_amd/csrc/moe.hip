@@ -9,8 +9,8 @@
 // Layout: the M·K (token, expert) selections are grouped by expert into P = M·K contiguous rows (expert e
 // at offsets[e] .. offsets[e] + counts[e]); a selection's row is pos[t][s]. The expert GEMMs run over those
 // rows against the stacked quantized weights (launch_qgemm_grouped), and the combine / its backward go
-// back to token order with fixed (selection-order) summation, so results do not depend on the order in
-// which the router's atomics handed out rows.
+// back to token order with fixed (selection-order) summation; an expert's rows are its selections in
+// selection order (a per-expert scan, no atomics), so the whole layer is deterministic.
 #include "moe.hpp"
 
 namespace hos {
@@ -72,8 +72,7 @@ __global__ void __launch_bounds__(NB) qknorm_bwd_kernel(float* __restrict__ g, l
 // ---- router: one wave per token, lane j = expert j (E ≤ 64) ----
 __global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict__ logits, int M, int E, int K,
                                                         float* __restrict__ pfull, int* __restrict__ sel_e,
-                                                        float* __restrict__ sel_p, int* __restrict__ slot,
-                                                        int* __restrict__ counts) {
+                                                        float* __restrict__ sel_p) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
   if (t >= M) return;
   const bool on = j < E;
@@ -101,9 +100,31 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict_
       const long long q = (long long)t * K + s;
       sel_e[q] = j;
       sel_p[q] = p;
-      slot[q] = atomicAdd(&counts[j], 1);
     }
   }
+}
+
+// Rows of expert e: one workgroup per expert ranks its selections in selection order (token, then slot):
+// slot[q] = #{q' < q : sel_e[q'] = e}, counts[e] = the total. Deterministic, no atomics.
+__global__ void __launch_bounds__(256) moe_slot_kernel(const int* __restrict__ sel_e, int P, int* __restrict__ slot,
+                                                       int* __restrict__ counts) {
+  __shared__ int scan[256];
+  const int e = blockIdx.x, tid = threadIdx.x;
+  const int per = (P + 255) / 256, q0 = tid * per, q1 = min(P, q0 + per);
+  int c = 0;
+  for (int q = q0; q < q1; q++) c += sel_e[q] == e ? 1 : 0;
+  scan[tid] = c;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {  // inclusive scan
+    const int v = tid >= o ? scan[tid - o] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
+  }
+  int r = scan[tid] - c;
+  for (int q = q0; q < q1; q++)
+    if (sel_e[q] == e) slot[q] = r++;
+  if (tid == 255) counts[e] = scan[255];
 }
 
 __global__ void moe_plan_kernel(const int* __restrict__ counts, int E, int* __restrict__ offsets,
@@ -128,6 +149,7 @@ __global__ void moe_plan_kernel(const int* __restrict__ counts, int E, int* __re
 }
 
 // one workgroup per selection: copy the token's operand row (hi, lo, row scale) to its expert-order row
+// (8 halves per 16-byte access: d and both row strides multiples of 8, checked by the launcher)
 __global__ void __launch_bounds__(NB) moe_gather_kernel(H16 src, long long lds, const int* __restrict__ sel_e,
                                                          const int* __restrict__ slot, const int* __restrict__ offsets,
                                                          int K, int d, int* __restrict__ pos, H16 dst, long long ldd) {
@@ -138,29 +160,41 @@ __global__ void __launch_bounds__(NB) moe_gather_kernel(H16 src, long long lds, 
     pos[q] = p;
     dst.rinv[p] = src.rinv[t];
   }
-  const _Float16* sh = src.data + (long long)t * lds;
-  _Float16* dh = dst.data + (long long)p * ldd;
-  for (int c = threadIdx.x; c < d; c += NB) dh[c] = sh[c];
+  const int d8 = d >> 3;
+  const int4* sh = reinterpret_cast<const int4*>(src.data + (long long)t * lds);
+  int4* dh = reinterpret_cast<int4*>(dst.data + (long long)p * ldd);
+  for (int c = threadIdx.x; c < d8; c += NB) dh[c] = sh[c];
   if (dst.lo) {
-    const _Float16* sl = src.lo + (long long)t * lds;
-    _Float16* dl = dst.lo + (long long)p * ldd;
-    for (int c = threadIdx.x; c < d; c += NB) dl[c] = sl[c];
+    const int4* sl = reinterpret_cast<const int4*>(src.lo + (long long)t * lds);
+    int4* dl = reinterpret_cast<int4*>(dst.lo + (long long)p * ldd);
+    for (int c = threadIdx.x; c < d8; c += NB) dl[c] = sl[c];
   }
 }
 
+// one thread per 4 consecutive output columns (d % 4 == 0, checked by the launcher); per element the same
+// selection-order sum as a scalar loop
 __global__ void moe_combine_kernel(const float* __restrict__ Y, const int* __restrict__ pos,
                                    const float* __restrict__ sel_p, const float* __restrict__ resid, int M, int K,
                                    int d, float* __restrict__ out) {
 #pragma clang fp contract(off)
+  const int d4 = d >> 2;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)M * d) return;
-  const int t = (int)(i / d), c = (int)(i % d);
-  float acc = 0.0f;
-  for (int s = 0; s < K; s++) acc += sel_p[t * K + s] * Y[(long long)pos[t * K + s] * d + c];
-  out[i] = resid[i] + acc;
+  if (i >= (long long)M * d4) return;
+  const int t = (int)(i / d4), c = 4 * (int)(i % d4);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int s = 0; s < K; s++) {
+    const float w = sel_p[t * K + s];
+    const float4 y = *reinterpret_cast<const float4*>(Y + (long long)pos[t * K + s] * d + c);
+    acc.x += w * y.x;
+    acc.y += w * y.y;
+    acc.z += w * y.z;
+    acc.w += w * y.w;
+  }
+  const float4 r = *reinterpret_cast<const float4*>(resid + (long long)t * d + c);
+  *reinterpret_cast<float4*>(out + (long long)t * d + c) = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
 }
 
-// one workgroup per selection
+// one workgroup per selection (float4 columns, d % 4 == 0)
 __global__ void __launch_bounds__(NB) moe_combine_bwd_kernel(const float* __restrict__ g, const float* __restrict__ Y,
                                                               const int* __restrict__ pos,
                                                               const float* __restrict__ sel_p, int K, int d,
@@ -170,13 +204,17 @@ __global__ void __launch_bounds__(NB) moe_combine_bwd_kernel(const float* __rest
   const int t = (int)(q / K);
   const long long p = pos[q];
   const float w = sel_p[q];
-  const float* gr = g + (long long)t * d;
-  const float* yr = Y + p * d;
-  float* dr = dY + p * d;
+  const float4* gr = reinterpret_cast<const float4*>(g + (long long)t * d);
+  const float4* yr = reinterpret_cast<const float4*>(Y + p * d);
+  float4* dr = reinterpret_cast<float4*>(dY + p * d);
   float s = 0.0f;
-  for (int c = threadIdx.x; c < d; c += NB) {
-    dr[c] = w * gr[c];
-    s += yr[c] * gr[c];
+  for (int c = threadIdx.x; c < (d >> 2); c += NB) {
+    const float4 gv = gr[c], yv = yr[c];
+    dr[c] = make_float4(w * gv.x, w * gv.y, w * gv.z, w * gv.w);
+    s += yv.x * gv.x;
+    s += yv.y * gv.y;
+    s += yv.z * gv.z;
+    s += yv.w * gv.w;
   }
   s = bsum(s, red);
   if (threadIdx.x == 0) dp[q] = s;
@@ -196,14 +234,22 @@ __global__ void __launch_bounds__(256) moe_router_bwd_kernel(const float* __rest
   if (j < E) dlogits[(long long)t * E + j] = p * (dpj - S);
 }
 
+// one thread per 4 consecutive columns (d % 4 == 0); per element the selection-order sum
 __global__ void moe_gather_sum_kernel(const float* __restrict__ dX, const int* __restrict__ pos, int M, int K, int d,
                                       float* __restrict__ dxn) {
+  const int d4 = d >> 2;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)M * d) return;
-  const int t = (int)(i / d), c = (int)(i % d);
-  float acc = 0.0f;
-  for (int s = 0; s < K; s++) acc += dX[(long long)pos[t * K + s] * d + c];
-  dxn[i] = acc;
+  if (i >= (long long)M * d4) return;
+  const int t = (int)(i / d4), c = 4 * (int)(i % d4);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int s = 0; s < K; s++) {
+    const float4 v = *reinterpret_cast<const float4*>(dX + (long long)pos[t * K + s] * d + c);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  *reinterpret_cast<float4*>(dxn + (long long)t * d + c) = acc;
 }
 
 __global__ void fill_i32_kernel(int* p, long long n, int v) {
@@ -229,7 +275,9 @@ void launch_moe_route(const float* logits, int M, int E, int K, float* pfull, in
                       int* counts, hipStream_t st) {
   HOS_REQUIRE(E >= 1 && E <= 64 && K >= 1 && K <= E, HOS_E_INVALID, "moe: need 1 <= experts used <= experts <= 64");
   if (M <= 0) return;
-  moe_route_kernel<<<ceil_div(M, 4), 256, 0, st>>>(logits, M, E, K, pfull, sel_e, sel_p, slot, counts);
+  moe_route_kernel<<<ceil_div(M, 4), 256, 0, st>>>(logits, M, E, K, pfull, sel_e, sel_p);
+  HOS_HIP_CHECK(hipGetLastError());
+  moe_slot_kernel<<<E, 256, 0, st>>>(sel_e, M * K, slot, counts);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_moe_plan(const int* counts, int E, int* offsets, int* tiles, int max_tiles, hipStream_t st) {
@@ -239,19 +287,22 @@ void launch_moe_plan(const int* counts, int E, int* offsets, int* tiles, int max
 void launch_moe_gather(H16 src, long long lds, const int* sel_e, const int* slot, const int* offsets, int M, int K,
                        int d, int* pos, H16 dst, long long ldd, hipStream_t st) {
   if (M <= 0) return;
+  HOS_REQUIRE(d % 8 == 0 && lds % 8 == 0 && ldd % 8 == 0, HOS_E_INVALID, "moe_gather: d and strides must be multiples of 8");
   moe_gather_kernel<<<(unsigned)((long long)M * K), NB, 0, st>>>(src, lds, sel_e, slot, offsets, K, d, pos, dst, ldd);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_moe_combine(const float* Y, const int* pos, const float* sel_p, const float* resid, int M, int K, int d,
                         float* out, hipStream_t st) {
-  const long long n = (long long)M * d;
+  const long long n = (long long)M * (d / 4);
   if (n <= 0) return;
+  HOS_REQUIRE(d % 4 == 0, HOS_E_INVALID, "moe_combine: d must be a multiple of 4");
   moe_combine_kernel<<<ceil_div(n, 256), 256, 0, st>>>(Y, pos, sel_p, resid, M, K, d, out);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_moe_combine_bwd(const float* g, const float* Y, const int* pos, const float* sel_p, int M, int K, int d,
                             float* dY, float* dp, hipStream_t st) {
   if (M <= 0) return;
+  HOS_REQUIRE(d % 4 == 0, HOS_E_INVALID, "moe_combine: d must be a multiple of 4");
   moe_combine_bwd_kernel<<<(unsigned)((long long)M * K), NB, 0, st>>>(g, Y, pos, sel_p, K, d, dY, dp);
   HOS_HIP_CHECK(hipGetLastError());
 }
@@ -262,8 +313,9 @@ void launch_moe_router_bwd(const float* pfull, const float* dp, const int* sel_e
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_moe_gather_sum(const float* dX, const int* pos, int M, int K, int d, float* dxn, hipStream_t st) {
-  const long long n = (long long)M * d;
+  const long long n = (long long)M * (d / 4);
   if (n <= 0) return;
+  HOS_REQUIRE(d % 4 == 0, HOS_E_INVALID, "moe_gather_sum: d must be a multiple of 4");
   moe_gather_sum_kernel<<<ceil_div(n, 256), 256, 0, st>>>(dX, pos, M, K, d, dxn);
   HOS_HIP_CHECK(hipGetLastError());
 }

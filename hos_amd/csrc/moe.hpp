@@ -12,8 +12,8 @@ void launch_qknorm_bwd(float* g, long long ld, int col0, int n, const float* w, 
                        int M, hipStream_t st);
 
 // Router: per row of logits [M][E] the softmax p (→ pfull), the top K by probability (ties: lower expert),
-// sel_e / sel_p [M][K] in selection order, and each selection's slot in its expert's list (counts[E] must
-// be zero on entry and end as the per-expert totals).
+// sel_e / sel_p [M][K] in selection order, each selection's slot in its expert's list (its rank among the
+// expert's selections in selection order) and counts[E], the per-expert totals.
 void launch_moe_route(const float* logits, int M, int E, int K, float* pfull, int* sel_e, float* sel_p, int* slot,
                       int* counts, hipStream_t st);
 // Per-expert offsets and the grouped-GEMM tile schedule (GROUP_BM-row tiles, max_tiles entries, unused = −1).

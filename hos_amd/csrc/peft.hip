@@ -494,7 +494,6 @@ struct hos_peft {
     {
       Scope s(this, "moe_route", 2.0 * M * d * E, 4.0 * ((double)M * d + (double)E * d + 4.0 * M * E) + 4.0 * P * d);
       launch_gemm_f32(M, E, d, 1.0f, a.xn2, d, 1, w.router, 1, d, 0.0f, mlogits, E, ws, ws_bytes, st);
-      launch_fill_i32(a.counts, E, 0, st);
       launch_moe_route(mlogits, M, E, K, a.pfull, a.sel_e, a.sel_p, a.slot, a.counts, st);
       launch_moe_plan(a.counts, E, a.offsets, a.tiles, max_tiles, st);
       launch_moe_gather(hs, d, a.sel_e, a.slot, a.offsets, M, K, d, a.pos, hx, d, st);
