@@ -220,6 +220,69 @@ __global__ void __launch_bounds__(NB) moe_combine_bwd_kernel(const float* __rest
   if (threadIdx.x == 0) dp[q] = s;
 }
 
+// The same backward writing dY straight as the fp16 row-scaled GEMM operand (hi, lo, 1/scale) of the expert
+// dX GEMM instead of f32: the row held in registers (d % 4 == 0, d <= 4·NB·4); scale and rounding as the
+// f32 → fp16 conversion applies them to the f32 row.
+typedef _Float16 moe_h16x4 __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(NB) moe_combine_bwd_h16_kernel(const float* __restrict__ g,
+                                                                  const float* __restrict__ Y,
+                                                                  const int* __restrict__ pos,
+                                                                  const float* __restrict__ sel_p, int K, int d,
+                                                                  H16 out, float* __restrict__ dp) {
+  constexpr int NV = 4;
+  __shared__ float red[4];
+  const long long q = blockIdx.x;
+  const int t = (int)(q / K), d4 = d >> 2;
+  const long long p = pos[q];
+  const float w = sel_p[q];
+  const float4* gr = reinterpret_cast<const float4*>(g + (long long)t * d);
+  const float4* yr = reinterpret_cast<const float4*>(Y + p * d);
+  float4 v[NV];
+  float s = 0.0f, amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + NB * j;
+    if (i < d4) {
+      const float4 gv = gr[i], yv = yr[i];
+      v[j] = make_float4(w * gv.x, w * gv.y, w * gv.z, w * gv.w);
+      s += yv.x * gv.x;
+      s += yv.y * gv.y;
+      s += yv.z * gv.z;
+      s += yv.w * gv.w;
+      amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+    }
+  }
+  s = bsum(s, red);
+  if (threadIdx.x == 0) dp[q] = s;
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (amax > 0.0f && amax < 3.0e38f) {
+    int ex;
+    frexpf(amax, &ex);
+    e = 15 - ex;
+    e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  }
+  const float sc = ldexpf(1.0f, e);
+  if (threadIdx.x == 0) out.rinv[p] = ldexpf(1.0f, -e);
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + NB * j;
+    if (i < d4) {
+      const float a = v[j].x * sc, b = v[j].y * sc, c = v[j].z * sc, dd = v[j].w * sc;
+      const moe_h16x4 h{(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)dd};
+      *reinterpret_cast<moe_h16x4*>(out.data + p * d + 4 * i) = h;
+      if (out.lo) {
+        const moe_h16x4 l{(_Float16)(a - (float)h.x), (_Float16)(b - (float)h.y), (_Float16)(c - (float)h.z),
+                          (_Float16)(dd - (float)h.w)};
+        *reinterpret_cast<moe_h16x4*>(out.lo + p * d + 4 * i) = l;
+      }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256) moe_router_bwd_kernel(const float* __restrict__ pfull,
                                                              const float* __restrict__ dp,
                                                              const int* __restrict__ sel_e, int M, int E, int K,
@@ -304,6 +367,14 @@ void launch_moe_combine_bwd(const float* g, const float* Y, const int* pos, cons
   if (M <= 0) return;
   HOS_REQUIRE(d % 4 == 0, HOS_E_INVALID, "moe_combine: d must be a multiple of 4");
   moe_combine_bwd_kernel<<<(unsigned)((long long)M * K), NB, 0, st>>>(g, Y, pos, sel_p, K, d, dY, dp);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+bool moe_combine_bwd_h16_ok(int d) { return d % 4 == 0 && d <= 4 * NB * 4; }
+void launch_moe_combine_bwd_h16(const float* g, const float* Y, const int* pos, const float* sel_p, int M, int K,
+                                int d, H16 out, float* dp, hipStream_t st) {
+  if (M <= 0) return;
+  HOS_REQUIRE(moe_combine_bwd_h16_ok(d), HOS_E_INVALID, "moe_combine_bwd_h16: d must be a multiple of 4, <= 4096");
+  moe_combine_bwd_h16_kernel<<<(unsigned)((long long)M * K), NB, 0, st>>>(g, Y, pos, sel_p, K, d, out, dp);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_moe_router_bwd(const float* pfull, const float* dp, const int* sel_e, int M, int E, int K, float* dlogits,

@@ -27,6 +27,11 @@ void launch_moe_combine(const float* Y, const int* pos, const float* sel_p, cons
 // Backward of the combine: dY[pos] = sel_p·g[t] (f32 rows), dp[t][s] = g[t]·Y[pos].
 void launch_moe_combine_bwd(const float* g, const float* Y, const int* pos, const float* sel_p, int M, int K, int d,
                             float* dY, float* dp, hipStream_t st);
+// The same with dY written as the fp16 row-scaled GEMM operand at row pos (what the f32 → fp16 conversion of
+// the f32 dY gives); for d % 4 == 0, d <= 4096 (moe_combine_bwd_h16_ok).
+bool moe_combine_bwd_h16_ok(int d);
+void launch_moe_combine_bwd_h16(const float* g, const float* Y, const int* pos, const float* sel_p, int M, int K,
+                                int d, H16 out, float* dp, hipStream_t st);
 // Softmax backward restricted to the selected probabilities: dlogits[t][j] = p_j·(dp_j − Σ_i p_i·dp_i),
 // dp_j = dp[t][s] for j = sel_e[t][s], else 0.
 void launch_moe_router_bwd(const float* pfull, const float* dp, const int* sel_e, int M, int E, int K, float* dlogits,

@@ -515,11 +515,14 @@ struct hos_peft {
     LayerAct& a = act[l];
     LayerW& w = lw[l];
     const long long P = (long long)M * K;
-    {
-      Scope s(this, "moe_combine", 0, 4.0 * (M * d + 2.0 * P * d));
-      launch_moe_combine_bwd(dx, a.yg, a.pos, a.sel_p, M, K, d, mdY, mdp, st);
-    }
-    {
+    if (moe_combine_bwd_h16_ok(d)) {
+      Scope s(this, "moe_combine", 0, 4.0 * (M * d + P * d) + 4.0 * P * d);
+      launch_moe_combine_bwd_h16(dx, a.yg, a.pos, a.sel_p, M, K, d, hx, mdp, st);
+    } else {
+      {
+        Scope s(this, "moe_combine", 0, 4.0 * (M * d + 2.0 * P * d));
+        launch_moe_combine_bwd(dx, a.yg, a.pos, a.sel_p, M, K, d, mdY, mdp, st);
+      }
       Scope s(this, "convert", 0, 6.0 * P * d);
       launch_to_h16(mdY, d, P, d, hx, st);
     }
