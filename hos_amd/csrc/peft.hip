@@ -695,10 +695,15 @@ struct hos_peft {
       }
       lora_grad_b(l, 0, dqkv, W3, W3, M);
       to16(dqkv, W3, M, W3);
-      H16 hk = h16_offset(hs, qd), hv = h16_offset(hs, qd + kvd);
-      qdx(w.w[TQ], hs, W3, M, dxn, d, 0, down_epi(l, TQ), tpd[TQ]);
-      qdx(w.w[TK], hk, W3, M, dxn, d, 1, down_epi(l, TK), tpd[TK]);
-      qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV), tpd[TV]);
+      if (w.qkv.q && group_uniform(0) && gcount(0) * r <= 64) {
+        // one dX GEMM over the stacked q|k|v contraction, the three LoRA terms as one rank-3r update
+        qdx(w.qkv, hs, W3, M, dxn, d, 0, stacked_down_epi(l, 0), tpd[TQ]);
+      } else {
+        H16 hk = h16_offset(hs, qd), hv = h16_offset(hs, qd + kvd);
+        qdx(w.w[TQ], hs, W3, M, dxn, d, 0, down_epi(l, TQ), tpd[TQ]);
+        qdx(w.w[TK], hk, W3, M, dxn, d, 1, down_epi(l, TK), tpd[TK]);
+        qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV), tpd[TV]);
+      }
       lora_grad_a(l, 0, a.xn1, d, M);
       {
         const bool emit = fuse16 && l > 0;

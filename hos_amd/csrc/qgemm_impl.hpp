@@ -201,7 +201,11 @@ struct Geo {
   static constexpr int ATILE = BM * AROW, BTILE = BROWS * BROW;
   static constexpr int BUF = NA * ATILE + NB * BTILE;   // halves per stage
   static constexpr int STAGES = BUF * 2 * 2 <= 65536 ? 2 : 1;
-  static constexpr int EPI = (BM * 32 + 32 * BN) * 2;   // halves for the fused rank-r staging
+  // rank capacity of the fused rank-r staging: the largest multiple of 16 up to 64 whose U [BM][RCAP] and
+  // L [RCAP][BN] fit in the LDS the main loop already uses, at least 32
+  static constexpr int RFIT = STAGES * BUF / ((BM + BN) * 2) / 16 * 16;
+  static constexpr int RCAP = RFIT >= 64 ? 64 : (RFIT >= 32 ? RFIT : 32);
+  static constexpr int EPI = (BM * RCAP + RCAP * BN) * 2;  // halves for the fused rank-r staging
   static constexpr int SMEM = (STAGES * BUF > EPI) ? STAGES * BUF : EPI;
 };
 
@@ -406,15 +410,16 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   // epilogue: D[i][j] of a 32×32 tile lives at lane j + 32·((i/4)&1), register (i&3) + 4·(i/8)
   const bool split = gridDim.z > 1;
   // fused rank-r update: stage U [BM][r] and L [r][BN] in the (now free) LDS
+  constexpr int RC = G::RCAP;
   float* Us = (float*)smem;
-  float* Ls = Us + BM * 32;
+  float* Ls = Us + BM * RC;
   const int rank = split ? 0 : epi.rank;
   if (rank > 0) {
     // a tile never straddles a column segment (the launcher picks BN to divide the boundaries)
     const float* Ub = epi.U + (epi.ustep ? epi.ustep * ((n0 >= epi.ub0) + (n0 >= epi.ub1)) : 0);
     for (int e = tid; e < BM * rank; e += G::NT) {
       int rr = e / rank, jj = e % rank, row = m0 + rr;
-      Us[rr * 32 + jj] = row < M ? Ub[(long long)row * epi.ldu + jj] : 0.0f;
+      Us[rr * RC + jj] = row < M ? Ub[(long long)row * epi.ldu + jj] : 0.0f;
     }
     for (int e = tid; e < rank * BN; e += G::NT) {
       int jj = e / BN, cc = e % BN, col = n0 + cc;
@@ -442,7 +447,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
           if (epi.bias) v += epi.bias[col];
           if (rank > 0) {
             float lv = 0.0f;
-            for (int q = 0; q < rank; q++) lv += Us[rr * 32 + q] * Ls[q * BN + cc];
+            for (int q = 0; q < rank; q++) lv += Us[rr * RC + q] * Ls[q * BN + cc];
             v += lv;
           }
           long long off = (long long)row * epi.ldo + col;
@@ -497,6 +502,8 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ w
 template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
 void launch_shape(const QWeight& w, H16 a, long long lda, long long M, int Nout, int C, int per, int splits,
                   GemmEpi epi, float* ws, hipStream_t st) {
+  constexpr int rcap = Geo<BM, BN, BK, DX, NP>::RCAP;
+  HOS_REQUIRE(epi.rank <= rcap, HOS_E_INVALID, "qgemm: fused rank exceeds the tile's staging");
   dim3 grid(ceil_div(Nout, BN), ceil_div(M, BM), splits);
   qgemm_kernel<QT, DX, BM, BN, BK, NP>
       <<<grid, Geo<BM, BN, BK, DX, NP>::NT, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, (int)M, Nout, C, per, epi, ws,
@@ -512,7 +519,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   HOS_REQUIRE((lda % 8) == 0, HOS_E_INVALID, "qgemm: activation row stride must be a multiple of 8");
   HOS_REQUIRE((NP != 2 && NP != 3) || a.lo != nullptr, HOS_E_INVALID,
               "qgemm: activation-split precision needs the operand residual");
-  HOS_REQUIRE(epi.rank >= 0 && epi.rank <= 32, HOS_E_INVALID, "qgemm: fused rank-r update supports r <= 32");
+  HOS_REQUIRE(epi.rank >= 0 && epi.rank <= 64, HOS_E_INVALID, "qgemm: fused rank-r update supports r <= 64");
   // Tile choice: the largest tile that still gives ~1.25 waves of workgroups over the 256 CUs; only when
   // even 64×64 tiles leave the chip idle is the contraction split (deterministic reduction after).
   auto ntiles = [&](int bm, int bn) { return ceil_div(M, bm) * ceil_div(Nout, bn); };
@@ -560,6 +567,13 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
       bk = z;
     }
   }
+  // A fused rank above 32 (stacked q|k|v dX): 64×64 tiles, whose LDS holds the rank-64 staging, and no split
+  // (the split-K reduction stages at most 32).
+  if (epi.rank > 32) {
+    bm = 64;
+    bn = 64;
+    bk = C % 64 == 0 ? 64 : 32;
+  }
   // Column-segmented U (stacked projections): tiles must not straddle a segment boundary, and the split-K
   // reduction (which stages one U block for all its columns) is not used.
   const bool useg = epi.rank > 0 && epi.ustep > 0;
@@ -575,7 +589,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   int tiles = ntiles(bm, bn);
   int nslab = C / bk;
   int splits = 1;
-  while (!useg && tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
+  while (!useg && epi.rank <= 32 && tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
          (size_t)(splits * 2) * M * Nout * sizeof(float) <= ws_bytes)
     splits *= 2;
   int per = ceil_div(nslab, splits) * bk;
