@@ -9,6 +9,7 @@
 // is read from L2. The contraction order inside an MFMA is free, so a lane's float4 of 4 consecutive
 // k (rows kernel) or 4 consecutive output columns (cols kernel) feeds 4 MFMAs directly.
 //
+// Short rows contractions run in one launch (16 waves per workgroup split K; see lora_rows_wide_kernel).
 // The long contraction is split across workgroups for parallelism. Each workgroup reduces its four
 // waves in LDS in a fixed order and writes its partial block; a reduce launch sums the partials in
 // split order. Deterministic. (An in-kernel "last workgroup reduces" variant with device-scope fences
@@ -178,6 +179,80 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
   });
 }
 
+// Short contractions (K <= ROWS_WIDE_KMAX, n <= 48): one 16-row block per workgroup of 16 waves, the waves
+// splitting K (wave w takes the 16-wide k steps w, w+16, …), their partial tiles summed in LDS in wave order.
+// No split over workgroups, so no partial buffer and no reduction launch; deterministic.
+constexpr int ROWS_WIDE_KMAX = 1536, ROWS_WIDE_NW = 16;
+template <int NJ>
+__global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M, int K, float alpha,
+                                                                           const float* __restrict__ X, long long ldx,
+                                                                           const float* __restrict__ Bt, long long ldb,
+                                                                           RowsSeg sg, float* __restrict__ C,
+                                                                           long long ldc) {
+  constexpr int NW = ROWS_WIDE_NW, NC = NJ * 16, E = 16 * NC, U = 2;
+  __shared__ float red[NW * E];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
+  const int m0 = blockIdx.x * 16, n = sg.nt * sg.r;
+  const float* bp[NJ];
+  int klo[NJ], khi[NJ];
+#pragma unroll
+  for (int jt = 0; jt < NJ; jt++) {
+    const int j = jt * 16 + p;
+    if (j < n) {
+      const int t = j / sg.r, jj = j - t * sg.r;
+      bp[jt] = Bt + sg.boff[t] + (long long)jj * ldb - sg.kbeg[t];
+      klo[jt] = sg.kbeg[t];
+      khi[jt] = sg.kend[t];
+    } else {
+      bp[jt] = Bt;
+      klo[jt] = 0;
+      khi[jt] = 0;
+    }
+  }
+  const int row = m0 + p;
+  const bool rv = row < M;
+  const float* xr = X + (long long)(rv ? row : 0) * ldx;
+  f4v acc[NJ];
+#pragma unroll
+  for (int jt = 0; jt < NJ; jt++) acc[jt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  // U steps per trip, loads first (zero steps past K add exact zeros)
+  for (int k0 = 16 * wave; k0 < K; k0 += 16 * NW * U) {
+    float4 xa[U], bv[U][NJ];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int kk = k0 + 16 * NW * u + 4 * q;
+      const bool kin = kk < K;
+      xa[u] = (rv && kin) ? *reinterpret_cast<const float4*>(xr + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int jt = 0; jt < NJ; jt++)
+        bv[u][jt] = (kin && kk >= klo[jt] && kk < khi[jt]) ? *reinterpret_cast<const float4*>(bp[jt] + kk)
+                                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (k0 + 16 * NW * u < K)  // wave-uniform
+#pragma unroll
+        for (int jt = 0; jt < NJ; jt++) {
+          acc[jt] = mfma16(xa[u].x, bv[u][jt].x, acc[jt]);
+          acc[jt] = mfma16(xa[u].y, bv[u][jt].y, acc[jt]);
+          acc[jt] = mfma16(xa[u].z, bv[u][jt].z, acc[jt]);
+          acc[jt] = mfma16(xa[u].w, bv[u][jt].w, acc[jt]);
+        }
+  }
+  // element (row 4q+i, col 16jt+p) of the 16×NC block
+#pragma unroll
+  for (int jt = 0; jt < NJ; jt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wave * E + (4 * q + i) * NC + 16 * jt + p] = acc[jt][i];
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 64 * NW) {
+    float v = 0.0f;
+    for (int w = 0; w < NW; w++) v += red[w * E + e];
+    const int rr = e / NC, c = e % NC, r2 = m0 + rr;
+    if (r2 < M && c < n) C[(long long)r2 * ldc + c] = alpha * v;
+  }
+}
+
 // ---------------- cols: C(j, c) = α·Σ_m S[m, j]·G[m, c] ----------------
 // Workgroup: 64 columns of one segment × all j × an m-chunk; wave w takes the chunk's 4-row steps
 // w, w+4, … Lane (q, p): m = step + q, columns c0+4p .. +3 (one float4; component e is MFMA tile e).
@@ -329,6 +404,18 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
     HOS_REQUIRE(sg.kbeg[t] % 4 == 0 && sg.kend[t] % 4 == 0 && sg.boff[t] % 4 == 0 && sg.kbeg[t] >= 0 &&
                     sg.kend[t] <= K,
                 HOS_E_INVALID, "lora_rows: segment bounds must be multiples of 4 within K");
+  if (K <= ROWS_WIDE_KMAX && n <= 48) {
+    const int NJw = (n + 15) / 16;
+    const unsigned gw = (unsigned)ceil_div_i(M, 16);
+    if (NJw == 1)
+      lora_rows_wide_kernel<1><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
+    else if (NJw == 2)
+      lora_rows_wide_kernel<2><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
+    else
+      lora_rows_wide_kernel<3><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
+    HOS_HIP_CHECK(hipGetLastError());
+    return;
+  }
   const int gx = ceil_div_i(M, 32);
   int S = std::max(1, std::min(ceil_div_i(split_target(), gx), ceil_div_i(K, 64)));
   int kchunk = ceil_div_i(ceil_div_i(K, S), 64) * 64;
