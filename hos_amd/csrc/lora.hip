@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
   });
 }
 
-// Short contractions (K <= ROWS_WIDE_KMAX, n <= 48): one 16-row block per workgroup of 16 waves, the waves
+// Short contractions (K <= ROWS_WIDE_KMAX): one 16-row × 16·NJ-column block per workgroup of 16 waves, the waves
 // splitting K (wave w takes the 16-wide k steps w, w+16, …), their partial tiles summed in LDS in wave order.
 // No split over workgroups, so no partial buffer and no reduction launch; deterministic.
 constexpr int ROWS_WIDE_KMAX = 1536, ROWS_WIDE_NW = 16;
@@ -192,12 +192,12 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
   constexpr int NW = ROWS_WIDE_NW, NC = NJ * 16, E = 16 * NC, U = 2;
   __shared__ float red[NW * E];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
-  const int m0 = blockIdx.x * 16, n = sg.nt * sg.r;
+  const int m0 = blockIdx.x * 16, n = sg.nt * sg.r, j0 = blockIdx.y * NC;  // this workgroup's column tiles
   const float* bp[NJ];
   int klo[NJ], khi[NJ];
 #pragma unroll
   for (int jt = 0; jt < NJ; jt++) {
-    const int j = jt * 16 + p;
+    const int j = j0 + jt * 16 + p;
     if (j < n) {
       const int t = j / sg.r, jj = j - t * sg.r;
       bp[jt] = Bt + sg.boff[t] + (long long)jj * ldb - sg.kbeg[t];
@@ -248,7 +248,7 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
   for (int e = threadIdx.x; e < E; e += 64 * NW) {
     float v = 0.0f;
     for (int w = 0; w < NW; w++) v += red[w * E + e];
-    const int rr = e / NC, c = e % NC, r2 = m0 + rr;
+    const int rr = e / NC, c = j0 + e % NC, r2 = m0 + rr;
     if (r2 < M && c < n) C[(long long)r2 * ldc + c] = alpha * v;
   }
 }
@@ -404,15 +404,10 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
     HOS_REQUIRE(sg.kbeg[t] % 4 == 0 && sg.kend[t] % 4 == 0 && sg.boff[t] % 4 == 0 && sg.kbeg[t] >= 0 &&
                     sg.kend[t] <= K,
                 HOS_E_INVALID, "lora_rows: segment bounds must be multiples of 4 within K");
-  if (K <= ROWS_WIDE_KMAX && n <= 48) {
-    const int NJw = (n + 15) / 16;
-    const unsigned gw = (unsigned)ceil_div_i(M, 16);
-    if (NJw == 1)
-      lora_rows_wide_kernel<1><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
-    else if (NJw == 2)
-      lora_rows_wide_kernel<2><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
-    else
-      lora_rows_wide_kernel<3><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
+  if (K <= ROWS_WIDE_KMAX && n <= 96) {
+    // one 16-column tile per workgroup (grid.y = tiles): 128-row-block grids alone leave half the CUs idle
+    const dim3 gw((unsigned)ceil_div_i(M, 16), (unsigned)((n + 15) / 16));
+    lora_rows_wide_kernel<1><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
     HOS_HIP_CHECK(hipGetLastError());
     return;
   }
