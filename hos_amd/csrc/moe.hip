@@ -105,47 +105,81 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict_
 }
 
 // Rows of expert e: one workgroup per expert ranks its selections in selection order (token, then slot):
-// slot[q] = #{q' < q : sel_e[q'] = e}, counts[e] = the total. Deterministic, no atomics.
-__global__ void __launch_bounds__(256) moe_slot_kernel(const int* __restrict__ sel_e, int P, int* __restrict__ slot,
-                                                       int* __restrict__ counts) {
-  __shared__ int scan[256];
-  const int e = blockIdx.x, tid = threadIdx.x;
-  const int per = (P + 255) / 256, q0 = tid * per, q1 = min(P, q0 + per);
+// slot[q] = #{q' < q : sel_e[q'] = e}, counts[e] = the total. Each wave takes a contiguous quarter of the
+// selections, 64 at a time (coalesced loads, ballot + popcount ranks). Deterministic, no atomics.
+constexpr int SLOT_NW = 16;  // waves per workgroup
+__global__ void __launch_bounds__(64 * SLOT_NW) moe_slot_kernel(const int* __restrict__ sel_e, int P,
+                                                                int* __restrict__ slot, int* __restrict__ counts) {
+  __shared__ int wsum[SLOT_NW];
+  const int e = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int per = (P + 64 * SLOT_NW - 1) / (64 * SLOT_NW) * 64, q0 = w * per, q1 = min(P, q0 + per);
+  constexpr int NB8 = 8;  // 64-selection groups whose loads are issued together
   int c = 0;
-  for (int q = q0; q < q1; q++) c += sel_e[q] == e ? 1 : 0;
-  scan[tid] = c;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {  // inclusive scan
-    const int v = tid >= o ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
+  for (int qb = q0; qb < q1; qb += 64 * NB8) {
+    bool f[NB8];
+#pragma unroll
+    for (int i = 0; i < NB8; i++) {
+      const int q = qb + 64 * i + lane;
+      f[i] = q < q1 && sel_e[q] == e;
+    }
+#pragma unroll
+    for (int i = 0; i < NB8; i++) c += __popcll(__ballot(f[i]));
   }
-  int r = scan[tid] - c;
-  for (int q = q0; q < q1; q++)
-    if (sel_e[q] == e) slot[q] = r++;
-  if (tid == 255) counts[e] = scan[255];
+  if (lane == 0) wsum[w] = c;
+  __syncthreads();
+  int r = 0;
+  for (int i = 0; i < w; i++) r += wsum[i];
+  const unsigned long long below = (1ull << lane) - 1ull;
+  for (int qb = q0; qb < q1; qb += 64 * NB8) {
+    bool f[NB8];
+#pragma unroll
+    for (int i = 0; i < NB8; i++) {
+      const int q = qb + 64 * i + lane;
+      f[i] = q < q1 && sel_e[q] == e;
+    }
+#pragma unroll
+    for (int i = 0; i < NB8; i++) {
+      const unsigned long long m = __ballot(f[i]);
+      if (f[i]) slot[qb + 64 * i + lane] = r + __popcll(m & below);
+      r += __popcll(m);
+    }
+  }
+  if (threadIdx.x == 0) {
+    int tot = 0;
+    for (int i = 0; i < SLOT_NW; i++) tot += wsum[i];
+    counts[e] = tot;
+  }
 }
 
-__global__ void moe_plan_kernel(const int* __restrict__ counts, int E, int* __restrict__ offsets,
-                                int* __restrict__ tiles, int max_tiles) {
-  if (threadIdx.x != 0) return;
-  int off = 0, nt = 0;
-  for (int e = 0; e < E; e++) {
-    offsets[e] = off;
-    const int n = counts[e];
-    for (int r = 0; r < n; r += GROUP_BM) {
-      if (nt < max_tiles) {
-        tiles[3 * nt] = e;
-        tiles[3 * nt + 1] = off + r;
-        tiles[3 * nt + 2] = min(GROUP_BM, n - r);
-      }
-      nt++;
+// One wave, lane e = expert e (E <= 64): exclusive scans of the row counts (→ offsets) and of the tile counts
+// (→ each expert's first schedule entry), each lane writing its expert's tiles, then the unused tail = −1.
+__global__ void __launch_bounds__(64) moe_plan_kernel(const int* __restrict__ counts, int E,
+                                                      int* __restrict__ offsets, int* __restrict__ tiles,
+                                                      int max_tiles) {
+  const int e = threadIdx.x;
+  const int n = e < E ? counts[e] : 0, nt = (n + GROUP_BM - 1) / GROUP_BM;
+  int off = n, t0 = nt;  // inclusive scans
+  for (int o = 1; o < 64; o <<= 1) {
+    const int a = __shfl_up(off, o), b = __shfl_up(t0, o);
+    if (e >= o) {
+      off += a;
+      t0 += b;
     }
-    off += n;
   }
-  offsets[E] = off;
-  for (int i = nt; i < max_tiles; i++) tiles[3 * i] = -1;
+  const int total = __shfl(off, 63), ttot = __shfl(t0, 63);
+  off -= n;
+  t0 -= nt;
+  if (e < E) offsets[e] = off;
+  if (e == 0) offsets[E] = total;
+  for (int i = 0; i < nt; i++) {
+    const int ti = t0 + i;
+    if (ti < max_tiles) {
+      tiles[3 * ti] = e;
+      tiles[3 * ti + 1] = off + i * GROUP_BM;
+      tiles[3 * ti + 2] = min(GROUP_BM, n - i * GROUP_BM);
+    }
+  }
+  for (int i = ttot + e; i < max_tiles; i += 64) tiles[3 * i] = -1;
 }
 
 // one workgroup per selection: copy the token's operand row (hi, lo, row scale) to its expert-order row
@@ -340,7 +374,7 @@ void launch_moe_route(const float* logits, int M, int E, int K, float* pfull, in
   if (M <= 0) return;
   moe_route_kernel<<<ceil_div(M, 4), 256, 0, st>>>(logits, M, E, K, pfull, sel_e, sel_p);
   HOS_HIP_CHECK(hipGetLastError());
-  moe_slot_kernel<<<E, 256, 0, st>>>(sel_e, M * K, slot, counts);
+  moe_slot_kernel<<<E, 64 * SLOT_NW, 0, st>>>(sel_e, M * K, slot, counts);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_moe_plan(const int* counts, int E, int* offsets, int* tiles, int max_tiles, hipStream_t st) {

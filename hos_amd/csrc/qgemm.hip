@@ -47,13 +47,13 @@ __global__ void to_h16_kernel(const float* __restrict__ x, long long ldx, int K,
                 rinv + row);
 }
 
-// The same conversion with the row held in registers (K % 4 == 0, K <= 4096, 16-byte aligned rows, 8-byte
+// The same conversion with the row held in registers (K % 4 == 0, K <= 8192, 16-byte aligned rows, 8-byte
 // aligned outputs): one read of the row; the same scale and per-element rounding as block_row_h16.
 typedef _Float16 h16x4_t __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(256) to_h16_reg_kernel(const float* __restrict__ x, long long ldx, int K,
                                                          _Float16* __restrict__ out, _Float16* __restrict__ lo,
                                                          float* __restrict__ rinv) {
-  constexpr int NV = 4;
+  constexpr int NV = 8;
   __shared__ float red[4];
   const int row = blockIdx.x, K4 = K >> 2;
   const float4* xr = reinterpret_cast<const float4*>(x + (long long)row * ldx);
@@ -132,7 +132,7 @@ void launch_qgemm_grouped(bool dx, const QWeight& w, GroupSched gs, H16 a, long 
 void launch_to_h16(const float* x, long long ldx, long long M, long long K, H16 out, hipStream_t st) {
   if (M <= 0) return;
   auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
-  if (K % 4 == 0 && K <= 4096 && ldx % 4 == 0 && al(x, 16) && al(out.data, 8) && al(out.lo, 8))
+  if (K % 4 == 0 && K <= 8192 && ldx % 4 == 0 && al(x, 16) && al(out.data, 8) && al(out.lo, 8))
     to_h16_reg_kernel<<<(unsigned)M, 256, 0, st>>>(x, ldx, (int)K, out.data, out.lo, out.rinv);
   else
     to_h16_kernel<<<(unsigned)M, 256, 0, st>>>(x, ldx, (int)K, out.data, out.lo, out.rinv);
