@@ -369,6 +369,18 @@ __device__ __forceinline__ void cols_reduce_one(const ColsJobDev& jb, const floa
   jb.C[(long long)j * jb.scj + ((long long)sg.ocol[t] + c) * jb.scc] =
       jb.alpha * sum_parts(part + jb.part_off, S, jb.gx, bx, E, e);
 }
+struct ColsBatchArgs {
+  ColsJobDev jobs[8];
+  long long start[9];  // first element of each job in the flattened index space
+  int n;
+};
+__global__ void lora_cols_reduce_batch(const float* __restrict__ base, ColsBatchArgs args) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= args.start[args.n]) return;
+  int j = 0;
+  while (j + 1 < args.n && i >= args.start[j + 1]) j++;
+  cols_reduce_one(args.jobs[j], base, args.jobs[j].S, i - args.start[j]);
+}
 __global__ void lora_cols_reduce(const float* __restrict__ part, int S, ColsJobDev a, ColsJobDev b) {
   const long long na = (long long)a.gx * a.nsr * 64, nb = (long long)b.gx * b.nsr * 64;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -467,7 +479,8 @@ ColsJobDev prepare(const ColsJob& j, int bx0) {
 }
 }  // namespace
 
-void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float* ws, size_t ws_bytes, hipStream_t st) {
+void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float* ws, size_t ws_bytes, hipStream_t st,
+                       ColsBatch* batch) {
   if (M <= 0) return;
   ColsJobDev a = prepare(ja, 0);
   ColsJobDev b{};
@@ -485,12 +498,24 @@ void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float*
   a.part_off = 0;
   b.part_off = (long long)S * a.gx * a.nsr * 64;
   const long long need = b.part_off + (long long)S * b.gx * b.nsr * 64;
-  HOS_REQUIRE(S == 1 || (size_t)need * 4 <= ws_bytes, HOS_E_INVALID, "lora_cols: workspace too small");
+  a.S = b.S = S;
+  // deferred: the partials go to the batch buffer (offsets relative to its base) and the reduction waits for
+  // the flush
+  const int njobs = jb ? 2 : 1;
+  const bool defer = batch && S > 1 && batch->n + njobs <= 8 && batch->used + (size_t)need <= batch->cap;
+  float* part = ws;
+  if (defer) {
+    a.part_off += (long long)batch->used;
+    b.part_off += (long long)batch->used;
+    part = batch->base;
+  } else {
+    HOS_REQUIRE(S == 1 || (size_t)need * 4 <= ws_bytes, HOS_E_INVALID, "lora_cols: workspace too small");
+  }
   const int NA = a.nsr / 16, NB = jb ? b.nsr / 16 : NA;
   dim3 grid(gx, S);
 #define COLS(X, Y)                                                                  \
   if (NA == X && NB == Y) {                                                         \
-    lora_cols_kernel<X, Y><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, ws);         \
+    lora_cols_kernel<X, Y><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, part);       \
     launched = true;                                                                \
   }
   bool launched = false;
@@ -499,16 +524,40 @@ void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float*
   if (!launched) {
     // width pair without a combined kernel: run the jobs one after the other
     HOS_REQUIRE(jb != nullptr, HOS_E_INVALID, "lora_cols: bad width");
-    launch_lora_cols2(M, ja, nullptr, ws, ws_bytes, st);
-    launch_lora_cols2(M, *jb, nullptr, ws, ws_bytes, st);
+    launch_lora_cols2(M, ja, nullptr, ws, ws_bytes, st, batch);
+    launch_lora_cols2(M, *jb, nullptr, ws, ws_bytes, st, batch);
     return;
   }
   HOS_HIP_CHECK(hipGetLastError());
+  if (defer) {
+    batch->jobs[batch->n++] = a;
+    if (jb) batch->jobs[batch->n++] = b;
+    batch->used += (size_t)need;
+    return;
+  }
   if (S > 1) {
     const long long tot = (long long)a.gx * a.nsr * 64 + (long long)b.gx * b.nsr * 64;
     lora_cols_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, a, b);
     HOS_HIP_CHECK(hipGetLastError());
   }
+}
+
+void launch_lora_cols_flush(ColsBatch& bt, hipStream_t st) {
+  if (bt.n > 0) {
+    ColsBatchArgs args{};
+    long long tot = 0;
+    for (int j = 0; j < bt.n; j++) {
+      args.jobs[j] = bt.jobs[j];
+      args.start[j] = tot;
+      tot += (long long)bt.jobs[j].gx * bt.jobs[j].nsr * 64;
+    }
+    args.start[bt.n] = tot;
+    args.n = bt.n;
+    lora_cols_reduce_batch<<<ceil_div_i(tot, 256), 256, 0, st>>>(bt.base, args);
+    HOS_HIP_CHECK(hipGetLastError());
+  }
+  bt.n = 0;
+  bt.used = 0;
 }
 
 void launch_lora_cols(long long M, int ns, float alpha, const float* Sm, long long lds, const float* Gm, long long ldg,

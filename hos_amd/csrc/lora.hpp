@@ -50,11 +50,23 @@ struct ColsJobDev {
   long long lds, ldg, scj, scc, part_off;
   float alpha;
   int ns, nsr, gx, bx0;
+  int S;  // splits of M the partials were written with
   ColsSeg sg;
 };
+// Deferred reductions: cols launches given a batch write their partials into the batch's buffer and leave the
+// reduction to one launch_lora_cols_flush for all of them (up to 8 jobs; a job that does not fit is reduced
+// at once as without a batch).
+struct ColsBatch {
+  float* base = nullptr;
+  size_t cap = 0, used = 0;  // floats
+  ColsJobDev jobs[8];
+  int n = 0;
+};
+void launch_lora_cols_flush(ColsBatch& b, hipStream_t st);
 // Two independent cols products over the same M in one launch (and one reduction launch); b may be null.
 // Deterministic: the split of M depends only on M and the combined block count, and every output element sums
 // its split partials in split order.
-void launch_lora_cols2(long long M, const ColsJob& a, const ColsJob* b, float* ws, size_t ws_bytes, hipStream_t st);
+void launch_lora_cols2(long long M, const ColsJob& a, const ColsJob* b, float* ws, size_t ws_bytes, hipStream_t st,
+                       ColsBatch* batch = nullptr);
 
 }  // namespace hos

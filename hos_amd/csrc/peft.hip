@@ -74,6 +74,7 @@ struct hos_peft {
   int d = 0, qd = 0, kvd = 0, W3 = 0, F = 0, V = 0, r = 0, L = 0, Mmax = 0, passes = 3;
   int pf = 3, pd = 3, phf = 3, phd = 3;  // precision mode per GEMM site: layer fwd / dX, head fwd / dX
   ColsJob pend_db;       // dB of the group whose backward is in progress, launched with its dA
+  ColsBatch cbatch;      // a layer's dA/dB partials, reduced in one launch at the end of the layer
   int pend_group = -1;
   int tpf[7] = {0, 0, 0, 0, 0, 0, 0}, tpd[7] = {0, 0, 0, 0, 0, 0, 0};  // per-target overrides (0 = site mode)
   float lscale = 0.0f;
@@ -445,7 +446,11 @@ struct hos_peft {
       by += 4.0 * ((double)M * pend_db.sg.len[t] + (double)M * r + (double)r * pend_db.sg.len[t]);
     }
     Scope s(this, "lora_dab", fl, by);
-    launch_lora_cols2(M, pend_db, &da, ws, ws_bytes, st);
+    launch_lora_cols2(M, pend_db, &da, ws, ws_bytes, st, &cbatch);
+  }
+  void flush_dab() {
+    Scope s(this, "lora_dab", 0, 0);
+    launch_lora_cols_flush(cbatch, st);
   }
   void check_ready() {
     check_tensors();
@@ -705,6 +710,7 @@ struct hos_peft {
         qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV), tpd[TV]);
       }
       lora_grad_a(l, 0, a.xn1, d, M);
+      flush_dab();  // the layer's dA/dB reductions
       {
         const bool emit = fuse16 && l > 0;
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4 + (emit ? 6.0 * M * d : 0));
@@ -1048,6 +1054,9 @@ struct hos_peft {
     if (c.n_heads != c.n_kv_heads) attn_part = alloc<float>(M * c.n_heads * 2 * c.head_dim);
     ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(d, F) * 4 * 8, 1ull << 30));
     ws = alloc<float>(ws_bytes / 4);
+    cbatch = ColsBatch{};
+    cbatch.cap = (64ull << 20) / 4;
+    cbatch.base = alloc<float>(cbatch.cap);
     hyp = alloc<AdamHyper>(1);
     launch_fill((float*)hyp, sizeof(AdamHyper) / 4, 0.0f, st);  // lr = wd = 0, t = 0 (all-zero bits)
     ids = alloc<int32_t>(M);
