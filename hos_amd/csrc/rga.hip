@@ -134,15 +134,30 @@ __global__ void __launch_bounds__(256) rga_gate_mean_kernel(const float* __restr
   if (threadIdx.x == 0) gm[blockIdx.x] = part[0] / (float)(T * K);
 }
 
-// loss += Σ_b (1/B)·(λ/L)·Σ_l gm[l·B + b] (layers in order, as loss_g adds the gate means)
-__global__ void rga_loss_kernel(const float* __restrict__ gm, int L, int B, float lambda, float* __restrict__ loss) {
+// loss += Σ_b (1/B)·(λ/L)·Σ_l gm[l·B + b] (layers in order, as loss_g adds the gate means). The means are
+// staged in LDS by the whole workgroup (LOSS_STAGE at a time, sequence-major) and summed in order by one thread.
+constexpr int LOSS_STAGE = 2048;
+__global__ void __launch_bounds__(256) rga_loss_kernel(const float* __restrict__ gm, int L, int B, float lambda,
+                                                       float* __restrict__ loss) {
+  __shared__ float buf[LOSS_STAGE];
+  const int per = LOSS_STAGE / L;  // sequences per stage (L <= LOSS_STAGE, checked by the launcher)
   float tot = 0.0f;
-  for (int b = 0; b < B; b++) {
-    float sl = 0.0f;
-    for (int l = 0; l < L; l++) sl += gm[l * B + b];
-    tot += sl * (lambda / (float)L) * (1.0f / (float)B);
+  for (int b0 = 0; b0 < B; b0 += per) {
+    const int nb = min(per, B - b0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb * L; i += blockDim.x) {
+      const int bb = i / L, l = i % L;
+      buf[i] = gm[l * B + b0 + bb];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int bb = 0; bb < nb; bb++) {
+        float sl = 0.0f;
+        for (int l = 0; l < L; l++) sl += buf[bb * L + l];
+        tot += sl * (lambda / (float)L) * (1.0f / (float)B);
+      }
   }
-  loss[0] += tot;
+  if (threadIdx.x == 0) loss[0] += tot;
 }
 
 }  // namespace
@@ -174,7 +189,8 @@ void launch_rga_loss(const float* gsum, long long ldl, int L, int B, int T, int 
                      float* loss, hipStream_t st) {
   rga_gate_mean_kernel<<<L * B, 256, 0, st>>>(gsum, ldl, B, T, K, gm);
   HOS_HIP_CHECK(hipGetLastError());
-  rga_loss_kernel<<<1, 1, 0, st>>>(gm, L, B, lambda, loss);
+  HOS_REQUIRE(L <= LOSS_STAGE, HOS_E_INVALID, "rga: too many layers for the loss staging");
+  rga_loss_kernel<<<1, 256, 0, st>>>(gm, L, B, lambda, loss);
   HOS_HIP_CHECK(hipGetLastError());
 }
 
