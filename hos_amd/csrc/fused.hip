@@ -142,6 +142,45 @@ __global__ void rope_kernel(float* __restrict__ buf, long long ld, int col0, int
   }
 }
 
+// RoPE over the first n_heads heads of each row of [M, ld] (col0 = 0) fused with the fp16 operand of the whole
+// row's first W columns: one workgroup per row rotates in place (the same arithmetic as rope_kernel), then
+// writes hi/lo/1-over-scale exactly as the f32 -> fp16 conversion of the rotated row would.
+__global__ void __launch_bounds__(256) rope_h16_kernel(float* __restrict__ buf, long long ld, int n_heads, int hd,
+                                                        int T, const float2* __restrict__ tab, int neox, int inverse,
+                                                        int W, _Float16* __restrict__ oh, _Float16* __restrict__ ol,
+                                                        float* __restrict__ orinv) {
+#pragma clang fp contract(off)
+  __shared__ float red[8];
+  const int m = blockIdx.x, half = hd >> 1, nrot = n_heads * half;
+  float* row = buf + (long long)m * ld;
+  float amax = 0.0f;
+  for (int i = threadIdx.x; i < nrot; i += RB) {
+    const int h = i / half, p = i % half;
+    const float2 sc2 = tab[(m % T) * half + p];
+    const float sn = sc2.x, cs = sc2.y;
+    float* base = row + h * hd;
+    const int ia = neox ? p : 2 * p, ib = neox ? p + half : 2 * p + 1;
+    const float a = base[ia], b = base[ib];
+    float ra, rb;
+    if (!inverse) {
+      ra = a * cs - b * sn;
+      rb = a * sn + b * cs;
+    } else {
+      ra = a * cs + b * sn;
+      rb = -a * sn + b * cs;
+    }
+    base[ia] = ra;
+    base[ib] = rb;
+    amax = fmaxf(amax, fmaxf(fabsf(ra), fabsf(rb)));
+  }
+  for (int c = n_heads * hd + threadIdx.x; c < W; c += RB) amax = fmaxf(amax, fabsf(row[c]));
+  amax = block_max(amax, red);  // its barriers also make the rotated row visible to the whole workgroup
+  const int e = row_exp(amax);
+  const float sc = ldexpf(1.0f, e);
+  for (int c = threadIdx.x; c < W; c += RB) put_h16(row[c] * sc, oh, ol, (long long)m * W + c);
+  if (threadIdx.x == 0) orinv[m] = ldexpf(1.0f, -e);
+}
+
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
 // gu rows = [gate (F) | up (F)] -> h = silu(gate)·up: f32 (optional) + fp16 operand.
@@ -687,6 +726,13 @@ void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T,
                  bool inverse, int M, hipStream_t st) {
   long long n = (long long)M * n_heads * (hd / 2);
   rope_kernel<<<ceil_div(n, 256), 256, 0, st>>>(buf, ld, col0, n_heads, hd, T, tab, neox, inverse, M);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_rope_h16(float* buf, long long ld, int n_heads, int hd, int T, const float2* tab, bool neox, bool inverse,
+                     int M, int W, H16 out, hipStream_t st) {
+  HOS_REQUIRE(n_heads * hd <= W && W <= ld, HOS_E_INVALID, "rope_h16: rotated heads must lie within the row");
+  if (M <= 0) return;
+  rope_h16_kernel<<<M, RB, 0, st>>>(buf, ld, n_heads, hd, T, tab, neox, inverse, W, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 // The register-resident kernels need F % 4 == 0, F <= 4·RB·SWIGLU_NV and 16-byte (f32) / 8-byte (fp16) aligned

@@ -11,6 +11,10 @@ void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const 
                         hipStream_t st, H16 out = H16{nullptr, nullptr, nullptr});
 void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,
                  bool inverse, int M, hipStream_t st);
+// RoPE (col0 = 0) fused with the fp16 row operand of the first W columns (row stride W), as launch_rope
+// followed by the f32 -> fp16 row conversion.
+void launch_rope_h16(float* buf, long long ld, int n_heads, int hd, int T, const float2* tab, bool neox, bool inverse,
+                     int M, int W, H16 out, hipStream_t st);
 void launch_swiglu_fwd(const float* gu, int M, int F, float* h, H16 out, hipStream_t st);
 void launch_swiglu_bwd(const float* gu, const float* dh, int M, int F, float* dgu, H16 out, hipStream_t st);
 // dl32 != null: write the gradient as plain f32 there instead of the fp16 operand dl.

@@ -690,8 +690,13 @@ struct hos_peft {
       }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
-        // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
-        launch_rope(dqkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+        // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both; without
+        // QK-norm in between it also writes the fp16 operand of the q|k|v dX GEMM
+        if (c.qk_norm)
+          launch_rope(dqkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+        else
+          launch_rope_h16(dqkv, W3, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, W3, hs,
+                          st);
       }
       if (c.qk_norm) {
         Scope s(this, "rmsnorm", 0, 4.0 * M * (qd + kvd) * 4);
@@ -699,7 +704,7 @@ struct hos_peft {
         launch_qknorm_bwd(dqkv, W3, qd, kvd, w.k_norm, a.qk_pre + (size_t)M * qd, a.qk_inv + M, M, st);
       }
       lora_grad_b(l, 0, dqkv, W3, W3, M);
-      to16(dqkv, W3, M, W3);
+      if (c.qk_norm) to16(dqkv, W3, M, W3);
       if (w.qkv.q && group_uniform(0) && gcount(0) * r <= 64) {
         // one dX GEMM over the stacked q|k|v contraction, the three LoRA terms as one rank-3r update
         qdx(w.qkv, hs, W3, M, dxn, d, 0, stacked_down_epi(l, 0), tpd[TQ]);
