@@ -69,6 +69,78 @@ __global__ void __launch_bounds__(NB) qknorm_bwd_kernel(float* __restrict__ g, l
   for (int c = threadIdx.x; c < n; c += NB) gr[c] = gr[c] * w[c] * iv - xr[c] * k;
 }
 
+// Register-resident variants (n % 4 == 0, n <= 4·NB·4, 16-byte aligned rows): the row is read once; the same
+// per-element arithmetic (the row sums are taken per thread over float4 columns, then across the block).
+__global__ void __launch_bounds__(NB) qknorm_fwd_reg_kernel(float* __restrict__ buf, long long ld, int col0, int n,
+                                                             const float* __restrict__ w, float eps,
+                                                             float* __restrict__ pre, float* __restrict__ inv) {
+  constexpr int NV = 4;
+  __shared__ float red[4];
+  const int row = blockIdx.x, n4 = n >> 2;
+  float4* xr = reinterpret_cast<float4*>(buf + (long long)row * ld + col0);
+  float4* pr = reinterpret_cast<float4*>(pre + (long long)row * n);
+  float4 v[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + NB * j;
+    if (i < n4) {
+      v[j] = xr[i];
+      pr[i] = v[j];
+      ss += v[j].x * v[j].x;
+      ss += v[j].y * v[j].y;
+      ss += v[j].z * v[j].z;
+      ss += v[j].w * v[j].w;
+    }
+  }
+  ss = bsum(ss, red) / (float)n;
+  const float iv = 1.0f / sqrtf(ss + eps);
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + NB * j;
+    if (i < n4) {
+      const float4 wv = reinterpret_cast<const float4*>(w)[i];
+      xr[i] = make_float4(v[j].x * iv * wv.x, v[j].y * iv * wv.y, v[j].z * iv * wv.z, v[j].w * iv * wv.w);
+    }
+  }
+  if (threadIdx.x == 0) inv[row] = iv;
+}
+__global__ void __launch_bounds__(NB) qknorm_bwd_reg_kernel(float* __restrict__ g, long long ld, int col0, int n,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ pre,
+                                                             const float* __restrict__ inv) {
+  constexpr int NV = 4;
+  __shared__ float red[4];
+  const int row = blockIdx.x, n4 = n >> 2;
+  float4* gr = reinterpret_cast<float4*>(g + (long long)row * ld + col0);
+  const float4* xr = reinterpret_cast<const float4*>(pre + (long long)row * n);
+  float4 gw[NV], xv[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + NB * j;
+    if (i < n4) {
+      const float4 gv = gr[i], wv = reinterpret_cast<const float4*>(w)[i];
+      xv[j] = xr[i];
+      gw[j] = make_float4(gv.x * wv.x, gv.y * wv.y, gv.z * wv.z, gv.w * wv.w);
+      s += gw[j].x * xv[j].x;
+      s += gw[j].y * xv[j].y;
+      s += gw[j].z * xv[j].z;
+      s += gw[j].w * xv[j].w;
+    }
+  }
+  s = bsum(s, red);
+  const float iv = inv[row];
+  const float k = iv * iv * iv / (float)n * s;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + NB * j;
+    if (i < n4)
+      gr[i] = make_float4(gw[j].x * iv - xv[j].x * k, gw[j].y * iv - xv[j].y * k, gw[j].z * iv - xv[j].z * k,
+                          gw[j].w * iv - xv[j].w * k);
+  }
+}
+
 // ---- router: one wave per token, lane j = expert j (E ≤ 64) ----
 __global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict__ logits, int M, int E, int K,
                                                         float* __restrict__ pfull, int* __restrict__ sel_e,
@@ -359,13 +431,21 @@ __global__ void fill_i32_kernel(int* p, long long n, int v) {
 void launch_qknorm_fwd(float* buf, long long ld, int col0, int n, const float* w, float eps, int M, float* pre,
                        float* inv, hipStream_t st) {
   if (M <= 0) return;
-  qknorm_fwd_kernel<<<M, NB, 0, st>>>(buf, ld, col0, n, w, eps, pre, inv);
+  auto al = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+  if (n % 4 == 0 && n <= 4 * NB * 4 && ld % 4 == 0 && col0 % 4 == 0 && al(buf) && al(w) && al(pre))
+    qknorm_fwd_reg_kernel<<<M, NB, 0, st>>>(buf, ld, col0, n, w, eps, pre, inv);
+  else
+    qknorm_fwd_kernel<<<M, NB, 0, st>>>(buf, ld, col0, n, w, eps, pre, inv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_qknorm_bwd(float* g, long long ld, int col0, int n, const float* w, const float* pre, const float* inv,
                        int M, hipStream_t st) {
   if (M <= 0) return;
-  qknorm_bwd_kernel<<<M, NB, 0, st>>>(g, ld, col0, n, w, pre, inv);
+  auto al = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+  if (n % 4 == 0 && n <= 4 * NB * 4 && ld % 4 == 0 && col0 % 4 == 0 && al(g) && al(w) && al(pre))
+    qknorm_bwd_reg_kernel<<<M, NB, 0, st>>>(g, ld, col0, n, w, pre, inv);
+  else
+    qknorm_bwd_kernel<<<M, NB, 0, st>>>(g, ld, col0, n, w, pre, inv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_moe_route(const float* logits, int M, int E, int K, float* pfull, int* sel_e, float* sel_p, int* slot,
