@@ -35,7 +35,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="qwen2.5-0.5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline sample")
-    ap.add_argument("--cpu-seq", type=int, default=256, help="tokens in the CPU baseline sample")
+    ap.add_argument("--cpu-seq", type=int, default=512, help="tokens in the CPU baseline sample")
+    ap.add_argument("--serial-seq", type=int, default=64,
+                    help="tokens of the 1-thread configs[0] (SmolLM2-135M) CPU sample (0: skip)")
     ap.add_argument("--rga", action="store_true",
                     help="train RGA adapters (4 genes of bottleneck 4, lambda 1e-3: cmd_peft's defaults) instead of LoRA")
     ap.add_argument("--finetune", action="store_true",
@@ -74,26 +76,52 @@ def traffic_per_launch(kernel_class, cfg):
     return None
 
 
-def dx_gemm_probe(gpu):
-    """configs[1]: dX = dY·deq(W), dY [4096,4096] ~N(0,1e-2), W [4096,4096] ~N(0,0.02) -> Q4_K."""
+def config1_probe(gpu):
+    """configs[1] on its own shapes: W [4096, 4096] ~N(0, 0.02) -> Q4_K; dX = dY·deq(W) with dY [4096, 4096]
+    ~N(0, 1e-2), the forward X·deq(W)ᵀ, both at 1 and 3 precision passes (kernel alone, fp16 operand already
+    converted, HIP events), and the LoRA r16 A/B gradient on the same shapes (u = x·A, du = s·dY·Bᵀ,
+    dB = s·uᵀ·dY, dA = xᵀ·du: hos_hip_lora without the y / dx products), timed on the context stream.
+    Parity of every leg at this size: tests/test_gpu_config1.py."""
     from hos_amd.hip_be import GGML_Q4_K
     T = N = K = 4096
+    r = 16
     rng = np.random.default_rng(2)
     w = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
     gpu.upload_quant(0xD0, gpu.quantize(w, GGML_Q4_K), GGML_Q4_K, N, K)
     dy = (rng.standard_normal((T, N), dtype=np.float32) * np.float32(1e-2))
-    din, dout = gpu.alloc(T * N * 4), gpu.alloc(T * K * 4)
-    gpu.h2d(din, dy)
+    x = rng.standard_normal((T, K), dtype=np.float32)
+    d_dy, d_x, dout = gpu.alloc(T * N * 4), gpu.alloc(T * K * 4), gpu.alloc(T * max(N, K) * 4)
+    gpu.h2d(d_dy, dy)
+    gpu.h2d(d_x, x)
+    flops = 2.0 * T * N * K
     out = {}
-    for passes in (1, 3):
-        gpu.set_gemm_passes(passes)
-        ms = gpu.time_qgemm(1, 0xD0, din, T, dout, 20)
-        tf = 2.0 * T * N * K / (ms * 1e-3) / 1e12
-        out[f"passes{passes}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
-                                  "frac_of_peak": round(tf / PEAK_MFMA_TFLOPS, 4)}
+    for leg, which, src in (("dx", 1, d_dy), ("fwd", 0, d_x)):
+        for passes in (1, 3):
+            gpu.set_gemm_passes(passes)
+            ms = gpu.time_qgemm(which, 0xD0, src, T, dout, 20)
+            tf = flops / (ms * 1e-3) / 1e12
+            out[f"{leg}_passes{passes}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                                            "frac_of_peak": round(tf / PEAK_MFMA_TFLOPS, 4)}
     gpu.set_gemm_passes(1)
-    gpu.free(din)
-    gpu.free(dout)
+    A = gpu.to_dev(rng.standard_normal((K, r), dtype=np.float32) * np.float32(0.02))
+    B = gpu.to_dev(rng.standard_normal((r, N), dtype=np.float32) * np.float32(0.02))
+    U, DU_A, DB = gpu.empty_dev((T, r)), gpu.empty_dev((K, r)), gpu.empty_dev((r, N))
+    args = (d_x, d_dy, T, K, N, r, A, B, 2.0, None, U, DU_A, DB, None)
+    gpu.op_async("lora", *args)  # warm-up
+    iters = 20
+    gpu.timer_begin()
+    for _ in range(iters):
+        gpu.op_async("lora", *args)
+    ms = gpu.timer_end() / iters
+    # algorithmic bytes: x and dY read once each (u, du, dA, dB need nothing else of size)
+    nbytes = 4.0 * T * (K + N)
+    out["lora_r16_dAdB"] = {"us": round(ms * 1e3, 1), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                            "algorithmic_bytes": int(nbytes)}
+    for a in (A, B, U, DU_A, DB):
+        a.free()
+    for p in (d_dy, d_x, dout):
+        gpu.free(p)
     gpu.evict(0xD0)
     return out
 
@@ -114,9 +142,10 @@ def workload(cfg):
     return f"{cfg.name} LoRA r{cfg.lora_rank} on {','.join(cfg.lora_targets)}; {base}; AdamW"
 
 
-def cpu_baseline(cfg, tensors, seq):
-    """The oracle (C++ restatement of HOS's CPU path, OpenMP row-parallel) on one sequence of `seq` tokens:
-    forward + backward + AdamW, timed on this host's cores."""
+def cpu_baseline(cfg, tensors, seq, threads=0):
+    """The oracle (C++ restatement of HOS's CPU path, OpenMP row-parallel, each element's summation order
+    serial) on one sequence of `seq` tokens: forward + backward + AdamW, timed on `threads` host threads
+    (0: every thread OpenMP is given)."""
     import types
     from oracle import binding as o
     from hos_amd import synth
@@ -124,6 +153,7 @@ def cpu_baseline(cfg, tensors, seq):
         "n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "rms_eps", "rope_base",
         "rope_neox", "attn_bias", "lora_rank", "lora_alpha", "rga_genes", "rga_bottleneck", "rga_lambda")})
     oc.lora_targets = cfg.target_mask
+    prev = o.set_threads(0)
     m = o.OracleModel(oc)
     for name, (raw, t, rows, cols) in tensors.items():
         m.set_tensor(name, raw, t, rows, cols)
@@ -133,13 +163,14 @@ def cpu_baseline(cfg, tensors, seq):
     for (l, t), (A, B) in synth.lora_init(cfg, seed=5).items():
         m.set_lora(l, ("q", "k", "v", "o", "gate", "up", "down").index(t), A, B)
     ids, tg = synth.tokens(cfg, 1, seq, seed=8)
+    cores = o.set_threads(threads)
     t0 = time.perf_counter()
     m.loss_grad(ids, tg)
     m.adamw(cfg.lr, 0.0)
     dt = time.perf_counter() - t0
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+    o.set_threads(prev)
     return {"value": round(seq / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"1 sequence x {seq} tokens (fwd+bwd+AdamW), {dt:.1f} s"}
+            "sample": f"{cfg.name}: 1 sequence x {seq} tokens (fwd+bwd+AdamW, micro-batch), {dt:.1f} s"}
 
 
 def finetune_bench(args):
@@ -265,10 +296,13 @@ def main():
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_per_launch(dom, cfg), "kernel": dom,
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"]}
 
-    dx = dx_gemm_probe(gpu)
-    cpu = None
+    c1 = config1_probe(gpu)
+    cpu = serial = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, tensors, args.cpu_seq)
+        if args.serial_seq > 0:  # the reference's training matmul is single-threaded (src/tensor.rs:319-378)
+            c0 = synth.CONFIGS["smollm2-135m"]
+            serial = cpu_baseline(c0, synth.build_tensors(gpu, c0, seed=1234), args.serial_seq, threads=1)
     line = {
         "metric": METRIC + (" [RGA adapters]" if cfg.is_rga else ""), "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
@@ -277,8 +311,9 @@ def main():
                    "parallelism": "dp1", "precision": "layer GEMMs 3-pass, head fwd 1-pass, head dX weight-split"},
         "roofline": roof,
         "mfma_roofline_frac_step": round(value * f_tok / 1e12 / PEAK_MFMA_TFLOPS, 4),
-        "dx_gemm_4096cubed_q4k": dx,
+        "config1_4096cubed_q4k": c1,
         "cpu_baseline": cpu,
+        "cpu_serial_config0": serial,
         "gpu_over_cpu": round(value / cpu["value"], 1) if cpu else None,
         "kernel_ms_per_step": kernel_ms,
         "loss": round(loss, 5),

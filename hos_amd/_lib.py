@@ -41,6 +41,8 @@ SIGNATURES = {
     "hos_hip_qgemm_fwd_dev": (i32, [vp, u64, vp, sz, vp]),
     "hos_hip_qgemm_dx_dev": (i32, [vp, u64, vp, sz, vp]),
     "hos_hip_time_qgemm": (i32, [vp, i32, u64, vp, sz, vp, i32, ctypes.POINTER(ctypes.c_float)]),
+    "hos_hip_timer_begin": (i32, [vp]),
+    "hos_hip_timer_end": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
     "hos_hip_quantize": (i32, [vp, vp, sz, u32, vp]),
     "hos_hip_bytes_for": (sz, [u32, sz]),
     "hos_hip_quantize_dev": (i32, [vp, vp, sz, u32, vp]),

@@ -70,6 +70,7 @@ struct hos_ctx {
   DevMem ws, t0, t1, t2, t3, t4, t5;
   DevMem ops[8];  // scratch of the op-level entry points (ops.hip)
   int passes = 1;
+  hipEvent_t tev[2] = {nullptr, nullptr};  // hos_hip_timer_begin / _end
   static constexpr size_t kWs = 256ull << 20;
 };
 
@@ -171,6 +172,8 @@ void hos_hip_destroy(hos_ctx* c) {
   for (auto& kv : c->qw) free_qweight(kv.second);
   c->qw.clear();
   c->f32cache.clear();
+  for (auto& e : c->tev)
+    if (e) (void)hipEventDestroy(e);
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -339,6 +342,23 @@ int hos_hip_time_qgemm(hos_ctx* c, int which, uint64_t key, const float* in_dev,
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     *avg_ms = ms / (float)iters;
+  });
+}
+
+int hos_hip_timer_begin(hos_ctx* c) {
+  return guard(c, [&] {
+    for (auto& e : c->tev)
+      if (!e) HOS_HIP_CHECK(hipEventCreate(&e));
+    HOS_HIP_CHECK(hipEventRecord(c->tev[0], c->stream));
+  });
+}
+
+int hos_hip_timer_end(hos_ctx* c, float* ms) {
+  return guard(c, [&] {
+    HOS_REQUIRE(ms && c->tev[0], HOS_E_INVALID, "timer_end: no timer_begin on this context");
+    HOS_HIP_CHECK(hipEventRecord(c->tev[1], c->stream));
+    HOS_HIP_CHECK(hipEventSynchronize(c->tev[1]));
+    HOS_HIP_CHECK(hipEventElapsedTime(ms, c->tev[0], c->tev[1]));
   });
 }
 

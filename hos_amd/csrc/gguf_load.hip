@@ -165,6 +165,8 @@ uint64_t n_elements(const TInfo& t) {
 // Raw bytes of a tensor (src/gguf.rs:513-533).
 const uint8_t* raw(const GgufFile& g, const std::string& name, const TInfo& t, size_t* nbytes) {
   const uint64_t n = n_elements(t);
+  // every byte count below is at most 4·n: bound n first so no product can wrap
+  HOS_REQUIRE(n <= (1ull << 48), HOS_E_FORMAT, "tensor '" + name + "' is larger than any file could hold");
   size_t nb = 0;
   switch (t.type) {
     case T_F32: nb = n * 4; break;
@@ -175,6 +177,7 @@ const uint8_t* raw(const GgufFile& g, const std::string& name, const TInfo& t, s
   HOS_REQUIRE(nb > 0 || n == 0, HOS_E_UNSUPPORTED_QUANT,
               "tensor '" + name + "' has GGUF type " + std::to_string(t.type) +
                   " (the fused GEMMs read Q8_0, Q4_K and Q6_K)");
+  HOS_REQUIRE(t.offset <= g.buf.size(), HOS_E_FORMAT, "tensor '" + name + "' data out of bounds");
   const uint64_t start = (uint64_t)g.data_offset + t.offset;
   HOS_REQUIRE(start <= g.buf.size() && nb <= g.buf.size() - start, HOS_E_FORMAT,
               "tensor '" + name + "' data out of bounds");

@@ -393,14 +393,8 @@ __global__ void lora_cols_reduce(const float* __restrict__ part, int S, ColsJobD
 int ceil_div_i(long long a, long long b) { return (int)((a + b - 1) / b); }
 
 // Workgroups a launch aims for; the long contraction is split until the grid reaches it.
-int split_target() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = std::getenv("HOS_LORA_WGS");
-    v = e ? std::max(1, std::atoi(e)) : 1024;
-  }
-  return v;
-}
+// (measured in the training step: 512 −1.6%, 2048 −1%, 4096 −3% tokens/s against 1024)
+int split_target() { return 1024; }
 
 }  // namespace
 

@@ -154,10 +154,12 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict_
   const float ex = on ? expf(l - mx) : 0.0f;
   const float p = ex / wsum(ex);
   if (on) pfull[(long long)t * E + j] = p;
-  // top K: repeated arg-max, ties to the lower expert (the stable descending sort of the reference)
+  // top K: repeated arg-max, ties to the lower expert (the stable descending sort of the reference). A NaN
+  // probability (diverged logits) ranks below every number but above taken lanes, so each slot is still
+  // written exactly once with a distinct in-range expert and the NaN reaches the loss, not an index.
   bool taken = !on;
   for (int s = 0; s < K; s++) {
-    float bv = taken ? -1.0f : p;
+    float bv = taken ? -2.0f : (p != p ? -1.0f : p);
     int bi = taken ? 64 : j;
     for (int o = 32; o > 0; o >>= 1) {
       const float ov = __shfl_xor(bv, o);

@@ -907,25 +907,6 @@ struct hos_peft {
     } else {
       pf = pd = phf = phd = passes;
     }
-    if (const char* e = std::getenv("HOS_PREC_TARGETS")) {  // diagnostics: 7 fwd modes then 7 dX modes
-      int v[14];
-      if (std::sscanf(e, "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d", v, v + 1, v + 2, v + 3, v + 4, v + 5, v + 6,
-                      v + 7, v + 8, v + 9, v + 10, v + 11, v + 12, v + 13) == 14)
-        for (int t = 0; t < 7; t++) {
-          tpf[t] = v[t];
-          tpd[t] = v[7 + t];
-        }
-    }
-    if (const char* e = std::getenv("HOS_PREC_SITES")) {  // diagnostics: "fwd,dx,head_fwd,head_dx"
-      int a = 0, b2 = 0, c2 = 0, d2 = 0;
-      if (std::sscanf(e, "%d,%d,%d,%d", &a, &b2, &c2, &d2) == 4 && a >= 1 && a <= 4 && b2 >= 1 && b2 <= 4 &&
-          c2 >= 1 && c2 <= 4 && d2 >= 1 && d2 <= 4) {
-        pf = a;
-        pd = b2;
-        phf = c2;
-        phd = d2;
-      }
-    }
     const size_t M = (size_t)Mmax;
     lw.resize(L);
     // LoRA arena

@@ -31,21 +31,12 @@
 
 #include "kernels.hpp"
 
-#ifndef HOS_QG_ABLATE
-#define HOS_QG_ABLATE 0  // diagnostics only: 1 no B loads/dequant, 2 no A loads, 4 no LDS fragment reads, 8 no MFMA
-#endif
 
 namespace hos {
 namespace {
 
 typedef short s4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ h8 zero_h8() {
-  h8 z;
-#pragma unroll
-  for (int i = 0; i < 8; i++) z[i] = (_Float16)0.0f;
-  return z;
-}
 
 // Signed byte i of a word as float (one bit-field extract + one convert).
 __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
@@ -283,20 +274,11 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
       int row = idx / (BK / 8), cv = idx % (BK / 8);
       int m = m0 + row;
       long long off = (long long)m * lda + c0 + 8 * cv;
-      if constexpr (HOS_QG_ABLATE & 2) {
-        R.a[v] = zero_h8();
-        R.al[v] = zero_h8();
-        continue;
-      }
       // Rows past M re-read row M-1: they only feed output rows past M, which are never stored. No
       // branch, so the compiler counts the loads in flight exactly and waits only for the slab it needs.
       const long long offc = m < M ? off : (long long)(M - 1) * lda + c0 + 8 * cv;
       R.a[v] = *(const h8*)(A + offc);
       if constexpr (ALO) R.al[v] = *(const h8*)(Alo + offc);
-    }
-    if constexpr (HOS_QG_ABLATE & 1) {
-      R.b.ok = false;
-      return;
     }
     if constexpr (DX) {
       const int col = n0 + bc;  // output column run; rows are the contraction
@@ -366,13 +348,6 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
           if constexpr (BLO) bfl[j] = *(const h8*)(bs + G::BTILE + ro);
         }
       }
-      if constexpr (HOS_QG_ABLATE & 4) {
-#pragma unroll
-        for (int i = 0; i < G::TM; i++) af[i] = afl[i] = zero_h8();
-#pragma unroll
-        for (int j = 0; j < G::TN; j++) bf[j] = bfl[j] = zero_h8();
-      }
-      if constexpr (HOS_QG_ABLATE & 8) continue;
 #pragma unroll
       for (int i = 0; i < G::TM; i++)
 #pragma unroll
@@ -556,16 +531,6 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bm = 256;
     bn = 128;
     bk = 32;
-  }
-  if (const char* ov = std::getenv("HOS_QGEMM_TILE")) {  // tuning override: "BMxBNxBK"
-    int x = 0, y = 0, z = 0;
-    if (std::sscanf(ov, "%dx%dx%d", &x, &y, &z) == 3 && (z == 32 || (z == 64 && C % 64 == 0)) &&
-        ((x == 128 && y == 128) || (x == 64 && y == 128) || (x == 128 && y == 64) || (x == 64 && y == 64) ||
-         (z == 32 && x == 256 && y == 128))) {
-      bm = x;
-      bn = y;
-      bk = z;
-    }
   }
   // A fused rank above 32 (stacked q|k|v dX): 64×64 tiles, whose LDS holds the rank-64 staging, and no split
   // (the split-K reduction stages at most 32).

@@ -179,6 +179,21 @@ class Gpu:
         self._chk(lib().hos_hip_time_qgemm(self.h, which, key, in_dev, t, out_dev, iters, ctypes.byref(ms)))
         return ms.value
 
+    def timer_begin(self):
+        """Start timing the context stream (HIP event); pair with timer_end."""
+        self._chk(lib().hos_hip_timer_begin(self.h))
+
+    def timer_end(self):
+        """Milliseconds of stream work since timer_begin (waits for the stream)."""
+        ms = ctypes.c_float()
+        self._chk(lib().hos_hip_timer_end(self.h, ctypes.byref(ms)))
+        return ms.value
+
+    def op_async(self, name, *args):
+        """Enqueue hos_hip_<name>(ctx, *args) without waiting for the stream."""
+        conv = [a.ptr if isinstance(a, DevArray) else a for a in args]
+        self._chk(getattr(lib(), "hos_hip_" + name)(self.h, *conv))
+
     # ---- op-level entry points (device pointers) ----
     def to_dev(self, arr):
         """Upload an array; returns a DevArray that frees itself with .free()."""

@@ -91,6 +91,10 @@ int hos_hip_qgemm_dx_dev(hos_ctx* ctx, uint64_t key, const float* dy_dev, size_t
  * Returns the mean kernel time in ms. */
 int hos_hip_time_qgemm(hos_ctx* ctx, int which, uint64_t key, const float* in_dev, size_t t, float* out_dev,
                        int iters, float* avg_ms);
+/* Elapsed time of whatever is enqueued on the context stream between the two calls, from HIP events
+ * (timer_end waits for the stream). No counterpart in the reference; measurement only. */
+int hos_hip_timer_begin(hos_ctx* ctx);
+int hos_hip_timer_end(hos_ctx* ctx, float* ms);
 /* quantize(x, ggml_type) of src/gguf_write.rs:41-50 (Q8_0 :178-196, Q4_K :355-416,
  * Q6_K :426-495), run on the device; byte-identical to the reference encoders.
  * x: n floats (host), out: bytes_for(type, n) bytes (host). */

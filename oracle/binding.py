@@ -48,6 +48,8 @@ def lib():
         L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.orc_f32_to_f16.restype = ctypes.c_uint16
         L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_set_threads.restype = ctypes.c_int
+        L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_bytes_for.restype = ctypes.c_size_t
         L.orc_bytes_for.argtypes = [ctypes.c_uint32, ctypes.c_size_t]
         L.orc_dequant.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_size_t, ctypes.c_void_p]
@@ -95,6 +97,11 @@ def _f32(a):
 
 
 # ---- codec ----
+
+def set_threads(n=0):
+    """OpenMP threads the oracle uses from now on (n <= 0: unchanged); returns the count in effect."""
+    return lib().orc_set_threads(n)
+
 
 def bytes_for(ggml_type, n):
     return lib().orc_bytes_for(ggml_type, n)

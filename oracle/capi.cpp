@@ -45,10 +45,17 @@ void backward_from(const Tensor& out, const float* gout) {
 
 struct orc_model;  // opaque handle = orc::Model
 
+#include <omp.h>
+
 extern "C" {
 
 float orc_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
 uint16_t orc_f32_to_f16(float f) { return f32_to_f16(f); }
+// OpenMP threads for the following calls (n <= 0 leaves the setting); returns the count now in effect.
+int orc_set_threads(int n) {
+  if (n > 0) omp_set_num_threads(n);
+  return omp_get_max_threads();
+}
 size_t orc_bytes_for(uint32_t type, size_t n) { return bytes_for(type, n); }
 int orc_dequant(const uint8_t* bytes, uint32_t type, size_t n, float* out) { return dequant_into(bytes, type, n, out); }
 int orc_quantize(const float* x, size_t n, uint32_t type, uint8_t* out) { return quantize(x, n, type, out); }
