@@ -93,6 +93,7 @@ SIGNATURES = {
     "hos_hip_adamw": (i32, [vp, vp, vp, vp, vp, sz, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                             ctypes.c_float, ctypes.c_float, i32, i32]),
     "hos_hip_lora": (i32, [vp, vp, vp, sz, sz, sz, i32, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp]),
+    "hos_hip_lora_noalloc": (i32, [vp, vp, vp, sz, sz, sz, i32, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp]),
     "hos_peft_profile": (i32, [vp, i32]),
     "hos_peft_use_graph": (i32, [vp, i32]),
     "hos_peft_profile_only": (i32, [vp, ctypes.c_char_p]),

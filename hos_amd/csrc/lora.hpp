@@ -69,4 +69,8 @@ void launch_lora_cols_flush(ColsBatch& b, hipStream_t st);
 void launch_lora_cols2(long long M, const ColsJob& a, const ColsJob* b, float* ws, size_t ws_bytes, hipStream_t st,
                        ColsBatch* batch = nullptr);
 
+// Workspace bytes the launches above need (no batch) for these shapes: 0 when they do not split.
+size_t lora_rows_ws_bytes(long long M, long long K, int n);
+size_t lora_cols2_ws_bytes(long long M, const ColsJob& a, const ColsJob* b);
+
 }  // namespace hos

@@ -2,7 +2,10 @@
 // the context's stream (hos_hip_synchronize waits). These are the reference's autograd ops
 // (src/tensor.rs) with their VJPs, so each can be checked against the CPU path on its own, as the
 // reference's tests/autograd.rs checks the ops; the training step (peft.hip) schedules the same kernels.
+#include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <string>
 #include <vector>
 
 #include "ctx.hpp"
@@ -10,6 +13,11 @@
 #include "lora.hpp"
 
 using namespace hos;
+
+// Scratch of hos_hip_lora_noalloc (64 MiB, one copy per GPU); host code uses only the per-device address
+// lora_scratch_ptr() looks up.
+constexpr size_t kLoraScratch = 64ull << 20;
+static __device__ __align__(256) char scratch[kLoraScratch];
 
 namespace {
 
@@ -60,6 +68,87 @@ void transpose(const float* src, int rows, int cols, float* dst, hipStream_t st)
   dim3 g(ceil_div(cols, 32), ceil_div(rows, 32));
   transpose_kernel<<<g, dim3(32, 8), 0, st>>>(src, rows, cols, dst);
   HOS_HIP_CHECK(hipGetLastError());
+}
+
+void lora_check(const float* x, const float* dy, size_t in, size_t out, int r, const float* A, const float* B,
+                const float* u, const float* dA, const float* dB) {
+  HOS_REQUIRE(x && dy && A && B && u && dA && dB && r > 0 && r <= 96, HOS_E_INVALID, "lora: bad arguments");
+  HOS_REQUIRE(in % 4 == 0 && out % 4 == 0, HOS_E_INVALID, "lora: in and out must be multiples of 4");
+}
+
+// The two cols jobs of the branch: dB = s·uᵀ·dy [r, out] and dAᵀ = duᵀ·x [r, in] (into at).
+void lora_cols_jobs(const float* dy, const float* x, size_t rows, size_t in, size_t out, int r, float scale,
+                    const float* u, const float* du, float* dB, float* at, ColsJob* jdb, ColsJob* jda) {
+  (void)rows;
+  ColsSeg cb;
+  cb.nseg = 1;
+  cb.len[0] = (int)out;
+  ColsSeg ca;
+  ca.nseg = 1;
+  ca.len[0] = (int)in;
+  *jdb = ColsJob{r, scale, u, r, dy, (long long)out, cb, dB, (long long)out, 1};
+  *jda = ColsJob{r, 1.0f, du, r, x, (long long)in, ca, at, (long long)in, 1};
+}
+
+// The LoRA branch on caller-provided scratch: at [r, in] (Aᵀ, then dAᵀ), du [rows, r], ws the split partials.
+void lora_run(const float* x, const float* dy, size_t rows, size_t in, size_t out, int r, const float* A,
+              const float* B, float scale, float* y, float* u, float* dA, float* dB, float* dx, float* at, float* du,
+              float* ws, size_t wsb, hipStream_t st) {
+  transpose(A, (int)in, r, at, st);
+  RowsSeg down;
+  down.nt = 1;
+  down.r = r;
+  down.kend[0] = (int)in;
+  launch_lora_rows((long long)rows, (long long)in, 1.0f, x, (long long)in, at, (long long)in, down, u, r, ws, wsb,
+                   st);
+  if (y)
+    launch_gemm_f32((long long)rows, (long long)out, r, scale, u, r, 1, B, (long long)out, 1, 1.0f, y, (long long)out,
+                    ws, wsb, st);
+  RowsSeg up;
+  up.nt = 1;
+  up.r = r;
+  up.kend[0] = (int)out;
+  launch_lora_rows((long long)rows, (long long)out, scale, dy, (long long)out, B, (long long)out, up, du, r, ws, wsb,
+                   st);
+  // dB = s·uᵀ·dy and dAᵀ = duᵀ·x in one launch
+  ColsJob jdb, jda;
+  lora_cols_jobs(dy, x, rows, in, out, r, scale, u, du, dB, at, &jdb, &jda);
+  launch_lora_cols2((long long)rows, jdb, &jda, ws, wsb, st);
+  transpose(at, r, (int)in, dA, st);
+  if (dx)
+    launch_gemm_f32((long long)rows, (long long)in, r, 1.0f, du, r, 1, A, 1, r, 1.0f, dx, (long long)in, ws, wsb, st);
+}
+
+// Workspace the branch's split launches need (the f32 GEMMs of y and dx split only into what is left).
+size_t lora_ws_need(size_t rows, size_t in, size_t out, int r) {
+  ColsJob jdb, jda;
+  lora_cols_jobs(nullptr, nullptr, rows, in, out, r, 1.0f, nullptr, nullptr, nullptr, nullptr, &jdb, &jda);
+  return std::max({lora_rows_ws_bytes((long long)rows, (long long)in, r),
+                   lora_rows_ws_bytes((long long)rows, (long long)out, r),
+                   lora_cols2_ws_bytes((long long)rows, jdb, &jda)});
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Scratch of hos_hip_lora_noalloc: a file-scope device array, one copy per GPU, held for the life of the
+// process. Host code never passes the array's name to a kernel (on the host it is only a stand-in symbol):
+// the device address is looked up once per device with hipGetSymbolAddress and kept per device. Every call
+// on one GPU shares the array and leaves its contents behind; the kernels write every scratch element before
+// reading it, so nothing needs clearing. Calls that overlap on one GPU (two streams or two contexts) race.
+void* lora_scratch_ptr() {
+  static std::mutex mu;
+  static void* ptr[64] = {};
+  int dev = 0;
+  HOS_HIP_CHECK(hipGetDevice(&dev));
+  HOS_REQUIRE(dev >= 0 && dev < 64, HOS_E_DEVICE, "lora_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    HOS_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    HOS_REQUIRE(p != nullptr, HOS_E_DEVICE, "lora_noalloc: no device address for the scratch array");
+    ptr[dev] = p;
+  }
+  return ptr[dev];
 }
 
 }  // namespace
@@ -195,46 +284,33 @@ int hos_hip_adamw(hos_ctx* c, float* p, const float* g, float* m, float* v, size
 int hos_hip_lora(hos_ctx* c, const float* x, const float* dy, size_t rows, size_t in, size_t out, int r,
                  const float* A, const float* B, float scale, float* y, float* u, float* dA, float* dB, float* dx) {
   return op_guard(c, [&](hipStream_t st) {
-    HOS_REQUIRE(x && dy && A && B && u && dA && dB && r > 0 && r <= 96, HOS_E_INVALID, "lora: bad arguments");
-    HOS_REQUIRE(in % 4 == 0 && out % 4 == 0, HOS_E_INVALID, "lora: in and out must be multiples of 4");
+    lora_check(x, dy, in, out, r, A, B, u, dA, dB);
     DevMem& wsm = internal_ws(c);
-    float* ws = (float*)wsm.p;
-    const size_t wsb = wsm.n;
     DevMem& at = internal_scratch(c, 5);  // Aᵀ [r, in], then dAᵀ
     at.ensure((size_t)r * in * 4);
     DevMem& dub = internal_scratch(c, 6);  // du [rows, r]
     dub.ensure(rows * r * 4 + 4);
-    float* du = (float*)dub.p;
-    transpose(A, (int)in, r, (float*)at.p, st);
-    RowsSeg down;
-    down.nt = 1;
-    down.r = r;
-    down.kend[0] = (int)in;
-    launch_lora_rows((long long)rows, (long long)in, 1.0f, x, (long long)in, (const float*)at.p, (long long)in, down, u,
-                     r, ws, wsb, st);
-    if (y)
-      launch_gemm_f32((long long)rows, (long long)out, r, scale, u, r, 1, B, (long long)out, 1, 1.0f, y,
-                      (long long)out, ws, wsb, st);
-    RowsSeg up;
-    up.nt = 1;
-    up.r = r;
-    up.kend[0] = (int)out;
-    launch_lora_rows((long long)rows, (long long)out, scale, dy, (long long)out, B, (long long)out, up, du, r, ws, wsb,
-                     st);
-    // dB = s·uᵀ·dy and dAᵀ = duᵀ·x in one launch
-    ColsSeg cb;
-    cb.nseg = 1;
-    cb.len[0] = (int)out;
-    ColsSeg ca;
-    ca.nseg = 1;
-    ca.len[0] = (int)in;
-    const ColsJob jdb{r, scale, u, r, dy, (long long)out, cb, dB, (long long)out, 1};
-    const ColsJob jda{r, 1.0f, du, r, x, (long long)in, ca, (float*)at.p, (long long)in, 1};
-    launch_lora_cols2((long long)rows, jdb, &jda, ws, wsb, st);
-    transpose((const float*)at.p, r, (int)in, dA, st);
-    if (dx)
-      launch_gemm_f32((long long)rows, (long long)in, r, 1.0f, du, r, 1, A, 1, r, 1.0f, dx, (long long)in, ws, wsb,
-                      st);
+    lora_run(x, dy, rows, in, out, r, A, B, scale, y, u, dA, dB, dx, (float*)at.p, (float*)dub.p, (float*)wsm.p,
+             wsm.n, st);
+  });
+}
+
+// hos_hip_lora without any device allocation: Aᵀ, du and the split partials live in `scratch`.
+int hos_hip_lora_noalloc(hos_ctx* c, const float* x, const float* dy, size_t rows, size_t in, size_t out, int r,
+                         const float* A, const float* B, float scale, float* y, float* u, float* dA, float* dB,
+                         float* dx) {
+  return op_guard(c, [&](hipStream_t st) {
+    lora_check(x, dy, in, out, r, A, B, u, dA, dB);
+    const size_t at_b = align256((size_t)r * in * 4), du_b = align256(rows * r * 4 + 4);
+    const size_t ws_b = lora_ws_need(rows, in, out, r);
+    HOS_REQUIRE(at_b + du_b + ws_b <= kLoraScratch, HOS_E_INVALID,
+                "lora_noalloc: rows " + std::to_string(rows) + ", in " + std::to_string(in) + ", out " +
+                    std::to_string(out) + ", r " + std::to_string(r) + " need " + std::to_string(at_b + du_b + ws_b) +
+                    " bytes of scratch; the maximum is " + std::to_string(kLoraScratch));
+    char* base = (char*)lora_scratch_ptr();
+    float* ws = (float*)(base + at_b + du_b);
+    lora_run(x, dy, rows, in, out, r, A, B, scale, y, u, dA, dB, dx, (float*)base, (float*)(base + at_b), ws,
+             kLoraScratch - at_b - du_b, st);
   });
 }
 

@@ -152,6 +152,16 @@ int hos_hip_adamw(hos_ctx* ctx, float* p, const float* g, float* m, float* v, si
 int hos_hip_lora(hos_ctx* ctx, const float* x, const float* dy, size_t rows, size_t in, size_t out, int r,
                  const float* A, const float* B, float scale, float* y, float* u, float* dA, float* dB, float* dx);
 
+/* hos_hip_lora without device allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as hos_hip_lora; its scratch (A transposed, du, split partials) is one
+ * 64 MiB device array per GPU, held until the process ends: shapes needing more fail with HOS_E_INVALID before
+ * any launch. Every call on one GPU shares that array, so calls that overlap on one GPU (two streams or two
+ * contexts) race; calls in one stream order are safe. */
+int hos_hip_lora_noalloc(hos_ctx* ctx, const float* x, const float* dy, size_t rows, size_t in, size_t out, int r,
+                         const float* A, const float* B, float scale, float* y, float* u, float* dA, float* dB,
+                         float* dx);
+
 /* ---- device memory (GpuBuf / download_buf analogue, src/metal_be_stub.rs:13-20) ---- */
 int hos_hip_dev_alloc(hos_ctx* ctx, size_t nbytes, void** dptr);
 int hos_hip_dev_free(hos_ctx* ctx, void* dptr);
