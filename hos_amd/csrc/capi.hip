@@ -39,23 +39,25 @@ void upload_qweight(hipStream_t st, const uint8_t* bytes, size_t nbytes, uint32_
   HOS_REQUIRE(bytes != nullptr, HOS_E_INVALID, "upload_quant: null bytes");
   size_t be = block_elems(type);
   HOS_REQUIRE(be != 0, HOS_E_UNSUPPORTED_QUANT,
-              "unsupported quantization type " + std::to_string(type) + " (supported: Q8_0/Q4_K/Q6_K)");
+              "unsupported quantization type " + std::to_string(type) +
+                  " (supported: F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)");
   HOS_REQUIRE(rows > 0 && cols > 0 && cols % be == 0, HOS_E_INVALID,
               "upload_quant: cols must be a positive multiple of the block size " + std::to_string(be));
   HOS_REQUIRE(cols % 32 == 0, HOS_E_INVALID, "upload_quant: cols must be a multiple of 32");
+  HOS_REQUIRE(rows <= (1ull << 40) / cols, HOS_E_INVALID, "upload_quant: matrix too large");
   size_t need = gguf_bytes_for(type, rows * cols);
   HOS_REQUIRE(nbytes == need, HOS_E_FORMAT,
               "upload_quant: got " + std::to_string(nbytes) + " bytes, expected " + std::to_string(need));
-  w.type = type;
+  w.type = storage_type(type);
   w.rows = (long long)rows;
   w.cols = (long long)cols;
-  qweight_sizes(type, w.rows, w.cols, &w.q_bytes, &w.s_bytes);
+  qweight_sizes(w.type, w.rows, w.cols, &w.q_bytes, &w.s_bytes);
   DevMem raw;
   raw.ensure(nbytes);
   HOS_HIP_CHECK(hipMalloc(&w.q, w.q_bytes));
-  HOS_HIP_CHECK(hipMalloc((void**)&w.s, w.s_bytes));
+  HOS_HIP_CHECK(hipMalloc((void**)&w.s, w.s_bytes > 0 ? w.s_bytes : 256));  // never read for unscaled types
   HOS_HIP_CHECK(hipMemcpyAsync(raw.p, bytes, nbytes, hipMemcpyHostToDevice, st));
-  repack_weight((const uint8_t*)raw.p, w, st);
+  repack_weight((const uint8_t*)raw.p, type, w, st);
   HOS_HIP_CHECK(hipStreamSynchronize(st));
 }
 

@@ -1,8 +1,9 @@
 // GGUF model loading (host code): the file reader of src/gguf.rs:225-286 and the config mapping of
 // Model::load (src/model.rs:713-921) for the decoder families the training step runs (llama, qwen2,
-// mistral: RMSNorm, SwiGLU, RoPE, optional QKV bias, optionally tied head). Linear weights are uploaded in
-// their GGUF encoding when the fused GEMMs read it (Q8_0, Q4_K, Q6_K); norms and biases are widened to
-// F32 from F32 / F16 / BF16.
+// mistral, qwen2moe, olmoe: RMSNorm, SwiGLU, RoPE, optional QKV bias, optionally tied head, optional mixture of
+// experts). Linear weights are uploaded in their GGUF encoding — every type the reference decodes
+// (src/gguf.rs:330-505: F32, F16, BF16, Q8_0, Q4_0, Q5_0, Q4_K, Q5_K, Q6_K); the device repack keeps them
+// quantized and bit-exact. Norms, biases and the router are widened to F32 from F32 / F16 / BF16.
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -149,7 +150,7 @@ void read_gguf(const char* path, GgufFile& g) {
   }
   uint64_t align = 32;
   (void)g.meta_u64("general.alignment", &align);
-  HOS_REQUIRE(align > 0, HOS_E_FORMAT, "general.alignment is 0");
+  HOS_REQUIRE(align > 0 && align <= (1u << 30), HOS_E_FORMAT, "general.alignment is 0 or absurdly large");
   g.data_offset = (size_t)((r.pos + align - 1) / align * align);
 }
 
@@ -176,13 +177,24 @@ const uint8_t* raw(const GgufFile& g, const std::string& name, const TInfo& t, s
   }
   HOS_REQUIRE(nb > 0 || n == 0, HOS_E_UNSUPPORTED_QUANT,
               "tensor '" + name + "' has GGUF type " + std::to_string(t.type) +
-                  " (the fused GEMMs read Q8_0, Q4_K and Q6_K)");
+                  " (supported: F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)");
   HOS_REQUIRE(t.offset <= g.buf.size(), HOS_E_FORMAT, "tensor '" + name + "' data out of bounds");
   const uint64_t start = (uint64_t)g.data_offset + t.offset;
   HOS_REQUIRE(start <= g.buf.size() && nb <= g.buf.size() - start, HOS_E_FORMAT,
               "tensor '" + name + "' data out of bounds");
   *nbytes = nb;
   return g.buf.data() + start;
+}
+
+// Every tensor's data must lie inside the file: checked once at open for every type whose size is known
+// (raw() checks again before a tensor is read), so a crafted header is a format error up front.
+void validate_extents(const GgufFile& g) {
+  for (const auto& kv : g.tensors) {
+    size_t nb = 0;
+    const TInfo& t = kv.second;
+    if (t.type == T_F32 || t.type == T_F16 || t.type == T_BF16 || gguf_bytes_for(t.type, 1 << 8) > 0)
+      (void)raw(g, kv.first, t, &nb);
+  }
 }
 
 float half_to_f32(uint16_t h) {
@@ -195,8 +207,10 @@ float half_to_f32(uint16_t h) {
 hos_peft_cfg map_config(const GgufFile& g, const hos_peft_cfg* train) {
   const std::string arch = g.meta_str("general.architecture", "llama");
   if (g.has("blk.0.ssm_a")) throw Error(HOS_E_UNSUPPORTED_ARCH, "hybrid SSM models are not trainable here");
-  HOS_REQUIRE(arch == "llama" || arch == "qwen2" || arch == "mistral" || arch == "olmoe", HOS_E_UNSUPPORTED_ARCH,
-              "architecture '" + arch + "' is not supported by the training step (llama, qwen2, mistral, olmoe)");
+  // Arch::detect (src/model.rs:27-42): qwen2moe is the Qwen2 family (shared experts, if any, are not read)
+  HOS_REQUIRE(arch == "llama" || arch == "qwen2" || arch == "qwen2moe" || arch == "mistral" || arch == "olmoe",
+              HOS_E_UNSUPPORTED_ARCH,
+              "architecture '" + arch + "' is not supported by the training step (llama, qwen2, qwen2moe, mistral, olmoe)");
   auto need = [&](const std::string& key) {
     uint64_t v = 0;
     HOS_REQUIRE(g.meta_u64(arch + "." + key, &v), HOS_E_MISSING_META, "missing metadata '" + arch + "." + key + "'");
@@ -222,7 +236,7 @@ hos_peft_cfg map_config(const GgufFile& g, const hos_peft_cfg* train) {
   HOS_REQUIRE(c.dim > 0, HOS_E_FORMAT, "embedding_length is 0");
   c.vocab = (int)(n_elements(it->second) / (uint64_t)c.dim);
   c.attn_bias = g.has("blk.0.attn_q.bias") ? 1 : 0;
-  c.rope_neox = (arch == "qwen2" || arch == "olmoe") ? 1 : 0;  // Arch::rope_neox, src/model.rs:80-82
+  c.rope_neox = (arch == "qwen2" || arch == "qwen2moe" || arch == "olmoe") ? 1 : 0;  // Arch::rope_neox, src/model.rs:80-82
   // mixture of experts (src/model.rs:792-795): expert_count > 0 and the stacked expert tensors present
   uint64_t ne = 0, nu = 0;
   (void)g.meta_u64(arch + ".expert_count", &ne);
@@ -243,6 +257,7 @@ int hos_gguf_config(const char* path, hos_peft_cfg* out, char* err, size_t err_l
     HOS_REQUIRE(out != nullptr, HOS_E_INVALID, "null output");
     GgufFile g;
     read_gguf(path, g);
+    validate_extents(g);
     *out = map_config(g, out);
     return HOS_OK;
   } catch (const Error& e) {
@@ -262,6 +277,7 @@ int hos_peft_create_from_gguf(hos_ctx* ctx, const char* path, const hos_peft_cfg
   hos_peft_cfg c{};
   try {
     read_gguf(path, g);
+    validate_extents(g);
     c = map_config(g, train);
   } catch (const Error& e) {
     std::fprintf(stderr, "hos_peft_create_from_gguf: %s\n", e.what());

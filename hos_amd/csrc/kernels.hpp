@@ -4,7 +4,19 @@
 
 namespace hos {
 
-enum : uint32_t { GGUF_F32 = 0, GGUF_Q8_0 = 8, GGUF_Q4_K = 12, GGUF_Q6_K = 14 };
+// GGUF type ids (src/gguf.rs). Q4_0 and Q5_0 are repacked exactly into the Q8_0 layout on upload; Q5_K, F16 and
+// BF16 matrices keep their own device layouts.
+enum : uint32_t {
+  GGUF_F32 = 0,
+  GGUF_F16 = 1,
+  GGUF_Q4_0 = 2,
+  GGUF_Q5_0 = 6,
+  GGUF_Q8_0 = 8,
+  GGUF_Q4_K = 12,
+  GGUF_Q5_K = 13,
+  GGUF_Q6_K = 14,
+  GGUF_BF16 = 30
+};
 
 // Plain-old-data view of a QWeight passed to kernels by value.
 struct QWeightView {
@@ -25,8 +37,10 @@ __device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt
 //   Q8_0  q·d                 (:354-367)
 //   Q4_K  (d·sc)·q − dmin·m   (:385-413; d·sc and dmin·m are precomputed in f32 at repack)
 //   Q6_K  (d·sc)·q            (:449-477)
+//   Q5_K  (d·sc)·q − dmin·m   (:414-448; q = 5-bit code, one byte per element on the device)
+//   F16 / BF16 widened exactly (:342-353)
 __device__ __forceinline__ float deq_q8(int8_t q, float d) { return __fmul_rn((float)q, d); }
-// (d·sc)·q is exact in f32 (d: 11 significant bits, sc ≤ 63, q ≤ 15 → ≤ 21 bits), so the reference's
+// (d·sc)·q is exact in f32 (d: 11 significant bits, sc ≤ 63, q ≤ 31 → ≤ 22 bits), so the reference's
 // multiply-then-subtract rounds once, at the subtraction — exactly what one fused multiply-add does.
 __device__ __forceinline__ float deq_q4k(uint32_t q, float2 dm) { return __builtin_fmaf(dm.x, (float)q, -dm.y); }
 __device__ __forceinline__ float deq_q4k_f(float q, float2 dm) { return __builtin_fmaf(dm.x, q, -dm.y); }
@@ -40,6 +54,10 @@ __device__ __forceinline__ float deq_one(const QWeightView& w, long long r, long
     uint32_t q = (i & 1) ? (b >> 4) : (b & 15u);
     return deq_q4k(q, ((const float2*)w.s)[i >> 5]);
   }
+  if (w.type == GGUF_Q5_K) return deq_q4k((uint32_t)((const uint8_t*)w.q)[i], ((const float2*)w.s)[i >> 5]);
+  if (w.type == GGUF_F16) return (float)((const _Float16*)w.q)[i];
+  if (w.type == GGUF_BF16) return __uint_as_float((uint32_t)((const uint16_t*)w.q)[i] << 16);
+  if (w.type == GGUF_F32) return ((const float*)w.q)[i];
   return deq_q6k(((const int8_t*)w.q)[i], w.s[i >> 4]);
 }
 
@@ -80,8 +98,10 @@ __device__ inline void block_row_h16(const float* xr, int K, _Float16* orow, _Fl
 // ---- quant.hip ----
 size_t gguf_bytes_for(uint32_t t, size_t n);
 size_t block_elems(uint32_t t);
+// Device layout a GGUF type is kept in (Q4_0 / Q5_0 -> Q8_0, exactly; every other type its own).
+uint32_t storage_type(uint32_t t);
 void qweight_sizes(uint32_t type, long long rows, long long cols, size_t* q_bytes, size_t* s_bytes);
-void repack_weight(const uint8_t* src_dev, QWeight& w, hipStream_t st);
+void repack_weight(const uint8_t* src_dev, uint32_t src_type, QWeight& w, hipStream_t st);
 void launch_dequant(const QWeight& w, float* out_dev, hipStream_t st);
 void launch_quantize(const float* x_dev, size_t n, uint32_t type, uint8_t* out_dev, hipStream_t st);
 

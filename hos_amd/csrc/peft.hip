@@ -378,7 +378,7 @@ struct hos_peft {
     out.cols = p0->cols;
     qweight_sizes(out.type, out.rows, out.cols, &out.q_bytes, &out.s_bytes);
     HOS_HIP_CHECK(hipMalloc(&out.q, out.q_bytes));
-    HOS_HIP_CHECK(hipMalloc((void**)&out.s, out.s_bytes));
+    HOS_HIP_CHECK(hipMalloc((void**)&out.s, out.s_bytes > 0 ? out.s_bytes : 256));
     size_t qo = 0, so = 0;
     for (const QWeight* p : parts) {
       HOS_HIP_CHECK(hipMemcpyAsync((uint8_t*)out.q + qo, p->q, p->q_bytes, hipMemcpyDeviceToDevice, st));

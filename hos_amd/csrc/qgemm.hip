@@ -25,16 +25,32 @@ namespace hos {
 
 
 void qgemm_launch_q8(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
-                     float* ws, size_t ws_bytes, hipStream_t st);
-void qgemm_launch_q4k(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
-                      float* ws, size_t ws_bytes, hipStream_t st);
-void qgemm_launch_q6k(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
                       float* ws, size_t ws_bytes, hipStream_t st);
 void qgemm_grouped_q8(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
-                      hipStream_t st);
+                       hipStream_t st);
+void qgemm_launch_q4k(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
+                      float* ws, size_t ws_bytes, hipStream_t st);
 void qgemm_grouped_q4k(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
                        hipStream_t st);
+void qgemm_launch_q6k(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
+                      float* ws, size_t ws_bytes, hipStream_t st);
 void qgemm_grouped_q6k(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                       hipStream_t st);
+void qgemm_launch_q5k(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
+                      float* ws, size_t ws_bytes, hipStream_t st);
+void qgemm_grouped_q5k(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                       hipStream_t st);
+void qgemm_launch_f16(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
+                      float* ws, size_t ws_bytes, hipStream_t st);
+void qgemm_grouped_f16(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                       hipStream_t st);
+void qgemm_launch_bf16(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
+                      float* ws, size_t ws_bytes, hipStream_t st);
+void qgemm_grouped_bf16(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
+                       hipStream_t st);
+void qgemm_launch_f32(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi,
+                      float* ws, size_t ws_bytes, hipStream_t st);
+void qgemm_grouped_f32(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi,
                        hipStream_t st);
 
 namespace {
@@ -104,6 +120,10 @@ void launch_any(bool dx, const QWeight& w, H16 a, long long lda, long long M, Ge
     case GGUF_Q8_0: qgemm_launch_q8(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
     case GGUF_Q4_K: qgemm_launch_q4k(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
     case GGUF_Q6_K: qgemm_launch_q6k(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
+    case GGUF_Q5_K: qgemm_launch_q5k(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
+    case GGUF_F16: qgemm_launch_f16(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
+    case GGUF_BF16: qgemm_launch_bf16(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
+    case GGUF_F32: qgemm_launch_f32(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
     default: throw Error(HOS_E_UNSUPPORTED_QUANT, "qgemm: unsupported quant type");
   }
 }
@@ -126,6 +146,10 @@ void launch_qgemm_grouped(bool dx, const QWeight& w, GroupSched gs, H16 a, long 
     case GGUF_Q8_0: qgemm_grouped_q8(dx, passes, w, gs, a, lda, epi, st); break;
     case GGUF_Q4_K: qgemm_grouped_q4k(dx, passes, w, gs, a, lda, epi, st); break;
     case GGUF_Q6_K: qgemm_grouped_q6k(dx, passes, w, gs, a, lda, epi, st); break;
+    case GGUF_Q5_K: qgemm_grouped_q5k(dx, passes, w, gs, a, lda, epi, st); break;
+    case GGUF_F16: qgemm_grouped_f16(dx, passes, w, gs, a, lda, epi, st); break;
+    case GGUF_BF16: qgemm_grouped_bf16(dx, passes, w, gs, a, lda, epi, st); break;
+    case GGUF_F32: qgemm_grouped_f32(dx, passes, w, gs, a, lda, epi, st); break;
     default: throw Error(HOS_E_UNSUPPORTED_QUANT, "qgemm: unsupported quant type");
   }
 }

@@ -44,7 +44,7 @@ __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)((int)
 __device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
 
 // Four consecutive dequantized values from one packed source: Q4_K a 16-bit half-word (4 nibbles),
-// Q8_0/Q6_K a 32-bit word (4 int8). Same arithmetic as deq_q4k / deq_q8 / deq_q6k.
+// Q8_0/Q6_K/Q5_K a 32-bit word (4 int8 / 4 uint8 codes). Same arithmetic as deq_q4k / deq_q8 / deq_q6k.
 template <uint32_t QT>
 __device__ __forceinline__ void deq4(uint32_t src, float2 s, float* v) {
   if constexpr (QT == GGUF_Q4_K) {
@@ -53,6 +53,9 @@ __device__ __forceinline__ void deq4(uint32_t src, float2 s, float* v) {
     v[1] = deq_q4k_f(ubyte(hi, 0), s);
     v[2] = deq_q4k_f(ubyte(lo, 1), s);
     v[3] = deq_q4k_f(ubyte(hi, 1), s);
+  } else if constexpr (QT == GGUF_Q5_K) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = deq_q4k_f(ubyte(src, i), s);
   } else if constexpr (QT == GGUF_Q8_0) {
 #pragma unroll
     for (int i = 0; i < 4; i++) v[i] = __fmul_rn(sbyte(src, i), s.x);
@@ -62,11 +65,17 @@ __device__ __forceinline__ void deq4(uint32_t src, float2 s, float* v) {
   }
 }
 
+// Bytes per element of a device weight layout (Q4_K: two per byte).
+template <uint32_t QT>
+constexpr int elem_bytes() {
+  return QT == GGUF_F32 ? 4 : ((QT == GGUF_F16 || QT == GGUF_BF16) ? 2 : 1);
+}
+
 // A run of E consecutive values of one W row (E ∈ {8, 16, 32}; it never leaves a 32-value Q8_0/Q4_K group;
 // Q6_K's 16-value groups give a second scale for E = 32).
 template <uint32_t QT, int E>
 struct Run {
-  static constexpr int VPW = QT == GGUF_Q4_K ? 8 : 4;  // values per 32-bit word
+  static constexpr int VPW = QT == GGUF_Q4_K ? 8 : 4 / elem_bytes<QT>();  // values per 32-bit word
   static constexpr int NW = E / VPW;
   uint32_t q[NW];
   float2 s[2];
@@ -81,7 +90,7 @@ __device__ __forceinline__ void run_load(const QWeightView& w, long long row, in
     col = 0;
   }
   const long long e = row * w.cols + col;
-  const uint32_t* src = (const uint32_t*)((const uint8_t*)w.q + (QT == GGUF_Q4_K ? (e >> 1) : e));
+  const uint32_t* src = (const uint32_t*)((const uint8_t*)w.q + (QT == GGUF_Q4_K ? (e >> 1) : e * elem_bytes<QT>()));
   if constexpr (Run<QT, E>::NW == 1) {
     r.q[0] = src[0];
   } else if constexpr (Run<QT, E>::NW == 2) {
@@ -98,8 +107,10 @@ __device__ __forceinline__ void run_load(const QWeightView& w, long long row, in
       r.q[i + 3] = v.w;
     }
   }
-  if constexpr (QT == GGUF_Q4_K) {
+  if constexpr (QT == GGUF_Q4_K || QT == GGUF_Q5_K) {
     r.s[0] = ((const float2*)w.s)[e >> 5];
+  } else if constexpr (QT == GGUF_F16 || QT == GGUF_BF16 || QT == GGUF_F32) {
+    // unscaled: the stored value is the weight
   } else if constexpr (QT == GGUF_Q8_0) {
     r.s[0].x = w.s[e >> 5];
   } else {
@@ -146,15 +157,33 @@ __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, in
           lv[4 * wv + 3] = l1[1];
         }
       }
+    } else if constexpr (QT == GGUF_F16) {
+      // the stored halves are the weight: hi is exact and lo is zero
+      __builtin_memcpy(&hv, &r.q[4 * v], 16);
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) lv[i] = (_Float16)0.0f;
+      }
     } else {
       float f[8];
-      const float2 sc = (QT == GGUF_Q6_K && v >= 2) ? r.s[1] : r.s[0];
-      if constexpr (QT == GGUF_Q4_K) {
-        deq4<QT>(r.q[v] & 0xffffu, sc, f);
-        deq4<QT>(r.q[v] >> 16, sc, f + 4);
+      if constexpr (QT == GGUF_BF16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          f[2 * i] = __uint_as_float(r.q[4 * v + i] << 16);
+          f[2 * i + 1] = __uint_as_float(r.q[4 * v + i] & 0xffff0000u);
+        }
+      } else if constexpr (QT == GGUF_F32) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) f[i] = __uint_as_float(r.q[8 * v + i]);
       } else {
-        deq4<QT>(r.q[2 * v], sc, f);
-        deq4<QT>(r.q[2 * v + 1], sc, f + 4);
+        const float2 sc = (QT == GGUF_Q6_K && v >= 2) ? r.s[1] : r.s[0];
+        if constexpr (QT == GGUF_Q4_K) {
+          deq4<QT>(r.q[v] & 0xffffu, sc, f);
+          deq4<QT>(r.q[v] >> 16, sc, f + 4);
+        } else {
+          deq4<QT>(r.q[2 * v], sc, f);
+          deq4<QT>(r.q[2 * v + 1], sc, f + 4);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 8; i++) {
@@ -594,8 +623,9 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
   gk.tiles = gs.tiles;
   gk.rows = er;
   const long long n = er * w.cols;  // elements of one expert
-  gk.q_stride = QT == GGUF_Q4_K ? n / 2 : n;
-  gk.s_stride = QT == GGUF_Q4_K ? n / 16 : (QT == GGUF_Q8_0 ? n / 32 : n / 16);
+  gk.q_stride = QT == GGUF_Q4_K ? n / 2 : n * elem_bytes<QT>();
+  gk.s_stride = (QT == GGUF_Q4_K || QT == GGUF_Q5_K) ? n / 16
+                : (QT == GGUF_Q8_0 ? n / 32 : (QT == GGUF_Q6_K ? n / 16 : 0));
   dim3 grid(ceil_div(Nout, 128), gs.max_tiles, 1);
   if (C % 64 == 0)
     qgemm_kernel<QT, DX, 128, 128, 64, NP><<<grid, 256, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, 0, Nout, C, C,
@@ -608,3 +638,37 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
 
 }  // namespace
 }  // namespace hos
+
+// Defines qgemm_launch_<NAME> and qgemm_grouped_<NAME> (declared in qgemm.hip) for one device weight layout:
+// every tile shape, both directions, precision modes 1-4. One translation unit per layout keeps builds parallel.
+#define HOS_QGEMM_INSTANTIATE(NAME, QT)                                                                          \
+  namespace hos {                                                                                                \
+  void qgemm_launch_##NAME(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, \
+                           float* ws, size_t ws_bytes, hipStream_t st) {                                         \
+    if (dx) {                                                                                                    \
+      if (passes == 1) launch_typed<QT, true, 1>(w, a, lda, M, epi, ws, ws_bytes, st);                           \
+      else if (passes == 2) launch_typed<QT, true, 2>(w, a, lda, M, epi, ws, ws_bytes, st);                      \
+      else if (passes == 3) launch_typed<QT, true, 3>(w, a, lda, M, epi, ws, ws_bytes, st);                      \
+      else launch_typed<QT, true, 4>(w, a, lda, M, epi, ws, ws_bytes, st);                                       \
+    } else {                                                                                                     \
+      if (passes == 1) launch_typed<QT, false, 1>(w, a, lda, M, epi, ws, ws_bytes, st);                          \
+      else if (passes == 2) launch_typed<QT, false, 2>(w, a, lda, M, epi, ws, ws_bytes, st);                     \
+      else if (passes == 3) launch_typed<QT, false, 3>(w, a, lda, M, epi, ws, ws_bytes, st);                     \
+      else launch_typed<QT, false, 4>(w, a, lda, M, epi, ws, ws_bytes, st);                                      \
+    }                                                                                                            \
+  }                                                                                                              \
+  void qgemm_grouped_##NAME(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda,          \
+                            GemmEpi epi, hipStream_t st) {                                                       \
+    if (dx) {                                                                                                    \
+      if (passes == 1) launch_typed_grouped<QT, true, 1>(w, gs, a, lda, epi, st);                                \
+      else if (passes == 2) launch_typed_grouped<QT, true, 2>(w, gs, a, lda, epi, st);                           \
+      else if (passes == 3) launch_typed_grouped<QT, true, 3>(w, gs, a, lda, epi, st);                           \
+      else launch_typed_grouped<QT, true, 4>(w, gs, a, lda, epi, st);                                            \
+    } else {                                                                                                     \
+      if (passes == 1) launch_typed_grouped<QT, false, 1>(w, gs, a, lda, epi, st);                               \
+      else if (passes == 2) launch_typed_grouped<QT, false, 2>(w, gs, a, lda, epi, st);                          \
+      else if (passes == 3) launch_typed_grouped<QT, false, 3>(w, gs, a, lda, epi, st);                          \
+      else launch_typed_grouped<QT, false, 4>(w, gs, a, lda, epi, st);                                           \
+    }                                                                                                            \
+  }                                                                                                              \
+  }

@@ -88,6 +88,63 @@ __global__ void repack_q6_k(const uint8_t* __restrict__ src, int8_t* __restrict_
   }
 }
 
+// Q4_0 block (18 B): d f16, qs[16]; element j < 16 is the low nibble of qs[j], j ≥ 16 the high nibble of
+// qs[j − 16], value (q − 8)·d (src/gguf.rs:368-384). Stored as the Q8_0 layout with int8 q − 8: the Q8_0 decode
+// (float)q · d is then the same product, bit for bit.
+__global__ void repack_q4_0(const uint8_t* __restrict__ src, int8_t* __restrict__ q, float* __restrict__ s,
+                            long long nblocks) {
+  long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  const uint8_t* blk = src + b * 18;
+  s[b] = f16bits_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+  int8_t* dst = q + b * 32;
+  for (int j = 0; j < 16; j++) {
+    dst[j] = (int8_t)((int)(blk[2 + j] & 15u) - 8);
+    dst[j + 16] = (int8_t)((int)(blk[2 + j] >> 4) - 8);
+  }
+}
+
+// Q5_0 block (22 B): d f16, qh u32 (bit j = 5th bit of element j), qs[16] as Q4_0; value (q − 16)·d
+// (src/gguf.rs:478-505). Stored as the Q8_0 layout with int8 q − 16.
+__global__ void repack_q5_0(const uint8_t* __restrict__ src, int8_t* __restrict__ q, float* __restrict__ s,
+                            long long nblocks) {
+  long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  const uint8_t* blk = src + b * 22;
+  s[b] = f16bits_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+  const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+  int8_t* dst = q + b * 32;
+  for (int j = 0; j < 16; j++) {
+    const int x0 = (int)((blk[6 + j] & 15u) | (((qh >> j) & 1u) << 4));
+    const int x1 = (int)((blk[6 + j] >> 4) | (((qh >> (j + 16)) & 1u) << 4));
+    dst[j] = (int8_t)(x0 - 16);
+    dst[j + 16] = (int8_t)(x1 - 16);
+  }
+}
+
+// Q5_K super-block (176 B): d f16, dmin f16, scales[12], qh[32], qs[128]; sub-block j (32 values) takes the low
+// (even j) or high (odd j) nibbles of qs[32·(j/2) + l] plus 16 when bit j of qh[l] is set (src/gguf.rs:414-448).
+// Stored as one byte per 5-bit code and float2 {d·sc, dmin·m} per sub-block, as Q4_K's scales.
+__global__ void repack_q5_k(const uint8_t* __restrict__ src, uint8_t* __restrict__ q, float2* __restrict__ s,
+                            long long nsub) {
+#pragma clang fp contract(off)
+  long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= nsub) return;
+  long long sb = g >> 3;
+  int j = (int)(g & 7);
+  const uint8_t* blk = src + sb * 176;
+  float d = f16bits_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+  float dmin = f16bits_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+  uint32_t sc, m;
+  scale_min_k4(j, blk + 4, &sc, &m);
+  s[g] = make_float2(__fmul_rn(d, (float)sc), __fmul_rn(dmin, (float)m));
+  const uint8_t* qh = blk + 16;
+  const uint8_t* qs = blk + 48 + 32 * (j >> 1);
+  const int sh = (j & 1) * 4;
+  uint8_t* dst = q + g * 32;
+  for (int l = 0; l < 32; l++) dst[l] = (uint8_t)(((qs[l] >> sh) & 15u) | (((qh[l] >> j) & 1u) << 4));
+}
+
 // Dequant of the whole weight to f32 (for the bit-exact check); one thread per element.
 __global__ void dequant_kernel(QWeightView w, float* __restrict__ out, long long n) {
   long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -297,25 +354,59 @@ __global__ void quantize_q6_k_kernel(const float* __restrict__ x, uint8_t* __res
 size_t gguf_bytes_for(uint32_t t, size_t n) {
   switch (t) {
     case GGUF_F32: return n * 4;
+    case GGUF_F16:
+    case GGUF_BF16: return n * 2;
+    case GGUF_Q4_0: return n / 32 * 18;
+    case GGUF_Q5_0: return n / 32 * 22;
     case GGUF_Q8_0: return n / 32 * 34;
     case GGUF_Q4_K: return n / 256 * 144;
+    case GGUF_Q5_K: return n / 256 * 176;
     case GGUF_Q6_K: return n / 256 * 210;
     default: return 0;
   }
 }
 
+// Elements per GGUF block of a matrix type the GEMMs read (0: not a weight encoding the GEMMs read).
 size_t block_elems(uint32_t t) {
   switch (t) {
+    case GGUF_F32:
+    case GGUF_F16:
+    case GGUF_BF16: return 1;
+    case GGUF_Q4_0:
+    case GGUF_Q5_0:
     case GGUF_Q8_0: return 32;
     case GGUF_Q4_K:
+    case GGUF_Q5_K:
     case GGUF_Q6_K: return 256;
     default: return 0;
   }
 }
 
-void repack_weight(const uint8_t* src_dev, QWeight& w, hipStream_t st) {
+uint32_t storage_type(uint32_t t) { return (t == GGUF_Q4_0 || t == GGUF_Q5_0) ? GGUF_Q8_0 : t; }
+
+void repack_weight(const uint8_t* src_dev, uint32_t src_type, QWeight& w, hipStream_t st) {
   long long n = w.rows * w.cols;
-  switch (w.type) {
+  switch (src_type) {
+    case GGUF_Q4_0: {
+      long long nb = n / 32;
+      repack_q4_0<<<ceil_div(nb, 256), 256, 0, st>>>(src_dev, (int8_t*)w.q, w.s, nb);
+      break;
+    }
+    case GGUF_Q5_0: {
+      long long nb = n / 32;
+      repack_q5_0<<<ceil_div(nb, 256), 256, 0, st>>>(src_dev, (int8_t*)w.q, w.s, nb);
+      break;
+    }
+    case GGUF_Q5_K: {
+      long long ns = n / 32;
+      repack_q5_k<<<ceil_div(ns, 256), 256, 0, st>>>(src_dev, (uint8_t*)w.q, (float2*)w.s, ns);
+      break;
+    }
+    case GGUF_F32:
+    case GGUF_F16:
+    case GGUF_BF16:  // stored as the file holds them
+      HOS_HIP_CHECK(hipMemcpyAsync(w.q, src_dev, w.q_bytes, hipMemcpyDeviceToDevice, st));
+      break;
     case GGUF_Q8_0: {
       long long nb = n / 32;
       repack_q8_0<<<ceil_div(nb, 256), 256, 0, st>>>(src_dev, (int8_t*)w.q, w.s, nb);
@@ -343,6 +434,10 @@ void qweight_sizes(uint32_t type, long long rows, long long cols, size_t* q_byte
     case GGUF_Q8_0: *q_bytes = n; *s_bytes = n / 32 * 4; break;
     case GGUF_Q4_K: *q_bytes = n / 2; *s_bytes = n / 32 * 8; break;
     case GGUF_Q6_K: *q_bytes = n; *s_bytes = n / 16 * 4; break;
+    case GGUF_Q5_K: *q_bytes = n; *s_bytes = n / 32 * 8; break;
+    case GGUF_F16:
+    case GGUF_BF16: *q_bytes = 2 * n; *s_bytes = 0; break;
+    case GGUF_F32: *q_bytes = 4 * n; *s_bytes = 0; break;
     default: throw Error(HOS_E_UNSUPPORTED_QUANT, "unsupported quant type " + std::to_string(type));
   }
 }

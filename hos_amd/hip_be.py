@@ -13,8 +13,11 @@ import numpy as np
 
 from ._lib import lib
 
-GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 8, 12, 14
-BLOCK = {GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_BF16 = \
+    0, 1, 2, 6, 8, 12, 13, 14, 30
+# elements per block of each weight encoding upload_quant takes (src/gguf.rs:330-505)
+BLOCK = {GGML_F32: 1, GGML_F16: 1, GGML_BF16: 1, GGML_Q4_0: 32, GGML_Q5_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256,
+         GGML_Q5_K: 256, GGML_Q6_K: 256}
 
 STATUS = {1: "Io", 2: "Format", 3: "MissingTensor", 4: "UnsupportedQuant", 5: "UnsupportedArch",
           6: "MissingMeta", 7: "Spec", 8: "Device", 9: "Invalid", 10: "OutOfMemory"}

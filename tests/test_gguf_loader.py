@@ -193,3 +193,26 @@ def test_olmoe_mapping(tmp_path):
     del t["blk.0.ffn_gate_exps.weight"]  # expert_count without expert tensors: dense (src/model.rs:795)
     rc, c, err = _config(_write(tmp_path, gguf_bytes(meta, t), "dense.gguf"))
     assert rc == 0 and c.n_experts == 0
+
+
+def test_qwen2moe_mapping(tmp_path):
+    """qwen2moe is the Qwen2 family (Arch::detect, src/model.rs:35): keys under `qwen2moe.`, NEOX RoPE, QKV
+    bias detection, experts from expert_count / expert_used_count with the stacked expert tensors present."""
+    cfg = Cfg()
+    meta = model_meta(cfg, "qwen2moe", extra={"qwen2moe.expert_count": (U32, 4), "qwen2moe.expert_used_count": (U32, 2)})
+    t = _tensors(cfg, bias=True)
+    t["blk.0.ffn_gate_exps.weight"] = (np.zeros(4 * 256 * 128 // 32 * 34, np.uint8), 8, [128, 256, 4])
+    rc, c, err = _config(_write(tmp_path, gguf_bytes(meta, t)))
+    assert rc == 0, err
+    assert (c.dim, c.n_layers, c.n_heads, c.n_kv_heads) == (cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads)
+    assert (c.rope_neox, c.attn_bias, c.n_experts, c.n_experts_used) == (1, 1, 4, 2)
+
+
+def test_oversized_tensor_dims_refused(tmp_path):
+    """Tensor dims whose byte count would overflow are a format error from the config call, not a wrapped
+    size (the data bounds are checked before any byte is read)."""
+    cfg = Cfg()
+    t = _tensors(cfg)
+    t["blk.0.attn_q.weight"] = (np.zeros(64, np.uint8), 0, [1 << 31, 1 << 31])
+    rc, _, err = _config(_write(tmp_path, gguf_bytes(model_meta(cfg, "qwen2"), t)))
+    assert rc == HOS_E_FORMAT, err

@@ -112,3 +112,71 @@ def test_keyed_f32_gemms(gpu, m, k, n):
     assert rel_l2(got_db, db) < 1e-5
     gpu.evict(77)
     gpu.clear_cache()
+
+
+# ---- the other encodings the reference decodes (src/gguf.rs:330-505): F32, F16, BF16, Q4_0, Q5_0, Q5_K ----
+F32, F16, Q4_0, Q5_0, Q5_K, BF16 = 0, 1, 2, 6, 13, 30
+OTHER = [F32, F16, BF16, Q4_0, Q5_0, Q5_K]
+
+
+def encoded(rows, cols, t, seed):
+    """GGUF bytes of a ~N(0, 0.02) [rows, cols] matrix in type t (the oracle's quantizers for the block types;
+    BF16 keeps the top half of each f32)."""
+    w = weights(rows, cols, seed)
+    if t == F32:
+        return w.view(np.uint8).ravel()
+    if t == BF16:
+        return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).ravel()
+    return o.quantize(w, t)
+
+
+def random_q5k(rows, cols, seed):
+    """Q5_K super-blocks with random scales, mins, high bits and nibbles (sane f16 d and dmin): every
+    code/scale/min combination the decode must handle, not only what the quantizer emits."""
+    rng = np.random.default_rng(seed)
+    nb = rows * cols // 256
+    blk = rng.integers(0, 256, size=(nb, 176), dtype=np.uint8)
+    d = (rng.uniform(1e-4, 4e-3, nb) * rng.choice([-1, 1], nb)).astype(np.float16)
+    dmin = rng.uniform(0, 4e-3, nb).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    return blk.ravel()
+
+
+@pytest.mark.parametrize("t", OTHER + ["q5k_random"])
+def test_dequant_other_encodings_bit_exact(gpu, t):
+    print(f"dequant encoding {t}", flush=True)
+    rows, cols = 64, 512
+    raw = random_q5k(rows, cols, 7) if t == "q5k_random" else encoded(rows, cols, t, 40)
+    t = Q5_K if t == "q5k_random" else t
+    gpu.upload_quant(200 + t, raw, t, rows, cols)
+    got = gpu.dequant(200 + t, rows, cols)
+    want = o.dequant(raw, t, rows * cols).reshape(rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    gpu.evict(200 + t)
+
+
+@pytest.mark.parametrize("passes", [1, 3])
+@pytest.mark.parametrize("t", OTHER)
+@pytest.mark.parametrize("shape", [(200, 576, 768), (2560, 2048, 2048)])
+def test_qgemm_other_encodings(gpu, t, shape, passes):
+    T, N, K = shape
+    print(f"qgemm encoding {t} T={T} N={N} K={K} passes={passes}", flush=True)
+    gpu.set_gemm_passes(passes)
+    raw = encoded(N, K, t, 50 + t)
+    gpu.upload_quant(300 + t, raw, t, N, K)
+    w = o.dequant(raw, t, N * K).reshape(N, K)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    dy = (rng.standard_normal((T, N)) * 1e-3).astype(np.float32)
+    y = gpu.qgemm_fwd(300 + t, x, N)
+    dx = gpu.qgemm_dx(300 + t, dy, K)
+    gpu.set_gemm_passes(1)
+    gpu.evict(300 + t)
+    ref_y, _, _ = o.op_matmul(x, w.T.copy())
+    ref_dx, _, _ = o.op_matmul(dy, w)
+    tol = {1: 1e-3, 3: 2e-6}[passes]
+    if t == F16 and passes == 1:
+        tol = 5e-4  # the weight is exact in fp16: only the activation rounds
+    assert rel_l2(y, ref_y) < tol
+    assert rel_l2(dx, ref_dx) < tol

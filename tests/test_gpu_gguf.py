@@ -79,9 +79,70 @@ def test_gguf_unsupported_quant_refused(gpu, tmp_path):
     print("gguf unsupported quant", flush=True)
     tensors = model_tensors(synth.build_tensors(gpu, cfg, seed=3))
     raw, _, dims = tensors["blk.0.ffn_up.weight"]
-    tensors["blk.0.ffn_up.weight"] = (np.zeros(dims[0] * dims[1] // 32 * 18, np.uint8), 2, dims)  # Q4_0
-    path = tmp_path / "q40.gguf"
+    tensors["blk.0.ffn_up.weight"] = (np.zeros(dims[0] * dims[1] // 32 * 20, np.uint8), 3, dims)  # Q4_1
+    path = tmp_path / "q41.gguf"
     path.write_bytes(gguf_bytes(model_meta(cfg, "qwen2"), tensors))
     with pytest.raises(HosError) as e:
         PeftModel.from_gguf(gpu, path, lora_rank=8, lora_targets=("q", "v"))
     assert e.value.code == 4
+
+
+def test_gguf_mixed_encodings_match_oracle(gpu, tmp_path):
+    """A GGUF file whose linear weights use every encoding the reference decodes (a Q4_K_M-style mix:
+    Q4_0, Q5_0, Q5_K, Q6_K, Q8_0, Q4_K, F16, BF16, F32; F16 norms), loaded by the library, against the oracle
+    loaded from the same bytes: loss and every LoRA gradient within 1e-3 relative L2,
+    the loss also to 1e-5 relative."""
+    import types
+
+    from hos_amd import synth
+    from hos_amd.peft import PeftModel
+    from oracle import binding as o
+    cfg = _tiny()
+    print("gguf mixed encodings vs oracle", flush=True)
+    enc = {0: {"attn_q": 2, "attn_k": 6, "attn_v": 13, "attn_output": 1, "ffn_gate": 30, "ffn_up": 12,
+               "ffn_down": 14},
+           1: {"attn_q": 13, "attn_k": 0, "attn_v": 8, "attn_output": 2, "ffn_gate": 6, "ffn_up": 1,
+               "ffn_down": 13}}
+    rng = np.random.default_rng(21)
+    tensors = _f16_round(synth.build_tensors(gpu, cfg, seed=20, quantize=o.quantize))
+    for name, (raw, t, rows, cols) in list(tensors.items()):
+        parts = name.split(".")
+        if len(parts) == 4 and parts[3] == "weight" and parts[2] in enc.get(int(parts[1]) if parts[0] == "blk" else -1, {}):
+            t2 = enc[int(parts[1])][parts[2]]
+            w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+            if t2 == 0:
+                raw2 = w.view(np.uint8).ravel()
+            elif t2 == 30:
+                raw2 = (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).ravel()
+            else:
+                raw2 = o.quantize(w, t2)
+            tensors[name] = (raw2, t2, rows, cols)
+    path = tmp_path / "mixed.gguf"
+    path.write_bytes(gguf_bytes(model_meta(cfg, "qwen2"), model_tensors(tensors, norm_type=1)))
+    B, T = 2, 32
+    pg = PeftModel.from_gguf(gpu, path, max_batch=B, max_seq=T, lora_rank=cfg.lora_rank,
+                             lora_alpha=cfg.lora_alpha, lora_targets=cfg.lora_targets)
+    oc = types.SimpleNamespace(**{k: getattr(cfg, k) for k in (
+        "n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab", "rms_eps", "rope_base",
+        "rope_neox", "attn_bias", "lora_rank", "lora_alpha")})
+    oc.lora_targets = cfg.target_mask
+    om = o.OracleModel(oc)
+    for name, (raw, t, rows, cols) in tensors.items():
+        om.set_tensor(name, raw, t, rows, cols)
+    lora = synth.lora_init(cfg, seed=22, b_std=0.02)
+    for (l, t), (A, Bm) in lora.items():
+        pg.set_lora(l, t, A, Bm)
+        om.set_lora(l, synth.ALL.index(t), A, Bm)
+    ids, tg = synth.tokens(cfg, B, T, seed=23)
+    loss, want = pg.loss_grad(ids, tg), om.loss_grad(ids, tg)
+    assert abs(loss - want) <= 1e-5 * abs(want), (loss, want)
+    worst = 0.0
+    for (l, t) in lora:
+        i, ou = cfg.target_dims(t)
+        got = pg.get_lora_grad(l, t)
+        ref = om.get_lora_grad(l, synth.ALL.index(t), ((i, cfg.lora_rank), (cfg.lora_rank, ou)))
+        for a, b in zip(got, ref):
+            worst = max(worst, float(np.linalg.norm(a - b) / np.linalg.norm(b)))
+    print(f"worst LoRA grad rel L2 {worst:.2e}", flush=True)
+    assert worst <= 1e-3
+    pg.close()
