@@ -252,3 +252,109 @@ def test_qkx_scale_min_constant_block():  # src/gguf_write.rs:303-305 (mx == mn)
     assert o.qkx_scale_min(np.full(32, -0.5, np.float32), 15) == (0.0, 0.5)
     s, m = o.qkx_scale_min(np.linspace(0, 1.5, 32).astype(np.float32), 15)
     assert s > 0 and m >= 0.0
+
+
+# ---- exact-byte pins of the K-quant quantizers (src/gguf_write.rs:293-495) ----
+# Values placed exactly on a grid the reference's search provably recovers, so every output byte is known in
+# closed form (header scales, packed 6-bit scales/mins, codes) without restating the algorithm; plus blocks that
+# force each branch of qkx_scale_min.
+
+
+def q4k_grid_block(rng, nmax=15):
+    """A super-block whose sub-block j holds v = s_j·l − m_j, l integers in 0..nmax with both ends present,
+    s_j = a_j·U, m_j = b_j·V (U, V powers of two, a_j, b_j in 1..63 with 63 present in each). Then for every
+    sub-block the candidate iscale (nmax − 1 + 0.1·10)/span = 1/s_j recovers l exactly, the least-squares refit
+    is exact (err 0, so (s_j, m_j) is returned), d = max s / 63 = U, dmin = V, ls = a, lm = b, codes = l."""
+    U, V = 2.0 ** -9, 2.0 ** -8
+    a = rng.integers(1, 64, 8)
+    b = rng.integers(1, 64, 8)
+    a[rng.integers(8)] = 63
+    b[rng.integers(8)] = 63
+    l = rng.integers(0, nmax + 1, (8, 32))
+    l[:, 0], l[:, 1] = 0, nmax
+    x = np.array([[a[j] * U * l[j, i] - b[j] * V for i in range(32)] for j in range(8)], np.float64)
+    assert np.array_equal(x.astype(np.float32).astype(np.float64), x)  # the grid is exact in f32
+    return x.astype(np.float32).ravel(), U, V, a, b, l
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_q4_k_quantizer_exact_bytes_on_grid(seed):
+    x, U, V, a, b, l = q4k_grid_block(np.random.default_rng(seed))
+    raw = o.quantize(x, Q4_K).tolist()
+    assert raw[0:2] == f16le(U) and raw[2:4] == f16le(V)
+    for j in range(8):
+        assert unpack_scale_min(j, raw[4:16]) == (a[j], b[j])
+    qs = raw[16:]
+    for j in range(8):
+        got = [(qs[32 * (j // 2) + i] >> (4 * (j % 2))) & 15 for i in range(32)]
+        assert got == l[j].tolist()
+    assert np.array_equal(o.dequant(np.array(raw, np.uint8), Q4_K, 256), x)  # and the round trip is exact
+
+
+def test_q5_k_quantizer_exact_bytes_on_grid():
+    x, U, V, a, b, l = q4k_grid_block(np.random.default_rng(5), nmax=31)
+    raw = o.quantize(x, Q5_K).tolist()
+    assert raw[0:2] == f16le(U) and raw[2:4] == f16le(V)
+    for j in range(8):
+        assert unpack_scale_min(j, raw[4:16]) == (a[j], b[j])
+    qh, qs = raw[16:48], raw[48:]
+    for j in range(8):
+        got = [((qs[32 * (j // 2) + i] >> (4 * (j % 2))) & 15) | (((qh[i] >> j) & 1) << 4) for i in range(32)]
+        assert got == l[j].tolist()
+
+
+def test_q6_k_quantizer_exact_bytes_on_grid():
+    """Sub-block s holds c_s·k with k integers in −32..31 and exactly one k = −32 (the unique max-abs element),
+    c_s = m_s·u, m_s in 1..128 with 128 present, u a power of two. Then subscale_s = max/−32 = c_s, max_scale =
+    128u, d = max_scale/−128 = −u, sc_s = round(c_s·(−128/max_scale)) = −m_s, scale = d·sc = c_s and q = k:
+    sc bytes = −m_s, d = f16(−u), codes k + 32."""
+    rng = np.random.default_rng(9)
+    u = 2.0 ** -12
+    m = rng.integers(1, 129, 16)
+    m[3] = 128
+    k = rng.integers(-31, 32, (16, 16))
+    k[:, 5] = -32
+    x = np.array([[m[s] * u * k[s, i] for i in range(16)] for s in range(16)], np.float32).ravel()
+    raw = o.quantize(x, Q6_K).tolist()
+    assert [(v if v < 128 else v - 256) for v in raw[192:208]] == (-m).tolist()
+    assert raw[208:210] == f16le(-u)
+    ql, qh = raw[0:128], raw[128:192]
+    q6 = []
+    for e in range(256):  # element e: half n128, quarter qq of 32, lane l (the layout of src/gguf.rs:449-477)
+        n128, r = divmod(e, 128)
+        qq, lane = divmod(r, 32)
+        low = ql[64 * n128 + lane + 32 * (qq & 1)] >> (4 * (qq >> 1)) & 15
+        high = (qh[32 * n128 + lane] >> (2 * qq)) & 3
+        q6.append((low | (high << 4)) - 32)
+    assert q6 == k.ravel().tolist()
+    assert np.array_equal(o.dequant(np.array(raw, np.uint8), Q6_K, 256), x)
+
+
+def test_q6_k_quantizer_all_zero_block():
+    """amax = 0 everywhere: subscale 0, d = 0, every code 0 (stored 32 = 0b10_0000): ql all 0, qh all
+    0b10101010, scales 0, d = +0."""
+    raw = o.quantize(np.zeros(256, np.float32), Q6_K).tolist()
+    assert raw[:128] == [0] * 128 and raw[128:192] == [0xAA] * 64 and raw[192:210] == [0] * 18
+
+
+def test_qkx_scale_min_branches():  # src/gguf_write.rs:293-351
+    # mx == mn (constant non-positive block): (0, −mn)
+    assert o.qkx_scale_min(np.full(32, -0.25, np.float32), 15) == (0.0, 0.25)
+    # mn > 0: the minimum is taken as 0; values s·l with l in 1..15 refit exactly to (s, 0)
+    s = 2.0 ** -6
+    l = np.random.default_rng(3).integers(1, 16, 32)
+    l[0], l[1] = 1, 15
+    sc, mn = o.qkx_scale_min((s * l).astype(np.float32), 15)
+    assert sc == s and mn == 0.0
+    # denom <= 0: a constant positive block puts every element on one level for every candidate scale, so the
+    # fallback (span / nmax, −mn) = (c / 15, 0) is returned
+    c = 15 * 2.0 ** -4
+    assert o.qkx_scale_min(np.full(32, c, np.float32), 15) == (2.0 ** -4, 0.0)
+    # (−b).max(0): two level clusters, the level-0 one {−ε, 0.4·step ×15} has a positive mean, so every
+    # candidate's refit intercept b is positive and the clamp returns a minimum of exactly 0 (unclamped: −b < 0)
+    step = 2.0 ** -5
+    x = np.array([-2.0 ** -12] + [0.4 * step] * 15 + [15 * step] * 16, np.float32)
+    sc, mn = o.qkx_scale_min(x, 15)
+    assert mn == 0.0 and sc > 0
+    # (s <= 0 is not forced: levels are a non-decreasing function of v, so with two or more distinct levels the
+    # refit slope is positive in exact arithmetic; the branch is the reference's guard against f32 cancellation.)
