@@ -67,6 +67,7 @@ SIGNATURES = {
     "hos_peft_adapter_id": (i32, [vp, ctypes.c_char_p]),
     "hos_peft_base_id": (i32, [vp, ctypes.c_char_p]),
     "hos_format_card": (i32, [ctypes.c_char_p, ctypes.c_char_p, sz, ctypes.POINTER(sz)]),
+    "hos_format_verify": (i32, [ctypes.c_char_p, ctypes.POINTER(sz), ctypes.c_char_p, sz]),
     "hos_gguf_config": (i32, [ctypes.c_char_p, ctypes.POINTER(PeftCfg), ctypes.c_char_p, sz]),
     "hos_peft_create_from_gguf": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(PeftCfg), ctypes.POINTER(vp),
                                         ctypes.POINTER(PeftCfg)]),

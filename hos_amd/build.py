@@ -30,10 +30,18 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src):
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer build (CPU tests of the file parsers only; device code
+# is compiled as usual, GPU sanitizers are not used): `python -m hos_amd.build --sanitize`.
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined", "-Xarch_host",
+             "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer", "-g"]
+SAN_BUILD = os.path.join(BUILD, "san")
+SAN_LIB = os.path.join(SAN_BUILD, "libhos_hip.so")
+
+
+def _compile(src, san=False):
+    obj = os.path.join(SAN_BUILD if san else BUILD, os.path.basename(src) + ".o")
     extra = ["-ffp-contract=off"] if os.path.basename(src) in NO_CONTRACT else []
-    cmd = [HIPCC] + FLAGS + extra + ["-c", src, "-o", obj]
+    cmd = [HIPCC] + FLAGS + extra + (SAN_FLAGS if san else []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
@@ -56,6 +64,38 @@ def build(verbose=False):
     return LIB
 
 
+def build_sanitized(verbose=False):
+    """libhos_hip.so with host code under ASan + UBSan, in _build/san/ (load it with HOS_HIP_LIB and
+    LD_PRELOAD=asan_runtime())."""
+    os.makedirs(SAN_BUILD, exist_ok=True)
+    srcs = sources()
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(lambda s: _compile(s, san=True), srcs))
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-fsanitize=address,undefined", "-o", SAN_LIB] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{r.stderr}")
+    if verbose:
+        print(f"built {SAN_LIB}")
+    return SAN_LIB
+
+
+def asan_runtime():
+    """The clang ASan runtime the sanitized library needs preloaded into an uninstrumented python."""
+    r = subprocess.run([HIPCC.replace("hipcc", "amdclang++") if "hipcc" in HIPCC else "amdclang++",
+                        "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = r.stdout.strip()
+    if not os.path.isabs(path):
+        import glob
+        found = glob.glob("/opt/rocm/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so")
+        path = found[0] if found else path
+    return path
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--sanitize" in sys.argv:
+        build_sanitized(verbose=True)
+        print(asan_runtime())
+    else:
+        build(verbose=True)
     sys.exit(0)

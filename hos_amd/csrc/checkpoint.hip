@@ -421,6 +421,24 @@ int hos_peft_load_hos(hos_peft* p, const char* path, int with_optimizer) {
   });
 }
 
+int hos_format_verify(const char* path, size_t* n_tensors, char* err, size_t err_len) {
+  try {
+    Capsule c;
+    read_capsule(path, c);
+    std::vector<float> v;
+    for (const Tensor& t : c.tensors)
+      if (t.dtype == DTYPE_F32) decode_f32(t, v);
+    if (n_tensors) *n_tensors = c.tensors.size();
+    return HOS_OK;
+  } catch (const Error& e) {
+    if (err && err_len) std::snprintf(err, err_len, "%s", e.what());
+    return e.code;
+  } catch (const std::exception& e) {
+    if (err && err_len) std::snprintf(err, err_len, "%s", e.what());
+    return HOS_E_IO;
+  }
+}
+
 int hos_format_card(const char* path, char* out, size_t len, size_t* needed) {
   try {
     Capsule c;

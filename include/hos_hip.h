@@ -282,6 +282,9 @@ int hos_peft_base_id(hos_peft* p, char* out17);
 /* read_card (src/format.rs:270-285): the card JSON of a .hos file into out (NUL-terminated, truncated to
  * len); *needed (may be NULL) = its length + 1. On error out receives the message. No device work. */
 int hos_format_card(const char* path, char* out, size_t len, size_t* needed);
+/* load_raw (src/format.rs:401-485) without a model: parse the header, card and tensor table and verify every
+ * tensor's checksum (and the F32 byte counts); *n_tensors (may be NULL) = the table size. No device work. */
+int hos_format_verify(const char* path, size_t* n_tensors, char* err, size_t err_len);
 /* ---- full-parameter finetune (FtModel, src/finetune.rs) ----
  * Every weight a trainable f32 parameter on the device: quantized tensors are dequantized once at load
  * (Weight::to_f32); a tied head becomes an untied copy of the embedding (src/finetune.rs:101-107). Dense
