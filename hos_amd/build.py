@@ -24,6 +24,9 @@ FLAGS = [
 # Files whose f32 arithmetic must round once per operation (byte-exact GGUF codec): no fusion of a·b + c
 # anywhere, including inside inlined header intrinsics.
 NO_CONTRACT = {"quant.hip"}
+# Files whose MFMA accumulators are read by VALU work every iteration (the attention softmax): keep them in
+# VGPRs (the default AGPR form costs a read and a write per accumulator register around that work).
+MFMA_VGPR = {"attention.hip"}
 
 
 def sources():
@@ -41,6 +44,8 @@ SAN_LIB = os.path.join(SAN_BUILD, "libhos_hip.so")
 def _compile(src, san=False):
     obj = os.path.join(SAN_BUILD if san else BUILD, os.path.basename(src) + ".o")
     extra = ["-ffp-contract=off"] if os.path.basename(src) in NO_CONTRACT else []
+    if os.path.basename(src) in MFMA_VGPR:
+        extra += ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
     cmd = [HIPCC] + FLAGS + extra + (SAN_FLAGS if san else []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -7,27 +7,43 @@
 // row softmax (src/tensor.rs:2460-2491), ctx = P·v, kv head = h / (n_heads / n_kv_heads)
 // (repeat_interleave_dim0, src/tensor.rs:2819-2841). Backward = the bmm/softmax/repeat VJPs
 // (src/tensor.rs:2260-2272, :2481-2490, :2831-2840) in flash form: P is recomputed from the saved
-// log-sum-exp, dS = P∘(dP − rowsum(dO∘O)), and GQA gradients are summed over the group.
+// log-sum-exp, dS = P∘(dP − rowsum(dO∘O)), and GQA gradients are summed over the group in head order.
 // The scale 1/√hd is folded into q (exactly 2^-3 for hd = 64; the f32 value of 1/√128 for hd = 128).
 //
-// MFMA layout used throughout (32×32 tiles, here of v_mfma_f32_32x32x16_bf16 on hi/lo-split operands): the D matrix X[i][j] sits with column j = lane%32 and
-// rows i = 8·(r/4) + 4·(lane/32) + r%4 in register r. Read back as an A operand, register r of that
-// layout supplies row (lane%32) of Xᵀ at contraction index κ(r, lane/32) = 8·(r/4) + 4·(lane/32) + r%4,
-// so a score tile feeds the next MFMA straight from registers provided the other operand is gathered
-// in the same κ order. Per wave: 32 queries (or keys) × HD head dims (HD = 64 or 128, a template
-// parameter); 4 waves per workgroup split the
-// other sequence axis and merge in LDS, so there is no workgroup barrier inside the main loops.
+// Data path. One split kernel per direction turns the f32 operands into bf16 hi/lo planes, head-major
+// ([b][head][t][d], so a 32-row tile of one head is one contiguous 32·hd run): q (pre-scaled), k, v, and for
+// the backward dO with D = rowsum(dO∘O) fused in. Every attention kernel is a workgroup of 4 waves over 128
+// rows of one (head, sequence) — queries for the forward and dQ, keys for dK/dV — each wave owning 32 of them
+// for the whole loop (its accumulators never leave registers, no cross-wave merge). The other axis streams
+// through LDS in 32-row tiles, loaded once per workgroup with 16-byte loads and double-buffered (one barrier
+// per tile), so every tile feeds four waves.
+//
+// MFMA layout (v_mfma_f32_32x32x16_bf16): register r of lane l holds D[i][j] with column j = l%32 and row
+// i = κ(r, l/32) = 8·(r/4) + 4·(l/32) + r%4. The first product puts
+// the streamed tile's rows on i (A operand: 16-byte LDS reads of row-major tiles) and this wave's own rows on j
+// (B operand: held in registers), so each lane ends up owning one of its wave's rows: softmax statistics are
+// per lane. The second product reads the score registers back as a B operand — register 8t+e of lane l is
+// contraction slot 8·(l/32)+e of step t, i.e. streamed row κ(8t+e, l/32) — and the A operand is the streamed
+// tile transposed, fetched in that same κ order with ds_read_b64_tr_b16 (two 4-row groups per step), giving
+// the output transposed: Oᵀ[d][row] with the row again on the lane.
 #include "fused.hpp"
 
 namespace hos {
 namespace {
 
-constexpr int TB = 32, KW = 4;  // tile rows, waves per workgroup
-// per head dim: LDS row (padded), 1/√hd
+constexpr int TB = 32;        // rows of one MFMA tile
+constexpr int NW = 4;         // waves per workgroup
+constexpr int BR = TB * NW;   // rows a workgroup owns
+
 template <int HD>
-struct HdC {
-  static constexpr int LP = HD + 1, NC = HD / 32;  // NC 32-column tiles per row
+struct AC {
+  static constexpr int NS = HD / 16;    // contraction steps over the head dims
+  static constexpr int NC = HD / 32;    // 32-wide column tiles of one head
+  static constexpr int LD = HD + 8;     // LDS row stride (bf16): 16 bytes of padding spread the row reads
+  static constexpr int TILE = TB * LD;  // one plane of one 32-row tile
+  static constexpr int CH = HD / 8;     // 16-byte chunks per row
 };
+
 template <int HD>
 __device__ __forceinline__ float qscale() {
   return HD == 64 ? 0.125f : 0.08838834764831845f;  // 1/√128 rounded to f32
@@ -35,386 +51,464 @@ __device__ __forceinline__ float qscale() {
 
 __device__ __forceinline__ int kap(int s, int h) { return 8 * (s >> 2) + 4 * h + (s & 3); }
 
-// Fragment of one row for a contraction over the HD head dims: frag[4j + e] = row[8j + 4·hl + e]·mul.
-// Any bijection of the contraction index works as long as both MFMA operands use it; this one lets a
-// lane fetch its 32 values as 8 float4.
+// e^(x − m) as 2^(x·log2 e − m·log2 e) on the hardware exp2 (v_exp_f32, ~1 ulp; one fma for the argument):
+// the exponentials are the bulk of the VALU work between two MFMA products. e^(−∞) = 0.
+constexpr float LOG2E = 1.4426950408889634f;
+__device__ __forceinline__ float exp_shift(float x, float m_log2e) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(x, LOG2E, -m_log2e));
+}
+
+typedef short s4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4v* lds_s4;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // a native vector: stays in registers
+
+// A operand of the second product: rows κ(8t + 0..7, hl) of a row-major LDS tile, at column `col` (this lane's
+// head dim), as one bf8. In a 16-lane group lane L addresses row r0 + L/4, columns c0 + 4·(L%4) .. +3, and the
+// transposing read hands lane i the four rows r0 .. r0+3 of column c0 + i.
 template <int HD>
-__device__ __forceinline__ void load_rowfrag(float* frag, const float* __restrict__ row, int hl, float mul) {
+__device__ __forceinline__ bf8 tr_frag(const __bf16* tile, int t, int i, int lane) {
+  const int g = lane >> 4, L = lane & 15;
+  const int row = 16 * t + 4 * (g >> 1) + (L >> 2);
+  const int col = 32 * i + 16 * (g & 1) + 4 * (L & 3);
+  const __bf16* p = tile + row * AC<HD>::LD + col;
+  const s4v x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p));
+  const s4v x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p + 8 * AC<HD>::LD));
+  bf8 f;
+  __builtin_memcpy(&f, &x0, 8);
+  __builtin_memcpy((char*)&f + 8, &x1, 8);
+  return f;
+}
+
+// A operand of the first product: row `lane%32` of a row-major LDS tile, head dims 16t + 8·(lane/32) .. +7.
+template <int HD>
+__device__ __forceinline__ bf8 row_frag(const __bf16* tile, int t, int lane) {
+  return *reinterpret_cast<const bf8*>(tile + (lane & 31) * AC<HD>::LD + 16 * t + 8 * (lane >> 5));
+}
+
+// B operand of the first product from a head-major plane: row `row`, head dims 16t + 8·hl .. +7, all steps.
+template <int HD>
+__device__ __forceinline__ void own_frags(const __bf16* __restrict__ ph, const __bf16* __restrict__ pl, long long row,
+                                          int hl, bf8* H, bf8* Lo) {
 #pragma unroll
-  for (int j = 0; j < HD / 8; j++) {
-    const float4 v = *reinterpret_cast<const float4*>(row + 8 * j + 4 * hl);
-    frag[4 * j] = v.x * mul;
-    frag[4 * j + 1] = v.y * mul;
-    frag[4 * j + 2] = v.z * mul;
-    frag[4 * j + 3] = v.w * mul;
+  for (int t = 0; t < AC<HD>::NS; t++) {
+    H[t] = *reinterpret_cast<const bf8*>(ph + row * HD + 16 * t + 8 * hl);
+    Lo[t] = *reinterpret_cast<const bf8*>(pl + row * HD + 16 * t + 8 * hl);
   }
 }
 
-// B operand over 32 rows indexed in κ order: col[16i + s] = X[r0 + κ(s, hl)][32i + c] for the NC column tiles.
+// 8 consecutive f32 -> bf16 hi/lo.
+__device__ __forceinline__ void split8(const float* v, float mul, bf8& H, bf8& L) {
+#pragma unroll
+  for (int e = 0; e < 8; e++) split_bf(v[e] * mul, H, L, e);
+}
+
+// Work item of this workgroup: (row block, head, sequence). Workgroup ids are dealt round-robin to the 8 XCDs,
+// each with its own L2; remapping so that each XCD gets a contiguous run of work items keeps the row blocks of
+// one head (which stream the same K/V or Q/dO tiles) and the heads of one GQA group on one L2.
+struct Work {
+  int xb, h, b;
+};
+__device__ __forceinline__ Work work_item() {
+  const int nwg = gridDim.x * gridDim.y * gridDim.z, full = nwg & ~7;
+  int L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  if (L < full) L = (L & 7) * (full >> 3) + (L >> 3);
+  const int rest = L / gridDim.x;
+  return Work{L % (int)gridDim.x, rest % (int)gridDim.y, rest / (int)gridDim.y};
+}
+
+// ---- split kernels ----
+// q (scaled), k, v of rows [M, ld] into head-major hi/lo planes; one thread per 8 columns.
 template <int HD>
-__device__ __forceinline__ void load_kapcols(float* col, const float* __restrict__ src, long long base_row, int r0,
-                                             int T, long long ld, int off, int hl, int c, float mul) {
-#pragma unroll
-  for (int s = 0; s < 16; s++) {
-    const int t = r0 + kap(s, hl);
-    const float* row = src + (base_row + (t < T ? t : T - 1)) * ld + off;
-#pragma unroll
-    for (int i = 0; i < HdC<HD>::NC; i++) col[16 * i + s] = row[32 * i + c] * mul;
+__global__ void attn_split_qkv(const float* __restrict__ qkv, long long ld, int kcol, int vcol, int T, int nh, int nkv,
+                               long long M, __bf16* __restrict__ qh, __bf16* __restrict__ ql, __bf16* __restrict__ kh,
+                               __bf16* __restrict__ kl, __bf16* __restrict__ vh, __bf16* __restrict__ vl) {
+  const int per_row = (nh + 2 * nkv) * AC<HD>::CH;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * per_row) return;
+  const long long m = i / per_row;
+  const int c8 = (int)(i % per_row) * 8, b = (int)(m / T), t = (int)(m % T);
+  const float* src;
+  __bf16 *dh, *dl;
+  float mul = 1.0f;
+  long long hrow;  // (b·heads + head)·T + t
+  if (c8 < nh * HD) {
+    src = qkv + m * ld + c8;
+    dh = qh;
+    dl = ql;
+    mul = qscale<HD>();
+    hrow = ((long long)b * nh + c8 / HD) * T + t;
+  } else if (c8 < (nh + nkv) * HD) {
+    const int c = c8 - nh * HD;
+    src = qkv + m * ld + kcol + c;
+    dh = kh;
+    dl = kl;
+    hrow = ((long long)b * nkv + c / HD) * T + t;
+  } else {
+    const int c = c8 - (nh + nkv) * HD;
+    src = qkv + m * ld + vcol + c;
+    dh = vh;
+    dl = vl;
+    hrow = ((long long)b * nkv + c / HD) * T + t;
   }
+  const float4 a0 = reinterpret_cast<const float4*>(src)[0], a1 = reinterpret_cast<const float4*>(src)[1];
+  const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  bf8 H, L;
+  split8(v, mul, H, L);
+  const long long o = hrow * HD + (c8 % HD);
+  *reinterpret_cast<bf8*>(dh + o) = H;
+  *reinterpret_cast<bf8*>(dl + o) = L;
 }
 
-// ---- bf16 hi/lo products: x = hi + lo with hi = bf16(x), lo = bf16(x − hi) (x − hi is exact in f32), and
-// a·b ≈ a_hi·b_hi + a_hi·b_lo + a_lo·b_hi on v_mfma_f32_32x32x16_bf16 — relative error ~2^-16 per product
-// (the dropped a_lo·b_lo and the rounding of lo), fp32 accumulation, f32 exponent range (no scaling of
-// tiny gradients), at 5.3× the throughput of fp32 MFMA per contraction element.
-// An HD-dim row fragment (rowfrag order) as HD/16 contraction steps of 8 values per lane.
+// dO into hi/lo planes and D = Σ_d dO·O per (row, head); HD/8 consecutive threads per (row, head).
 template <int HD>
-struct DFrag {
-  bf8 h[HD / 16], l[HD / 16];
-};
-template <int HD>
-__device__ __forceinline__ void to_dfrag(const float* f, DFrag<HD>& F) {
+__global__ void attn_split_do(const float* __restrict__ o, const float* __restrict__ dout, long long ldo, int T, int nh,
+                              long long M, __bf16* __restrict__ dh, __bf16* __restrict__ dl, float* __restrict__ dvec) {
+  constexpr int CH = AC<HD>::CH;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool ok = i < M * nh * CH;
+  const long long mh = ok ? i / CH : 0;
+  const int ch = (int)(i % CH);
+  const long long m = mh / nh;
+  const int h = (int)(mh % nh), b = (int)(m / T), t = (int)(m % T);
+  float s = 0.0f;
+  if (ok) {
+    const float* dp = dout + m * ldo + h * HD + 8 * ch;
+    const float* op = o + m * ldo + h * HD + 8 * ch;
+    const float4 d0 = reinterpret_cast<const float4*>(dp)[0], d1 = reinterpret_cast<const float4*>(dp)[1];
+    const float4 o0 = reinterpret_cast<const float4*>(op)[0], o1 = reinterpret_cast<const float4*>(op)[1];
+    const float v[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    s = d0.x * o0.x + d0.y * o0.y + d0.z * o0.z + d0.w * o0.w + d1.x * o1.x + d1.y * o1.y + d1.z * o1.z + d1.w * o1.w;
+    bf8 H, L;
+    split8(v, 1.0f, H, L);
+    const long long off = (((long long)b * nh + h) * T + t) * HD + 8 * ch;
+    *reinterpret_cast<bf8*>(dh + off) = H;
+    *reinterpret_cast<bf8*>(dl + off) = L;
+  }
 #pragma unroll
-  for (int t = 0; t < HD / 16; t++)
-#pragma unroll
-    for (int i = 0; i < 8; i++) split_bf(f[8 * t + i], F.h[t], F.l[t], i);
-}
-// 16 κ-ordered values (a 32-row contraction shared by the two half-waves) as 2 steps of 8.
-struct KFrag {
-  bf8 h[2], l[2];
-};
-__device__ __forceinline__ void to_kfrag(const float* f, KFrag& F) {
-#pragma unroll
-  for (int t = 0; t < 2; t++)
-#pragma unroll
-    for (int i = 0; i < 8; i++) split_bf(f[8 * t + i], F.h[t], F.l[t], i);
-}
-__device__ __forceinline__ f16v mma3(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, f16v c) {
-  return mma3_bf16(ah, al, bh, bl, c);
-}
-// Σ over the HD head dims: D[i][j] += A_row_i · B_row_j (both in rowfrag order)
-template <int HD>
-__device__ __forceinline__ f16v mma_d(const DFrag<HD>& a, const DFrag<HD>& b, f16v c) {
-#pragma unroll
-  for (int t = 0; t < HD / 16; t++) c = mma3(a.h[t], a.l[t], b.h[t], b.l[t], c);
-  return c;
-}
-// Σ over 32 κ-ordered rows: D += A(κ) · B(κ)
-__device__ __forceinline__ f16v mma_k(const KFrag& a, const KFrag& b, f16v c) {
-#pragma unroll
-  for (int t = 0; t < 2; t++) c = mma3(a.h[t], a.l[t], b.h[t], b.l[t], c);
-  return c;
+  for (int k = CH / 2; k > 0; k >>= 1) s += __shfl_xor(s, k);
+  if (ok && ch == 0) dvec[((long long)b * nh + h) * T + t] = s;
 }
 
-// Forward. Workgroup = (32 queries, head, sequence); its 4 waves take key blocks w, w+4, … up to the
-// diagonal, each keeping its own online-softmax state (m, l, O); the states are merged in LDS at the end.
+// Cooperative load of 4 planes' 32-row tiles (rows r0 .. r0+31 of head-major planes, clamped to T-1) into
+// registers, then into LDS tiles of stride LD. Thread tid moves chunk tid + 256·v of the tile set, so the plane
+// and row of every chunk are compile-time functions of v plus tid.
+struct Planes4 {
+  const __bf16* p[4];
+};
 template <int HD>
-__global__ void __launch_bounds__(256) attn_fwd_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
+struct TileLoader {
+  static constexpr int PER = TB * AC<HD>::CH;   // 16-byte chunks per plane tile (256 or 512)
+  static constexpr int VPP = PER / (NW * 64);   // register chunks per plane per thread
+  static constexpr int NL = 4 * VPP;
+  static_assert(PER % (NW * 64) == 0, "tile chunks");
+  u32x4 reg[NL];
+  __device__ __forceinline__ void load(const Planes4& P, long long hbase, int r0, int T, int tid) {
+#pragma unroll
+    for (int v = 0; v < NL; v++) {
+      const int rem = (v % VPP) * NW * 64 + tid, row = rem / AC<HD>::CH, ch = rem % AC<HD>::CH;
+      const int t = min(r0 + row, T - 1);
+      reg[v] = *reinterpret_cast<const u32x4*>(P.p[v / VPP] + (hbase + t) * HD + 8 * ch);
+    }
+  }
+  __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+#pragma unroll
+    for (int v = 0; v < NL; v++) {
+      const int rem = (v % VPP) * NW * 64 + tid, row = rem / AC<HD>::CH, ch = rem % AC<HD>::CH;
+      *reinterpret_cast<u32x4*>(lds + (v / VPP) * AC<HD>::TILE + row * AC<HD>::LD + 8 * ch) = reg[v];
+    }
+  }
+};
+
+// ---- forward: a wave owns 32 queries; K and V tiles stream through LDS ----
+template <int HD>
+__global__ void __launch_bounds__(256) attn_fwd_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
+                                                       const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
+                                                       const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
                                                        int T, int nh, int group, float* __restrict__ o, long long ldo,
                                                        float* __restrict__ lse) {
-  constexpr int NC = HdC<HD>::NC;
-  __shared__ float Os[KW][TB][HdC<HD>::LP];
-  __shared__ float Ms[KW][TB], Ls[KW][TB];
-  const int nqb = (T + TB - 1) / TB;
-  const int qb = nqb - 1 - (int)blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;  // long rows first
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31, q0 = qb * TB;
-  const int myq = q0 + c;  // this lane's query in the Sᵀ layout
-  const long long base = (long long)b * T;
-  DFrag<HD> qd;
-  {
-    float qf[HD / 2];
-    load_rowfrag<HD>(qf, qkv + (base + (myq < T ? myq : T - 1)) * ld + h * HD, hl, qscale<HD>());
-    to_dfrag(qf, qd);
-  }
-  f16v O[NC];
+  using C = AC<HD>;
+  __shared__ __attribute__((aligned(16))) __bf16 sm[2][4 * C::TILE];  // stage: Kh, Kl, Vh, Vl
+  const int nqb = (T + BR - 1) / BR;
+  const Work wk = work_item();
+  const int qb = nqb - 1 - wk.xb, h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hl = lane >> 5,
+            c = lane & 31;
+  const int q0 = qb * BR + w * TB, myq = q0 + c;
+  const bool active = q0 < T;
+  const long long qrow0 = ((long long)b * nh + h) * T, krow0 = ((long long)b * nkv + g) * T;
+  bf8 Qh[C::NS], Ql[C::NS];
+  own_frags<HD>(qh, ql, qrow0 + min(myq, T - 1), hl, Qh, Ql);
+  f16v O[C::NC];
 #pragma unroll
-  for (int i = 0; i < NC; i++)
+  for (int i = 0; i < C::NC; i++)
 #pragma unroll
     for (int r = 0; r < 16; r++) O[i][r] = 0.0f;
   float m = -INFINITY, l = 0.0f;
-  for (int kb = w; kb <= qb; kb += KW) {
-    const int k0 = kb * TB, kr = k0 + c;
-    float kf[HD / 2], vv[HD / 2];
-    load_rowfrag<HD>(kf, qkv + (base + (kr < T ? kr : T - 1)) * ld + kcol + g * HD, hl, 1.0f);
-    load_kapcols<HD>(vv, qkv, base, k0, T, ld, vcol + g * HD, hl, c, 1.0f);
-    DFrag<HD> kd;
-    to_dfrag(kf, kd);
-    f16v S;
-#pragma unroll
-    for (int r = 0; r < 16; r++) S[r] = 0.0f;
-    S = mma_d(kd, qd, S);
-    // S[r] = score(key k0 + κ(r, hl), query myq)
-    float mb = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int key = k0 + kap(r, hl);
-      if (key > myq || key >= T) S[r] = -INFINITY;
-      mb = fmaxf(mb, S[r]);
-    }
-    mb = fmaxf(mb, __shfl_xor(mb, 32));
-    const float mn = fmaxf(m, mb);
-    const float alpha = (m == -INFINITY) ? 0.0f : expf(m - mn);
-    float ps = 0.0f, p[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      p[r] = (S[r] == -INFINITY) ? 0.0f : expf(S[r] - mn);
-      ps += p[r];
-    }
-    ps += __shfl_xor(ps, 32);
-    l = l * alpha + ps;
-    m = mn;
-    // O rows are queries q0 + κ(r, hl): fetch their alpha from the lane that owns that query
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float a = __shfl(alpha, kap(r, hl));
-#pragma unroll
-      for (int i = 0; i < NC; i++) O[i][r] *= a;
-    }
-    KFrag pk;
-    to_kfrag(p, pk);
-#pragma unroll
-    for (int i = 0; i < NC; i++) {
-      KFrag vi;
-      to_kfrag(vv + 16 * i, vi);
-      O[i] = mma_k(pk, vi, O[i]);
-    }
-  }
-  if (hl == 0) {
-    Ms[w][c] = m;
-    Ls[w][c] = l;
-  }
-#pragma unroll
-  for (int r = 0; r < 16; r++)
-#pragma unroll
-    for (int i = 0; i < NC; i++) Os[w][kap(r, hl)][32 * i + c] = O[i][r];
+  const int nkb = (min(qb * BR + BR, T) - 1) / TB + 1;  // key tiles the workgroup needs
+  const int my_last = active ? (min(q0 + TB, T) - 1) / TB : -1;
+  const Planes4 planes{{kh, kl, vh, vl}};
+  TileLoader<HD> ld;
+  ld.load(planes, krow0, 0, T, tid);
+  ld.store(sm[0], tid);
   __syncthreads();
-  // merge the four states: thread → (query tid/8, dims (HD/8)·(tid%8) .. +HD/8)
-  const int qi = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * (HD / 8), t = q0 + qi;
-  if (t >= T) return;
-  float mx = -INFINITY;
+  for (int kb = 0; kb < nkb; kb++) {
+    const __bf16* st = sm[kb & 1];
+    ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, tid);  // past the end: a harmless re-read
+    if (kb <= my_last) {
+      f16v S;
 #pragma unroll
-  for (int v = 0; v < KW; v++) mx = fmaxf(mx, Ms[v][qi]);
-  float e[KW], den = 0.0f;
+      for (int r = 0; r < 16; r++) S[r] = 0.0f;
 #pragma unroll
-  for (int v = 0; v < KW; v++) {
-    e[v] = Ms[v][qi] == -INFINITY ? 0.0f : expf(Ms[v][qi] - mx);
-    den += Ls[v][qi] * e[v];
+      for (int t = 0; t < C::NS; t++)
+        S = mma3_bf16(row_frag<HD>(st, t, lane), row_frag<HD>(st + C::TILE, t, lane), Qh[t], Ql[t], S);
+      // S[r] = score(key k0 + κ(r, hl), query myq)
+      const int k0 = kb * TB;
+      float mb = -INFINITY;
+      if (kb == my_last) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int key = k0 + kap(r, hl);
+          if (key > myq || key >= T) S[r] = -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) mb = fmaxf(mb, S[r]);
+      mb = fmaxf(mb, __shfl_xor(mb, 32));
+      const float mn = fmaxf(m, mb), mn2 = mn * LOG2E;
+      const float alpha = m == mn ? 1.0f : exp_shift(m, mn2);  // 0 while m = −∞
+      float ps = 0.0f, p[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        p[r] = exp_shift(S[r], mn2);
+        ps += p[r];
+      }
+      ps += __shfl_xor(ps, 32);
+      l = l * alpha + ps;
+      m = mn;
+      // rescale the running output only when some row's maximum moved (wave-uniform test)
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int i = 0; i < C::NC; i++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) O[i][r] *= alpha;
+      }
+      // Oᵀ += Vᵀ·Pᵀ
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        bf8 ph, pl;
+        split8(p + 8 * t, 1.0f, ph, pl);
+#pragma unroll
+        for (int i = 0; i < C::NC; i++)
+          O[i] = mma3_bf16(tr_frag<HD>(st + 2 * C::TILE, t, i, lane), tr_frag<HD>(st + 3 * C::TILE, t, i, lane), ph,
+                           pl, O[i]);
+      }
+    }
+    ld.store(sm[(kb + 1) & 1], tid);
+    __syncthreads();
   }
-  const float inv = 1.0f / den;
-  float* orow = o + (base + t) * ldo + h * HD;
+  if (!active || myq >= T) return;
+  const float inv = 1.0f / l;
+  float* orow = o + ((long long)b * T + myq) * ldo + h * HD;
 #pragma unroll
-  for (int d = d0; d < d0 + HD / 8; d++) {
-    float num = 0.0f;
+  for (int i = 0; i < C::NC; i++)
 #pragma unroll
-    for (int v = 0; v < KW; v++) num += Os[v][qi][d] * e[v];
-    orow[d] = num * inv;
-  }
-  if (d0 == 0) lse[((long long)b * nh + h) * T + t] = mx + logf(den);
+    for (int j = 0; j < 4; j++)
+      *reinterpret_cast<float4*>(orow + 32 * i + 8 * j + 4 * hl) =
+          make_float4(O[i][4 * j] * inv, O[i][4 * j + 1] * inv, O[i][4 * j + 2] * inv, O[i][4 * j + 3] * inv);
+  if (hl == 0) lse[((long long)b * nh + h) * T + myq] = m + logf(l);
 }
 
-// Dvec[b,h,t] = Σ_d dO·O over the head's HD columns.
+// ---- dQ: a wave owns 32 queries; K and V tiles stream through LDS ----
 template <int HD>
-__global__ void attn_dvec_kernel(const float* __restrict__ o, const float* __restrict__ dout, long long ld, int T,
-                                 int nh, int B, float* __restrict__ dvec) {
-  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)B * nh * T) return;
-  int t = (int)(i % T);
-  int h = (int)((i / T) % nh);
-  int b = (int)(i / ((long long)T * nh));
-  const float* orow = o + ((long long)b * T + t) * ld + h * HD;
-  const float* drow = dout + ((long long)b * T + t) * ld + h * HD;
-  float s = 0.0f;
-  for (int d = 0; d < HD; d++) s += drow[d] * orow[d];
-  dvec[i] = s;
-}
-
-// dQ for 32 queries of head h: Sᵀ and dPᵀ with lanes on queries, dQ = (dS·K)·2^-3. The 4 waves take
-// key blocks w, w+4, …; their partial dQ are summed in wave order.
-template <int HD>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 2 : 1))) attn_dq_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
-                                                      const float* __restrict__ dout, long long ldd,
+__global__ void __launch_bounds__(256) attn_dq_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
+                                                      const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
+                                                      const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
+                                                      const __bf16* __restrict__ doh, const __bf16* __restrict__ dol,
                                                       const float* __restrict__ lse, const float* __restrict__ dvec,
                                                       int T, int nh, int group, float* __restrict__ dq,
                                                       long long ldq) {
-  constexpr int NC = HdC<HD>::NC;
-  __shared__ float As[KW][TB][HdC<HD>::LP];
-  const int nqb = (T + TB - 1) / TB;
-  const int qb = nqb - 1 - (int)blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31, q0 = qb * TB;
-  const int myq = q0 + c;
-  const long long base = (long long)b * T, qrow = base + (myq < T ? myq : T - 1);
-  DFrag<HD> qd, dd;
-  {
-    float qf[HD / 2], df[HD / 2];
-    load_rowfrag<HD>(qf, qkv + qrow * ld + h * HD, hl, qscale<HD>());
-    load_rowfrag<HD>(df, dout + qrow * ldd + h * HD, hl, 1.0f);
-    to_dfrag(qf, qd);
-    to_dfrag(df, dd);
-  }
-  const long long si = ((long long)b * nh + h) * T + (myq < T ? myq : T - 1);
-  const float L = lse[si], Dv = dvec[si];
-  f16v A[NC];
+  using C = AC<HD>;
+  __shared__ __attribute__((aligned(16))) __bf16 sm[2][4 * C::TILE];  // stage: Kh, Kl, Vh, Vl
+  const int nqb = (T + BR - 1) / BR;
+  const Work wk = work_item();
+  const int qb = nqb - 1 - wk.xb, h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hl = lane >> 5,
+            c = lane & 31;
+  const int q0 = qb * BR + w * TB, myq = q0 + c;
+  const bool active = q0 < T;
+  const long long qrow0 = ((long long)b * nh + h) * T, krow0 = ((long long)b * nkv + g) * T;
+  const long long qr = qrow0 + min(myq, T - 1);
+  bf8 Qh[C::NS], Ql[C::NS], Dh[C::NS], Dl[C::NS];
+  own_frags<HD>(qh, ql, qr, hl, Qh, Ql);
+  own_frags<HD>(doh, dol, qr, hl, Dh, Dl);
+  const float Lq2 = lse[qr] * LOG2E, Dq = dvec[qr];
+  f16v A[C::NC];
 #pragma unroll
-  for (int i = 0; i < NC; i++)
+  for (int i = 0; i < C::NC; i++)
 #pragma unroll
     for (int r = 0; r < 16; r++) A[i][r] = 0.0f;
-  for (int kb = w; kb <= qb; kb += KW) {
-    const int k0 = kb * TB, kr = k0 + c;
-    const long long krow = base + (kr < T ? kr : T - 1);
-    DFrag<HD> kd, vd;
-    {
-      float kf[HD / 2], vf[HD / 2];
-      load_rowfrag<HD>(kf, qkv + krow * ld + kcol + g * HD, hl, 1.0f);
-      load_rowfrag<HD>(vf, qkv + krow * ld + vcol + g * HD, hl, 1.0f);
-      to_dfrag(kf, kd);
-      to_dfrag(vf, vd);
-    }
-    f16v S, dP;
-#pragma unroll
-    for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
-    S = mma_d(kd, qd, S);
-    dP = mma_d(vd, dd, dP);
-    float ds[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int key = k0 + kap(r, hl);
-      const float pv = (key > myq || key >= T || myq >= T) ? 0.0f : expf(S[r] - L);
-      ds[r] = pv * (dP[r] - Dv);
-    }
-    float kk[HD / 2];
-    load_kapcols<HD>(kk, qkv, base, k0, T, ld, kcol + g * HD, hl, c, 1.0f);
-    KFrag dk;
-    to_kfrag(ds, dk);
-#pragma unroll
-    for (int i = 0; i < NC; i++) {
-      KFrag ki;
-      to_kfrag(kk + 16 * i, ki);
-      A[i] = mma_k(dk, ki, A[i]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 16; r++)
-#pragma unroll
-    for (int i = 0; i < NC; i++) As[w][kap(r, hl)][32 * i + c] = A[i][r];
+  const int nkb = (min(qb * BR + BR, T) - 1) / TB + 1;
+  const int my_last = active ? (min(q0 + TB, T) - 1) / TB : -1;
+  const Planes4 planes{{kh, kl, vh, vl}};
+  TileLoader<HD> ld;
+  ld.load(planes, krow0, 0, T, tid);
+  ld.store(sm[0], tid);
   __syncthreads();
-  const int qi = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * (HD / 8), t = q0 + qi;
-  if (t >= T) return;
-  float* out = dq + (base + t) * ldq + h * HD;
+  for (int kb = 0; kb < nkb; kb++) {
+    const __bf16* st = sm[kb & 1];
+    ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, tid);  // past the end: a harmless re-read
+    if (kb <= my_last) {
+      f16v S, dP;
 #pragma unroll
-  for (int d = d0; d < d0 + HD / 8; d++) {
-    float v = As[0][qi][d];
+      for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
 #pragma unroll
-    for (int u = 1; u < KW; u++) v += As[u][qi][d];
-    out[d] = v * qscale<HD>();
-  }
-}
-
-// dK, dV for 32 keys against query head h (kv head g = h / group): S and dP with lanes on keys. The
-// 4 waves take query blocks kb + w, kb + w + 4, …; partials are summed in wave order. With group > 1
-// each head's result goes to part[(b·T + key)][h][2·64] and attn_group_sum adds the group in head
-// order; with group == 1 it is written in place.
-template <int HD>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 2 : 1))) attn_dkdv_kernel(const float* __restrict__ qkv, long long ld, int kcol, int vcol,
-                                                        const float* __restrict__ dout, long long ldd,
-                                                        const float* __restrict__ lse,
-                                                        const float* __restrict__ dvec, int T, int nh, int group,
-                                                        float* __restrict__ dkv, long long ldk,
-                                                        float* __restrict__ part) {
-  constexpr int NC = HdC<HD>::NC;
-  __shared__ float Ps[KW][TB][HdC<HD>::LP];
-  const int nkb = (T + TB - 1) / TB;
-  const int kb = blockIdx.x, h = blockIdx.y, b = blockIdx.z, g = h / group;  // long columns first
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31, k0 = kb * TB;
-  const int mykey = k0 + c;
-  const long long base = (long long)b * T, krow = base + (mykey < T ? mykey : T - 1);
-  DFrag<HD> kd, vd;
-  {
-    float kf[HD / 2], vf[HD / 2];
-    load_rowfrag<HD>(kf, qkv + krow * ld + kcol + g * HD, hl, 1.0f);
-    load_rowfrag<HD>(vf, qkv + krow * ld + vcol + g * HD, hl, 1.0f);
-    to_dfrag(kf, kd);
-    to_dfrag(vf, vd);
-  }
-  f16v K[NC], V[NC];
+      for (int t = 0; t < C::NS; t++) {
+        S = mma3_bf16(row_frag<HD>(st, t, lane), row_frag<HD>(st + C::TILE, t, lane), Qh[t], Ql[t], S);
+        dP = mma3_bf16(row_frag<HD>(st + 2 * C::TILE, t, lane), row_frag<HD>(st + 3 * C::TILE, t, lane), Dh[t], Dl[t],
+                       dP);
+      }
+      const int k0 = kb * TB;
+      float ds[16];
 #pragma unroll
-  for (int i = 0; i < NC; i++)
+      for (int r = 0; r < 16; r++) {
+        const int key = k0 + kap(r, hl);
+        const float pv = (key > myq || key >= T || myq >= T) ? 0.0f : exp_shift(S[r], Lq2);
+        ds[r] = pv * (dP[r] - Dq);
+      }
+      // dQᵀ += Kᵀ·dSᵀ
 #pragma unroll
-    for (int r = 0; r < 16; r++) K[i][r] = V[i][r] = 0.0f;
-  for (int qb = kb + w; qb < nkb; qb += KW) {
-    const int q0 = qb * TB, qr = q0 + c;
-    const long long qrow = base + (qr < T ? qr : T - 1);
-    const long long si = ((long long)b * nh + h) * T + (qr < T ? qr : T - 1);
-    const float Lq = lse[si], Dq = dvec[si];
-    DFrag<HD> qd, dd;
-    {
-      float qa[HD / 2], da[HD / 2];
-      load_rowfrag<HD>(qa, qkv + qrow * ld + h * HD, hl, qscale<HD>());
-      load_rowfrag<HD>(da, dout + qrow * ldd + h * HD, hl, 1.0f);
-      to_dfrag(qa, qd);
-      to_dfrag(da, dd);
-    }
-    f16v S, dP;
+      for (int t = 0; t < 2; t++) {
+        bf8 sh, sl;
+        split8(ds + 8 * t, 1.0f, sh, sl);
 #pragma unroll
-    for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
-    S = mma_d(qd, kd, S);
-    dP = mma_d(dd, vd, dP);
-    // S[r] = score(query q0 + κ(r, hl), key mykey)
-    float p[16], ds[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int qi = kap(r, hl), q = q0 + qi;
-      const float Lr = __shfl(Lq, qi), Dr = __shfl(Dq, qi);
-      const float pv = (mykey > q || q >= T || mykey >= T) ? 0.0f : expf(S[r] - Lr);
-      p[r] = pv;
-      ds[r] = pv * (dP[r] - Dr);
-    }
-    float qs[HD / 2], dos[HD / 2];
-    load_kapcols<HD>(qs, qkv, base, q0, T, ld, h * HD, hl, c, qscale<HD>());
-    load_kapcols<HD>(dos, dout, base, q0, T, ldd, h * HD, hl, c, 1.0f);
-    KFrag pf, dsf;
-    to_kfrag(p, pf);
-    to_kfrag(ds, dsf);
-#pragma unroll
-    for (int i = 0; i < NC; i++) {
-      KFrag doi, qi;
-      to_kfrag(dos + 16 * i, doi);
-      to_kfrag(qs + 16 * i, qi);
-      V[i] = mma_k(pf, doi, V[i]);
-      K[i] = mma_k(dsf, qi, K[i]);
-    }
-  }
-  // Q carried the scale, so K already holds dK = dSᵀ·Q·scale. Merge K, then V.
-  const int ki = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * (HD / 8), key = k0 + ki;
-  float* kr = nullptr;
-  float* vr = nullptr;
-  if (key < T) {
-    if (group == 1) {
-      kr = dkv + (base + key) * ldk + kcol + g * HD;
-      vr = dkv + (base + key) * ldk + vcol + g * HD;
-    } else {
-      kr = part + ((base + key) * nh + h) * 2 * HD;
-      vr = kr + HD;
-    }
-  }
-#pragma unroll
-  for (int pass = 0; pass < 2; pass++) {
-    if (pass) __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 16; r++)
-#pragma unroll
-      for (int i = 0; i < NC; i++) Ps[w][kap(r, hl)][32 * i + c] = pass == 0 ? K[i][r] : V[i][r];
-    __syncthreads();
-    float* dst = pass == 0 ? kr : vr;
-    if (dst) {
-#pragma unroll
-      for (int d = d0; d < d0 + HD / 8; d++) {
-        float v = Ps[0][ki][d];
-#pragma unroll
-        for (int u = 1; u < KW; u++) v += Ps[u][ki][d];
-        dst[d] = v;
+        for (int i = 0; i < C::NC; i++)
+          A[i] = mma3_bf16(tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, A[i]);
       }
     }
+    ld.store(sm[(kb + 1) & 1], tid);
+    __syncthreads();
   }
+  if (!active || myq >= T) return;
+  float* out = dq + ((long long)b * T + myq) * ldq + h * HD;
+  const float s = qscale<HD>();
+#pragma unroll
+  for (int i = 0; i < C::NC; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      *reinterpret_cast<float4*>(out + 32 * i + 8 * j + 4 * hl) =
+          make_float4(A[i][4 * j] * s, A[i][4 * j + 1] * s, A[i][4 * j + 2] * s, A[i][4 * j + 3] * s);
+}
+
+// ---- dK, dV for query head h: a wave owns 32 keys; Q and dO tiles (with their LSE and D) stream through LDS.
+// With group > 1 each head's result goes to part[(b·T + key)][h][2·HD] and attn_group_sum adds the group in head
+// order; with group == 1 it is written in place.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_dkdv_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
+                                                        const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
+                                                        const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
+                                                        const __bf16* __restrict__ doh, const __bf16* __restrict__ dol,
+                                                        const float* __restrict__ lse, const float* __restrict__ dvec,
+                                                        int T, int nh, int group, float* __restrict__ dkv,
+                                                        long long ldk, int kcol, int vcol, float* __restrict__ part) {
+  using C = AC<HD>;
+  __shared__ __attribute__((aligned(16))) __bf16 sm[2][4 * C::TILE];  // stage: Qh, Ql, dOh, dOl
+  __shared__ float ld_s[2][2][TB];                                    // stage: LSE·log2 e, D of the tile's queries
+  const Work wk = work_item();
+  const int h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hl = lane >> 5,
+            c = lane & 31;
+  const int kw0 = wk.xb * BR + w * TB, mykey = kw0 + c;
+  const bool active = kw0 < T;
+  const long long qrow0 = ((long long)b * nh + h) * T, krow0 = ((long long)b * nkv + g) * T;
+  bf8 Kh[C::NS], Kl[C::NS], Vh[C::NS], Vl[C::NS];
+  own_frags<HD>(kh, kl, krow0 + min(mykey, T - 1), hl, Kh, Kl);
+  own_frags<HD>(vh, vl, krow0 + min(mykey, T - 1), hl, Vh, Vl);
+  f16v dK[C::NC], dV[C::NC];
+#pragma unroll
+  for (int i = 0; i < C::NC; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) dK[i][r] = dV[i][r] = 0.0f;
+  const int nqt = (T + TB - 1) / TB;                 // query tiles of the sequence
+  const int qt0 = (wk.xb * BR) / TB;                 // the first one that sees any of the workgroup's keys
+  const int my_first = active ? kw0 / TB : nqt;      // this wave's first (diagonal) query tile
+  const Planes4 planes{{qh, ql, doh, dol}};
+  TileLoader<HD> ld;
+  float ldv = 0.0f;
+  auto load = [&](int qt) {
+    ld.load(planes, qrow0, qt * TB, T, tid);
+    if (tid < 2 * TB) {
+      const long long r = qrow0 + min(qt * TB + (tid & (TB - 1)), T - 1);
+      ldv = tid < TB ? lse[r] * LOG2E : dvec[r];
+    }
+  };
+  auto store = [&](int s) {
+    ld.store(sm[s], tid);
+    if (tid < 2 * TB) ld_s[s][tid / TB][tid & (TB - 1)] = ldv;
+  };
+  load(qt0);
+  store(0);
+  __syncthreads();
+  for (int qt = qt0; qt < nqt; qt++) {
+    const int s = (qt - qt0) & 1;
+    const __bf16* st = sm[s];
+    load(min(qt + 1, nqt - 1));  // past the end: a harmless re-read
+    if (qt >= my_first) {
+      f16v S, dP;
+#pragma unroll
+      for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < C::NS; t++) {
+        S = mma3_bf16(row_frag<HD>(st, t, lane), row_frag<HD>(st + C::TILE, t, lane), Kh[t], Kl[t], S);
+        dP = mma3_bf16(row_frag<HD>(st + 2 * C::TILE, t, lane), row_frag<HD>(st + 3 * C::TILE, t, lane), Vh[t], Vl[t],
+                       dP);
+      }
+      // S[r] = score(query q0 + κ(r, hl), key mykey); LSE and D of those queries from LDS (4 runs of 4)
+      const int q0 = qt * TB;
+      float Lr[16], Dr[16];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 a = *reinterpret_cast<const float4*>(&ld_s[s][0][8 * j + 4 * hl]);
+        const float4 d = *reinterpret_cast<const float4*>(&ld_s[s][1][8 * j + 4 * hl]);
+        Lr[4 * j] = a.x, Lr[4 * j + 1] = a.y, Lr[4 * j + 2] = a.z, Lr[4 * j + 3] = a.w;
+        Dr[4 * j] = d.x, Dr[4 * j + 1] = d.y, Dr[4 * j + 2] = d.z, Dr[4 * j + 3] = d.w;
+      }
+      float p[16], ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int q = q0 + kap(r, hl);
+        const float pv = (mykey > q || q >= T || mykey >= T) ? 0.0f : exp_shift(S[r], Lr[r]);
+        p[r] = pv;
+        ds[r] = pv * (dP[r] - Dr[r]);
+      }
+      // dVᵀ += dOᵀ·P, dKᵀ += Qᵀ·dS (Q carries the scale, so this is already dK)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        bf8 ph, pl, sh, sl;
+        split8(p + 8 * t, 1.0f, ph, pl);
+        split8(ds + 8 * t, 1.0f, sh, sl);
+#pragma unroll
+        for (int i = 0; i < C::NC; i++) {
+          dV[i] = mma3_bf16(tr_frag<HD>(st + 2 * C::TILE, t, i, lane), tr_frag<HD>(st + 3 * C::TILE, t, i, lane), ph, pl,
+                            dV[i]);
+          dK[i] = mma3_bf16(tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, dK[i]);
+        }
+      }
+    }
+    store(s ^ 1);
+    __syncthreads();
+  }
+  if (!active || mykey >= T) return;
+  const long long row = (long long)b * T + mykey;
+  float* kr = group == 1 ? dkv + row * ldk + kcol + g * HD : part + (row * nh + h) * 2 * HD;
+  float* vr = group == 1 ? dkv + row * ldk + vcol + g * HD : kr + HD;
+#pragma unroll
+  for (int i = 0; i < C::NC; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int d = 32 * i + 8 * j + 4 * hl;
+      *reinterpret_cast<float4*>(kr + d) = make_float4(dK[i][4 * j], dK[i][4 * j + 1], dK[i][4 * j + 2], dK[i][4 * j + 3]);
+      *reinterpret_cast<float4*>(vr + d) = make_float4(dV[i][4 * j], dV[i][4 * j + 1], dV[i][4 * j + 2], dV[i][4 * j + 3]);
+    }
 }
 
 // dK/dV of kv head g = Σ over its group's heads, in head order (deterministic).
@@ -433,32 +527,65 @@ __global__ void attn_group_sum(const float* __restrict__ part, int M, int nh, in
   dkv[m * ldk + col] = s;
 }
 
-}  // namespace
+// Plane pointers inside the caller's scratch: q, k, v, dO, each hi then lo.
+struct Planes {
+  __bf16 *qh, *ql, *kh, *kl, *vh, *vl, *dh, *dl;
+};
+Planes planes_of(void* scratch, int B, int T, int nh, int nkv, int hd) {
+  const long long nq = (long long)B * nh * T * hd, nk = (long long)B * nkv * T * hd;
+  __bf16* p = (__bf16*)scratch;
+  Planes P;
+  P.qh = p;
+  P.ql = P.qh + nq;
+  P.kh = P.ql + nq;
+  P.kl = P.kh + nk;
+  P.vh = P.kl + nk;
+  P.vl = P.vh + nk;
+  P.dh = P.vl + nk;
+  P.dl = P.dh + nq;
+  return P;
+}
 
-void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,
-                     float* o, long long ldo, float* lse, hipStream_t st) {
+void check_layout(long long ld, int kcol, int vcol, int hd, const void* scratch) {
   HOS_REQUIRE(hd == 64 || hd == 128, HOS_E_INVALID, "attention: head_dim must be 64 or 128");
   HOS_REQUIRE(ld % 4 == 0 && kcol % 4 == 0 && vcol % 4 == 0, HOS_E_INVALID, "attention: unaligned qkv layout");
-  dim3 grid(ceil_div(T, TB), nh, B);
-  if (hd == 64)
-    attn_fwd_kernel<64><<<grid, 256, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nh / nkv, o, ldo, lse);
-  else
-    attn_fwd_kernel<128><<<grid, 256, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nh / nkv, o, ldo, lse);
+  HOS_REQUIRE(scratch != nullptr && ((uintptr_t)scratch & 15) == 0, HOS_E_INVALID, "attention: no plane scratch");
+}
+
+template <int HD>
+void split_qkv(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, const Planes& P,
+               hipStream_t st) {
+  const long long M = (long long)B * T, n = M * (nh + 2 * nkv) * AC<HD>::CH;
+  attn_split_qkv<HD><<<ceil_div(n, 256), 256, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nkv, M, P.qh, P.ql, P.kh, P.kl,
+                                                       P.vh, P.vl);
   HOS_HIP_CHECK(hipGetLastError());
 }
 
 template <int HD>
-static void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
-                        long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, float* dqkv,
-                        long long ldd, float* part, hipStream_t st) {
-  long long n = (long long)B * nh * T;
-  attn_dvec_kernel<HD><<<ceil_div(n, 256), 256, 0, st>>>(o, dout, ldo, T, nh, B, dvec);
+void attn_fwd_hd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, float* o,
+                 long long ldo, float* lse, void* scratch, hipStream_t st) {
+  const Planes P = planes_of(scratch, B, T, nh, nkv, HD);
+  split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
+  dim3 grid(ceil_div(T, BR), nh, B);
+  attn_fwd_kernel<HD><<<grid, 256, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, T, nh, nh / nkv, o, ldo, lse);
   HOS_HIP_CHECK(hipGetLastError());
-  dim3 gq(ceil_div(T, TB), nh, B);
-  attn_dq_kernel<HD><<<gq, 256, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd);
+}
+
+template <int HD>
+void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout, long long ldo,
+                 const float* lse, float* dvec, int B, int T, int nh, int nkv, float* dqkv, long long ldd, float* part,
+                 void* scratch, hipStream_t st) {
+  const Planes P = planes_of(scratch, B, T, nh, nkv, HD);
+  split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
+  const long long M = (long long)B * T, n = M * nh * AC<HD>::CH;
+  attn_split_do<HD><<<ceil_div(n, 256), 256, 0, st>>>(o, dout, ldo, T, nh, M, P.dh, P.dl, dvec);
   HOS_HIP_CHECK(hipGetLastError());
-  dim3 gk(ceil_div(T, TB), nh, B);
-  attn_dkdv_kernel<HD><<<gk, 256, 0, st>>>(qkv, ld, kcol, vcol, dout, ldo, lse, dvec, T, nh, nh / nkv, dqkv, ldd, part);
+  dim3 grid(ceil_div(T, BR), nh, B);
+  attn_dq_kernel<HD><<<grid, 256, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse, dvec, T, nh, nh / nkv,
+                                           dqkv, ldd);
+  HOS_HIP_CHECK(hipGetLastError());
+  attn_dkdv_kernel<HD><<<grid, 256, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse, dvec, T, nh, nh / nkv,
+                                             dqkv, ldd, kcol, vcol, part);
   HOS_HIP_CHECK(hipGetLastError());
   if (nh != nkv) {
     long long ne = (long long)B * T * nkv * 2 * HD;
@@ -467,16 +594,34 @@ static void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, cons
   }
 }
 
+}  // namespace
+
+size_t attn_scratch_bytes(int B, int T, int nh, int nkv, int hd) {
+  return (size_t)B * T * hd * (2 * (size_t)nh + 2 * (size_t)nkv) * 2 * sizeof(__bf16);
+}
+
+void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,
+                     float* o, long long ldo, float* lse, void* scratch, hipStream_t st) {
+  check_layout(ld, kcol, vcol, hd, scratch);
+  HOS_REQUIRE(ldo % 4 == 0 && nkv > 0 && nh % nkv == 0, HOS_E_INVALID, "attention: bad output layout or heads");
+  if (B <= 0 || T <= 0) return;
+  if (hd == 64)
+    attn_fwd_hd<64>(qkv, ld, kcol, vcol, B, T, nh, nkv, o, ldo, lse, scratch, st);
+  else
+    attn_fwd_hd<128>(qkv, ld, kcol, vcol, B, T, nh, nkv, o, ldo, lse, scratch, st);
+}
+
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
-                     long long ldd, float* part, hipStream_t st) {
-  HOS_REQUIRE(hd == 64 || hd == 128, HOS_E_INVALID, "attention: head_dim must be 64 or 128");
+                     long long ldd, float* part, void* scratch, hipStream_t st) {
+  check_layout(ld, kcol, vcol, hd, scratch);
   HOS_REQUIRE(nh == nkv || part != nullptr, HOS_E_INVALID, "attention: GQA backward needs a partial buffer");
-  HOS_REQUIRE(ldo % 4 == 0 && ld % 4 == 0 && kcol % 4 == 0 && vcol % 4 == 0, HOS_E_INVALID, "attention: unaligned layout");
+  HOS_REQUIRE(ldo % 4 == 0 && ldd % 4 == 0 && nkv > 0 && nh % nkv == 0, HOS_E_INVALID, "attention: unaligned layout");
+  if (B <= 0 || T <= 0) return;
   if (hd == 64)
-    attn_bwd_hd<64>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, st);
+    attn_bwd_hd<64>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st);
   else
-    attn_bwd_hd<128>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, st);
+    attn_bwd_hd<128>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st);
 }
 
 }  // namespace hos

@@ -96,6 +96,7 @@ struct hos_ft {
   float *xf = nullptr, *xfn = nullptr, *invf = nullptr, *logits = nullptr, *dl = nullptr, *row_loss = nullptr,
         *loss = nullptr, *dx = nullptr, *dxn = nullptr, *dqkv = nullptr, *dout = nullptr, *dh = nullptr,
         *dgu = nullptr, *dvec = nullptr, *part = nullptr, *ws = nullptr;
+  void* attn_planes = nullptr;  // bf16 hi/lo planes of q, k, v, dO (attention scratch)
   size_t ws_bytes = 0;
   H16 hs{};
   float2* rope_tab = nullptr;
@@ -207,6 +208,7 @@ struct hos_ft {
     dgu = alloc<float>(M * 2 * F);
     dvec = alloc<float>(M * c.n_heads);
     if (c.n_heads != c.n_kv_heads) part = alloc<float>(M * c.n_heads * 2 * c.head_dim);
+    attn_planes = alloc<float>(attn_scratch_bytes(c.max_batch, c.max_seq, c.n_heads, c.n_kv_heads, c.head_dim) / 4);
     const size_t hc = std::max<size_t>({(size_t)d, 2 * (size_t)F});
     hs.data = alloc<half_t>(M * hc);  // fp16 operand the fused norm / SwiGLU kernels also write (unused here)
     hs.rinv = alloc<float>(M);
@@ -344,7 +346,8 @@ struct hos_ft {
       }
       // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
       launch_rope(a.qkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
-      launch_attn_fwd(a.qkv, W3, qd, qd + kvd, B, T, c.n_heads, c.n_kv_heads, c.head_dim, a.o, qd, a.lse, st);
+      launch_attn_fwd(a.qkv, W3, qd, qd + kvd, B, T, c.n_heads, c.n_kv_heads, c.head_dim, a.o, qd, a.lse, attn_planes,
+                      st);
       launch_copy_rows(a.x, d, a.x2, d, M, d, st);
       fwd(a.o, qd, W(l, WO), d, qd, M, 1.0f, a.x2, d);
       launch_rmsnorm_fwd(a.x2, Vp(l, NF), c.rms_eps, M, d, a.xn2, hs, a.inv2, st);
@@ -385,7 +388,7 @@ struct hos_ft {
       bwd_w(dx, d, a.o, qd, d, qd, M, dW(l, WO));
       bwd_x(dx, d, W(l, WO), d, qd, M, 0.0f, dout, qd);
       launch_attn_bwd(a.qkv, W3, qd, qd + kvd, a.o, dout, qd, a.lse, dvec, B, T, c.n_heads, c.n_kv_heads,
-                      c.head_dim, dqkv, W3, part, st);
+                      c.head_dim, dqkv, W3, part, attn_planes, st);
       // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
       launch_rope(dqkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
       if (c.attn_bias) {

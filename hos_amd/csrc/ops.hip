@@ -231,8 +231,10 @@ int hos_hip_attention_fwd(hos_ctx* c, const float* qkv, size_t ld, size_t kcol, 
   return op_guard(c, [&](hipStream_t st) {
     HOS_REQUIRE(qkv && o && lse && B > 0 && T > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, HOS_E_INVALID,
                 "attention: bad arguments");
+    DevMem& pl = internal_scratch(c, 7);  // bf16 planes of q, k, v, dO
+    pl.ensure(attn_scratch_bytes(B, T, n_heads, n_kv_heads, head_dim));
     launch_attn_fwd(qkv, (long long)ld, (int)kcol, (int)vcol, B, T, n_heads, n_kv_heads, head_dim, o, (long long)ldo,
-                    lse, st);
+                    lse, pl.p, st);
   });
 }
 // Its backward: dqkv (same layout as qkv, row stride ldd) receives dq, dk, dv.
@@ -251,8 +253,10 @@ int hos_hip_attention_bwd(hos_ctx* c, const float* qkv, size_t ld, size_t kcol, 
       pm.ensure(M * n_heads * 2 * head_dim * 4);
       part = (float*)pm.p;
     }
+    DevMem& pl = internal_scratch(c, 7);  // bf16 planes of q, k, v, dO
+    pl.ensure(attn_scratch_bytes(B, T, n_heads, n_kv_heads, head_dim));
     launch_attn_bwd(qkv, (long long)ld, (int)kcol, (int)vcol, o, dout, (long long)ldo, lse, (float*)dv.p, B, T,
-                    n_heads, n_kv_heads, head_dim, dqkv, (long long)ldd, part, st);
+                    n_heads, n_kv_heads, head_dim, dqkv, (long long)ldd, part, pl.p, st);
   });
 }
 

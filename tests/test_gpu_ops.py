@@ -91,7 +91,9 @@ def test_swiglu_fwd_bwd(gpu):
 
 @pytest.mark.parametrize("B,T,nh,nkv,hd", [(1, 128, 9, 3, 64), (2, 77, 14, 2, 64), (1, 64, 4, 4, 64),
                                            # OLMoE's head dim (16 heads of 128, no GQA) and a GQA case
-                                           (2, 70, 4, 4, 128), (1, 97, 6, 2, 128)])
+                                           (2, 70, 4, 4, 128), (1, 97, 6, 2, 128),
+                                           # one token; several 128-row workgroups with a ragged last one
+                                           (1, 1, 4, 4, 64), (2, 300, 8, 2, 64), (1, 512, 14, 2, 64)])
 def test_attention_fwd_bwd(gpu, B, T, nh, nkv, hd):
     print(f"attention B={B} T={T} heads={nh}/{nkv} hd={hd}", flush=True)
     rng = np.random.default_rng(B * T + nh)
@@ -108,9 +110,12 @@ def test_attention_fwd_bwd(gpu, B, T, nh, nkv, hd):
     out, dqkv = O.get().reshape(B, T, -1), D.get().reshape(B, T, W3)
     for b in range(B):  # the reference runs one sequence at a time
         ref, dq, dk, dv = o.op_attention(q[b], k[b], v[b], nh, nkv, hd, gout=go[b])
+        # dq and dk vanish at T = 1 (a single key has P = 1 and dS = dP − D = 0): measure them against dv's size
+        floor = float(np.linalg.norm(dv))
+        err = lambda a, r: float(np.linalg.norm(np.asarray(a, np.float64) - r)) / max(float(np.linalg.norm(r)), floor)
         assert rel_l2(out[b], ref) < 1e-4
-        assert rel_l2(dqkv[b, :, :nh * hd], dq) < 1e-4
-        assert rel_l2(dqkv[b, :, nh * hd:(nh + nkv) * hd], dk) < 1e-4
+        assert err(dqkv[b, :, :nh * hd], dq) < 1e-4
+        assert err(dqkv[b, :, nh * hd:(nh + nkv) * hd], dk) < 1e-4
         assert rel_l2(dqkv[b, :, (nh + nkv) * hd:], dv) < 1e-4
     for a in (QKV, GO, O, LSE, D):
         a.free()
