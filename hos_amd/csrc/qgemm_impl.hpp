@@ -462,44 +462,52 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
     }
 }
 
-// Deterministic split-K reduction + the same epilogue. Workgroup = 16 rows × 256 columns; the fused
-// rank-r term reads U rows from LDS and this thread's column of L from registers.
+// Deterministic split-K reduction + the same epilogue. Workgroup = RED_ROWS rows × 256 columns, a thread per
+// column; rows go four at a time with all their partial loads issued together. The fused rank-r term (RK = 0,
+// 16 or 32: the rank rounded up, zero-padded) reads the U rows from LDS (one broadcast read per rank step) and
+// this thread's column of s·L from registers.
 constexpr int RED_ROWS = 16;
+template <int RK>
 __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ ws, int splits, int M, int N,
                                                      const float* __restrict__ rinv, GemmEpi epi) {
-  __shared__ float Us[RED_ROWS][33];
+  __shared__ float Us[RED_ROWS][RK > 0 ? RK : 1];
   const int r0 = blockIdx.y * RED_ROWS, col = blockIdx.x * 256 + threadIdx.x;
   const int rank = epi.rank;
-  float lc[32];
-  if (rank > 0) {
-    for (int e = threadIdx.x; e < RED_ROWS * rank; e += 256) {
-      int rr = e / rank, q = e % rank, row = r0 + rr;
-      Us[rr][q] = row < M ? epi.U[(long long)row * epi.ldu + q] : 0.0f;
+  float lc[RK > 0 ? RK : 1];
+  if constexpr (RK > 0) {
+    for (int e = threadIdx.x; e < RED_ROWS * RK; e += 256) {
+      const int rr = e / RK, q = e % RK, row = r0 + rr;
+      Us[rr][q] = (row < M && q < rank) ? epi.U[(long long)row * epi.ldu + q] : 0.0f;
     }
 #pragma unroll
-    for (int q = 0; q < 32; q++)
+    for (int q = 0; q < RK; q++)
       lc[q] = (q < rank && col < N) ? epi.L[(long long)q * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
     __syncthreads();
   }
   if (col >= N) return;
-  for (int rr = 0; rr < RED_ROWS; rr++) {
-    const int row = r0 + rr;
-    if (row >= M) break;
-    const long long i = (long long)row * N + col;
-    float v = 0.0f;
-    for (int z = 0; z < splits; z++) v += ws[(long long)z * M * N + i];
-    v *= rinv[row];
-    if (epi.bias) v += epi.bias[col];
-    if (rank > 0) {
-      float lv = 0.0f;
+  const long long MN = (long long)M * N;
 #pragma unroll
-      for (int q = 0; q < 32; q++)
-        if (q < rank) lv += Us[rr][q] * lc[q];
-      v += lv;
+  for (int rq = 0; rq < RED_ROWS; rq += 4) {
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int z = 0; z < splits; z++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[u] += ws[z * MN + (long long)min(r0 + rq + u, M - 1) * N + col];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int row = r0 + rq + u;
+      if (row >= M) return;
+      float x = v[u] * rinv[row];
+      if (epi.bias) x += epi.bias[col];
+      if constexpr (RK > 0) {
+        float lv = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RK; q++) lv += Us[rq + u][q] * lc[q];
+        x += lv;
+      }
+      const long long off = (long long)row * epi.ldo + col;
+      float* o = epi.out + off;
+      *o = epi.accumulate ? *o + x : (epi.resid ? epi.resid[off] + x : x);
     }
-    long long off = (long long)row * epi.ldo + col;
-    float* o = epi.out + off;
-    *o = epi.accumulate ? *o + v : (epi.resid ? epi.resid[off] + v : v);
   }
 }
 
@@ -604,7 +612,12 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   HOS_HIP_CHECK(hipGetLastError());
   if (splits > 1) {
     dim3 rg(ceil_div(Nout, 256), ceil_div(M, RED_ROWS));
-    splitk_reduce<<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
+    if (epi.rank <= 0)
+      splitk_reduce<0><<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
+    else if (epi.rank <= 16)
+      splitk_reduce<16><<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
+    else
+      splitk_reduce<32><<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
     HOS_HIP_CHECK(hipGetLastError());
   }
 }
