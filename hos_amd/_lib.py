@@ -40,6 +40,7 @@ SIGNATURES = {
     "hos_hip_qgemm_dx": (i32, [vp, u64, vp, sz, vp]),
     "hos_hip_qgemm_fwd_dev": (i32, [vp, u64, vp, sz, vp]),
     "hos_hip_qgemm_dx_dev": (i32, [vp, u64, vp, sz, vp]),
+    "hos_hip_qgemm_lora_dev": (i32, [vp, i32, u64, vp, sz, vp, sz, vp, sz, sz, i32, ctypes.c_float, vp]),
     "hos_hip_time_qgemm": (i32, [vp, i32, u64, vp, sz, vp, i32, ctypes.POINTER(ctypes.c_float)]),
     "hos_hip_timer_begin": (i32, [vp]),
     "hos_hip_timer_end": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),

@@ -132,7 +132,8 @@ H16 operand_h16(hos_ctx* c, long long K, size_t t) {
   return a;
 }
 
-void qgemm_dev(hos_ctx* c, bool dx, uint64_t key, const float* in_dev, size_t t, float* out_dev) {
+void qgemm_dev(hos_ctx* c, bool dx, uint64_t key, const float* in_dev, size_t t, float* out_dev,
+               const GemmEpi* lora = nullptr) {
   const QWeight& w = get_qw(c, key);
   long long K = dx ? w.rows : w.cols;
   long long N = dx ? w.cols : w.rows;
@@ -140,7 +141,9 @@ void qgemm_dev(hos_ctx* c, bool dx, uint64_t key, const float* in_dev, size_t t,
   H16 a = operand_h16(c, K, t);
   launch_to_h16(in_dev, K, (long long)t, K, a, c->stream);
   c->ws.ensure(hos_ctx::kWs);
-  GemmEpi epi{out_dev, N, nullptr, 0, nullptr};
+  GemmEpi epi = lora ? *lora : GemmEpi{};
+  epi.out = out_dev;
+  epi.ldo = N;
   if (dx)
     launch_qgemm_dx(w, a, K, (long long)t, epi, (float*)c->ws.p, c->ws.n, c->passes, c->stream);
   else
@@ -312,6 +315,24 @@ int hos_hip_qgemm_fwd_dev(hos_ctx* c, uint64_t key, const float* x, size_t t, fl
 }
 int hos_hip_qgemm_dx_dev(hos_ctx* c, uint64_t key, const float* dy, size_t t, float* dx) {
   return guard(c, [&] { qgemm_dev(c, true, key, dy, t, dx); });
+}
+
+int hos_hip_qgemm_lora_dev(hos_ctx* c, int which, uint64_t key, const float* in_dev, size_t t, const float* u_dev,
+                           size_t ldu, const float* l_dev, size_t slj, size_t sln, int rank, float scale,
+                           float* out_dev) {
+  return guard(c, [&] {
+    HOS_REQUIRE(which == 0 || which == 1, HOS_E_INVALID, "qgemm_lora: which must be 0 (forward) or 1 (dX)");
+    HOS_REQUIRE(rank >= 1 && u_dev && l_dev && ldu >= (size_t)rank, HOS_E_INVALID, "qgemm_lora: bad rank-r factors");
+    GemmEpi e{};
+    e.U = u_dev;
+    e.ldu = (long long)ldu;
+    e.L = l_dev;
+    e.slj = (long long)slj;
+    e.sln = (long long)sln;
+    e.rank = rank;
+    e.scale = scale;
+    qgemm_dev(c, which == 1, key, in_dev, t, out_dev, &e);
+  });
 }
 
 int hos_hip_time_qgemm(hos_ctx* c, int which, uint64_t key, const float* in_dev, size_t t, float* out_dev, int iters,

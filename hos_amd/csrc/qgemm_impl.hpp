@@ -221,11 +221,11 @@ struct Geo {
   static constexpr int ATILE = BM * AROW, BTILE = BROWS * BROW;
   static constexpr int BUF = NA * ATILE + NB * BTILE;   // halves per stage
   static constexpr int STAGES = BUF * 2 * 2 <= 65536 ? 2 : 1;
-  // rank capacity of the fused rank-r staging: the largest multiple of 16 up to 64 whose U [BM][RCAP] and
-  // L [RCAP][BN] fit in the LDS the main loop already uses, at least 32
+  // rank capacity of the fused rank-r staging: the largest multiple of 16 up to 64 whose bf16 hi/lo planes of
+  // U [BM][RCAP] and (s·L)ᵀ [BN][RCAP] fit in the LDS the main loop already uses, at least 32
   static constexpr int RFIT = STAGES * BUF / ((BM + BN) * 2) / 16 * 16;
   static constexpr int RCAP = RFIT >= 64 ? 64 : (RFIT >= 32 ? RFIT : 32);
-  static constexpr int EPI = (BM * RCAP + RCAP * BN) * 2;  // halves for the fused rank-r staging
+  static constexpr int EPI = (BM + BN) * RCAP * 2;  // halves for the fused rank-r staging
   static constexpr int SMEM = (STAGES * BUF > EPI) ? STAGES * BUF : EPI;
 };
 
@@ -413,23 +413,52 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
 
   // epilogue: D[i][j] of a 32×32 tile lives at lane j + 32·((i/4)&1), register (i&3) + 4·(i/8)
   const bool split = gridDim.z > 1;
-  // fused rank-r update: stage U [BM][r] and L [r][BN] in the (now free) LDS
-  constexpr int RC = G::RCAP;
-  float* Us = (float*)smem;
-  float* Ls = Us + BM * RC;
+  // Fused rank-r update s·U·L on bf16 MFMA, accumulated into acc before the row scale: U [BM][r] (each row
+  // divided by its power-of-two rinv, exact) and the transposed (s·L)ᵀ [BN][r] are staged in the (now free)
+  // LDS as bf16 hi/lo planes, zero-padded to a multiple of 16, and each 32×32 tile takes three products per
+  // 16 ranks (hi·hi + lo·hi + hi·lo: ~2^-16 relative to the rank-r term, fp32 range). A staged row is rpad
+  // bf16 long; its 16-byte chunks are XOR-swizzled by the row so that the 32 rows of one fragment read spread
+  // over the LDS banks.
   const int rank = split ? 0 : epi.rank;
+  const int rpad = (rank + 15) & ~15;
+  const int nch = rpad >> 3, swz = (nch & (nch - 1)) ? 1 : nch - 1;
+  auto sidx = [&](int row, int q) { return row * rpad + ((((q >> 3) ^ (row & swz))) << 3) + (q & 7); };
+  __bf16* Uh = (__bf16*)smem;
+  __bf16* Ul = Uh + BM * rpad;
+  __bf16* Lh = Ul + BM * rpad;
+  __bf16* Ll = Lh + BN * rpad;
   if (rank > 0) {
     // a tile never straddles a column segment (the launcher picks BN to divide the boundaries)
     const float* Ub = epi.U + (epi.ustep ? epi.ustep * ((n0 >= epi.ub0) + (n0 >= epi.ub1)) : 0);
-    for (int e = tid; e < BM * rank; e += G::NT) {
-      int rr = e / rank, jj = e % rank, row = m0 + rr;
-      Us[rr * RC + jj] = row < M ? Ub[(long long)row * epi.ldu + jj] : 0.0f;
+    for (int e = tid; e < BM * rpad; e += G::NT) {
+      const int rr = e / rpad, jj = e % rpad, row = m0 + rr;
+      const float x = (row < M && jj < rank) ? Ub[(long long)row * epi.ldu + jj] / rinv[row] : 0.0f;
+      const __bf16 h = (__bf16)x;
+      Uh[sidx(rr, jj)] = h;
+      Ul[sidx(rr, jj)] = (__bf16)(x - (float)h);
     }
-    for (int e = tid; e < rank * BN; e += G::NT) {
-      int jj = e / BN, cc = e % BN, col = n0 + cc;
-      Ls[jj * BN + cc] = col < Nout ? epi.L[(long long)jj * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
+    for (int e = tid; e < rpad * BN; e += G::NT) {
+      const int jj = e / BN, cc = e % BN, col = n0 + cc;
+      const float x =
+          (col < Nout && jj < rank) ? epi.L[(long long)jj * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
+      const __bf16 h = (__bf16)x;
+      Lh[sidx(cc, jj)] = h;
+      Ll[sidx(cc, jj)] = (__bf16)(x - (float)h);
     }
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < G::TM; i++)
+#pragma unroll
+      for (int j = 0; j < G::TN; j++) {
+        const int ra = wm * (BM / G::WGM) + 32 * i + (lane & 31);
+        const int rb = wn * (BN / 2) + 32 * j + (lane & 31);
+        for (int k0 = 0; k0 < rpad; k0 += 16) {
+          const int k = k0 + 8 * (lane >> 5);
+          const bf8 ah = *(const bf8*)(Uh + sidx(ra, k)), al = *(const bf8*)(Ul + sidx(ra, k));
+          const bf8 bh = *(const bf8*)(Lh + sidx(rb, k)), bl = *(const bf8*)(Ll + sidx(rb, k));
+          acc[i][j] = mma3_bf16(ah, al, bh, bl, acc[i][j]);
+        }
+      }
   }
 #pragma unroll
   for (int i = 0; i < G::TM; i++)
@@ -449,11 +478,6 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
         } else {
           v *= rinv[row];
           if (epi.bias) v += epi.bias[col];
-          if (rank > 0) {
-            float lv = 0.0f;
-            for (int q = 0; q < rank; q++) lv += Us[rr * RC + q] * Ls[q * BN + cc];
-            v += lv;
-          }
           long long off = (long long)row * epi.ldo + col;
           float* o = epi.out + off;
           *o = epi.accumulate ? *o + v : (epi.resid ? epi.resid[off] + v : v);

@@ -3,7 +3,7 @@ UndefinedBehaviorSanitizer: the CPU parser tests — including the reference's f
 (tests/fuzz_gguf.rs:64-88) and the capsule fuzz — run in a child python against the sanitized build of the
 library (`python -m hos_amd.build --sanitize`, host code instrumented, device code as usual). Any report
 aborts the child. Skipped when the sanitized build is absent (it takes minutes to build, so build() does not
-make it)."""
+make it) or older than a source of the library (rebuild it after a change)."""
 import os
 import subprocess
 import sys
@@ -17,6 +17,10 @@ def test_parsers_clean_under_asan_ubsan():
     from hos_amd import build as hb
     if not os.path.exists(hb.SAN_LIB):
         pytest.skip("sanitized library not built (python -m hos_amd.build --sanitize)")
+    csrc = os.path.join(ROOT, "hos_amd", "csrc")
+    srcs = [os.path.join(csrc, f) for f in os.listdir(csrc)] + [os.path.join(ROOT, "include", "hos_hip.h")]
+    if max(os.path.getmtime(f) for f in srcs) > os.path.getmtime(hb.SAN_LIB):
+        pytest.skip("sanitized library older than its sources (python -m hos_amd.build --sanitize)")
     rt = hb.asan_runtime()
     assert os.path.exists(rt), rt
     env = dict(os.environ, HOS_HIP_LIB=hb.SAN_LIB, LD_PRELOAD=rt,
