@@ -125,7 +125,7 @@ H16 operand_h16(hos_ctx* c, long long K, size_t t) {
   c->t2.ensure(t * K * 2);
   c->t3.ensure(t * 4 + 4);
   H16 a{(half_t*)c->t2.p, (float*)c->t3.p, nullptr};
-  if (c->passes == 2 || c->passes == 3) {
+  if (c->passes == 2 || c->passes == 3 || c->passes == 5) {
     c->t5.ensure(t * K * 2);
     a.lo = (half_t*)c->t5.p;
   }
@@ -424,7 +424,7 @@ size_t hos_hip_bytes_for(uint32_t type, size_t n) { return gguf_bytes_for(type, 
 
 int hos_hip_set_gemm_passes(hos_ctx* c, int passes) {
   return guard(c, [&] {
-    HOS_REQUIRE(passes >= 1 && passes <= 4, HOS_E_INVALID, "gemm precision mode must be 1, 2, 3 or 4");
+    HOS_REQUIRE(passes >= 1 && passes <= 5, HOS_E_INVALID, "gemm precision mode must be 1 to 5");
     c->passes = passes;
   });
 }

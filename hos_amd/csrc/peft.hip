@@ -25,6 +25,9 @@
 using namespace hos;
 
 namespace {
+// Precision modes that carry the activation as fp16 hi + lo (the operand's residual plane is needed).
+static inline bool alo_mode(int m) { return m == 2 || m == 3 || m == 5; }
+
 
 // LoRA targets in order: q k v o gate up down.
 enum { TQ, TK, TV, TO, TG, TU, TD, NT };
@@ -897,13 +900,15 @@ struct hos_peft {
     lscale = c.lora_alpha / (float)r;  // src/peft.rs:195
     Mmax = c.max_batch * c.max_seq;
     passes = c.gemm_passes == 0 ? 3 : c.gemm_passes;
-    HOS_REQUIRE(passes >= 1 && passes <= 4, HOS_E_INVALID, "peft: gemm_passes must be 0 (default), 1, 2, 3 or 4");
+    HOS_REQUIRE(passes >= 1 && passes <= 5, HOS_E_INVALID, "peft: gemm_passes must be 0 (default) or 1 to 5");
     // Default precision policy (measured against the f32 path, worst LoRA-gradient rel L2 at the
-    // SmolLM2-135M / Qwen2.5-0.5B configs): the per-layer GEMMs need both operands split (3 passes);
-    // the head's forward is fine in one pass (+2e-5) and its dX needs only the weight split (mode 4).
+    // SmolLM2-135M / Qwen2.5-0.5B configs): the per-layer GEMMs need both operands to ~22 bits — the forward
+    // as mode 5 (activation split, weight as its exact integer codes; mode 3 where the layout has none), the dX
+    // as mode 3; the head's forward is fine in one pass (+2e-5) and its dX needs only the weight split (mode 4).
     // An explicit gemm_passes applies to every GEMM.
     if (c.gemm_passes == 0) {
-      pf = pd = 3;
+      pf = 5;
+      pd = 3;
       phf = 1;
       phd = 4;
     } else {
@@ -1001,7 +1006,7 @@ struct hos_peft {
       const size_t P = M * K, xc = std::max<size_t>((size_t)d, 2 * (size_t)F);
       hx.data = alloc<half_t>(P * xc);
       hx.rinv = alloc<float>(P);
-      hx.lo = (pf == 2 || pf == 3 || pd == 2 || pd == 3) ? alloc<half_t>(P * xc) : nullptr;
+      hx.lo = (alo_mode(pf) || alo_mode(pd)) ? alloc<half_t>(P * xc) : nullptr;
       mlogits = alloc<float>(M * E);
       mdY = alloc<float>(P * d);
       mdH = alloc<float>(P * F);
@@ -1022,7 +1027,6 @@ struct hos_peft {
     size_t hcols = std::max<size_t>({(size_t)d, (size_t)W3, (size_t)qd, 2 * (size_t)F});
     hs.data = alloc<half_t>(M * hcols);
     hs.rinv = alloc<float>(M);
-    auto alo_mode = [](int m) { return m == 2 || m == 3; };
     const bool alo = alo_mode(pf) || alo_mode(pd) || alo_mode(phf);
     hs.lo = alo ? alloc<half_t>(M * hcols) : nullptr;
     logits = alloc<float>(M * V);
@@ -1183,6 +1187,7 @@ void check_ids(hos_peft* p, const int32_t* ids, int n) {
 }  // namespace
 
 namespace hos {
+
 
 // One (layer, target) factor pair of an arena buffer in the reference layout (A [in, r], B [r, out]
 // row-major); the device keeps A_tᵀ [r][in] inside its group's At block and B_t as columns of Bcat.

@@ -115,7 +115,7 @@ __global__ void __launch_bounds__(256) to_h16_reg_kernel(const float* __restrict
 void launch_any(bool dx, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws,
                 size_t ws_bytes, int passes, hipStream_t st) {
   if (M <= 0) return;
-  HOS_REQUIRE(passes >= 1 && passes <= 4, HOS_E_INVALID, "qgemm: precision mode must be 1, 2, 3 or 4");
+  HOS_REQUIRE(passes >= 1 && passes <= 5, HOS_E_INVALID, "qgemm: precision mode must be 1 to 5");
   switch (w.type) {
     case GGUF_Q8_0: qgemm_launch_q8(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
     case GGUF_Q4_K: qgemm_launch_q4k(dx, passes, w, a, lda, M, epi, ws, ws_bytes, st); break;
@@ -140,7 +140,7 @@ void launch_qgemm_dx(const QWeight& w, H16 a, long long lda, long long M, GemmEp
 }
 void launch_qgemm_grouped(bool dx, const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi, int passes,
                           hipStream_t st) {
-  HOS_REQUIRE(passes >= 1 && passes <= 4, HOS_E_INVALID, "qgemm: precision mode must be 1, 2, 3 or 4");
+  HOS_REQUIRE(passes >= 1 && passes <= 5, HOS_E_INVALID, "qgemm: precision mode must be 1 to 5");
   if (gs.max_tiles <= 0) return;
   switch (w.type) {
     case GGUF_Q8_0: qgemm_grouped_q8(dx, passes, w, gs, a, lda, epi, st); break;

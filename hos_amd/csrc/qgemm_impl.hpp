@@ -20,7 +20,12 @@
 //   NP = 2: A_hi·W + A_lo·W                       (activation carried to ~22 bits)
 //   NP = 3: A_hi·W_hi + A_lo·W_hi + A_hi·W_lo     (both operands to ~22 bits; dropped A_lo·W_lo ~2^-22)
 //   NP = 4: A·W_hi + A·W_lo                       (weight to ~22 bits, activation rounded once)
-// where W_hi = fp16(w), W_lo = fp16(w − W_hi) of the f32 dequantized w.
+//   NP = 5: Σ_b s_b·(A_hi·Q_b + A_lo·Q_b)         (forward, Q8_0 layout: the weight exact)
+// where W_hi = fp16(w), W_lo = fp16(w − W_hi) of the f32 dequantized w. In mode 5 the B operand is the integer
+// code q itself (|q| ≤ 128: exact in fp16), each 32-deep block of the contraction is accumulated on its own and
+// added into the output accumulator times its scale d (f32 fma, per output column): w = d·q exactly, so the
+// result carries only the activation's ~2^-22 and the fp32 accumulation — the precision of mode 3 from two
+// products instead of three.
 //
 // Work decomposition: 4 waves (2×2), or 8 (4×2) for 256-row tiles; workgroup tile BM×BN, wave tile 64×(BN/2) of
 // 32×32 MFMA tiles, LDS double-buffered when both stages fit in 64 KB, register prefetch of the next slab,
@@ -120,8 +125,9 @@ __device__ __forceinline__ void run_load(const QWeightView& w, long long row, in
 }
 
 // Dequantize a run and store it as E/8 h8 vectors at dst (hi) and dst + lo_off (lo, when SPLIT).
-template <uint32_t QT, int E, bool SPLIT>
+template <uint32_t QT, int E, bool SPLIT, bool CODES = false>
 __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, int lo_off) {
+  static_assert(!CODES || (QT == GGUF_Q8_0 && !SPLIT), "integer codes: Q8_0 layout, one plane");
 #pragma unroll
   for (int v = 0; v < E / 8; v++) {
     // (a run clamped past the last output column only feeds columns that are never stored)
@@ -144,6 +150,13 @@ __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, in
         __builtin_memcpy(&x1, &p1, 4);
         x0 -= bias;
         x1 -= bias;
+        if constexpr (CODES) {  // the codes themselves; the block scale is applied to the accumulator
+          hv[4 * wv] = x0[0];
+          hv[4 * wv + 1] = x0[1];
+          hv[4 * wv + 2] = x1[0];
+          hv[4 * wv + 3] = x1[1];
+          continue;
+        }
         const h2 h0 = x0 * d2, h1 = x1 * d2;
         hv[4 * wv] = h0[0];
         hv[4 * wv + 1] = h0[1];
@@ -217,7 +230,8 @@ struct Geo {
   static constexpr int BROW = DX ? BN + 32 : BK + 8;
   static constexpr int BROWS = DX ? BK : BN;            // B tile rows
   static constexpr int TPR = (DX ? BN : BK) / E;        // threads per B tile row
-  static constexpr int NA = (NP == 2 || NP == 3) ? 2 : 1, NB = NP >= 3 ? 2 : 1;
+  static constexpr int NA = (NP == 2 || NP == 3 || NP == 5) ? 2 : 1, NB = (NP == 3 || NP == 4) ? 2 : 1;
+  static constexpr int NSB = NP == 5 ? BK / 32 : 0;  // mode 5: 32-deep scale blocks per slab
   static constexpr int ATILE = BM * AROW, BTILE = BROWS * BROW;
   static constexpr int BUF = NA * ATILE + NB * BTILE;   // halves per stage
   static constexpr int STAGES = BUF * 2 * 2 <= 65536 ? 2 : 1;
@@ -254,7 +268,9 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   }
   static_assert(G::E == 8 || G::E == 16 || G::E == 32, "B run length");
   static_assert(BK % 32 == 0 || (BK == 32), "slab depth");
-  constexpr bool ALO = NP == 2 || NP == 3, BLO = NP >= 3;
+  constexpr bool ICODE = NP == 5;
+  static_assert(!ICODE || (!DX && QT == GGUF_Q8_0), "mode 5: forward, Q8_0 layout");
+  constexpr bool ALO = NP == 2 || NP == 3 || ICODE, BLO = NP == 3 || NP == 4;
   __shared__ __attribute__((aligned(16))) _Float16 smem[G::SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -273,8 +289,11 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   // A wave with fewer than four 32×32 tiles gets several accumulator sets: the passes and k-steps rotate
   // over them, so the MFMA pipe always has independent chains instead of one chain that waits for each
   // previous MFMA's result. They are summed in a fixed order before the epilogue.
-  constexpr int NACC = G::TM * G::TN >= 4 ? 1 : (G::TM * G::TN == 2 ? 2 : 4);
+  constexpr int NACC = (ICODE || G::TM * G::TN >= 4) ? 1 : (G::TM * G::TN == 2 ? 2 : 4);
   constexpr int NPASS = 1 + (ALO ? 1 : 0) + (BLO ? 1 : 0);
+  // mode 5: block accumulators, one set (the hi and lo products of all tiles interleave) or, with fewer than four
+  // tiles per wave, one set per product so that consecutive MFMAs never share an accumulator
+  constexpr int NBLK = G::TM * G::TN >= 4 ? 1 : 2;
   f16v accs[NACC][G::TM][G::TN];
 #pragma unroll
   for (int a = 0; a < NACC; a++)
@@ -291,7 +310,9 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   struct Regs {
     h8 a[G::A_H8], al[G::A_H8];
     Run<QT, G::E> b;
+    float sc[ICODE ? G::TN * G::NSB : 1];  // mode 5: d of this lane's output columns, per 32-block of the slab
   };
+  float scur[ICODE ? G::TN * G::NSB : 1];  // the scales of the slab in LDS
   Regs R0, R1;
   // this thread's B run: tile row br, first column bc
   const int br = tid / G::TPR, bc = G::E * (tid % G::TPR);
@@ -316,6 +337,15 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
       const long long row = n0 + br;  // W row = output column; run along the contraction
       run_load<QT, G::E>(w, row, c0 + bc, row < w.rows, R.b);
     }
+    if constexpr (ICODE) {
+#pragma unroll
+      for (int j = 0; j < G::TN; j++) {
+        const long long n = n0 + wn * (BN / 2) + 32 * j + (lane & 31);
+        const long long base = (n < w.rows ? n : 0) * (w.cols >> 5) + (c0 >> 5);
+#pragma unroll
+        for (int b = 0; b < G::NSB; b++) R.sc[j * G::NSB + b] = w.s[base + b];
+      }
+    }
   };
   auto store = [&](const Regs& R, _Float16* buf) {
 #pragma unroll
@@ -326,12 +356,19 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
       if constexpr (ALO) *(h8*)(buf + G::ATILE + row * G::AROW + 8 * cv) = R.al[v];
     }
     _Float16* bs = buf + G::NA * G::ATILE;
-    run_store<QT, G::E, BLO>(R.b, bs + br * G::BROW + bc, G::BTILE);
+    run_store<QT, G::E, BLO, ICODE>(R.b, bs + br * G::BROW + bc, G::BTILE);
+  };
+  auto take_scales = [&](const Regs& R) {
+    if constexpr (ICODE) {
+#pragma unroll
+      for (int i = 0; i < G::TN * G::NSB; i++) scur[i] = R.sc[i];
+    }
   };
 
   if (nslab > 0) {
     load(R0, cbeg);
     store(R0, smem);
+    take_scales(R0);
     load(R0, cbeg + min(1, nslab - 1) * BK);
   }
   __syncthreads();
@@ -342,6 +379,53 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
     load(R1, cbeg + min(s + 2, nslab - 1) * BK);  // past the end: a harmless re-read of the last slab
     const _Float16* as = smem + buf * G::BUF;
     const _Float16* bs = as + G::NA * G::ATILE;
+    if constexpr (ICODE) {
+#pragma unroll
+      for (int kb = 0; kb < BK; kb += 32) {
+        f16v blk[NBLK][G::TM][G::TN];
+#pragma unroll
+        for (int k2 = 0; k2 < 32; k2 += 16) {
+          h8 af[G::TM], afl[G::TM], bf[G::TN];
+          const int koff = kb + k2 + 8 * (lane >> 5);
+#pragma unroll
+          for (int i = 0; i < G::TM; i++) {
+            int ro = (wm * (BM / G::WGM) + 32 * i + (lane & 31)) * G::AROW + koff;
+            af[i] = *(const h8*)(as + ro);
+            afl[i] = *(const h8*)(as + G::ATILE + ro);
+          }
+#pragma unroll
+          for (int j = 0; j < G::TN; j++) {
+            int ro = (wn * (BN / 2) + 32 * j + (lane & 31)) * G::BROW + koff;
+            bf[j] = *(const h8*)(bs + ro);
+          }
+          const f16v z = {};
+#pragma unroll
+          for (int i = 0; i < G::TM; i++)
+#pragma unroll
+            for (int j = 0; j < G::TN; j++)
+              blk[0][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], k2 == 0 ? z : blk[0][i][j], 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < G::TM; i++)
+#pragma unroll
+            for (int j = 0; j < G::TN; j++) {
+              f16v& t = blk[NBLK - 1][i][j];
+              t = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], (NBLK == 2 && k2 == 0) ? z : t, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < G::TM; i++)
+#pragma unroll
+          for (int j = 0; j < G::TN; j++) {
+            const float sj = scur[j * G::NSB + kb / 32];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              float v = blk[0][i][j][r];
+              if constexpr (NBLK == 2) v += blk[1][i][j][r];
+              accs[0][i][j][r] = __builtin_fmaf(sj, v, accs[0][i][j][r]);
+            }
+          }
+      }
+    } else
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       h8 af[G::TM], afl[G::TM], bf[G::TN], bfl[G::TN];
@@ -398,6 +482,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
     if (more) {
       if constexpr (G::STAGES == 1) __syncthreads();  // everyone is done reading the single stage
       store(R0, smem + (G::STAGES == 2 ? (buf ^ 1) : 0) * G::BUF);
+      take_scales(R0);
     }
     R0 = R1;
     __syncthreads();
@@ -553,7 +638,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   const int C = DX ? (int)w.rows : (int)w.cols;
   HOS_REQUIRE(C % 32 == 0, HOS_E_INVALID, "qgemm: contraction length must be a multiple of 32");
   HOS_REQUIRE((lda % 8) == 0, HOS_E_INVALID, "qgemm: activation row stride must be a multiple of 8");
-  HOS_REQUIRE((NP != 2 && NP != 3) || a.lo != nullptr, HOS_E_INVALID,
+  HOS_REQUIRE((NP != 2 && NP != 3 && NP != 5) || a.lo != nullptr, HOS_E_INVALID,
               "qgemm: activation-split precision needs the operand residual");
   HOS_REQUIRE(epi.rank >= 0 && epi.rank <= 64, HOS_E_INVALID, "qgemm: fused rank-r update supports r <= 64");
   // Tile choice: the largest tile that still gives ~1.25 waves of workgroups over the 256 CUs; only when
@@ -654,7 +739,8 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
   const int Nout = DX ? (int)w.cols : (int)er;
   const int C = DX ? (int)er : (int)w.cols;
   HOS_REQUIRE(C % 32 == 0 && lda % 8 == 0, HOS_E_INVALID, "grouped qgemm: contraction must be a multiple of 32");
-  HOS_REQUIRE((NP != 2 && NP != 3) || a.lo != nullptr, HOS_E_INVALID, "grouped qgemm: needs the operand residual");
+  HOS_REQUIRE((NP != 2 && NP != 3 && NP != 5) || a.lo != nullptr, HOS_E_INVALID,
+              "grouped qgemm: needs the operand residual");
   HOS_REQUIRE(epi.rank == 0, HOS_E_INVALID, "grouped qgemm: no fused rank-r term");
   GroupKernelArgs gk;
   gk.tiles = gs.tiles;
@@ -673,11 +759,25 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
   HOS_HIP_CHECK(hipGetLastError());
 }
 
+// Mode 5 where the layout has integer codes and the direction allows it (forward, Q8_0 layout); elsewhere the
+// same precision class is mode 3.
+template <uint32_t QT, bool DX>
+void launch_exact(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
+                  hipStream_t st) {
+  if constexpr (!DX && QT == GGUF_Q8_0) launch_typed<QT, false, 5>(w, a, lda, M, epi, ws, ws_bytes, st);
+  else launch_typed<QT, DX, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+}
+template <uint32_t QT, bool DX>
+void launch_exact_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi, hipStream_t st) {
+  if constexpr (!DX && QT == GGUF_Q8_0) launch_typed_grouped<QT, false, 5>(w, gs, a, lda, epi, st);
+  else launch_typed_grouped<QT, DX, 3>(w, gs, a, lda, epi, st);
+}
+
 }  // namespace
 }  // namespace hos
 
 // Defines qgemm_launch_<NAME> and qgemm_grouped_<NAME> (declared in qgemm.hip) for one device weight layout:
-// every tile shape, both directions, precision modes 1-4. One translation unit per layout keeps builds parallel.
+// every tile shape, both directions, precision modes 1-5. One translation unit per layout keeps builds parallel.
 #define HOS_QGEMM_INSTANTIATE(NAME, QT)                                                                          \
   namespace hos {                                                                                                \
   void qgemm_launch_##NAME(bool dx, int passes, const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, \
@@ -686,12 +786,14 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
       if (passes == 1) launch_typed<QT, true, 1>(w, a, lda, M, epi, ws, ws_bytes, st);                           \
       else if (passes == 2) launch_typed<QT, true, 2>(w, a, lda, M, epi, ws, ws_bytes, st);                      \
       else if (passes == 3) launch_typed<QT, true, 3>(w, a, lda, M, epi, ws, ws_bytes, st);                      \
-      else launch_typed<QT, true, 4>(w, a, lda, M, epi, ws, ws_bytes, st);                                       \
+      else if (passes == 4) launch_typed<QT, true, 4>(w, a, lda, M, epi, ws, ws_bytes, st);                      \
+      else launch_exact<QT, true>(w, a, lda, M, epi, ws, ws_bytes, st);                                          \
     } else {                                                                                                     \
       if (passes == 1) launch_typed<QT, false, 1>(w, a, lda, M, epi, ws, ws_bytes, st);                          \
       else if (passes == 2) launch_typed<QT, false, 2>(w, a, lda, M, epi, ws, ws_bytes, st);                     \
       else if (passes == 3) launch_typed<QT, false, 3>(w, a, lda, M, epi, ws, ws_bytes, st);                     \
-      else launch_typed<QT, false, 4>(w, a, lda, M, epi, ws, ws_bytes, st);                                      \
+      else if (passes == 4) launch_typed<QT, false, 4>(w, a, lda, M, epi, ws, ws_bytes, st);                     \
+      else launch_exact<QT, false>(w, a, lda, M, epi, ws, ws_bytes, st);                                         \
     }                                                                                                            \
   }                                                                                                              \
   void qgemm_grouped_##NAME(bool dx, int passes, const QWeight& w, GroupSched gs, H16 a, long long lda,          \
@@ -700,12 +802,14 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
       if (passes == 1) launch_typed_grouped<QT, true, 1>(w, gs, a, lda, epi, st);                                \
       else if (passes == 2) launch_typed_grouped<QT, true, 2>(w, gs, a, lda, epi, st);                           \
       else if (passes == 3) launch_typed_grouped<QT, true, 3>(w, gs, a, lda, epi, st);                           \
-      else launch_typed_grouped<QT, true, 4>(w, gs, a, lda, epi, st);                                            \
+      else if (passes == 4) launch_typed_grouped<QT, true, 4>(w, gs, a, lda, epi, st);                           \
+      else launch_exact_grouped<QT, true>(w, gs, a, lda, epi, st);                                               \
     } else {                                                                                                     \
       if (passes == 1) launch_typed_grouped<QT, false, 1>(w, gs, a, lda, epi, st);                               \
       else if (passes == 2) launch_typed_grouped<QT, false, 2>(w, gs, a, lda, epi, st);                          \
       else if (passes == 3) launch_typed_grouped<QT, false, 3>(w, gs, a, lda, epi, st);                          \
-      else launch_typed_grouped<QT, false, 4>(w, gs, a, lda, epi, st);                                           \
+      else if (passes == 4) launch_typed_grouped<QT, false, 4>(w, gs, a, lda, epi, st);                          \
+      else launch_exact_grouped<QT, false>(w, gs, a, lda, epi, st);                                              \
     }                                                                                                            \
   }                                                                                                              \
   }

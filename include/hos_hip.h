@@ -114,7 +114,10 @@ int hos_hip_quantize_dev(hos_ctx* ctx, const float* x_dev, size_t n, uint32_t gg
 int hos_hip_randn_dev(hos_ctx* ctx, float* out_dev, size_t n, uint64_t seed, float stddev);
 /* Precision of this context's qGEMMs: 1 = single fp16 pass (both operands rounded to 11 bits),
  * 2 = activation carried as fp16 hi + lo (2 MFMA passes), 3 = weight split too (3 passes),
- * 4 = weight carried as fp16 hi + lo, activation rounded once (2 passes). Default 1.
+ * 4 = weight carried as fp16 hi + lo, activation rounded once (2 passes), 5 = the precision of 3 from two
+ * passes where the weight layout has integer codes and the direction allows it (forward GEMMs on Q8_0, Q4_0
+ * and Q5_0 weights: activation hi + lo against the exact codes, block scales applied in f32), else mode 3.
+ * Default 1.
  * (The reference has no counterpart: its GPU GEMMs are f32, src/metal_be.rs:1095-1142.) */
 int hos_hip_set_gemm_passes(hos_ctx* ctx, int passes);
 /* bytes_for (src/gguf.rs:548-561); 0 for an unsupported type. */
@@ -200,7 +203,7 @@ typedef struct {
   uint32_t lora_targets;
   int max_batch, max_seq; /* sizes the device-resident activation arena */
   int gemm_passes;        /* qGEMM precision mode for every GEMM, as hos_hip_set_gemm_passes; 0 = default
-                           * policy: layer GEMMs 3, head forward 1, head dX 4 */
+                           * policy: layer forward 5, layer dX 3, head forward 1, head dX 4 */
   /* Mixture-of-experts FFN (src/model.rs:642-643; OLMoE): n_experts stacked SwiGLU experts
    * (blk.N.ffn_{gate,up,down}_exps.weight) behind an f32 router (blk.N.ffn_gate_inp.weight), top
    * n_experts_used by softmax probability, raw probabilities as weights (src/forward.rs:542-572).
