@@ -759,18 +759,26 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
   HOS_HIP_CHECK(hipGetLastError());
 }
 
-// Mode 5 where the layout has integer codes and the direction allows it (forward, Q8_0 layout); elsewhere the
-// same precision class is mode 3.
+// Precision of mode 3, by the faster kernel for the launch: the integer-code kernel (mode 5) where the layout has
+// codes and the direction allows it (forward, Q8_0 layout) and the launch is large — its extra block
+// accumulators cost occupancy (2 waves per SIMD instead of 3 on 128×128 tiles), which the saved third of the MFMA
+// work repays only from about 64 GFLOP per launch on (measured on the MI355X, M 2048: N 8192 × K 2048 −14%,
+// N 2048 × K 8192 −15%, 4096³ −15%; N 9728 × K 896 +5%, 2048³ +8%) — else mode 3. Grouped (mixture-of-experts)
+// launches are per-expert sized and stay mode 3.
 template <uint32_t QT, bool DX>
 void launch_exact(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
                   hipStream_t st) {
-  if constexpr (!DX && QT == GGUF_Q8_0) launch_typed<QT, false, 5>(w, a, lda, M, epi, ws, ws_bytes, st);
-  else launch_typed<QT, DX, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
+  if constexpr (!DX && QT == GGUF_Q8_0) {
+    if (2.0 * (double)M * (double)w.rows * (double)w.cols >= 6.4e10) {
+      launch_typed<QT, false, 5>(w, a, lda, M, epi, ws, ws_bytes, st);
+      return;
+    }
+  }
+  launch_typed<QT, DX, 3>(w, a, lda, M, epi, ws, ws_bytes, st);
 }
 template <uint32_t QT, bool DX>
 void launch_exact_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda, GemmEpi epi, hipStream_t st) {
-  if constexpr (!DX && QT == GGUF_Q8_0) launch_typed_grouped<QT, false, 5>(w, gs, a, lda, epi, st);
-  else launch_typed_grouped<QT, DX, 3>(w, gs, a, lda, epi, st);
+  launch_typed_grouped<QT, DX, 3>(w, gs, a, lda, epi, st);
 }
 
 }  // namespace

@@ -114,9 +114,9 @@ int hos_hip_quantize_dev(hos_ctx* ctx, const float* x_dev, size_t n, uint32_t gg
 int hos_hip_randn_dev(hos_ctx* ctx, float* out_dev, size_t n, uint64_t seed, float stddev);
 /* Precision of this context's qGEMMs: 1 = single fp16 pass (both operands rounded to 11 bits),
  * 2 = activation carried as fp16 hi + lo (2 MFMA passes), 3 = weight split too (3 passes),
- * 4 = weight carried as fp16 hi + lo, activation rounded once (2 passes), 5 = the precision of 3 from two
- * passes where the weight layout has integer codes and the direction allows it (forward GEMMs on Q8_0, Q4_0
- * and Q5_0 weights: activation hi + lo against the exact codes, block scales applied in f32), else mode 3.
+ * 4 = weight carried as fp16 hi + lo, activation rounded once (2 passes), 5 = the precision of 3 by the faster
+ * kernel for the launch: two passes against the exact integer codes (block scales applied in f32) for large
+ * forward GEMMs on Q8_0, Q4_0 and Q5_0 weights, else mode 3.
  * Default 1.
  * (The reference has no counterpart: its GPU GEMMs are f32, src/metal_be.rs:1095-1142.) */
 int hos_hip_set_gemm_passes(hos_ctx* ctx, int passes);

@@ -106,3 +106,29 @@ def test_lora_r16_gradient_4096(setup):
     assert rel_l2(DX.get()[rows], dxl) < 1e-5
     for a in (X, DY, AA, BB, Y, DX, U, DA, DB):
         a.free()
+
+
+def test_exact_mode_large_q8_0_forward():
+    """Precision mode 5 at a size where the launcher picks the integer-code kernel (forward, Q8_0, >= 64 GFLOP
+    per launch: here 4096³): activation hi + lo against the exact codes, the 32-block scales applied in f32 —
+    the mode-3 bar against the oracle's f32 matmul on the bit-exact dequantized weight (src/gguf.rs:354-367,
+    src/tensor.rs:307-327), on the same row sample and column-sum identity as the Q4_K checks above."""
+    from hos_amd import Gpu
+    print("exact-mode forward 4096^3 Q8_0 passes=5", flush=True)
+    g = Gpu(0)
+    rng = np.random.default_rng(8)
+    w = rng.standard_normal((N, N), dtype=np.float32) * np.float32(0.02)
+    raw = o.quantize(w, 8)
+    g.upload_quant(0xC5, raw, 8, N, N)
+    wd = o.dequant(raw, 8, N * N).reshape(N, N)
+    x = rng.standard_normal((N, N), dtype=np.float32)
+    rows = np.concatenate([np.arange(t, t + 256, 16) + (t // 256) % 16 for t in range(0, N, 256)])
+    g.set_gemm_passes(5)
+    y = g.qgemm_fwd(0xC5, x, N)
+    g.set_gemm_passes(1)
+    g.evict(0xC5)
+    g.close()
+    ref, _, _ = o.op_matmul(x[rows], wd.T.copy())
+    assert rel_l2(y[rows], ref) < TOL[3]
+    colsum = x.astype(np.float64).sum(0) @ wd.T.astype(np.float64)
+    assert rel_l2(y.astype(np.float64).sum(0), colsum) < 1e-5
