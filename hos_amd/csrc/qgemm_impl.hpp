@@ -504,7 +504,9 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
   // 16 ranks (hi·hi + lo·hi + hi·lo: ~2^-16 relative to the rank-r term, fp32 range). A staged row is rpad
   // bf16 long; its 16-byte chunks are XOR-swizzled by the row so that the 32 rows of one fragment read spread
   // over the LDS banks.
-  const int rank = split ? 0 : epi.rank;
+  // (split contraction: the first split's workgroups carry the rank-r term in their partial; U is pre-divided by
+  // the row's power-of-two rinv, so the reduction's (Σ partials)·rinv is exactly the unsplit result's form)
+  const int rank = (split && blockIdx.z != 0) ? 0 : epi.rank;
   const int rpad = (rank + 15) & ~15;
   const int nch = rpad >> 3, swz = (nch & (nch - 1)) ? 1 : nch - 1;
   auto sidx = [&](int row, int q) { return row * rpad + ((((q >> 3) ^ (row & swz))) << 3) + (q & 7); };
@@ -571,28 +573,59 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
     }
 }
 
-// Deterministic split-K reduction + the same epilogue. Workgroup = RED_ROWS rows × 256 columns, a thread per
-// column; rows go four at a time with all their partial loads issued together. The fused rank-r term (RK = 0,
-// 16 or 32: the rank rounded up, zero-padded) reads the U rows from LDS (one broadcast read per rank step) and
-// this thread's column of s·L from registers.
+// Deterministic split-K reduction + the same epilogue (the rank-r term is already in the first split's partial).
+// Workgroup = RED_ROWS rows × 1024 columns, a thread per 4 columns (16-byte loads); rows go four at a time with all
+// their partial loads issued together; partials are summed in split order.
 constexpr int RED_ROWS = 16;
-template <int RK>
-__global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ ws, int splits, int M, int N,
-                                                     const float* __restrict__ rinv, GemmEpi epi) {
-  __shared__ float Us[RED_ROWS][RK > 0 ? RK : 1];
-  const int r0 = blockIdx.y * RED_ROWS, col = blockIdx.x * 256 + threadIdx.x;
-  const int rank = epi.rank;
-  float lc[RK > 0 ? RK : 1];
-  if constexpr (RK > 0) {
-    for (int e = threadIdx.x; e < RED_ROWS * RK; e += 256) {
-      const int rr = e / RK, q = e % RK, row = r0 + rr;
-      Us[rr][q] = (row < M && q < rank) ? epi.U[(long long)row * epi.ldu + q] : 0.0f;
-    }
+__global__ void __launch_bounds__(256) splitk_reduce4(const float* __restrict__ ws, int splits, int M, int N,
+                                                      const float* __restrict__ rinv, GemmEpi epi) {
+  const int r0 = blockIdx.y * RED_ROWS, col = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (col >= N) return;
+  const long long MN = (long long)M * N;
+  const float4 bias = epi.bias ? *(const float4*)(epi.bias + col) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int q = 0; q < RK; q++)
-      lc[q] = (q < rank && col < N) ? epi.L[(long long)q * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
-    __syncthreads();
+  for (int rq = 0; rq < RED_ROWS; rq += 4) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < splits; z++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const float4 p = *(const float4*)(ws + z * MN + (long long)min(r0 + rq + u, M - 1) * N + col);
+        v[u].x += p.x;
+        v[u].y += p.y;
+        v[u].z += p.z;
+        v[u].w += p.w;
+      }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int row = r0 + rq + u;
+      if (row >= M) return;
+      const float ri = rinv[row];
+      float4 x = make_float4(v[u].x * ri, v[u].y * ri, v[u].z * ri, v[u].w * ri);
+      if (epi.bias) {
+        x.x += bias.x;
+        x.y += bias.y;
+        x.z += bias.z;
+        x.w += bias.w;
+      }
+      const long long off = (long long)row * epi.ldo + col;
+      float4* o = (float4*)(epi.out + off);
+      if (epi.accumulate) {
+        const float4 a = *o;
+        x = make_float4(a.x + x.x, a.y + x.y, a.z + x.z, a.w + x.w);
+      } else if (epi.resid) {
+        const float4 a = *(const float4*)(epi.resid + off);
+        x = make_float4(a.x + x.x, a.y + x.y, a.z + x.z, a.w + x.w);
+      }
+      *o = x;
+    }
   }
+}
+// The same for shapes the 16-byte form does not fit (a thread per column).
+__global__ void __launch_bounds__(256) splitk_reduce1(const float* __restrict__ ws, int splits, int M, int N,
+                                                      const float* __restrict__ rinv, GemmEpi epi) {
+  const int r0 = blockIdx.y * RED_ROWS, col = blockIdx.x * 256 + threadIdx.x;
   if (col >= N) return;
   const long long MN = (long long)M * N;
 #pragma unroll
@@ -607,17 +640,25 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ w
       if (row >= M) return;
       float x = v[u] * rinv[row];
       if (epi.bias) x += epi.bias[col];
-      if constexpr (RK > 0) {
-        float lv = 0.0f;
-#pragma unroll
-        for (int q = 0; q < RK; q++) lv += Us[rq + u][q] * lc[q];
-        x += lv;
-      }
       const long long off = (long long)row * epi.ldo + col;
       float* o = epi.out + off;
       *o = epi.accumulate ? *o + x : (epi.resid ? epi.resid[off] + x : x);
     }
   }
+}
+void launch_splitk_reduce(const float* ws, int splits, long long M, int N, const float* rinv, const GemmEpi& epi,
+                          hipStream_t st) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool v4 = N % 4 == 0 && epi.ldo % 4 == 0 && al16(ws) && al16(epi.out) && (!epi.bias || al16(epi.bias)) &&
+                  (!epi.resid || al16(epi.resid));
+  if (v4) {
+    dim3 rg(ceil_div(N, 1024), ceil_div(M, RED_ROWS));
+    splitk_reduce4<<<rg, 256, 0, st>>>(ws, splits, (int)M, N, rinv, epi);
+  } else {
+    dim3 rg(ceil_div(N, 256), ceil_div(M, RED_ROWS));
+    splitk_reduce1<<<rg, 256, 0, st>>>(ws, splits, (int)M, N, rinv, epi);
+  }
+  HOS_HIP_CHECK(hipGetLastError());
 }
 
 template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
@@ -678,8 +719,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bn = 128;
     bk = 32;
   }
-  // A fused rank above 32 (stacked q|k|v dX): 64×64 tiles, whose LDS holds the rank-64 staging, and no split
-  // (the split-K reduction stages at most 32).
+  // A fused rank above 32 (stacked q|k|v dX): 64×64 tiles, whose LDS holds the rank-64 staging, and no split.
   if (epi.rank > 32) {
     bm = 64;
     bn = 64;
@@ -719,16 +759,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   else throw Error(HOS_E_INVALID, "qgemm: no kernel for the chosen tile");
 #undef HOS_QG
   HOS_HIP_CHECK(hipGetLastError());
-  if (splits > 1) {
-    dim3 rg(ceil_div(Nout, 256), ceil_div(M, RED_ROWS));
-    if (epi.rank <= 0)
-      splitk_reduce<0><<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
-    else if (epi.rank <= 16)
-      splitk_reduce<16><<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
-    else
-      splitk_reduce<32><<<rg, 256, 0, st>>>(ws, splits, (int)M, Nout, a.rinv, epi);
-    HOS_HIP_CHECK(hipGetLastError());
-  }
+  if (splits > 1) launch_splitk_reduce(ws, splits, M, Nout, a.rinv, epi, st);
 }
 
 // Grouped launch (mixture-of-experts): W = n_experts stacked blocks, 128×128 tiles, no split.

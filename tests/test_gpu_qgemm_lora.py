@@ -9,8 +9,8 @@ term); the test makes it as large as the base term, so a dropped or misplaced ra
 
 Cases: ragged row counts (not a multiple of any tile), an output width that is not a multiple of the tile
 (forward), ranks 16 / 20 (zero-padded to 32) / 48 / 64 (the stacked q|k|v dX), L read through both stride
-orders (B [r, N] rows, A [N, r] transposed), a narrow output with a long contraction (the split-K reduction
-applies the term instead of the tile epilogue), rows whose magnitudes span 1e-20 .. 1e6 (the activation row
+orders (B [r, N] rows, A [N, r] transposed), a narrow output with a long contraction (split over the contraction:
+the first split's workgroups carry the term in their partial), rows whose magnitudes span 1e-20 .. 1e6 (the activation row
 scale the term is divided by before it joins the accumulator), and 1 and 3 precision passes.
 """
 import numpy as np
