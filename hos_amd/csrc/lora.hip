@@ -21,6 +21,18 @@
 namespace hos {
 namespace {
 
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+// Four consecutive values of an activation row: f32, or the fp16 operand's hi + lo (exact in f32; the row's rinv is
+// applied by the caller).
+__device__ __forceinline__ float4 load4(const float* xf, const HIn& xh, long long off) {
+  if (xh.hi) {
+    const h4v a = *reinterpret_cast<const h4v*>(xh.hi + off), b = *reinterpret_cast<const h4v*>(xh.lo + off);
+    return make_float4((float)a.x + (float)b.x, (float)a.y + (float)b.y, (float)a.z + (float)b.z,
+                       (float)a.w + (float)b.w);
+  }
+  return *reinterpret_cast<const float4*>(xf + off);
+}
+
 __device__ __forceinline__ f4v mfma16(float a, float b, f4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -90,7 +102,7 @@ template <int NJ, int RT = 2>
 __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk, float alpha,
                                                         const float* __restrict__ X, long long ldx,
                                                         const float* __restrict__ Bt, long long ldb, RowsSeg sg,
-                                                        float* __restrict__ C, long long ldc, float* part) {
+                                                        float* __restrict__ C, long long ldc, float* part, HIn xh) {
   constexpr int NC = NJ * 16, E = 16 * RT * NC;
   __shared__ float red[2 * E];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
@@ -114,13 +126,13 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
       khi[jt] = 0;
     }
   }
-  const float* xr[RT];
+  long long xr[RT];  // row offsets (elements)
   bool rv[RT];
 #pragma unroll
   for (int t = 0; t < RT; t++) {
     const int row = m0 + 16 * t + p;
     rv[t] = row < M;
-    xr[t] = X + (long long)(rv[t] ? row : 0) * ldx;
+    xr[t] = (long long)(rv[t] ? row : 0) * ldx;
   }
 
   f4v acc[RT][NJ];
@@ -141,7 +153,7 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
       const bool kin = kk < ke;
 #pragma unroll
       for (int t = 0; t < RT; t++)
-        xa[u][t] = (rv[t] && kin) ? *reinterpret_cast<const float4*>(xr[t] + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+        xa[u][t] = (rv[t] && kin) ? load4(X, xh, xr[t] + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int jt = 0; jt < NJ; jt++)
         bv[u][jt] = (kin && kk >= klo[jt] && kk < khi[jt]) ? *reinterpret_cast<const float4*>(bp[jt] + kk)
@@ -161,6 +173,16 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
         }
   }
 
+  if (xh.hi)  // the operand's row scale: element i of tile t is row m0 + 16t + 4q + i
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = m0 + 16 * t + 4 * q + i;
+        const float ri = row < M ? xh.rinv[row] : 0.0f;
+#pragma unroll
+        for (int jt = 0; jt < NJ; jt++) acc[t][jt][i] *= ri;
+      }
   // flatten: element (row 16t+4q+i, col 16jt+p) of the 32×NC block
   float v[RT * NJ * 4];
 #pragma unroll
@@ -188,7 +210,7 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
                                                                            const float* __restrict__ X, long long ldx,
                                                                            const float* __restrict__ Bt, long long ldb,
                                                                            RowsSeg sg, float* __restrict__ C,
-                                                                           long long ldc) {
+                                                                           long long ldc, HIn xh) {
   constexpr int NW = ROWS_WIDE_NW, NC = NJ * 16, E = 16 * NC, U = 2;
   __shared__ float red[NW * E];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
@@ -211,7 +233,7 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
   }
   const int row = m0 + p;
   const bool rv = row < M;
-  const float* xr = X + (long long)(rv ? row : 0) * ldx;
+  const long long xr = (long long)(rv ? row : 0) * ldx;
   f4v acc[NJ];
 #pragma unroll
   for (int jt = 0; jt < NJ; jt++) acc[jt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -222,7 +244,7 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
     for (int u = 0; u < U; u++) {
       const int kk = k0 + 16 * NW * u + 4 * q;
       const bool kin = kk < K;
-      xa[u] = (rv && kin) ? *reinterpret_cast<const float4*>(xr + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      xa[u] = (rv && kin) ? load4(X, xh, xr + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int jt = 0; jt < NJ; jt++)
         bv[u][jt] = (kin && kk >= klo[jt] && kk < khi[jt]) ? *reinterpret_cast<const float4*>(bp[jt] + kk)
@@ -239,6 +261,14 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
           acc[jt] = mfma16(xa[u].w, bv[u][jt].w, acc[jt]);
         }
   }
+  if (xh.hi)  // the operand's row scale: element i is row m0 + 4q + i
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r2 = m0 + 4 * q + i;
+      const float ri = r2 < M ? xh.rinv[r2] : 0.0f;
+#pragma unroll
+      for (int jt = 0; jt < NJ; jt++) acc[jt][i] *= ri;
+    }
   // element (row 4q+i, col 16jt+p) of the 16×NC block
 #pragma unroll
   for (int jt = 0; jt < NJ; jt++)
@@ -269,7 +299,8 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
   const int c0 = (bx - sg.blk0[t]) * 64, len = sg.len[t];
   const int mb = blockIdx.y * mchunk, me = min(M, mb + mchunk);
   const bool cv = c0 + 4 * p < len;
-  const float* gcol = jb.Gm + sg.gbeg[t] + c0 + 4 * p;
+  const long long gcol = sg.gbeg[t] + c0 + 4 * p;
+  const bool gh = jb.gh.hi != nullptr;
   const float* scol = jb.Sm + sg.soff[t];
   const long long lds = jb.lds, ldg = jb.ldg;
   const int ns = jb.ns;
@@ -290,11 +321,13 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
     for (int u = 0; u < U; u++) {
       const int m = m40 + 16 * u + q;
       const bool mv = m < me;
-      g[u] = (mv && cv) ? *reinterpret_cast<const float4*>(gcol + (long long)m * ldg) : make_float4(0.f, 0.f, 0.f, 0.f);
+      g[u] = (mv && cv) ? load4(jb.Gm, jb.gh, gcol + (long long)m * ldg) : make_float4(0.f, 0.f, 0.f, 0.f);
+      // G given as the fp16 operand: its row scale joins S (Σ_m S[m,j]·rinv[m]·(hi+lo)[m,c])
+      const float ri = (gh && mv) ? jb.gh.rinv[m] : 1.0f;
 #pragma unroll
       for (int js = 0; js < NS; js++) {
         const int j = js * 16 + p;
-        s[u][js] = (mv && j < ns) ? scol[(long long)m * lds + j] : 0.0f;
+        s[u][js] = (mv && j < ns) ? scol[(long long)m * lds + j] * ri : 0.0f;
       }
     }
 #pragma unroll
@@ -422,11 +455,13 @@ size_t lora_rows_ws_bytes(long long M, long long K, int n) {
 
 void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
                       long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
-                      hipStream_t st) {
+                      hipStream_t st, HIn xh) {
   const int n = sg.nt * sg.r;
   if (M <= 0 || n <= 0) return;
   HOS_REQUIRE(n <= 96 && sg.nt >= 1 && sg.nt <= 4, HOS_E_INVALID, "lora_rows: n = nt·r must be <= 96");
-  HOS_REQUIRE(K % 4 == 0 && ldx % 4 == 0 && ldb % 4 == 0 && ((uintptr_t)X & 15) == 0 && ((uintptr_t)Bt & 15) == 0,
+  HOS_REQUIRE(K % 4 == 0 && ldx % 4 == 0 && ldb % 4 == 0 && ((uintptr_t)Bt & 15) == 0 &&
+                  (xh.hi ? (((uintptr_t)xh.hi & 7) == 0 && ((uintptr_t)xh.lo & 7) == 0 && xh.rinv)
+                         : ((uintptr_t)X & 15) == 0),
               HOS_E_INVALID, "lora_rows: K, strides and pointers must be 16-byte aligned");
   for (int t = 0; t < sg.nt; t++)
     HOS_REQUIRE(sg.kbeg[t] % 4 == 0 && sg.kend[t] % 4 == 0 && sg.boff[t] % 4 == 0 && sg.kbeg[t] >= 0 &&
@@ -435,7 +470,7 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
   if (K <= ROWS_WIDE_KMAX && n <= 96) {
     // one 16-column tile per workgroup (grid.y = tiles): 128-row-block grids alone leave half the CUs idle
     const dim3 gw((unsigned)ceil_div_i(M, 16), (unsigned)((n + 15) / 16));
-    lora_rows_wide_kernel<1><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc);
+    lora_rows_wide_kernel<1><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc, xh);
     HOS_HIP_CHECK(hipGetLastError());
     return;
   }
@@ -448,7 +483,7 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
 #define ROWS(NJV)                                                                                         \
   case NJV:                                                                                               \
     lora_rows_kernel<NJV><<<grid, 256, 0, st>>>((int)M, (int)K, kchunk, alpha, X, ldx, Bt, ldb, sg, C, ldc, \
-                                                ws);                                             \
+                                                ws, xh);                                         \
     break;
   switch (NJ) {
     ROWS(1) ROWS(2) ROWS(3) ROWS(4) ROWS(5) ROWS(6)
@@ -469,7 +504,9 @@ ColsJobDev prepare(const ColsJob& j, int bx0) {
   ColsJobDev d{};
   HOS_REQUIRE(j.ns > 0 && j.ns <= 96 && j.sg.nseg > 0 && j.sg.nseg <= 4, HOS_E_INVALID,
               "lora_cols: ns must be in 1..96, 1 to 4 segments");
-  HOS_REQUIRE(j.ldg % 4 == 0 && ((uintptr_t)j.Gm & 15) == 0, HOS_E_INVALID, "lora_cols: G must be 16-byte aligned");
+  HOS_REQUIRE(j.ldg % 4 == 0 && (j.gh.hi ? (((uintptr_t)j.gh.hi & 7) == 0 && ((uintptr_t)j.gh.lo & 7) == 0 && j.gh.rinv)
+                                          : ((uintptr_t)j.Gm & 15) == 0),
+              HOS_E_INVALID, "lora_cols: G must be 16-byte aligned");
   d.Sm = j.Sm;
   d.Gm = j.Gm;
   d.C = j.C;
@@ -481,6 +518,7 @@ ColsJobDev prepare(const ColsJob& j, int bx0) {
   d.ns = j.ns;
   d.nsr = (j.ns + 15) / 16 * 16;
   d.sg = j.sg;
+  d.gh = j.gh;
   int gx = 0;
   for (int t = 0; t < j.sg.nseg; t++) {
     HOS_REQUIRE(j.sg.gbeg[t] % 4 == 0 && j.sg.len[t] % 4 == 0 && j.sg.len[t] > 0, HOS_E_INVALID,

@@ -6,6 +6,14 @@
 
 namespace hos {
 
+// An activation given as the fp16 GEMM operand instead of f32: X[m, k] = (hi[m, k] + lo[m, k])·rinv[m] (hi + lo is
+// exact in f32 and rinv is a power of two, so this is the operand's ~22-bit value). hi == nullptr: not given.
+struct HIn {
+  const _Float16* hi = nullptr;
+  const _Float16* lo = nullptr;
+  const float* rinv = nullptr;
+};
+
 // Output columns of the rows kernel come in nt slots of r columns (one per adapter target). Slot t
 // contracts over X columns [kbeg[t], kend[t]) against Bt[boff[t] + jj·ldb + (k − kbeg[t])], jj < r.
 struct RowsSeg {
@@ -13,10 +21,11 @@ struct RowsSeg {
   int kbeg[4] = {0, 0, 0, 0}, kend[4] = {0, 0, 0, 0};
   long long boff[4] = {0, 0, 0, 0};
 };
-// C[m, j] = α·Σ_k X[m, k]·B(j, k) for m < M, j < nt·r. X rows 16-byte aligned, K % 4 == 0.
+// C[m, j] = α·Σ_k X[m, k]·B(j, k) for m < M, j < nt·r. X rows 16-byte aligned, K % 4 == 0. xh.hi set: X is
+// that operand (row stride ldx, 8-byte aligned rows) and the f32 pointer is not read.
 void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
                       long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
-                      hipStream_t st);
+                      hipStream_t st, HIn xh = HIn{});
 
 // Column segments of the cols kernel: segment t covers G columns [gbeg, gbeg + len), uses S columns
 // starting at soff and writes output columns starting at ocol. blk0 is filled in by the launcher.
@@ -41,6 +50,7 @@ struct ColsJob {
   ColsSeg sg;
   float* C = nullptr;
   long long scj = 0, scc = 0;
+  HIn gh;  // gh.hi set: G is that operand (row stride ldg) and Gm is not read
 };
 // Kernel-side job: the above with its block range and partial-sum region.
 struct ColsJobDev {
@@ -52,6 +62,7 @@ struct ColsJobDev {
   int ns, nsr, gx, bx0;
   int S;  // splits of M the partials were written with
   ColsSeg sg;
+  HIn gh;
 };
 // Deferred reductions: cols launches given a batch write their partials into the batch's buffer and leave the
 // reduction to one launch_lora_cols_flush for all of them (up to 8 jobs; a job that does not fit is reduced

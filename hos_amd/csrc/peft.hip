@@ -265,9 +265,9 @@ struct hos_peft {
   int ycol(int t) const { return t == TK ? qd : (t == TV ? qd + kvd : (t == TU ? F : 0)); }
 
   void lora_rows(const char* cls, long long M, long long K, float alpha, const float* X, long long ldx,
-                 const float* Bt, long long ldb, const RowsSeg& sg, float* C, long long ldc) {
+                 const float* Bt, long long ldb, const RowsSeg& sg, float* C, long long ldc, HIn xh = HIn{}) {
     Scope s(this, cls, 2.0 * M * K * sg.nt * sg.r, 4.0 * (M * K + (double)M * sg.nt * sg.r));
-    launch_lora_rows(M, K, alpha, X, ldx, Bt, ldb, sg, C, ldc, ws, ws_bytes, st);
+    launch_lora_rows(M, K, alpha, X, ldx, Bt, ldb, sg, C, ldc, ws, ws_bytes, st, xh);
   }
   void lora_cols(const char* cls, long long M, int ns, float alpha, const float* Sm, long long lds, const float* Gm,
                  long long ldg, const ColsSeg& sg, float* C, long long scj, long long scc) {
@@ -395,7 +395,8 @@ struct hos_peft {
   // From dy, the gradient of the group's fused projection output (row stride ldy, target t at column
   // ycol(t)): du_t = s·dy_t·B_tᵀ for every adapted t (one launch). dB_t = s·u_tᵀ·dy_t is queued and launched with
   // the group's dA by lora_grad_a: dy, u, x and du are all unchanged in between.
-  void lora_grad_b(int l, int g, const float* dy, long long ldy, long long kspan, int M) {
+  // dyh set: the output gradient is read from that fp16 operand (dy is not read)
+  void lora_grad_b(int l, int g, const float* dy, long long ldy, long long kspan, int M, HIn dyh = HIn{}) {
     const int n = gcount(g);
     if (n == 0) return;
     ColsSeg cs;
@@ -415,8 +416,8 @@ struct hos_peft {
     }
     const int w = bw(g);
     lora_rows("lora_du", M, kspan, lscale, dy, ldy, P + offBg[l * 4 + g], w, rs, du + ucol(first_adapted(g)),
-              NT * r);
-    pend_db = ColsJob{r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1};
+              NT * r, dyh);
+    pend_db = ColsJob{r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1, dyh};
     pend_group = g;
   }
   // Epilogue term dx_in += du_t·A_tᵀ of the base dX GEMM: L(j, col) = At[(slot·r + j)·in + col]
@@ -665,11 +666,14 @@ struct hos_peft {
       lora_grad_b(l, 3, dx, d, d, M);
       qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD), tpd[TD]);
       lora_grad_a(l, 3, a.h, F, M);
+      // The gate|up LoRA gradients read d(gate|up) from the fp16 operand the SwiGLU backward writes for the dX
+      // GEMM when it carries the residual plane (an f32 copy only for single-plane precision modes).
+      const bool gu_lora = has(TG) || has(TU), gu_f32 = gu_lora && !hs.lo;
       {
-        Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (dgu ? 8.0 * M * F : 0));
-        launch_swiglu_bwd(a.gu, dh, M, F, (has(TG) || has(TU)) ? dgu : nullptr, hs, st);
+        Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (gu_f32 ? 8.0 * M * F : 0));
+        launch_swiglu_bwd(a.gu, dh, M, F, gu_f32 ? dgu : nullptr, hs, st);
       }
-      if (dgu) lora_grad_b(l, 2, dgu, 2LL * F, 2LL * F, M);
+      if (gu_lora) lora_grad_b(l, 2, dgu, 2LL * F, 2LL * F, M, gu_f32 ? HIn{} : HIn{hs.data, hs.lo, hs.rinv});
       if (w.gu.q && group_uniform(2) && gcount(2) * r <= 32) {
         qdx(w.gu, hs, 2LL * F, M, dxn, d, 0, stacked_down_epi(l, 2), tpd[TG]);
       } else {
