@@ -34,6 +34,11 @@ namespace {
 constexpr int TB = 32;        // rows of one MFMA tile
 constexpr int NW = 4;         // waves per workgroup
 constexpr int BR = TB * NW;   // rows a workgroup owns
+// Wave groups splitting the streamed axis of a workgroup: two, except for the head-dim-128 backward kernels, whose
+// accumulators need more than the 256 registers two waves per SIMD leave (they spill).
+constexpr int ATT_NG = 2;
+template <int HD>
+constexpr int bwd_groups() { return HD == 64 ? 2 : 1; }
 
 template <int HD>
 struct AC {
@@ -220,18 +225,23 @@ struct TileLoader {
 };
 
 // ---- forward: a wave owns 32 queries; K and V tiles stream through LDS ----
-template <int HD>
-__global__ void __launch_bounds__(256) attn_fwd_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
-                                                       const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
-                                                       const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
-                                                       int T, int nh, int group, float* __restrict__ o, long long ldo,
-                                                       float* __restrict__ lse) {
+// NG wave groups of 4 waves own the same 128 queries and split the key tiles into NG consecutive ranges (the
+// causal block's last query rows need every key tile: splitting halves the longest workgroup's loop); each group
+// streams its range through its own double-buffered LDS stages, and the groups' (m, l, O) merge in group order
+// through LDS at the end.
+template <int HD, int NG>
+__global__ void __launch_bounds__(256 * NG) attn_fwd_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
+                                                            const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
+                                                            const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
+                                                            int T, int nh, int group, float* __restrict__ o,
+                                                            long long ldo, float* __restrict__ lse) {
   using C = AC<HD>;
-  __shared__ __attribute__((aligned(16))) __bf16 sm[2][4 * C::TILE];  // stage: Kh, Kl, Vh, Vl
+  __shared__ __attribute__((aligned(16))) __bf16 sm[NG][2][4 * C::TILE];  // per group, stage: Kh, Kl, Vh, Vl
   const int nqb = (T + BR - 1) / BR;
   const Work wk = work_item();
   const int qb = nqb - 1 - wk.xb, h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hl = lane >> 5,
+  const int tid = threadIdx.x, gt = tid & (NW * 64 - 1), grp = __builtin_amdgcn_readfirstlane(tid >> 8);
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane((tid >> 6) & (NW - 1)), hl = lane >> 5,
             c = lane & 31;
   const int q0 = qb * BR + w * TB, myq = q0 + c;
   const bool active = q0 < T;
@@ -245,16 +255,18 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const __bf16* __restrict_
     for (int r = 0; r < 16; r++) O[i][r] = 0.0f;
   float m = -INFINITY, l = 0.0f;
   const int nkb = (min(qb * BR + BR, T) - 1) / TB + 1;  // key tiles the workgroup needs
+  const int per = (nkb + NG - 1) / NG, kbeg = grp * per, kend = min(nkb, kbeg + per);  // this group's range
   const int my_last = active ? (min(q0 + TB, T) - 1) / TB : -1;
   const Planes4 planes{{kh, kl, vh, vl}};
   TileLoader<HD> ld;
-  ld.load(planes, krow0, 0, T, tid);
-  ld.store(sm[0], tid);
+  ld.load(planes, krow0, min(kbeg, nkb - 1) * TB, T, gt);
+  ld.store(sm[grp][0], gt);
   __syncthreads();
-  for (int kb = 0; kb < nkb; kb++) {
-    const __bf16* st = sm[kb & 1];
-    ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, tid);  // past the end: a harmless re-read
-    if (kb <= my_last) {
+  for (int it = 0; it < per; it++) {
+    const int kb = kbeg + it;
+    const __bf16* st = sm[grp][it & 1];
+    ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, gt);  // past the range: a harmless re-read
+    if (kb < kend && kb <= my_last) {
       f16v S;
 #pragma unroll
       for (int r = 0; r < 16; r++) S[r] = 0.0f;
@@ -303,8 +315,38 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const __bf16* __restrict_
                            pl, O[i]);
       }
     }
-    ld.store(sm[(kb + 1) & 1], tid);
+    ld.store(sm[grp][(it + 1) & 1], gt);
     __syncthreads();
+  }
+  if constexpr (NG > 1) {
+    // groups 1.. hand (m, l, O) to group 0 through the (now free) stages; group 0 merges them in group order
+    constexpr int SL = C::NC * 16 + 2;  // floats per lane
+    static_assert((NG - 1) * NW * 64 * SL * 4 <= (int)sizeof(sm), "merge staging");
+    float* mg = reinterpret_cast<float*>(&sm[0][0][0]);
+    if (grp > 0) {
+      float* d = mg + (size_t)(((grp - 1) * NW + w) * 64 + lane) * SL;
+      d[0] = m;
+      d[1] = l;
+#pragma unroll
+      for (int i = 0; i < C::NC; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) d[2 + 16 * i + r] = O[i][r];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int gg = 1; gg < NG; gg++) {
+      const float* d = mg + (size_t)(((gg - 1) * NW + w) * 64 + lane) * SL;
+      const float mo = d[0], lo = d[1], mn = fmaxf(m, mo), mn2 = mn * LOG2E;
+      const float a = m == mn ? 1.0f : exp_shift(m, mn2);
+      const float bo = mo == -INFINITY ? 0.0f : (mo == mn ? 1.0f : exp_shift(mo, mn2));
+      l = l * a + lo * bo;
+      m = mn;
+#pragma unroll
+      for (int i = 0; i < C::NC; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) O[i][r] = O[i][r] * a + d[2 + 16 * i + r] * bo;
+    }
   }
   if (!active || myq >= T) return;
   const float inv = 1.0f / l;
@@ -319,8 +361,9 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const __bf16* __restrict_
 }
 
 // ---- dQ: a wave owns 32 queries; K and V tiles stream through LDS ----
-template <int HD>
-__global__ void __launch_bounds__(256) attn_dq_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
+// NG wave groups split the key tiles as in the forward; their partial dQ sums add in group order at the end.
+template <int HD, int NG>
+__global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
                                                       const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
                                                       const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
                                                       const __bf16* __restrict__ doh, const __bf16* __restrict__ dol,
@@ -328,11 +371,12 @@ __global__ void __launch_bounds__(256) attn_dq_kernel(const __bf16* __restrict__
                                                       int T, int nh, int group, float* __restrict__ dq,
                                                       long long ldq) {
   using C = AC<HD>;
-  __shared__ __attribute__((aligned(16))) __bf16 sm[2][4 * C::TILE];  // stage: Kh, Kl, Vh, Vl
+  __shared__ __attribute__((aligned(16))) __bf16 sm[NG][2][4 * C::TILE];  // per group, stage: Kh, Kl, Vh, Vl
   const int nqb = (T + BR - 1) / BR;
   const Work wk = work_item();
   const int qb = nqb - 1 - wk.xb, h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hl = lane >> 5,
+  const int tid = threadIdx.x, gt = tid & (NW * 64 - 1), grp = __builtin_amdgcn_readfirstlane(tid >> 8);
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane((tid >> 6) & (NW - 1)), hl = lane >> 5,
             c = lane & 31;
   const int q0 = qb * BR + w * TB, myq = q0 + c;
   const bool active = q0 < T;
@@ -348,16 +392,18 @@ __global__ void __launch_bounds__(256) attn_dq_kernel(const __bf16* __restrict__
 #pragma unroll
     for (int r = 0; r < 16; r++) A[i][r] = 0.0f;
   const int nkb = (min(qb * BR + BR, T) - 1) / TB + 1;
+  const int per = (nkb + NG - 1) / NG, kbeg = grp * per, kend = min(nkb, kbeg + per);  // this group's range
   const int my_last = active ? (min(q0 + TB, T) - 1) / TB : -1;
   const Planes4 planes{{kh, kl, vh, vl}};
   TileLoader<HD> ld;
-  ld.load(planes, krow0, 0, T, tid);
-  ld.store(sm[0], tid);
+  ld.load(planes, krow0, min(kbeg, nkb - 1) * TB, T, gt);
+  ld.store(sm[grp][0], gt);
   __syncthreads();
-  for (int kb = 0; kb < nkb; kb++) {
-    const __bf16* st = sm[kb & 1];
-    ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, tid);  // past the end: a harmless re-read
-    if (kb <= my_last) {
+  for (int it = 0; it < per; it++) {
+    const int kb = kbeg + it;
+    const __bf16* st = sm[grp][it & 1];
+    ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, gt);  // past the range: a harmless re-read
+    if (kb < kend && kb <= my_last) {
       f16v S, dP;
 #pragma unroll
       for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
@@ -385,8 +431,30 @@ __global__ void __launch_bounds__(256) attn_dq_kernel(const __bf16* __restrict__
           A[i] = mma3_bf16(tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, A[i]);
       }
     }
-    ld.store(sm[(kb + 1) & 1], tid);
+    ld.store(sm[grp][(it + 1) & 1], gt);
     __syncthreads();
+  }
+  if constexpr (NG > 1) {
+    constexpr int SL = C::NC * 16;
+    static_assert((NG - 1) * NW * 64 * SL * 4 <= (int)sizeof(sm), "merge staging");
+    float* mg = reinterpret_cast<float*>(&sm[0][0][0]);
+    if (grp > 0) {
+      float* d = mg + (size_t)(((grp - 1) * NW + w) * 64 + lane) * SL;
+#pragma unroll
+      for (int i = 0; i < C::NC; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) d[16 * i + r] = A[i][r];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int gg = 1; gg < NG; gg++) {
+      const float* d = mg + (size_t)(((gg - 1) * NW + w) * 64 + lane) * SL;
+#pragma unroll
+      for (int i = 0; i < C::NC; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) A[i][r] += d[16 * i + r];
+    }
   }
   if (!active || myq >= T) return;
   float* out = dq + ((long long)b * T + myq) * ldq + h * HD;
@@ -401,9 +469,10 @@ __global__ void __launch_bounds__(256) attn_dq_kernel(const __bf16* __restrict__
 
 // ---- dK, dV for query head h: a wave owns 32 keys; Q and dO tiles (with their LSE and D) stream through LDS.
 // With group > 1 each head's result goes to part[(b·T + key)][h][2·HD] and attn_group_sum adds the group in head
-// order; with group == 1 it is written in place.
-template <int HD>
-__global__ void __launch_bounds__(256) attn_dkdv_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
+// order; with group == 1 it is written in place. NG wave groups split the query tiles into consecutive ranges;
+// their partial dK / dV sums add in group order at the end.
+template <int HD, int NG>
+__global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
                                                         const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
                                                         const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
                                                         const __bf16* __restrict__ doh, const __bf16* __restrict__ dol,
@@ -411,11 +480,12 @@ __global__ void __launch_bounds__(256) attn_dkdv_kernel(const __bf16* __restrict
                                                         int T, int nh, int group, float* __restrict__ dkv,
                                                         long long ldk, int kcol, int vcol, float* __restrict__ part) {
   using C = AC<HD>;
-  __shared__ __attribute__((aligned(16))) __bf16 sm[2][4 * C::TILE];  // stage: Qh, Ql, dOh, dOl
-  __shared__ float ld_s[2][2][TB];                                    // stage: LSE·log2 e, D of the tile's queries
+  __shared__ __attribute__((aligned(16))) __bf16 sm[NG][2][4 * C::TILE];  // per group, stage: Qh, Ql, dOh, dOl
+  __shared__ float ld_s[NG][2][2][TB];  // per group, stage: LSE·log2 e, D of the tile's queries
   const Work wk = work_item();
   const int h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), hl = lane >> 5,
+  const int tid = threadIdx.x, gt = tid & (NW * 64 - 1), grp = __builtin_amdgcn_readfirstlane(tid >> 8);
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane((tid >> 6) & (NW - 1)), hl = lane >> 5,
             c = lane & 31;
   const int kw0 = wk.xb * BR + w * TB, mykey = kw0 + c;
   const bool active = kw0 < T;
@@ -431,28 +501,30 @@ __global__ void __launch_bounds__(256) attn_dkdv_kernel(const __bf16* __restrict
   const int nqt = (T + TB - 1) / TB;                 // query tiles of the sequence
   const int qt0 = (wk.xb * BR) / TB;                 // the first one that sees any of the workgroup's keys
   const int my_first = active ? kw0 / TB : nqt;      // this wave's first (diagonal) query tile
+  const int per = (nqt - qt0 + NG - 1) / NG, qbeg = qt0 + grp * per, qend = min(nqt, qbeg + per);  // group range
   const Planes4 planes{{qh, ql, doh, dol}};
   TileLoader<HD> ld;
   float ldv = 0.0f;
   auto load = [&](int qt) {
-    ld.load(planes, qrow0, qt * TB, T, tid);
-    if (tid < 2 * TB) {
-      const long long r = qrow0 + min(qt * TB + (tid & (TB - 1)), T - 1);
-      ldv = tid < TB ? lse[r] * LOG2E : dvec[r];
+    ld.load(planes, qrow0, qt * TB, T, gt);
+    if (gt < 2 * TB) {
+      const long long r = qrow0 + min(qt * TB + (gt & (TB - 1)), T - 1);
+      ldv = gt < TB ? lse[r] * LOG2E : dvec[r];
     }
   };
   auto store = [&](int s) {
-    ld.store(sm[s], tid);
-    if (tid < 2 * TB) ld_s[s][tid / TB][tid & (TB - 1)] = ldv;
+    ld.store(sm[grp][s], gt);
+    if (gt < 2 * TB) ld_s[grp][s][gt / TB][gt & (TB - 1)] = ldv;
   };
-  load(qt0);
+  load(min(qbeg, nqt - 1));
   store(0);
   __syncthreads();
-  for (int qt = qt0; qt < nqt; qt++) {
-    const int s = (qt - qt0) & 1;
-    const __bf16* st = sm[s];
-    load(min(qt + 1, nqt - 1));  // past the end: a harmless re-read
-    if (qt >= my_first) {
+  for (int it = 0; it < per; it++) {
+    const int qt = qbeg + it;
+    const int s = it & 1;
+    const __bf16* st = sm[grp][s];
+    load(min(qt + 1, nqt - 1));  // past the range: a harmless re-read
+    if (qt < qend && qt >= my_first) {
       f16v S, dP;
 #pragma unroll
       for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
@@ -467,8 +539,8 @@ __global__ void __launch_bounds__(256) attn_dkdv_kernel(const __bf16* __restrict
       float Lr[16], Dr[16];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float4 a = *reinterpret_cast<const float4*>(&ld_s[s][0][8 * j + 4 * hl]);
-        const float4 d = *reinterpret_cast<const float4*>(&ld_s[s][1][8 * j + 4 * hl]);
+        const float4 a = *reinterpret_cast<const float4*>(&ld_s[grp][s][0][8 * j + 4 * hl]);
+        const float4 d = *reinterpret_cast<const float4*>(&ld_s[grp][s][1][8 * j + 4 * hl]);
         Lr[4 * j] = a.x, Lr[4 * j + 1] = a.y, Lr[4 * j + 2] = a.z, Lr[4 * j + 3] = a.w;
         Dr[4 * j] = d.x, Dr[4 * j + 1] = d.y, Dr[4 * j + 2] = d.z, Dr[4 * j + 3] = d.w;
       }
@@ -496,6 +568,34 @@ __global__ void __launch_bounds__(256) attn_dkdv_kernel(const __bf16* __restrict
     }
     store(s ^ 1);
     __syncthreads();
+  }
+  if constexpr (NG > 1) {
+    constexpr int SL = C::NC * 32;
+    static_assert((NG - 1) * NW * 64 * SL * 4 <= (int)sizeof(sm), "merge staging");
+    float* mg = reinterpret_cast<float*>(&sm[0][0][0]);
+    if (grp > 0) {
+      float* d = mg + (size_t)(((grp - 1) * NW + w) * 64 + lane) * SL;
+#pragma unroll
+      for (int i = 0; i < C::NC; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          d[32 * i + r] = dK[i][r];
+          d[32 * i + 16 + r] = dV[i][r];
+        }
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int gg = 1; gg < NG; gg++) {
+      const float* d = mg + (size_t)(((gg - 1) * NW + w) * 64 + lane) * SL;
+#pragma unroll
+      for (int i = 0; i < C::NC; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          dK[i][r] += d[32 * i + r];
+          dV[i][r] += d[32 * i + 16 + r];
+        }
+    }
   }
   if (!active || mykey >= T) return;
   const long long row = (long long)b * T + mykey;
@@ -567,7 +667,8 @@ void attn_fwd_hd(const float* qkv, long long ld, int kcol, int vcol, int B, int 
   const Planes P = planes_of(scratch, B, T, nh, nkv, HD);
   split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
   dim3 grid(ceil_div(T, BR), nh, B);
-  attn_fwd_kernel<HD><<<grid, 256, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, T, nh, nh / nkv, o, ldo, lse);
+  attn_fwd_kernel<HD, ATT_NG><<<grid, 256 * ATT_NG, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, T, nh, nh / nkv, o,
+                                                             ldo, lse);
   HOS_HIP_CHECK(hipGetLastError());
 }
 
@@ -581,11 +682,12 @@ void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float
   attn_split_do<HD><<<ceil_div(n, 256), 256, 0, st>>>(o, dout, ldo, T, nh, M, P.dh, P.dl, dvec);
   HOS_HIP_CHECK(hipGetLastError());
   dim3 grid(ceil_div(T, BR), nh, B);
-  attn_dq_kernel<HD><<<grid, 256, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse, dvec, T, nh, nh / nkv,
-                                           dqkv, ldd);
+  constexpr int NGB = bwd_groups<HD>();
+  attn_dq_kernel<HD, NGB><<<grid, 256 * NGB, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse, dvec,
+                                                            T, nh, nh / nkv, dqkv, ldd);
   HOS_HIP_CHECK(hipGetLastError());
-  attn_dkdv_kernel<HD><<<grid, 256, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse, dvec, T, nh, nh / nkv,
-                                             dqkv, ldd, kcol, vcol, part);
+  attn_dkdv_kernel<HD, NGB><<<grid, 256 * NGB, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse,
+                                                              dvec, T, nh, nh / nkv, dqkv, ldd, kcol, vcol, part);
   HOS_HIP_CHECK(hipGetLastError());
   if (nh != nkv) {
     long long ne = (long long)B * T * nkv * 2 * HD;

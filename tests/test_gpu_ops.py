@@ -93,7 +93,9 @@ def test_swiglu_fwd_bwd(gpu):
                                            # OLMoE's head dim (16 heads of 128, no GQA) and a GQA case
                                            (2, 70, 4, 4, 128), (1, 97, 6, 2, 128),
                                            # one token; several 128-row workgroups with a ragged last one
-                                           (1, 1, 4, 4, 64), (2, 300, 8, 2, 64), (1, 512, 14, 2, 64)])
+                                           (1, 1, 4, 4, 64), (2, 300, 8, 2, 64), (1, 512, 14, 2, 64),
+                                           # long ragged sequence: both wave groups of every workgroup busy
+                                           (1, 1000, 4, 2, 64)])
 def test_attention_fwd_bwd(gpu, B, T, nh, nkv, hd):
     print(f"attention B={B} T={T} heads={nh}/{nkv} hd={hd}", flush=True)
     rng = np.random.default_rng(B * T + nh)
