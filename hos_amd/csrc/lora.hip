@@ -24,13 +24,13 @@ namespace {
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 // Four consecutive values of an activation row: f32, or the fp16 operand's hi + lo (exact in f32; the row's rinv is
 // applied by the caller).
+__device__ __forceinline__ float4 load4h(const HIn& xh, long long off) {
+  const h4v a = *reinterpret_cast<const h4v*>(xh.hi + off), b = *reinterpret_cast<const h4v*>(xh.lo + off);
+  return make_float4((float)a.x + (float)b.x, (float)a.y + (float)b.y, (float)a.z + (float)b.z,
+                     (float)a.w + (float)b.w);
+}
 __device__ __forceinline__ float4 load4(const float* xf, const HIn& xh, long long off) {
-  if (xh.hi) {
-    const h4v a = *reinterpret_cast<const h4v*>(xh.hi + off), b = *reinterpret_cast<const h4v*>(xh.lo + off);
-    return make_float4((float)a.x + (float)b.x, (float)a.y + (float)b.y, (float)a.z + (float)b.z,
-                       (float)a.w + (float)b.w);
-  }
-  return *reinterpret_cast<const float4*>(xf + off);
+  return xh.hi ? load4h(xh, off) : *reinterpret_cast<const float4*>(xf + off);
 }
 
 __device__ __forceinline__ f4v mfma16(float a, float b, f4v c) {
@@ -287,7 +287,7 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
 // Workgroup: 64 columns of one segment × all j × an m-chunk; wave w takes the chunk's 4-row steps
 // w, w+4, … Lane (q, p): m = step + q, columns c0+4p .. +3 (one float4; component e is MFMA tile e).
 // bx: the workgroup's column block within its job; red: LDS of at least 2·NS·16·64 floats.
-template <int NS>
+template <int NS, bool GH>
 __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, int mchunk, float* red, float* part) {
   constexpr int NJR = NS * 16, E = NJR * 64;
   const ColsSeg& sg = jb.sg;
@@ -300,7 +300,6 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
   const int mb = blockIdx.y * mchunk, me = min(M, mb + mchunk);
   const bool cv = c0 + 4 * p < len;
   const long long gcol = sg.gbeg[t] + c0 + 4 * p;
-  const bool gh = jb.gh.hi != nullptr;
   const float* scol = jb.Sm + sg.soff[t];
   const long long lds = jb.lds, ldg = jb.ldg;
   const int ns = jb.ns;
@@ -321,9 +320,15 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
     for (int u = 0; u < U; u++) {
       const int m = m40 + 16 * u + q;
       const bool mv = m < me;
-      g[u] = (mv && cv) ? load4(jb.Gm, jb.gh, gcol + (long long)m * ldg) : make_float4(0.f, 0.f, 0.f, 0.f);
-      // G given as the fp16 operand: its row scale joins S (Σ_m S[m,j]·rinv[m]·(hi+lo)[m,c])
-      const float ri = (gh && mv) ? jb.gh.rinv[m] : 1.0f;
+      // G given as the fp16 operand (GH): its row scale joins S (Σ_m S[m,j]·rinv[m]·(hi+lo)[m,c])
+      float ri = 1.0f;
+      if constexpr (GH) {
+        g[u] = (mv && cv) ? load4h(jb.gh, gcol + (long long)m * ldg) : make_float4(0.f, 0.f, 0.f, 0.f);
+        ri = mv ? jb.gh.rinv[m] : 0.0f;
+      } else {
+        g[u] = (mv && cv) ? *reinterpret_cast<const float4*>(jb.Gm + gcol + (long long)m * ldg)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
 #pragma unroll
       for (int js = 0; js < NS; js++) {
         const int j = js * 16 + p;
@@ -368,15 +373,16 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
 }
 
 // Two independent jobs over the same contraction length in one launch: workgroups [0, b.bx0) run job a with
-// NSA row tiles, the rest job b with NSB. A single job passes b with bx0 = the grid width.
-template <int NSA, int NSB>
+// NSA row tiles, the rest job b with NSB. A single job passes b with bx0 = the grid width. GHA: job a reads G
+// as the fp16 operand (job b never does).
+template <int NSA, int NSB, bool GHA>
 __global__ void __launch_bounds__(256) lora_cols_kernel(int M, int mchunk, ColsJobDev a, ColsJobDev b, float* part) {
   constexpr int EMAX = (NSA > NSB ? NSA : NSB) * 16 * 64;
   __shared__ float red[2 * EMAX];
   if ((int)blockIdx.x < b.bx0)
-    cols_body<NSA>(a, (int)blockIdx.x, M, mchunk, red, part);
+    cols_body<NSA, GHA>(a, (int)blockIdx.x, M, mchunk, red, part);
   else
-    cols_body<NSB>(b, (int)blockIdx.x - b.bx0, M, mchunk, red, part);
+    cols_body<NSB, false>(b, (int)blockIdx.x - b.bx0, M, mchunk, red, part);
 }
 
 // Separate-launch reductions of the partials (one thread per output element of every block).
@@ -423,6 +429,124 @@ __global__ void lora_cols_reduce(const float* __restrict__ part, int S, ColsJobD
     cols_reduce_one(b, part, S, i - na);
 }
 
+
+// ---------------- rows on fp16 MFMA ----------------
+// C[M, n] = α·rinv[m]·Σ_k (Xh + Xl)[m, k]·(Bh + Bl)(j, k)·sc(j), dropping Xl·Bl (~2^-22): v_mfma_f32_16x16x32_f16,
+// one 16-row block × all n columns per workgroup of 16 waves splitting the contraction in 32-deep steps (wave w
+// takes steps w, w+16, …), their tiles summed in LDS in wave order; long contractions are also split over
+// workgroups (partials reduced by lora_rows_reduce). Lane (q = lane/16, p = lane%16): A row p, B column p, k 8q .. +7.
+constexpr int R16_NW = 16;
+typedef _Float16 h8l __attribute__((ext_vector_type(8)));
+template <int NJ>
+__global__ void __launch_bounds__(64 * R16_NW) lora_rows16_kernel(int M, int K, int kchunk, float alpha, HIn xh,
+                                                                  long long ldx, B16 bt, long long ldb, RowsSeg sg,
+                                                                  float* __restrict__ C, long long ldc, float* part) {
+  constexpr int NC = NJ * 16, E = 16 * NC;
+  __shared__ float red[R16_NW * E];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
+  const int m0 = blockIdx.x * 16, n = sg.nt * sg.r;
+  const int kb = blockIdx.y * kchunk, ke = min(K, kb + kchunk);
+  long long bbase[NJ];
+  int klo[NJ], khi[NJ];
+  float bsc[NJ];
+#pragma unroll
+  for (int jt = 0; jt < NJ; jt++) {
+    const int j = jt * 16 + p;
+    if (j < n) {
+      const int t = j / sg.r, jj = j - t * sg.r;
+      bbase[jt] = sg.boff[t] + (long long)jj * ldb - sg.kbeg[t];
+      klo[jt] = sg.kbeg[t];
+      khi[jt] = sg.kend[t];
+      bsc[jt] = bt.sc[sg.boff[t] / ldb + jj];
+    } else {
+      bbase[jt] = 0;
+      klo[jt] = khi[jt] = 0;
+      bsc[jt] = 0.0f;
+    }
+  }
+  const int row = m0 + p;
+  const bool rv = row < M;
+  const long long xr = (long long)(rv ? row : 0) * ldx;
+  f4v acc[NJ];
+#pragma unroll
+  for (int jt = 0; jt < NJ; jt++) acc[jt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  const h8l z8 = {};
+  constexpr int U = NJ <= 2 ? 2 : 1;  // steps per trip, loads first (steps past the end add exact zeros)
+  for (int k0 = kb + 32 * wave; k0 < ke; k0 += 32 * R16_NW * U) {
+    h8l ah[U], al[U], bh[U][NJ], bl[U][NJ];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int kk = k0 + 32 * R16_NW * u + 8 * q;
+      const bool kin = kk < ke;
+      ah[u] = (rv && kin) ? *reinterpret_cast<const h8l*>(xh.hi + xr + kk) : z8;
+      al[u] = (rv && kin) ? *reinterpret_cast<const h8l*>(xh.lo + xr + kk) : z8;
+#pragma unroll
+      for (int jt = 0; jt < NJ; jt++) {
+        const bool in = kin && kk >= klo[jt] && kk < khi[jt];
+        bh[u][jt] = in ? *reinterpret_cast<const h8l*>(bt.hi + bbase[jt] + kk) : z8;
+        bl[u][jt] = in ? *reinterpret_cast<const h8l*>(bt.lo + bbase[jt] + kk) : z8;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+      for (int jt = 0; jt < NJ; jt++) {
+        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[u], bh[u][jt], acc[jt], 0, 0, 0);
+        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u], bl[u][jt], acc[jt], 0, 0, 0);
+        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u], bh[u][jt], acc[jt], 0, 0, 0);
+      }
+  }
+  // element (row 4q+i, col 16jt+p): the operand's row scale and the factor row's scale
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r2 = m0 + 4 * q + i;
+    const float ri = r2 < M ? xh.rinv[r2] : 0.0f;
+#pragma unroll
+    for (int jt = 0; jt < NJ; jt++) red[wave * E + (4 * q + i) * NC + 16 * jt + p] = acc[jt][i] * ri * bsc[jt];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 64 * R16_NW) {
+    float v = 0.0f;
+    for (int w = 0; w < R16_NW; w++) v += red[w * E + e];
+    const int rr = e / NC, c = e % NC, r2 = m0 + rr;
+    if (gridDim.y == 1) {
+      if (r2 < M && c < n) C[(long long)r2 * ldc + c] = alpha * v;
+    } else {
+      part[((long long)blockIdx.y * gridDim.x + blockIdx.x) * E + e] = v;
+    }
+  }
+}
+
+// One workgroup per row: max-abs, the power-of-two scale, fp16 hi/lo.
+__global__ void __launch_bounds__(256) split_rows16_kernel(const SplitRow* __restrict__ rows, const float* __restrict__ src,
+                                                           _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                           float* __restrict__ sc) {
+  __shared__ float red[4];
+  const SplitRow rw = rows[blockIdx.x];
+  const float* x = src + rw.off;
+  float amax = 0.0f;
+  for (int c = threadIdx.x; c < rw.len; c += 256) amax = fmaxf(amax, fabsf(x[c]));
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (amax > 0.0f && amax < 3.0e38f) {
+    int ex;
+    frexpf(amax, &ex);
+    e = 15 - ex;
+    e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  }
+  const float s = ldexpf(1.0f, e);
+  if (threadIdx.x == 0) sc[blockIdx.x] = ldexpf(1.0f, -e);
+  for (int c = threadIdx.x; c < rw.len; c += 256) {
+    const float v = x[c] * s;
+    const _Float16 h = (_Float16)v;
+    hi[rw.off + c] = h;
+    lo[rw.off + c] = (_Float16)(v - (float)h);
+  }
+}
+
 int ceil_div_i(long long a, long long b) { return (int)((a + b - 1) / b); }
 
 // Workgroups a launch aims for; the long contraction is split until the grid reaches it.
@@ -446,19 +570,75 @@ void cols_split(long long M, int gx, int* S, int* mchunk) {
 
 }  // namespace
 
+// Split of an fp16 rows launch: enough workgroups (16-row blocks × contraction chunks of whole 32·16-deep
+// wave rounds) to cover the chip about twice, each chunk at least HOS_R16_MINROUNDS rounds (the reduction
+// launch costs more than a short chunk saves).
+#ifndef HOS_R16_MINROUNDS
+#define HOS_R16_MINROUNDS 4
+#endif
+void rows16_split(long long M, long long K, int* S, int* kchunk) {
+  const int gx = ceil_div_i(M, 16), round = 32 * R16_NW;
+  int s = std::max(1, std::min(ceil_div_i(512, gx), (int)(K / ((long long)round * HOS_R16_MINROUNDS))));
+  *kchunk = ceil_div_i(ceil_div_i(K, s), round) * round;
+  *S = std::max(1, ceil_div_i(K, *kchunk));
+}
+
 size_t lora_rows_ws_bytes(long long M, long long K, int n) {
-  if (M <= 0 || n <= 0 || K <= ROWS_WIDE_KMAX) return 0;
+  if (M <= 0 || n <= 0) return 0;
+  int S16 = 0, kc16 = 0;
+  rows16_split(M, K, &S16, &kc16);
+  const size_t w16 = S16 > 1 ? (size_t)S16 * ceil_div_i(M, 16) * 16 * ((n + 15) / 16) * 16 * 4 : 0;
+  if (K <= ROWS_WIDE_KMAX) return w16;
   int S = 0, kchunk = 0;
   rows_split(M, K, &S, &kchunk);
-  return S > 1 ? (size_t)S * ceil_div_i(M, 32) * 32 * ((n + 15) / 16) * 16 * 4 : 0;
+  return std::max(w16, S > 1 ? (size_t)S * ceil_div_i(M, 32) * 32 * ((n + 15) / 16) * 16 * 4 : (size_t)0);
+}
+
+void launch_split_rows16(const SplitRow* rows, int nrows, const float* src, _Float16* hi, _Float16* lo, float* sc,
+                         hipStream_t st) {
+  if (nrows <= 0) return;
+  split_rows16_kernel<<<nrows, 256, 0, st>>>(rows, src, hi, lo, sc);
+  HOS_HIP_CHECK(hipGetLastError());
 }
 
 void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
                       long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
-                      hipStream_t st, HIn xh) {
+                      hipStream_t st, HIn xh, B16 b16) {
   const int n = sg.nt * sg.r;
   if (M <= 0 || n <= 0) return;
   HOS_REQUIRE(n <= 96 && sg.nt >= 1 && sg.nt <= 4, HOS_E_INVALID, "lora_rows: n = nt·r must be <= 96");
+  // fp16 path: 16-byte rows and segments on 8-element bounds (otherwise the f32 kernels, reading xh)
+  bool f16 = xh.hi && xh.lo && b16.hi && b16.lo && b16.sc && K % 32 == 0 && ldx % 8 == 0 && ldb % 8 == 0 &&
+             ((uintptr_t)xh.hi & 15) == 0 && ((uintptr_t)xh.lo & 15) == 0 && ((uintptr_t)b16.hi & 15) == 0 &&
+             ((uintptr_t)b16.lo & 15) == 0;
+  for (int t = 0; t < sg.nt; t++)
+    f16 = f16 && sg.kbeg[t] % 8 == 0 && sg.kend[t] % 8 == 0 && sg.boff[t] % 8 == 0 && sg.kbeg[t] >= 0 &&
+          sg.kend[t] <= K;
+  if (f16) {
+    HOS_REQUIRE(xh.rinv, HOS_E_INVALID, "lora_rows: the fp16 operand needs its row scales");
+    const int gx = ceil_div_i(M, 16), NJ = (n + 15) / 16;
+    int S = 0, kchunk = 0;
+    rows16_split(M, K, &S, &kchunk);
+    HOS_REQUIRE(S == 1 || (size_t)S * gx * 16 * NJ * 16 * 4 <= ws_bytes, HOS_E_INVALID, "lora_rows: workspace too small");
+    dim3 grid(gx, S);
+#define ROWS16(NJV)                                                                                                  \
+  case NJV:                                                                                                          \
+    lora_rows16_kernel<NJV><<<grid, 64 * R16_NW, 0, st>>>((int)M, (int)K, kchunk, alpha, xh, ldx, b16, ldb, sg, C, ldc, \
+                                                         ws);                                                        \
+    break;
+    switch (NJ) {
+      ROWS16(1) ROWS16(2) ROWS16(3) ROWS16(4) ROWS16(5) ROWS16(6)
+      default: throw Error(HOS_E_INVALID, "lora_rows: bad width");
+    }
+#undef ROWS16
+    HOS_HIP_CHECK(hipGetLastError());
+    if (S > 1) {
+      const long long tot = (long long)gx * 16 * NJ * 16;
+      lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, 16, NJ * 16, (int)M, n, alpha, C, ldc);
+      HOS_HIP_CHECK(hipGetLastError());
+    }
+    return;
+  }
   HOS_REQUIRE(K % 4 == 0 && ldx % 4 == 0 && ldb % 4 == 0 && ((uintptr_t)Bt & 15) == 0 &&
                   (xh.hi ? (((uintptr_t)xh.hi & 7) == 0 && ((uintptr_t)xh.lo & 7) == 0 && xh.rinv)
                          : ((uintptr_t)X & 15) == 0),
@@ -565,16 +745,20 @@ void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float*
   }
   const int NA = a.nsr / 16, NB = jb ? b.nsr / 16 : NA;
   dim3 grid(gx, S);
-#define COLS(X, Y)                                                                  \
-  if (NA == X && NB == Y) {                                                         \
-    lora_cols_kernel<X, Y><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, part);       \
-    launched = true;                                                                \
+#define COLS(X, Y)                                                                          \
+  if (NA == X && NB == Y && !bgh) {                                                         \
+    if (a.gh.hi)                                                                            \
+      lora_cols_kernel<X, Y, true><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, part);       \
+    else                                                                                    \
+      lora_cols_kernel<X, Y, false><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, part);      \
+    launched = true;                                                                        \
   }
+  const bool bgh = jb && b.gh.hi;
   bool launched = false;
   COLS(1, 1) COLS(2, 2) COLS(3, 3) COLS(4, 4) COLS(5, 5) COLS(6, 6) COLS(1, 2) COLS(1, 3) COLS(2, 4) COLS(2, 6)
 #undef COLS
   if (!launched) {
-    // width pair without a combined kernel: run the jobs one after the other
+    // width pair without a combined kernel (or a second job on the fp16 operand): run the jobs one after the other
     HOS_REQUIRE(jb != nullptr, HOS_E_INVALID, "lora_cols: bad width");
     launch_lora_cols2(M, ja, nullptr, ws, ws_bytes, st, batch);
     launch_lora_cols2(M, *jb, nullptr, ws, ws_bytes, st, batch);

@@ -14,6 +14,15 @@ struct HIn {
   const float* rinv = nullptr;
 };
 
+// A factor matrix split for fp16 MFMA: Bt(j, k) = (hi + lo)[same index as the f32 Bt]·sc[row], where the scale row of
+// output column j (slot t, jj < r) is boff[t] / ldb + jj — the stacked row for x·A (boff = t·r·ldb) and row jj for
+// dy·Bᵀ (boff a column offset < ldb). sc are powers of two putting each row's max-abs in [2^14, 2^15).
+struct B16 {
+  const _Float16* hi = nullptr;
+  const _Float16* lo = nullptr;
+  const float* sc = nullptr;
+};
+
 // Output columns of the rows kernel come in nt slots of r columns (one per adapter target). Slot t
 // contracts over X columns [kbeg[t], kend[t]) against Bt[boff[t] + jj·ldb + (k − kbeg[t])], jj < r.
 struct RowsSeg {
@@ -25,7 +34,18 @@ struct RowsSeg {
 // that operand (row stride ldx, 8-byte aligned rows) and the f32 pointer is not read.
 void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
                       long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
-                      hipStream_t st, HIn xh = HIn{});
+                      hipStream_t st, HIn xh = HIn{}, B16 b16 = B16{});
+// With both xh and b16 given the product runs on fp16 MFMA (three products, hi·hi + lo·hi + hi·lo: ~2^-22 relative
+// to the f32 one) — the rows kernel's fp32 MFMA rate bounds the long contractions otherwise.
+
+// Split f32 rows into fp16 hi/lo with a power-of-two scale per row (rows[i] = {offset, length} into src / hi / lo;
+// scale of row i to sc[i]): the per-step preparation of the factors a B16 reads.
+struct SplitRow {
+  long long off;
+  int len;
+};
+void launch_split_rows16(const SplitRow* rows, int nrows, const float* src, _Float16* hi, _Float16* lo, float* sc,
+                         hipStream_t st);
 
 // Column segments of the cols kernel: segment t covers G columns [gbeg, gbeg + len), uses S columns
 // starting at soff and writes output columns starting at ocol. blk0 is filled in by the launcher.

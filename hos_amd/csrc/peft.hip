@@ -104,6 +104,14 @@ struct hos_peft {
   std::vector<long long> offRT, offUp;
   float *rz = nullptr, *rdg = nullptr, *rgb = nullptr, *rdgb = nullptr, *rgsum = nullptr, *rgm = nullptr;
   float *P = nullptr, *G = nullptr, *M1 = nullptr, *V1 = nullptr;
+  // fp16 hi/lo split of the LoRA factors (arena-parallel), one power-of-two scale per factor row: At rows of a
+  // group from scA, Bcat rows from scB; written at the start of each forward from the table split_tab.
+  _Float16 *P16h = nullptr, *P16l = nullptr;
+  float* psc = nullptr;
+  std::vector<int> scA, scB;
+  SplitRow* split_tab = nullptr;
+  int n_split = 0;
+  long long nfac = 0;
   uint64_t adam_t = 0;
 
   std::vector<LayerAct> act;
@@ -265,9 +273,22 @@ struct hos_peft {
   int ycol(int t) const { return t == TK ? qd : (t == TV ? qd + kvd : (t == TU ? F : 0)); }
 
   void lora_rows(const char* cls, long long M, long long K, float alpha, const float* X, long long ldx,
-                 const float* Bt, long long ldb, const RowsSeg& sg, float* C, long long ldc, HIn xh = HIn{}) {
+                 const float* Bt, long long ldb, const RowsSeg& sg, float* C, long long ldc, HIn xh = HIn{},
+                 B16 b16 = B16{}) {
     Scope s(this, cls, 2.0 * M * K * sg.nt * sg.r, 4.0 * (M * K + (double)M * sg.nt * sg.r));
-    launch_lora_rows(M, K, alpha, X, ldx, Bt, ldb, sg, C, ldc, ws, ws_bytes, st, xh);
+    launch_lora_rows(M, K, alpha, X, ldx, Bt, ldb, sg, C, ldc, ws, ws_bytes, st, xh, b16);
+  }
+  // The fp16 operand of the activation the current GEMM reads (when it carries the residual plane) and the
+  // factor split of a group's At (a) or Bcat: the LoRA rows products then run on fp16 MFMA.
+  HIn hs_in() const { return hs.lo ? HIn{hs.data, hs.lo, hs.rinv} : HIn{}; }
+  B16 fac16(int l, int g, bool a) const {
+    const long long off = a ? offAg[l * 4 + g] : offBg[l * 4 + g];
+    return B16{P16h + off, P16l + off, psc + (a ? scA : scB)[l * 4 + g]};
+  }
+  void split_factors() {
+    if (n_split == 0) return;
+    Scope s(this, "convert", 0, 8.0 * nfac);
+    launch_split_rows16(split_tab, n_split, P, P16h, P16l, psc, st);
   }
   void lora_cols(const char* cls, long long M, int ns, float alpha, const float* Sm, long long lds, const float* Gm,
                  long long ldg, const ColsSeg& sg, float* C, long long scj, long long scc) {
@@ -278,7 +299,8 @@ struct hos_peft {
   }
 
   // u[:, group columns] = x · [A_1 … A_G]   (forward)
-  void lora_down(int l, int g, const float* x, long long ldx, int M) {
+  // xh: x as the fp16 operand (row stride ldx)
+  void lora_down(int l, int g, const float* x, long long ldx, int M, HIn xh = HIn{}) {
     const int n = gcount(g);
     if (n == 0) return;
     const int first = first_adapted(g), in = in_dim(first);
@@ -290,7 +312,8 @@ struct hos_peft {
       sg.kend[i] = in;
       sg.boff[i] = (long long)i * r * in;
     }
-    lora_rows("lora_down", M, in, 1.0f, x, ldx, P + offAg[l * 4 + g], in, sg, act[l].u + ucol(first), NT * r);
+    lora_rows("lora_down", M, in, 1.0f, x, ldx, P + offAg[l * 4 + g], in, sg, act[l].u + ucol(first), NT * r, xh,
+              xh.hi ? fac16(l, g, true) : B16{});
   }
   // Epilogue term y += s·u_t·B_t of the base forward GEMM: L(j, n) = Bcat[j·bw + bcol(t) + n]
   GemmEpi up_epi(int l, int t) {
@@ -395,7 +418,8 @@ struct hos_peft {
   // From dy, the gradient of the group's fused projection output (row stride ldy, target t at column
   // ycol(t)): du_t = s·dy_t·B_tᵀ for every adapted t (one launch). dB_t = s·u_tᵀ·dy_t is queued and launched with
   // the group's dA by lora_grad_a: dy, u, x and du are all unchanged in between.
-  // dyh set: the output gradient is read from that fp16 operand (dy is not read)
+  // dyh set: the du product reads the output gradient from that fp16 operand; the queued dB reads dy (f32) unless
+  // it is null
   void lora_grad_b(int l, int g, const float* dy, long long ldy, long long kspan, int M, HIn dyh = HIn{}) {
     const int n = gcount(g);
     if (n == 0) return;
@@ -416,8 +440,8 @@ struct hos_peft {
     }
     const int w = bw(g);
     lora_rows("lora_du", M, kspan, lscale, dy, ldy, P + offBg[l * 4 + g], w, rs, du + ucol(first_adapted(g)),
-              NT * r, dyh);
-    pend_db = ColsJob{r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1, dyh};
+              NT * r, dyh, dyh.hi ? fac16(l, g, false) : B16{});
+    pend_db = ColsJob{r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1, dy ? HIn{} : dyh};
     pend_group = g;
   }
   // Epilogue term dx_in += du_t·A_tᵀ of the base dX GEMM: L(j, col) = At[(slot·r + j)·in + col]
@@ -558,6 +582,7 @@ struct hos_peft {
       Scope s(this, "embed", 0, 4.0 * M * d + (double)M * d);
       launch_embed(tok, ids, act[0].x, M, d, st);
     }
+    split_factors();
     if (rga) {
       Scope s(this, "rga", 0, 4.0 * (16.0 * Kg + Kg));
       launch_rga_bias(P + offGen, P + offWg, Kg, rgb, st);
@@ -571,7 +596,7 @@ struct hos_peft {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lqkv ? 2 : 1) + 2.0 * M * d);
         launch_rmsnorm_fwd(a.x, w.attn_norm, c.rms_eps, M, d, lqkv ? a.xn1 : nullptr, hs, a.inv1, st);
       }
-      lora_down(l, 0, a.xn1, d, M);
+      lora_down(l, 0, a.xn1, d, M, hs_in());
       if (w.qkv.q && group_uniform(0) && (!c.attn_bias || w.bias_qkv)) {
         qfwd(w.qkv, hs, d, M, a.qkv, W3, c.attn_bias ? w.bias_qkv : nullptr, nullptr, 0, stacked_up_epi(l, 0),
              tpf[TQ]);
@@ -597,7 +622,7 @@ struct hos_peft {
                         attn_planes, st);
       }
       to16(a.o, qd, M, qd);
-      lora_down(l, 1, a.o, qd, M);
+      lora_down(l, 1, a.o, qd, M, hs_in());
       qfwd(w.w[TO], hs, qd, M, a.x2, d, nullptr, a.x, 0, up_epi(l, TO), tpf[TO]);
       const bool lgu = has(TG) || has(TU) || E;
       {
@@ -608,7 +633,7 @@ struct hos_peft {
         moe_forward(l, M, xnext);
         continue;
       }
-      lora_down(l, 2, a.xn2, d, M);
+      lora_down(l, 2, a.xn2, d, M, hs_in());
       if (w.gu.q && group_uniform(2)) {
         qfwd(w.gu, hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, stacked_up_epi(l, 2), tpf[TG]);
       } else {
@@ -619,7 +644,7 @@ struct hos_peft {
         Scope s(this, "swiglu", 0, 8.0 * M * F + 2.0 * M * F + (has(TD) ? 4.0 * M * F : 0));
         launch_swiglu_fwd(a.gu, M, F, has(TD) ? a.h : nullptr, hs, st);
       }
-      lora_down(l, 3, a.h, F, M);
+      lora_down(l, 3, a.h, F, M, hs_in());
       qfwd(w.w[TD], hs, F, M, rga ? a.xr : xnext, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
       if (rga) rga_forward(l, M, xnext);
     }
@@ -663,17 +688,19 @@ struct hos_peft {
         moe_backward(l, M);
       } else {
       if (!fuse16) to16(dx, d, M, d);
-      lora_grad_b(l, 3, dx, d, d, M);
+      lora_grad_b(l, 3, dx, d, d, M, hs_in());
       qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD), tpd[TD]);
       lora_grad_a(l, 3, a.h, F, M);
       // The gate|up LoRA gradients read d(gate|up) from the fp16 operand the SwiGLU backward writes for the dX
-      // GEMM when it carries the residual plane (an f32 copy only for single-plane precision modes).
-      const bool gu_lora = has(TG) || has(TU), gu_f32 = gu_lora && !hs.lo;
+      // GEMM when it carries the residual plane and is small enough to stay in the last-level cache (128 MB):
+      // the dB pass reads each plane in 128-byte row pieces, at half the rate of the f32 copy's 256 from HBM.
+      const bool gu_lora = has(TG) || has(TU),
+                 gu_f32 = gu_lora && (!hs.lo || (double)M * 2 * F * 4 > 128.0 * (1 << 20));
       {
         Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (gu_f32 ? 8.0 * M * F : 0));
         launch_swiglu_bwd(a.gu, dh, M, F, gu_f32 ? dgu : nullptr, hs, st);
       }
-      if (gu_lora) lora_grad_b(l, 2, dgu, 2LL * F, 2LL * F, M, gu_f32 ? HIn{} : HIn{hs.data, hs.lo, hs.rinv});
+      if (gu_lora) lora_grad_b(l, 2, gu_f32 ? dgu : nullptr, 2LL * F, 2LL * F, M, hs_in());
       if (w.gu.q && group_uniform(2) && gcount(2) * r <= 32) {
         qdx(w.gu, hs, 2LL * F, M, dxn, d, 0, stacked_down_epi(l, 2), tpd[TG]);
       } else {
@@ -688,7 +715,7 @@ struct hos_peft {
         launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st, hs);
       }
       // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
-      lora_grad_b(l, 1, dx, d, d, M);
+      lora_grad_b(l, 1, dx, d, d, M, hs_in());
       qdx(w.w[TO], hs, d, M, dout, qd, 0, down_epi(l, TO), tpd[TO]);
       lora_grad_a(l, 1, a.o, qd, M);
       {
@@ -712,8 +739,8 @@ struct hos_peft {
         launch_qknorm_bwd(dqkv, W3, 0, qd, w.q_norm, a.qk_pre, a.qk_inv, M, st);
         launch_qknorm_bwd(dqkv, W3, qd, kvd, w.k_norm, a.qk_pre + (size_t)M * qd, a.qk_inv + M, M, st);
       }
-      lora_grad_b(l, 0, dqkv, W3, W3, M);
       if (c.qk_norm) to16(dqkv, W3, M, W3);
+      lora_grad_b(l, 0, dqkv, W3, W3, M, hs_in());
       if (w.qkv.q && group_uniform(0) && gcount(0) * r <= 64) {
         // one dX GEMM over the stacked q|k|v contraction, the three LoRA terms as one rank-3r update
         qdx(w.qkv, hs, W3, M, dxn, d, 0, stacked_down_epi(l, 0), tpd[TQ]);
@@ -958,6 +985,30 @@ struct hos_peft {
       off = pad(off + RGA_GLEN);
     }
     nparams = off;
+    {
+      std::vector<SplitRow> tab;
+      scA.assign((size_t)L * 4, 0);
+      scB.assign((size_t)L * 4, 0);
+      nfac = 0;
+      for (int l = 0; l < L; l++)
+        for (int g = 0; g < 4; g++) {
+          if (offAg[l * 4 + g] < 0) continue;
+          const int n = gcount(g), in = in_dim(group_first(g)), w = bw(g);
+          scA[l * 4 + g] = (int)tab.size();
+          for (int i = 0; i < n * r; i++) tab.push_back(SplitRow{offAg[l * 4 + g] + (long long)i * in, in});
+          scB[l * 4 + g] = (int)tab.size();
+          for (int j = 0; j < r; j++) tab.push_back(SplitRow{offBg[l * 4 + g] + (long long)j * w, w});
+          nfac += (long long)n * r * in + (long long)r * w;
+        }
+      n_split = (int)tab.size();
+      if (n_split > 0) {
+        split_tab = alloc<SplitRow>(tab.size());
+        HOS_HIP_CHECK(hipMemcpy(split_tab, tab.data(), tab.size() * sizeof(SplitRow), hipMemcpyHostToDevice));
+        P16h = alloc<_Float16>(nparams);
+        P16l = alloc<_Float16>(nparams);
+        psc = alloc<float>(tab.size());
+      }
+    }
     P = alloc<float>(nparams);
     G = alloc<float>(nparams);
     M1 = alloc<float>(nparams);
