@@ -699,15 +699,22 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bm = 128;
     bn = 64;
   }
-  // dX with a long contraction over a narrow output (the stacked gate|up dX): big tiles split over the
-  // contraction beat small unsplit tiles (measured in the step: −0.2 ms; the forward of the same shape, the FFN
-  // down projection, measured slower split and keeps small tiles).
-  const bool split_big = DX && !longc && C >= 4096 && ntiles(128, 128) < 320;
+  // A long contraction over a narrow output (the stacked gate|up dX, the FFN down projection forward): big
+  // tiles split over the contraction beat small unsplit tiles (measured on the MI355X at M 2048: dX 9728 -> 896
+  // 155 vs 210 us, forward 4864 -> 896 81 vs 108 us).
+  const bool split_big = !longc && C >= 4096 && ntiles(128, 128) < 320;
   if (split_big) {
     bm = 128;
     bn = 128;
   }
-  if (C % 64 == 0 && ((bm == 64 && bn == 64) || ((NP == 1 || longc || split_big) && bm == 128 && bn == 128))) bk = 64;
+  // 64-deep slabs where the contraction is long enough to amortize the deeper prologue: two-plane forwards from
+  // C 2048 on (M 8192, Q4_K: 2048 -> 16384 1788 vs 1811 us, 8192 -> 2048 899 vs 960; at C 896 32-deep slabs win,
+  // 163 vs 171 us) and the split forward; the two-plane dX keeps 32 (equal or faster at every step shape: split
+  // 9728 -> 896 148 vs 155 us).
+  const bool deep_fwd = !DX && (NP == 2 || NP == 3) && (C >= 2048 || split_big);
+  if (C % 64 == 0 &&
+      ((bm == 64 && bn == 64) || ((NP == 1 || longc || deep_fwd) && bm == 128 && bn == 128)))
+    bk = 64;
   // Single-pass GEMMs are bound by the weight dequantization (VALU) as much as by MFMA: 8 waves on a
   // 256-row tile dequantize each B slab once for twice the MFMA work.
   // The same holds for the weight-split mode 4 (one activation plane) and for the vocabulary-wide head in either
@@ -743,6 +750,15 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   while (!useg && epi.rank <= 32 && tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
          (size_t)(splits * 2) * M * Nout * sizeof(float) <= ws_bytes)
     splits *= 2;
+#ifdef HOS_QG_ENV_TILE
+  if (const char* f = getenv("QG_TILE")) {
+    int a1, a2, a3, a4;
+    if (sscanf(f, "%d,%d,%d,%d", &a1, &a2, &a3, &a4) == 4) { bm = a1; bn = a2; bk = a3; splits = a4; nslab = C / bk; }
+    HOS_REQUIRE(splits == 1 || (size_t)splits * M * Nout * sizeof(float) <= ws_bytes, HOS_E_INVALID,
+                "forced tile: split-K partials exceed the workspace");
+    HOS_REQUIRE(C % bk == 0 && epi.rank <= 32 && !useg, HOS_E_INVALID, "forced tile: unsupported");
+  }
+#endif
   int per = ceil_div(nslab, splits) * bk;
   splits = ceil_div(C, per);
 #define HOS_QG(BM_, BN_, BK_) \
