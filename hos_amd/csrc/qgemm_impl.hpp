@@ -246,7 +246,9 @@ struct Geo {
 // ---- the GEMM ----
 // out[m][n] (over n < Nout) = Σ_c A[m][c] · B(n, c); contraction C split over gridDim.z.
 template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
-__global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightView w, const _Float16* __restrict__ A,
+// (256-row one-plane tiles: at least 4 waves per SIMD, two workgroups per CU, i.e. at most 128 VGPRs — the
+// register file, not the LDS, would otherwise cut their occupancy)
+__global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 || NP == 4)) ? 4 : 1) qgemm_kernel(QWeightView w, const _Float16* __restrict__ A,
                                                     const _Float16* __restrict__ Alo, const float* __restrict__ rinv,
                                                     long long lda, int M, int Nout, int C, int c_per_split,
                                                     GemmEpi epi, float* __restrict__ ws, GroupKernelArgs gk) {
@@ -546,6 +548,60 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256) qgemm_kernel(QWeightVie
           acc[i][j] = mma3_bf16(ah, al, bh, bl, acc[i][j]);
         }
       }
+  }
+  // Output stores. Each 32×32 tile goes through a per-wave LDS transpose and leaves as row-major float4 runs
+  // (8 lanes per 128-byte row piece): a quarter of the store instructions of the MFMA layout's one-float-per-lane
+  // stores, and one row scale per lane per pass.
+  constexpr int TS = 40;  // f32 row stride of a staged tile (4·TS ≡ 32 banks: the two half-waves' rows are disjoint)
+  if constexpr (G::SMEM * 2 >= G::NT / 64 * 32 * TS * 4) {
+    __syncthreads();  // every wave is done with the main loop's and the rank term's LDS
+    float* tb = reinterpret_cast<float*>(smem) + wave * 32 * TS;
+    const bool vec = (Nout & 3) == 0 && (split || ((epi.ldo & 3) == 0 && ((uintptr_t)epi.out & 15) == 0 &&
+                                                  (!epi.resid || ((uintptr_t)epi.resid & 15) == 0) &&
+                                                  (!epi.bias || ((uintptr_t)epi.bias & 15) == 0)));
+#pragma unroll
+    for (int i = 0; i < G::TM; i++)
+#pragma unroll
+      for (int j = 0; j < G::TN; j++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) tb[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * TS + (lane & 31)] = acc[i][j][r];
+#pragma unroll
+        for (int pz = 0; pz < 4; pz++) {
+          const int lr = 8 * pz + (lane >> 3), c4 = 4 * (lane & 7);
+          const float4 t4 = *reinterpret_cast<const float4*>(tb + lr * TS + c4);
+          const int row = m0 + wm * (BM / G::WGM) + 32 * i + lr, col = n0 + wn * (BN / 2) + 32 * j + c4;
+          if (row >= M || col >= Nout) continue;
+          float v[4] = {t4.x, t4.y, t4.z, t4.w};
+          if (split) {
+            float* d = ws + ((long long)blockIdx.z * M + row) * Nout + col;
+            if (vec) {
+              *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+              for (int e = 0; e < 4 && col + e < Nout; e++) d[e] = v[e];
+            }
+            continue;
+          }
+          const float ri = rinv[row];
+          const long long off = (long long)row * epi.ldo + col;
+          float* o = epi.out + off;
+          if (vec) {
+            const float4 b4 = epi.bias ? *reinterpret_cast<const float4*>(epi.bias + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 y = make_float4(v[0] * ri + b4.x, v[1] * ri + b4.y, v[2] * ri + b4.z, v[3] * ri + b4.w);
+            if (epi.accumulate || epi.resid) {
+              const float4 q = *reinterpret_cast<const float4*>(epi.accumulate ? o : epi.resid + off);
+              y = make_float4(q.x + y.x, q.y + y.y, q.z + y.z, q.w + y.w);
+            }
+            *reinterpret_cast<float4*>(o) = y;
+          } else {
+            for (int e = 0; e < 4 && col + e < Nout; e++) {
+              float x = v[e] * ri;
+              if (epi.bias) x += epi.bias[col + e];
+              o[e] = epi.accumulate ? o[e] + x : (epi.resid ? epi.resid[off + e] + x : x);
+            }
+          }
+        }
+      }
+    return;
   }
 #pragma unroll
   for (int i = 0; i < G::TM; i++)
