@@ -632,7 +632,10 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
 // Deterministic split-K reduction + the same epilogue (the rank-r term is already in the first split's partial).
 // Workgroup = RED_ROWS rows × 1024 columns, a thread per 4 columns (16-byte loads); rows go four at a time with all
 // their partial loads issued together; partials are summed in split order.
-constexpr int RED_ROWS = 16;
+#ifndef HOS_RED_ROWS
+#define HOS_RED_ROWS 4
+#endif
+constexpr int RED_ROWS = HOS_RED_ROWS;  // 4: one pass of four rows, so the grid spreads over every CU
 __global__ void __launch_bounds__(256) splitk_reduce4(const float* __restrict__ ws, int splits, int M, int N,
                                                       const float* __restrict__ rinv, GemmEpi epi) {
   const int r0 = blockIdx.y * RED_ROWS, col = (blockIdx.x * 256 + threadIdx.x) * 4;
