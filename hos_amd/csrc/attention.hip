@@ -675,9 +675,9 @@ void attn_fwd_hd(const float* qkv, long long ld, int kcol, int vcol, int B, int 
 template <int HD>
 void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout, long long ldo,
                  const float* lse, float* dvec, int B, int T, int nh, int nkv, float* dqkv, long long ldd, float* part,
-                 void* scratch, hipStream_t st) {
+                 void* scratch, hipStream_t st, bool qkv_planes) {
   const Planes P = planes_of(scratch, B, T, nh, nkv, HD);
-  split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
+  if (!qkv_planes) split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
   const long long M = (long long)B * T, n = M * nh * AC<HD>::CH;
   attn_split_do<HD><<<ceil_div(n, 256), 256, 0, st>>>(o, dout, ldo, T, nh, M, P.dh, P.dl, dvec);
   HOS_HIP_CHECK(hipGetLastError());
@@ -715,15 +715,17 @@ void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, 
 
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
-                     long long ldd, float* part, void* scratch, hipStream_t st) {
+                     long long ldd, float* part, void* scratch, hipStream_t st, bool qkv_planes) {
   check_layout(ld, kcol, vcol, hd, scratch);
   HOS_REQUIRE(nh == nkv || part != nullptr, HOS_E_INVALID, "attention: GQA backward needs a partial buffer");
   HOS_REQUIRE(ldo % 4 == 0 && ldd % 4 == 0 && nkv > 0 && nh % nkv == 0, HOS_E_INVALID, "attention: unaligned layout");
   if (B <= 0 || T <= 0) return;
   if (hd == 64)
-    attn_bwd_hd<64>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st);
+    attn_bwd_hd<64>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st,
+                    qkv_planes);
   else
-    attn_bwd_hd<128>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st);
+    attn_bwd_hd<128>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st,
+                     qkv_planes);
 }
 
 }  // namespace hos

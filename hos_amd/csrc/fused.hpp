@@ -35,11 +35,12 @@ void launch_fill(float* p, long long n, float v, hipStream_t st);
 void launch_copy_rows(const float* src, long long lds, float* dst, long long ldd, int rows, int cols,
                       hipStream_t st);
 // Attention (attention.hip). `scratch` holds the bf16 hi/lo planes of q, k, v and dO: attn_scratch_bytes(...)
-// bytes, 16-byte aligned; its contents need not survive between the calls.
+// bytes, 16-byte aligned; its contents need not survive between the calls — except that a backward with
+// qkv_planes = true reuses the q, k, v planes the forward of the same qkv left in the same scratch.
 size_t attn_scratch_bytes(int B, int T, int nh, int nkv, int hd);
 void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,
                      float* o, long long ldo, float* lse, void* scratch, hipStream_t st);
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
-                     long long ldd, float* part, void* scratch, hipStream_t st);
+                     long long ldd, float* part, void* scratch, hipStream_t st, bool qkv_planes = false);
 }  // namespace hos

@@ -123,7 +123,9 @@ struct hos_peft {
   float *row_loss = nullptr, *loss = nullptr;
   float *dx = nullptr, *dxn = nullptr, *dqkv = nullptr, *dout = nullptr, *dh = nullptr, *dgu = nullptr,
         *du = nullptr, *dvec = nullptr, *attn_part = nullptr;
-  void* attn_planes = nullptr;  // bf16 hi/lo planes of q, k, v, dO (attention scratch)
+  // bf16 hi/lo planes of q, k, v, dO (attention scratch), one per layer: the backward reuses the q, k, v planes
+  // its layer's forward made
+  std::vector<void*> attn_planes;
   float* ws = nullptr;
   size_t ws_bytes = 0;
   float2* rope_tab = nullptr;
@@ -619,7 +621,7 @@ struct hos_peft {
         Scope s(this, "attn_fwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 2,
                 4.0 * M * (W3 + qd) + 4.0 * B * c.n_heads * T);
         launch_attn_fwd(a.qkv, W3, qd, qd + kvd, B, T, c.n_heads, c.n_kv_heads, c.head_dim, a.o, qd, a.lse,
-                        attn_planes, st);
+                        attn_planes[l], st);
       }
       to16(a.o, qd, M, qd);
       lora_down(l, 1, a.o, qd, M, hs_in());
@@ -722,7 +724,7 @@ struct hos_peft {
         Scope s(this, "attn_bwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 5,
                 4.0 * M * (W3 * 2 + qd * 2) + 8.0 * B * c.n_heads * T);
         launch_attn_bwd(a.qkv, W3, qd, qd + kvd, a.o, dout, qd, a.lse, dvec, B, T, c.n_heads, c.n_kv_heads,
-                        c.head_dim, dqkv, W3, attn_part, attn_planes, st);
+                        c.head_dim, dqkv, W3, attn_part, attn_planes[l], st, true);
       }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
@@ -1099,7 +1101,9 @@ struct hos_peft {
     du = alloc<float>(M * NT * r);
     dvec = alloc<float>(M * c.n_heads);
     if (c.n_heads != c.n_kv_heads) attn_part = alloc<float>(M * c.n_heads * 2 * c.head_dim);
-    attn_planes = alloc<float>(attn_scratch_bytes(c.max_batch, c.max_seq, c.n_heads, c.n_kv_heads, c.head_dim) / 4);
+    attn_planes.resize(L);
+    for (int l = 0; l < L; l++)
+      attn_planes[l] = alloc<float>(attn_scratch_bytes(c.max_batch, c.max_seq, c.n_heads, c.n_kv_heads, c.head_dim) / 4);
     ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(d, F) * 4 * 8, 1ull << 30));
     ws = alloc<float>(ws_bytes / 4);
     cbatch = ColsBatch{};
