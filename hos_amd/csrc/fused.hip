@@ -496,19 +496,26 @@ __device__ __forceinline__ void sm_merge(float& m, float& s, float m2, float s2)
 }
 
 // Softmax cross-entropy forward + backward of one row (src/tensor.rs:2709-2743): one read of the logits
-// for the row max and exp-sum together (online softmax), one more to write the gradient
+// for the row max and exp-sum together (online softmax) — or, given rstat, the (max, exp-sum) of each 64-column
+// chunk that the head GEMM's epilogue computed, merged in chunk order — and one more to write the gradient
 // (p − onehot)·gscale as the fp16 row-scaled operand of the head's dX GEMM.
 __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits, int V,
                                                  const int32_t* __restrict__ targets, float gscale,
                                                  float* __restrict__ row_loss, _Float16* __restrict__ dl,
                                                  _Float16* __restrict__ dll, float* __restrict__ rinv,
-                                                 float* __restrict__ dl32) {
+                                                 float* __restrict__ dl32, const float2* __restrict__ rstat, int nch) {
   __shared__ float rm[RB / 64], rs[RB / 64];
   const int row = blockIdx.x;
   const float* lr = logits + (long long)row * V;
   float m = -INFINITY, sum = 0.0f;
   const bool vec = (V & 3) == 0;
-  if (vec) {
+  if (rstat) {
+    const float2* rr = rstat + (long long)row * nch;
+    for (int c = threadIdx.x; c < nch; c += RB) {
+      const float2 x = rr[c];
+      sm_merge(m, sum, x.x, x.y);
+    }
+  } else if (vec) {
     const float4* l4 = reinterpret_cast<const float4*>(lr);
     auto add4 = [&](float4 x) {
       sm_add(m, sum, x.x);
@@ -767,8 +774,9 @@ void launch_swiglu_bwd(const float* gu, const float* dh, int M, int F, float* dg
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_ce(const float* logits, int M, int V, const int32_t* targets, float gscale, float* row_loss, H16 dl,
-               hipStream_t st, float* dl32) {
-  ce_kernel<<<M, RB, 0, st>>>(logits, V, targets, gscale, row_loss, dl.data, dl.lo, dl.rinv, dl32);
+               hipStream_t st, float* dl32, const float2* rstat) {
+  ce_kernel<<<M, RB, 0, st>>>(logits, V, targets, gscale, row_loss, dl.data, dl.lo, dl.rinv, dl32, rstat,
+                              (V + 63) / 64);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_loss_reduce(const float* row_loss, int B, int T, float* loss, hipStream_t st) {

@@ -17,9 +17,10 @@ void launch_rope_h16(float* buf, long long ld, int n_heads, int hd, int T, const
                      int M, int W, H16 out, hipStream_t st);
 void launch_swiglu_fwd(const float* gu, int M, int F, float* h, H16 out, hipStream_t st);
 void launch_swiglu_bwd(const float* gu, const float* dh, int M, int F, float* dgu, H16 out, hipStream_t st);
-// dl32 != null: write the gradient as plain f32 there instead of the fp16 operand dl.
+// dl32 != null: write the gradient as plain f32 there instead of the fp16 operand dl. rstat != null: the row's
+// (max, exp-sum) per 64-column chunk, from the epilogue of the GEMM that wrote the logits (one read of them less).
 void launch_ce(const float* logits, int M, int V, const int32_t* targets, float gscale, float* row_loss, H16 dl,
-               hipStream_t st, float* dl32 = nullptr);
+               hipStream_t st, float* dl32 = nullptr, const float2* rstat = nullptr);
 void launch_loss_reduce(const float* row_loss, int B, int T, float* loss, hipStream_t st);
 void launch_adamw(float* p, const float* g, float* m, float* v, long long n, float lr, float b1, float b2, float eps,
                   float wd, float bc1, float bc2, bool decay, hipStream_t st);

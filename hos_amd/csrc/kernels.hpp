@@ -125,6 +125,10 @@ struct GemmEpi {
   // Column segments of a stacked projection (q|k|v, gate|up): output columns n >= ub0 (and >= ub1) take their U
   // block ustep (2·ustep) columns further on — each target's own rank-r factor. 0 = one U for all columns.
   int ustep = 0, ub0 = 0, ub1 = 0;
+  // Row statistics of the output for a softmax over each row (forward launches): rstat[row·rstat_ld + col/64] =
+  // (max, Σ e^(y − max)) over the 64-column chunk of that row (set: the launch takes unsplit 128-column tiles).
+  float2* rstat = nullptr;
+  long long rstat_ld = 0;
 };
 // Grouped (mixture-of-experts) GEMM schedule: W holds n_experts stacked [rows, cols] blocks; workgroup row
 // y of the launch computes rows tiles[3y+1] .. +tiles[3y+2] of the operand against expert tiles[3y]

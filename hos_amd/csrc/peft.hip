@@ -119,6 +119,7 @@ struct hos_peft {
   float* invf = nullptr;
   H16 hs{};                 // fp16 operand scratch [Mmax, hs_cols]
   float* logits = nullptr;
+  float2* lstat = nullptr;  // (max, exp-sum) of each 64-column chunk of the logit rows, from the head GEMM
   H16 dl{};
   float *row_loss = nullptr, *loss = nullptr;
   float *dx = nullptr, *dxn = nullptr, *dqkv = nullptr, *dout = nullptr, *dh = nullptr, *dgu = nullptr,
@@ -654,7 +655,10 @@ struct hos_peft {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d + 2.0 * M * d);
       launch_rmsnorm_fwd(xfinal, out_norm, c.rms_eps, M, d, nullptr, hs, invf, st);
     }
-    qfwd(out_set ? out : tok, hs, d, M, logits, V, nullptr, nullptr, 0, GemmEpi{}, phf);
+    GemmEpi he{};
+    he.rstat = lstat;  // the cross-entropy's softmax statistics come out of the head GEMM's epilogue
+    he.rstat_ld = (V + 63) / 64;
+    qfwd(out_set ? out : tok, hs, d, M, logits, V, nullptr, nullptr, 0, he, phf);
     (void)need_logits_only;
   }
 
@@ -664,7 +668,7 @@ struct hos_peft {
     {
       Scope s(this, "ce", 0, 4.0 * M * V + 2.0 * M * V);
       float gscale = (1.0f / (float)B) / (float)T;  // scale(1/B) then CE's g/n (src/tensor.rs:2736-2741)
-      launch_ce(logits, M, V, tgts, gscale, row_loss, dl, st);
+      launch_ce(logits, M, V, tgts, gscale, row_loss, dl, st, nullptr, lstat);
       launch_loss_reduce(row_loss, B, T, loss, st);
     }
     if (rga && rlambda > 0.0f) {
@@ -1087,6 +1091,7 @@ struct hos_peft {
     const bool alo = alo_mode(pf) || alo_mode(pd) || alo_mode(phf);
     hs.lo = alo ? alloc<half_t>(M * hcols) : nullptr;
     logits = alloc<float>(M * V);
+    lstat = alloc<float2>(M * (size_t)((V + 63) / 64));
     dl.data = alloc<half_t>(M * V);
     dl.rinv = alloc<float>(M);
     dl.lo = alo_mode(phd) ? alloc<half_t>(M * V) : nullptr;

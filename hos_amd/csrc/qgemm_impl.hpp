@@ -43,6 +43,10 @@ namespace {
 typedef short s4v __attribute__((ext_vector_type(4)));
 
 
+// e^d for the row statistics of a softmax: hardware exp2 of d·log2 e (one rounding of the product, ~1 ulp exp2;
+// the exponents that matter are small).
+__device__ __forceinline__ float exp_rs(float d) { return __builtin_amdgcn_exp2f(d * 1.4426950408889634f); }
+
 // Signed byte i of a word as float (one bit-field extract + one convert).
 __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
 // Unsigned byte i as float (maps to v_cvt_f32_ubyte<i>).
@@ -556,6 +560,17 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
   if constexpr (G::SMEM * 2 >= G::NT / 64 * 32 * TS * 4) {
     __syncthreads();  // every wave is done with the main loop's and the rank term's LDS
     float* tb = reinterpret_cast<float*>(smem) + wave * 32 * TS;
+    // row statistics (epi.rstat): this wave's rows over its 64 columns, one (max, exp-sum) per lane per (i, pass)
+    // folded over the TN column tiles, then over the 8 lanes of a row
+    const bool stats = epi.rstat != nullptr && !split;
+    float smx[G::TM][4], ssm[G::TM][4];
+#pragma unroll
+    for (int i = 0; i < G::TM; i++)
+#pragma unroll
+      for (int pz = 0; pz < 4; pz++) {
+        smx[i][pz] = -INFINITY;
+        ssm[i][pz] = 0.0f;
+      }
     const bool vec = (Nout & 3) == 0 && (split || ((epi.ldo & 3) == 0 && ((uintptr_t)epi.out & 15) == 0 &&
                                                   (!epi.resid || ((uintptr_t)epi.resid & 15) == 0) &&
                                                   (!epi.bias || ((uintptr_t)epi.bias & 15) == 0)));
@@ -592,15 +607,60 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
               y = make_float4(q.x + y.x, q.y + y.y, q.z + y.z, q.w + y.w);
             }
             *reinterpret_cast<float4*>(o) = y;
+            if (stats) {
+              const float yv[4] = {y.x, y.y, y.z, y.w};
+              float mx = -INFINITY;
+#pragma unroll
+              for (int e = 0; e < 4; e++)
+                if (col + e < Nout) mx = fmaxf(mx, yv[e]);
+              float& m = smx[i][pz];
+              float& sm = ssm[i][pz];
+              if (mx > m) {
+                sm = m == -INFINITY ? 0.0f : sm * exp_rs(m - mx);
+                m = mx;
+              }
+#pragma unroll
+              for (int e = 0; e < 4; e++)
+                if (col + e < Nout) sm += exp_rs(yv[e] - m);
+            }
           } else {
             for (int e = 0; e < 4 && col + e < Nout; e++) {
               float x = v[e] * ri;
               if (epi.bias) x += epi.bias[col + e];
-              o[e] = epi.accumulate ? o[e] + x : (epi.resid ? epi.resid[off + e] + x : x);
+              x = epi.accumulate ? o[e] + x : (epi.resid ? epi.resid[off + e] + x : x);
+              o[e] = x;
+              if (stats) {
+                float& m = smx[i][pz];
+                float& sm = ssm[i][pz];
+                if (x > m) {
+                  sm = m == -INFINITY ? 0.0f : sm * exp_rs(m - x);
+                  m = x;
+                }
+                sm += exp_rs(x - m);
+              }
             }
           }
         }
       }
+    if (stats) {
+      // the 8 lanes of a row (lane bits 0-2) merge in a fixed tree order; lane 8·k writes row 8·pz + k
+      const long long chunk = (n0 + wn * (BN / 2)) / 64;
+#pragma unroll
+      for (int i = 0; i < G::TM; i++)
+#pragma unroll
+        for (int pz = 0; pz < 4; pz++) {
+          float m = smx[i][pz], sm = ssm[i][pz];
+#pragma unroll
+          for (int o = 1; o < 8; o <<= 1) {
+            const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(sm, o), mn = fmaxf(m, m2);
+            sm = (m == -INFINITY ? 0.0f : sm * exp_rs(m - mn)) + (m2 == -INFINITY ? 0.0f : s2 * exp_rs(m2 - mn));
+            m = mn;
+          }
+          const int row = m0 + wm * (BM / G::WGM) + 32 * i + 8 * pz + (lane >> 3);
+          if ((lane & 7) == 0 && row < M && n0 + wn * (BN / 2) < Nout)
+            epi.rstat[(long long)row * epi.rstat_ld + chunk] = make_float2(m, sm);
+        }
+    }
     return;
   }
 #pragma unroll
@@ -725,6 +785,9 @@ void launch_shape(const QWeight& w, H16 a, long long lda, long long M, int Nout,
                   GemmEpi epi, float* ws, hipStream_t st) {
   constexpr int rcap = Geo<BM, BN, BK, DX, NP>::RCAP;
   HOS_REQUIRE(epi.rank <= rcap, HOS_E_INVALID, "qgemm: fused rank exceeds the tile's staging");
+  HOS_REQUIRE(!epi.rstat || (BN == 128 && splits == 1 &&
+                             Geo<BM, BN, BK, DX, NP>::SMEM * 2 >= Geo<BM, BN, BK, DX, NP>::NT / 64 * 32 * 40 * 4),
+              HOS_E_INVALID, "qgemm: row statistics need the staged epilogue on unsplit 128-column tiles");
   dim3 grid(ceil_div(Nout, BN), ceil_div(M, BM), splits);
   qgemm_kernel<QT, DX, BM, BN, BK, NP>
       <<<grid, Geo<BM, BN, BK, DX, NP>::NT, 0, st>>>(view(w), a.data, a.lo, a.rinv, lda, (int)M, Nout, C, per, epi, ws,
@@ -803,10 +866,17 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     }
     HOS_REQUIRE(fits(bn), HOS_E_INVALID, "qgemm: column segments must be multiples of 64");
   }
+  // Row statistics: the epilogue folds them per wave over 64 output columns, i.e. unsplit 128-column tiles.
+  if (epi.rstat) {
+    HOS_REQUIRE(!DX && !useg, HOS_E_INVALID, "qgemm: row statistics are for plain forward launches");
+    bm = one_plane ? 256 : 128;
+    bn = 128;
+    bk = 32;
+  }
   int tiles = ntiles(bm, bn);
   int nslab = C / bk;
   int splits = 1;
-  while (!useg && epi.rank <= 32 && tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
+  while (!epi.rstat && !useg && epi.rank <= 32 && tiles * splits < 320 && nslab / (splits * 2) >= 8 &&
          (size_t)(splits * 2) * M * Nout * sizeof(float) <= ws_bytes)
     splits *= 2;
 #ifdef HOS_QG_ENV_TILE
@@ -847,7 +917,7 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
   HOS_REQUIRE(C % 32 == 0 && lda % 8 == 0, HOS_E_INVALID, "grouped qgemm: contraction must be a multiple of 32");
   HOS_REQUIRE((NP != 2 && NP != 3 && NP != 5) || a.lo != nullptr, HOS_E_INVALID,
               "grouped qgemm: needs the operand residual");
-  HOS_REQUIRE(epi.rank == 0, HOS_E_INVALID, "grouped qgemm: no fused rank-r term");
+  HOS_REQUIRE(epi.rank == 0 && !epi.rstat, HOS_E_INVALID, "grouped qgemm: no fused rank-r term or row statistics");
   GroupKernelArgs gk;
   gk.tiles = gs.tiles;
   gk.rows = er;
