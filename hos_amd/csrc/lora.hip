@@ -287,34 +287,37 @@ __global__ void __launch_bounds__(64 * ROWS_WIDE_NW) lora_rows_wide_kernel(int M
 // Workgroup: 64 columns of one segment × all j × an m-chunk; wave w takes the chunk's 4-row steps
 // w, w+4, … Lane (q, p): m = step + q, columns c0+4p .. +3 (one float4; component e is MFMA tile e).
 // bx: the workgroup's column block within its job; red: LDS of at least 2·NS·16·64 floats.
-template <int NS, bool GH>
+// CW = 8 (GH only): a lane takes 8 consecutive columns (16-byte loads of each plane, 8 MFMA tiles), the block is
+// 128 columns wide.
+template <int NS, bool GH, int CW = 4>
 __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, int mchunk, float* red, float* part) {
-  constexpr int NJR = NS * 16, E = NJR * 64;
+  static_assert(CW == 4 || (CW == 8 && GH), "column run");
+  constexpr int BW = 16 * CW, NJR = NS * 16, E = NJR * BW;
   const ColsSeg& sg = jb.sg;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
   int t = 0;
 #pragma unroll
   for (int i = 1; i < 4; i++)
     if (i < sg.nseg && bx >= sg.blk0[i]) t = i;
-  const int c0 = (bx - sg.blk0[t]) * 64, len = sg.len[t];
+  const int c0 = (bx - sg.blk0[t]) * BW, len = sg.len[t];
   const int mb = blockIdx.y * mchunk, me = min(M, mb + mchunk);
-  const bool cv = c0 + 4 * p < len;
-  const long long gcol = sg.gbeg[t] + c0 + 4 * p;
+  const bool cv = c0 + CW * p < len;
+  const long long gcol = sg.gbeg[t] + c0 + CW * p;
   const float* scol = jb.Sm + sg.soff[t];
   const long long lds = jb.lds, ldg = jb.ldg;
   const int ns = jb.ns;
 
-  f4v acc[NS][4];
+  f4v acc[NS][CW];
 #pragma unroll
   for (int js = 0; js < NS; js++)
 #pragma unroll
-    for (int e = 0; e < 4; e++) acc[js][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int e = 0; e < CW; e++) acc[js][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
   // HOS_COLS_UNROLL 4-row steps per trip, loads first (as in the rows kernel; zero steps past the end add
   // exact zeros, so the summation order per accumulator is that of one step per trip).
   constexpr int U = HOS_COLS_UNROLL;
   for (int m40 = mb + 4 * wave; m40 < me; m40 += 16 * U) {
-    float4 g[U];
+    float g[U][CW];
     float s[U][NS];
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -322,12 +325,27 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
       const bool mv = m < me;
       // G given as the fp16 operand (GH): its row scale joins S (Σ_m S[m,j]·rinv[m]·(hi+lo)[m,c])
       float ri = 1.0f;
-      if constexpr (GH) {
-        g[u] = (mv && cv) ? load4h(jb.gh, gcol + (long long)m * ldg) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (CW == 8) {
+        const long long off = gcol + (long long)m * ldg;
+        const h8 zh = {};
+        const h8 a = (mv && cv) ? *reinterpret_cast<const h8*>(jb.gh.hi + off) : zh;
+        const h8 b = (mv && cv) ? *reinterpret_cast<const h8*>(jb.gh.lo + off) : zh;
+#pragma unroll
+        for (int e = 0; e < 8; e++) g[u][e] = (float)a[e] + (float)b[e];
         ri = mv ? jb.gh.rinv[m] : 0.0f;
       } else {
-        g[u] = (mv && cv) ? *reinterpret_cast<const float4*>(jb.Gm + gcol + (long long)m * ldg)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 x;
+        if constexpr (GH) {
+          x = (mv && cv) ? load4h(jb.gh, gcol + (long long)m * ldg) : make_float4(0.f, 0.f, 0.f, 0.f);
+          ri = mv ? jb.gh.rinv[m] : 0.0f;
+        } else {
+          x = (mv && cv) ? *reinterpret_cast<const float4*>(jb.Gm + gcol + (long long)m * ldg)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        g[u][0] = x.x;
+        g[u][1] = x.y;
+        g[u][2] = x.z;
+        g[u][3] = x.w;
       }
 #pragma unroll
       for (int js = 0; js < NS; js++) {
@@ -339,30 +357,27 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
     for (int u = 0; u < U; u++)
       if (m40 + 16 * u < me)  // wave-uniform
 #pragma unroll
-      for (int js = 0; js < NS; js++) {
-        acc[js][0] = mfma16(s[u][js], g[u].x, acc[js][0]);
-        acc[js][1] = mfma16(s[u][js], g[u].y, acc[js][1]);
-        acc[js][2] = mfma16(s[u][js], g[u].z, acc[js][2]);
-        acc[js][3] = mfma16(s[u][js], g[u].w, acc[js][3]);
-      }
+      for (int js = 0; js < NS; js++)
+#pragma unroll
+        for (int e = 0; e < CW; e++) acc[js][e] = mfma16(s[u][js], g[u][e], acc[js][e]);
   }
 
-  // flatten: element (j = 16js+4q+i, column 4p+e) of the NJR×64 block
-  float v[NS * 16];
+  // flatten: element (j = 16js+4q+i, column CW·p+e) of the NJR×BW block
+  float v[NS * 4 * CW];
 #pragma unroll
   for (int js = 0; js < NS; js++)
 #pragma unroll
-    for (int e = 0; e < 4; e++)
+    for (int e = 0; e < CW; e++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) v[(js * 4 + e) * 4 + i] = acc[js][e][i];
+      for (int i = 0; i < 4; i++) v[(js * CW + e) * 4 + i] = acc[js][e][i];
   wave_reduce(v, red, E, [&](int idx) {
-    const int i = idx & 3, e = (idx >> 2) & 3, js = idx >> 4;
-    return (16 * js + 4 * q + i) * 64 + 4 * p + e;
+    const int i = idx & 3, e = (idx >> 2) % CW, js = idx / (4 * CW);
+    return (16 * js + 4 * q + i) * BW + CW * p + e;
   });
   if (gridDim.y == 1) {
     const long long ocol = sg.ocol[t];
     for (int e = threadIdx.x; e < E; e += 256) {
-      const int j = e / 64, c = c0 + e % 64;
+      const int j = e / BW, c = c0 + e % BW;
       if (j < ns && c < len) jb.C[(long long)j * jb.scj + (ocol + c) * jb.scc] = jb.alpha * red[e];
     }
     return;
@@ -375,12 +390,12 @@ __device__ __forceinline__ void cols_body(const ColsJobDev& jb, int bx, int M, i
 // Two independent jobs over the same contraction length in one launch: workgroups [0, b.bx0) run job a with
 // NSA row tiles, the rest job b with NSB. A single job passes b with bx0 = the grid width. GHA: job a reads G
 // as the fp16 operand (job b never does).
-template <int NSA, int NSB, bool GHA>
+template <int NSA, int NSB, bool GHA, int CWA = 4>
 __global__ void __launch_bounds__(256) lora_cols_kernel(int M, int mchunk, ColsJobDev a, ColsJobDev b, float* part) {
-  constexpr int EMAX = (NSA > NSB ? NSA : NSB) * 16 * 64;
+  constexpr int EA = NSA * 16 * 16 * CWA, EB = NSB * 16 * 64, EMAX = EA > EB ? EA : EB;
   __shared__ float red[2 * EMAX];
   if ((int)blockIdx.x < b.bx0)
-    cols_body<NSA, GHA>(a, (int)blockIdx.x, M, mchunk, red, part);
+    cols_body<NSA, GHA, CWA>(a, (int)blockIdx.x, M, mchunk, red, part);
   else
     cols_body<NSB, false>(b, (int)blockIdx.x - b.bx0, M, mchunk, red, part);
 }
@@ -397,13 +412,13 @@ __global__ void lora_rows_reduce(const float* __restrict__ part, int S, int gx, 
 }
 // One thread per output element of every block of both jobs (job a's elements first).
 __device__ __forceinline__ void cols_reduce_one(const ColsJobDev& jb, const float* part, int S, long long i) {
-  const int E = jb.nsr * 64;
+  const int E = jb.nsr * jb.bw;
   const int bx = (int)(i / E), e = (int)(i % E);
   const ColsSeg& sg = jb.sg;
   int t = 0;
   for (int k = 1; k < sg.nseg; k++)
     if (bx >= sg.blk0[k]) t = k;
-  const int j = e / 64, c = (bx - sg.blk0[t]) * 64 + e % 64;
+  const int j = e / jb.bw, c = (bx - sg.blk0[t]) * jb.bw + e % jb.bw;
   if (j >= jb.ns || c >= sg.len[t]) return;
   jb.C[(long long)j * jb.scj + ((long long)sg.ocol[t] + c) * jb.scc] =
       jb.alpha * sum_parts(part + jb.part_off, S, jb.gx, bx, E, e);
@@ -421,7 +436,7 @@ __global__ void lora_cols_reduce_batch(const float* __restrict__ base, ColsBatch
   cols_reduce_one(args.jobs[j], base, args.jobs[j].S, i - args.start[j]);
 }
 __global__ void lora_cols_reduce(const float* __restrict__ part, int S, ColsJobDev a, ColsJobDev b) {
-  const long long na = (long long)a.gx * a.nsr * 64, nb = (long long)b.gx * b.nsr * 64;
+  const long long na = (long long)a.gx * a.nsr * a.bw, nb = (long long)b.gx * b.nsr * b.bw;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < na)
     cols_reduce_one(a, part, S, i);
@@ -699,12 +714,16 @@ ColsJobDev prepare(const ColsJob& j, int bx0) {
   d.nsr = (j.ns + 15) / 16 * 16;
   d.sg = j.sg;
   d.gh = j.gh;
+  // the fp16 operand in 16-byte runs where its rows, planes and segments allow (128-column blocks)
+  bool wide = j.gh.hi && j.ldg % 8 == 0 && ((uintptr_t)j.gh.hi & 15) == 0 && ((uintptr_t)j.gh.lo & 15) == 0;
+  for (int t = 0; t < j.sg.nseg; t++) wide = wide && j.sg.gbeg[t] % 8 == 0 && j.sg.len[t] % 8 == 0;
+  d.bw = wide ? 128 : 64;
   int gx = 0;
   for (int t = 0; t < j.sg.nseg; t++) {
     HOS_REQUIRE(j.sg.gbeg[t] % 4 == 0 && j.sg.len[t] % 4 == 0 && j.sg.len[t] > 0, HOS_E_INVALID,
                 "lora_cols: segment columns must be multiples of 4");
     d.sg.blk0[t] = gx;
-    gx += ceil_div_i(j.sg.len[t], 64);
+    gx += ceil_div_i(j.sg.len[t], d.bw);
   }
   d.gx = gx;
   d.bx0 = bx0;
@@ -728,8 +747,8 @@ void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float*
   int S = 0, mchunk = 0;
   cols_split(M, gx, &S, &mchunk);
   a.part_off = 0;
-  b.part_off = (long long)S * a.gx * a.nsr * 64;
-  const long long need = b.part_off + (long long)S * b.gx * b.nsr * 64;
+  b.part_off = (long long)S * a.gx * a.nsr * a.bw;
+  const long long need = b.part_off + (long long)S * b.gx * b.nsr * b.bw;
   a.S = b.S = S;
   // deferred: the partials go to the batch buffer (offsets relative to its base) and the reduction waits for
   // the flush
@@ -747,7 +766,9 @@ void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float*
   dim3 grid(gx, S);
 #define COLS(X, Y)                                                                          \
   if (NA == X && NB == Y && !bgh) {                                                         \
-    if (a.gh.hi)                                                                            \
+    if (a.gh.hi && a.bw == 128)                                                             \
+      lora_cols_kernel<X, Y, true, 8><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, part);    \
+    else if (a.gh.hi)                                                                       \
       lora_cols_kernel<X, Y, true><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, part);       \
     else                                                                                    \
       lora_cols_kernel<X, Y, false><<<grid, 256, 0, st>>>((int)M, mchunk, a, b, part);      \
@@ -772,7 +793,7 @@ void launch_lora_cols2(long long M, const ColsJob& ja, const ColsJob* jb, float*
     return;
   }
   if (S > 1) {
-    const long long tot = (long long)a.gx * a.nsr * 64 + (long long)b.gx * b.nsr * 64;
+    const long long tot = (long long)a.gx * a.nsr * a.bw + (long long)b.gx * b.nsr * b.bw;
     lora_cols_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, a, b);
     HOS_HIP_CHECK(hipGetLastError());
   }
@@ -784,7 +805,7 @@ size_t lora_cols2_ws_bytes(long long M, const ColsJob& ja, const ColsJob* jb) {
   const ColsJobDev b = jb ? prepare(*jb, a.gx) : ColsJobDev{};
   int S = 0, mchunk = 0;
   cols_split(M, a.gx + (jb ? b.gx : 0), &S, &mchunk);
-  size_t need = S > 1 ? (size_t)S * ((size_t)a.gx * a.nsr + (jb ? (size_t)b.gx * b.nsr : 0)) * 64 * 4 : 0;
+  size_t need = S > 1 ? (size_t)S * ((size_t)a.gx * a.nsr * a.bw + (jb ? (size_t)b.gx * b.nsr * b.bw : 0)) * 4 : 0;
   if (jb && a.nsr != b.nsr)  // some width pairs have no combined kernel and run as two launches in turn
     need = std::max({need, lora_cols2_ws_bytes(M, ja, nullptr), lora_cols2_ws_bytes(M, *jb, nullptr)});
   return need;
@@ -797,7 +818,7 @@ void launch_lora_cols_flush(ColsBatch& bt, hipStream_t st) {
     for (int j = 0; j < bt.n; j++) {
       args.jobs[j] = bt.jobs[j];
       args.start[j] = tot;
-      tot += (long long)bt.jobs[j].gx * bt.jobs[j].nsr * 64;
+      tot += (long long)bt.jobs[j].gx * bt.jobs[j].nsr * bt.jobs[j].bw;
     }
     args.start[bt.n] = tot;
     args.n = bt.n;

@@ -80,7 +80,8 @@ struct ColsJobDev {
   long long lds, ldg, scj, scc, part_off;
   float alpha;
   int ns, nsr, gx, bx0;
-  int S;  // splits of M the partials were written with
+  int bw;  // columns per workgroup block: 64, or 128 for a G read as 16-byte runs of the fp16 operand's planes
+  int S;   // splits of M the partials were written with
   ColsSeg sg;
   HIn gh;
 };

@@ -698,10 +698,9 @@ struct hos_peft {
       qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD), tpd[TD]);
       lora_grad_a(l, 3, a.h, F, M);
       // The gate|up LoRA gradients read d(gate|up) from the fp16 operand the SwiGLU backward writes for the dX
-      // GEMM when it carries the residual plane and is small enough to stay in the last-level cache (128 MB):
-      // the dB pass reads each plane in 128-byte row pieces, at half the rate of the f32 copy's 256 from HBM.
-      const bool gu_lora = has(TG) || has(TU),
-                 gu_f32 = gu_lora && (!hs.lo || (double)M * 2 * F * 4 > 128.0 * (1 << 20));
+      // GEMM when it carries the residual plane (the dB pass in 16-byte runs of each plane); an f32 copy only for
+      // single-plane precision modes.
+      const bool gu_lora = has(TG) || has(TU), gu_f32 = gu_lora && !hs.lo;
       {
         Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (gu_f32 ? 8.0 * M * F : 0));
         launch_swiglu_bwd(a.gu, dh, M, F, gu_f32 ? dgu : nullptr, hs, st);
