@@ -585,15 +585,19 @@ void cols_split(long long M, int gx, int* S, int* mchunk) {
 
 }  // namespace
 
-// Split of an fp16 rows launch: enough workgroups (16-row blocks × contraction chunks of whole 32·16-deep
-// wave rounds) to cover the chip about twice, each chunk at least HOS_R16_MINROUNDS rounds (the reduction
-// launch costs more than a short chunk saves).
+// Split of an fp16 rows launch: about HOS_R16_TARGET workgroups (16-row blocks × contraction chunks of whole
+// 32·16-deep wave rounds; one 16-wave workgroup per CU — measured at Qwen2.5-0.5B: 256 beat 128 and 512, e.g. the
+// gate|up du 24.4 µs at 2 splits against 27.7 at 4 and 31.7 at 7), each chunk at least HOS_R16_MINROUNDS rounds
+// (the reduction launch costs more than a short chunk saves).
+#ifndef HOS_R16_TARGET
+#define HOS_R16_TARGET 256
+#endif
 #ifndef HOS_R16_MINROUNDS
 #define HOS_R16_MINROUNDS 4
 #endif
 void rows16_split(long long M, long long K, int* S, int* kchunk) {
   const int gx = ceil_div_i(M, 16), round = 32 * R16_NW;
-  int s = std::max(1, std::min(ceil_div_i(512, gx), (int)(K / ((long long)round * HOS_R16_MINROUNDS))));
+  int s = std::max(1, std::min(ceil_div_i(HOS_R16_TARGET, gx), (int)(K / ((long long)round * HOS_R16_MINROUNDS))));
   *kchunk = ceil_div_i(ceil_div_i(K, s), round) * round;
   *S = std::max(1, ceil_div_i(K, *kchunk));
 }
