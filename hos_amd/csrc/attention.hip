@@ -37,6 +37,11 @@ constexpr int BR = TB * NW;   // rows a workgroup owns
 // Wave groups splitting the streamed axis of a workgroup. Forward: three at head dim 64 (a third of the key range
 // each, 110 KB of LDS; measured 3-6% faster than two), two at 128 (three would need 204 KB). Backward: two, except
 // for head dim 128, whose accumulators need more than the 256 registers two waves per SIMD leave (they spill).
+#ifndef HOS_ATT_PRIO
+#define HOS_ATT_PRIO 1
+#endif
+// a wave's products and softmax of one streamed tile run at raised issue priority, its loads and LDS stores not
+constexpr bool ATT_PRIO = HOS_ATT_PRIO;
 template <int HD>
 constexpr int fwd_groups() { return HD == 64 ? 3 : 2; }
 template <int HD>
@@ -268,6 +273,7 @@ __global__ void __launch_bounds__(256 * NG) attn_fwd_kernel(const __bf16* __rest
     const int kb = kbeg + it;
     const __bf16* st = sm[grp][it & 1];
     ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, gt);  // past the range: a harmless re-read
+    if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(1);
     if (kb < kend && kb <= my_last) {
       f16v S;
 #pragma unroll
@@ -317,6 +323,7 @@ __global__ void __launch_bounds__(256 * NG) attn_fwd_kernel(const __bf16* __rest
                            pl, O[i]);
       }
     }
+    if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(0);
     ld.store(sm[grp][(it + 1) & 1], gt);
     __syncthreads();
   }
@@ -405,6 +412,7 @@ __global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restr
     const int kb = kbeg + it;
     const __bf16* st = sm[grp][it & 1];
     ld.load(planes, krow0, min(kb + 1, nkb - 1) * TB, T, gt);  // past the range: a harmless re-read
+    if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(1);
     if (kb < kend && kb <= my_last) {
       f16v S, dP;
 #pragma unroll
@@ -433,6 +441,7 @@ __global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restr
           A[i] = mma3_bf16(tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, A[i]);
       }
     }
+    if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(0);
     ld.store(sm[grp][(it + 1) & 1], gt);
     __syncthreads();
   }
@@ -526,6 +535,7 @@ __global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __res
     const int s = it & 1;
     const __bf16* st = sm[grp][s];
     load(min(qt + 1, nqt - 1));  // past the range: a harmless re-read
+    if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(1);
     if (qt < qend && qt >= my_first) {
       f16v S, dP;
 #pragma unroll
@@ -568,6 +578,7 @@ __global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __res
         }
       }
     }
+    if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(0);
     store(s ^ 1);
     __syncthreads();
   }
