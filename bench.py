@@ -221,7 +221,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards as data parallel over sequences, described in DESIGN.md)", file=sys.stderr)
+              "(the path shards as data parallel over sequences: one all-reduce of the LoRA gradient arena per step)", file=sys.stderr)
         sys.exit(2)
     from hos_amd import Gpu, synth
     from hos_amd.peft import PeftModel
