@@ -48,6 +48,9 @@ struct LayerW {
 
 struct LayerAct {
   float *x, *xn1, *inv1, *qkv, *o, *lse, *x2, *xn2, *inv2, *gu, *h, *u;
+  // the SwiGLU output as the down projection's fp16 operand, kept for the layer's backward (replaces h when the
+  // precision modes carry the residual plane: the down GEMM, its LoRA down-projection and its dA all read it)
+  H16 hd{nullptr, nullptr, nullptr};
   float *qk_pre = nullptr, *qk_inv = nullptr;  // QK-norm: pre-norm q|k [M][qd+kvd], 1/rms [2][M]
   // RGA: residual before the adapter [M][d], gates | relu'd bottlenecks [M][Rp], H ⊙ gate [M][Kbp]
   float *xr = nullptr, *ra = nullptr, *hg = nullptr;
@@ -462,7 +465,8 @@ struct hos_peft {
   }
   // [dA_1 … dA_G]ᵀ = ([du_1 … du_G])ᵀ·x, written straight into the stacked At layout, in one launch with the
   // group's queued dB
-  void lora_grad_a(int l, int g, const float* x, long long ldx, int M) {
+  // xh set: the input is read from that fp16 operand (x is not read)
+  void lora_grad_a(int l, int g, const float* x, long long ldx, int M, HIn xh = HIn{}) {
     const int n = gcount(g);
     if (n == 0) return;
     HOS_REQUIRE(pend_group == g, HOS_E_INVALID, "peft: dA without the group's dB queued");
@@ -471,14 +475,18 @@ struct hos_peft {
     ColsSeg cs;
     cs.nseg = 1;
     cs.len[0] = in;
-    const ColsJob da{n * r, 1.0f, du + ucol(first), NT * r, x, ldx, cs, G + offAg[l * 4 + g], in, 1};
+    const ColsJob da{n * r, 1.0f, du + ucol(first), NT * r, x, ldx, cs, G + offAg[l * 4 + g], in, 1, xh};
     double fl = 2.0 * M * n * r * in, by = 4.0 * (M * (double)in + (double)M * n * r + (double)n * r * in);
     for (int t = 0; t < pend_db.sg.nseg; t++) {
       fl += 2.0 * M * r * pend_db.sg.len[t];
       by += 4.0 * ((double)M * pend_db.sg.len[t] + (double)M * r + (double)r * pend_db.sg.len[t]);
     }
     Scope s(this, "lora_dab", fl, by);
-    launch_lora_cols2(M, pend_db, &da, ws, ws_bytes, st, &cbatch);
+    // (the cols launch takes a job on the fp16 operand first)
+    if (xh.hi)
+      launch_lora_cols2(M, da, &pend_db, ws, ws_bytes, st, &cbatch);
+    else
+      launch_lora_cols2(M, pend_db, &da, ws, ws_bytes, st, &cbatch);
   }
   void flush_dab() {
     Scope s(this, "lora_dab", 0, 0);
@@ -643,12 +651,13 @@ struct hos_peft {
         qfwd(w.w[TG], hs, d, M, a.gu, 2LL * F, nullptr, nullptr, 0, up_epi(l, TG), tpf[TG]);
         qfwd(w.w[TU], hs, d, M, a.gu + F, 2LL * F, nullptr, nullptr, 0, up_epi(l, TU), tpf[TU]);
       }
+      const H16 hdn = a.hd.data ? a.hd : hs;  // the down projection's operand
       {
-        Scope s(this, "swiglu", 0, 8.0 * M * F + 2.0 * M * F + (has(TD) ? 4.0 * M * F : 0));
-        launch_swiglu_fwd(a.gu, M, F, has(TD) ? a.h : nullptr, hs, st);
+        Scope s(this, "swiglu", 0, 8.0 * M * F + 2.0 * M * F + (a.h ? 4.0 * M * F : 0));
+        launch_swiglu_fwd(a.gu, M, F, a.h, hdn, st);
       }
-      lora_down(l, 3, a.h, F, M, hs_in());
-      qfwd(w.w[TD], hs, F, M, rga ? a.xr : xnext, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
+      lora_down(l, 3, a.h, F, M, hdn.lo ? HIn{hdn.data, hdn.lo, hdn.rinv} : HIn{});
+      qfwd(w.w[TD], hdn, F, M, rga ? a.xr : xnext, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
       if (rga) rga_forward(l, M, xnext);
     }
     {
@@ -696,7 +705,7 @@ struct hos_peft {
       if (!fuse16) to16(dx, d, M, d);
       lora_grad_b(l, 3, dx, d, d, M, hs_in());
       qdx(w.w[TD], hs, d, M, dh, F, 0, down_epi(l, TD), tpd[TD]);
-      lora_grad_a(l, 3, a.h, F, M);
+      lora_grad_a(l, 3, a.h, F, M, a.hd.data ? HIn{a.hd.data, a.hd.lo, a.hd.rinv} : HIn{});
       // The gate|up LoRA gradients read d(gate|up) from the fp16 operand the SwiGLU backward writes for the dX
       // GEMM when it carries the residual plane (the dB pass in 16-byte runs of each plane); an f32 copy only for
       // single-plane precision modes.
@@ -1036,7 +1045,14 @@ struct hos_peft {
       a.xn2 = (has(TG) || has(TU) || E) ? alloc<float>(M * d) : nullptr;
       a.inv2 = alloc<float>(M);
       a.gu = E ? nullptr : alloc<float>(M * 2 * F);
-      a.h = has(TD) ? alloc<float>(M * F) : nullptr;
+      if (has(TD) && !E && (alo_mode(pf) || alo_mode(pd) || alo_mode(phf))) {
+        a.h = nullptr;
+        a.hd.data = alloc<half_t>(M * F);
+        a.hd.lo = alloc<half_t>(M * F);
+        a.hd.rinv = alloc<float>(M);
+      } else {
+        a.h = has(TD) ? alloc<float>(M * F) : nullptr;
+      }
       a.u = alloc<float>(M * NT * r);
       if (rga) {
         a.xr = alloc<float>(M * d);
