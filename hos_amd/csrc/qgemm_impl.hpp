@@ -841,11 +841,13 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   }
   // 64-deep slabs where the contraction is long enough to amortize the deeper prologue: two-plane forwards from
   // C 2048 on (M 8192, Q4_K: 2048 -> 16384 1788 vs 1811 us, 8192 -> 2048 899 vs 960; at C 896 32-deep slabs win,
-  // 163 vs 171 us) and the split forward; the two-plane dX keeps 32 (equal or faster at every step shape: split
-  // 9728 -> 896 148 vs 155 us).
+  // 163 vs 171 us) and the split forward; two-plane dX launches from C 2048 on with narrow outputs (≤ 4096 columns:
+  // Llama-3.2-1B's q|k|v and o dX, the step's dX −2.4%), else 32 (equal or faster at the other step shapes: split
+  // 9728 -> 896 148 vs 155 us, 2048 -> 8192 897 vs 912 us).
   const bool deep_fwd = !DX && (NP == 2 || NP == 3) && (C >= 2048 || split_big);
+  const bool deep_dx = DX && (NP == 2 || NP == 3) && C >= 2048 && Nout <= 4096 && !split_big;
   if (C % 64 == 0 &&
-      ((bm == 64 && bn == 64) || ((NP == 1 || longc || deep_fwd) && bm == 128 && bn == 128)))
+      ((bm == 64 && bn == 64) || ((NP == 1 || longc || deep_fwd || deep_dx) && bm == 128 && bn == 128)))
     bk = 64;
   // Single-pass GEMMs are bound by the weight dequantization (VALU) as much as by MFMA: 8 waves on a
   // 256-row tile dequantize each B slab once for twice the MFMA work.
