@@ -66,14 +66,23 @@ def copy_calibration():
 
 def traffic_per_launch(kernel_class, cfg):
     """HBM bytes per launch of `kernel_class` measured by rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated
-    against a plain copy), read from the committed profile summary of this workload when one exists."""
+    against a plain copy), read from the committed profile summary of this workload when one exists, with where it
+    came from: the file, the source revision it was measured on and that run's average launch time (so a tile-rule
+    change that moves the live launch time shows the figure as stale)."""
     path = os.path.join(ROOT, "profiles", f"{kernel_class}_traffic_{cfg.name}_b{cfg.batch}x{cfg.seq}.md")
     if not os.path.exists(path):
-        return None
+        return None, None
+    meta = {"file": os.path.relpath(path, ROOT)}
+    val = None
     for line in open(path):
-        if line.startswith("bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+        for key in ("bytes_per_launch", "measured_at", "avg_launch_us"):
+            if line.startswith(key + ":"):
+                v = line.split(":", 1)[1].strip()
+                if key == "bytes_per_launch":
+                    val = float(v)
+                else:
+                    meta[key] = float(v) if key == "avg_launch_us" else v
+    return val, meta
 
 
 def config1_probe(gpu):
@@ -101,7 +110,21 @@ def config1_probe(gpu):
             ms = gpu.time_qgemm(which, 0xD0, src, T, dout, 20)
             tf = flops / (ms * 1e-3) / 1e12
             out[f"{leg}_passes{passes}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
-                                            "frac_of_peak": round(tf / PEAK_MFMA_TFLOPS, 4)}
+                                            "frac_of_peak": round(tf / PEAK_MFMA_TFLOPS, 4),
+                                            "timed": "GEMM kernel alone (operand already fp16)"}
+            # the same GEMM from the f32 operand, as the per-op entry point runs it: the f32 -> fp16 row-scaled
+            # split (hi, and lo for two-plane modes) plus the GEMM, which is what the 4 B/element f32 dY count of
+            # the algorithmic bytes starts from
+            entry = "qgemm_dx_dev" if which == 1 else "qgemm_fwd_dev"
+            gpu.op_async(entry, 0xD0, src, T, dout)  # warm-up
+            gpu.timer_begin()
+            for _ in range(20):
+                gpu.op_async(entry, 0xD0, src, T, dout)
+            ms2 = gpu.timer_end() / 20
+            tf2 = flops / (ms2 * 1e-3) / 1e12
+            out[f"{leg}_passes{passes}_from_f32"] = {"us": round(ms2 * 1e3, 1), "tflops": round(tf2, 1),
+                                                     "frac_of_peak": round(tf2 / PEAK_MFMA_TFLOPS, 4),
+                                                     "timed": "f32 -> fp16 operand split + GEMM"}
     gpu.set_gemm_passes(1)
     A = gpu.to_dev(rng.standard_normal((K, r), dtype=np.float32) * np.float32(0.02))
     B = gpu.to_dev(rng.standard_normal((r, N), dtype=np.float32) * np.float32(0.02))
@@ -285,16 +308,20 @@ def main():
     f_tok = synth.algorithmic_flops_per_token(cfg, T)
     kernel_ms = {c: round(s["ms"] / args.steps, 3) for c, s in brk.items()}
     avg_launch_s = ds["ms"] / max(ds["launches"], 1) * 1e-3  # over the last timed step
+    traffic, tsrc = traffic_per_launch(dom, cfg)
+    if tsrc and "avg_launch_us" in tsrc:
+        # the counter run's launches against this run's: a >15% move means the kernels changed since the profile
+        tsrc["stale"] = abs(avg_launch_s * 1e6 / tsrc["avg_launch_us"] - 1.0) > 0.15
     if ds["flops"] > 0:
         achieved = ds["flops"] / max(ds["launches"], 1) / avg_launch_s / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": traffic_per_launch(dom, cfg), "kernel": dom,
-                "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"]}
+                "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": traffic, "traffic_source": tsrc,
+                "kernel": dom, "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"]}
     else:
         achieved = ds["bytes"] / max(ds["launches"], 1) / avg_launch_s / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_per_launch(dom, cfg), "kernel": dom,
-                "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"]}
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_source": tsrc,
+                "kernel": dom, "avg_launch_us": round(avg_launch_s * 1e6, 2), "launches_per_step": ds["launches"]}
 
     c1 = config1_probe(gpu)
     cpu = serial = None
@@ -308,7 +335,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16 MFMA (hi/lo split: 3 passes per layer GEMM, 1-2 on the head) + f32", "data": "synthetic",
         "config": {"workload": workload(cfg), "global_batch": B, "seq_len": T,
-                   "parallelism": "dp1", "precision": "layer GEMMs 3-pass, head fwd 1-pass, head dX weight-split"},
+                   "parallelism": "dp1", "precision": "layer fwd mode 5 (integer-code kernel for large Q8_0 forwards, else 3-pass: mode-3 precision), "
+                                "layer dX 3-pass, head fwd 1-pass, head dX weight-split (mode 4)"},
         "roofline": roof,
         "mfma_roofline_frac_step": round(value * f_tok / 1e12 / PEAK_MFMA_TFLOPS, 4),
         "config1_4096cubed_q4k": c1,

@@ -92,6 +92,7 @@ SIGNATURES = {
     "hos_hip_attention_fwd": (i32, [vp, vp, sz, sz, sz, i32, i32, i32, i32, i32, vp, sz, vp]),
     "hos_hip_attention_bwd": (i32, [vp, vp, sz, sz, sz, vp, vp, sz, vp, i32, i32, i32, i32, i32, vp, sz]),
     "hos_hip_cross_entropy": (i32, [vp, vp, sz, sz, vp, ctypes.c_float, vp, vp]),
+    "hos_hip_moe_route": (i32, [vp, vp, sz, i32, i32, vp, vp, vp, vp, vp]),
     "hos_hip_adamw": (i32, [vp, vp, vp, vp, vp, sz, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                             ctypes.c_float, ctypes.c_float, i32, i32]),
     "hos_hip_lora": (i32, [vp, vp, vp, sz, sz, sz, i32, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp]),

@@ -73,6 +73,7 @@ struct hos_ctx {
   DevMem ops[8];  // scratch of the op-level entry points (ops.hip)
   int passes = 1;
   hipEvent_t tev[2] = {nullptr, nullptr};  // hos_hip_timer_begin / _end
+  bool tarmed = false;                     // a timer_begin not yet closed by a timer_end
   static constexpr size_t kWs = 256ull << 20;
 };
 
@@ -373,12 +374,14 @@ int hos_hip_timer_begin(hos_ctx* c) {
     for (auto& e : c->tev)
       if (!e) HOS_HIP_CHECK(hipEventCreate(&e));
     HOS_HIP_CHECK(hipEventRecord(c->tev[0], c->stream));
+    c->tarmed = true;
   });
 }
 
 int hos_hip_timer_end(hos_ctx* c, float* ms) {
   return guard(c, [&] {
-    HOS_REQUIRE(ms && c->tev[0], HOS_E_INVALID, "timer_end: no timer_begin on this context");
+    HOS_REQUIRE(ms && c->tev[0] && c->tarmed, HOS_E_INVALID, "timer_end: no open timer_begin on this context");
+    c->tarmed = false;
     HOS_HIP_CHECK(hipEventRecord(c->tev[1], c->stream));
     HOS_HIP_CHECK(hipEventSynchronize(c->tev[1]));
     HOS_HIP_CHECK(hipEventElapsedTime(ms, c->tev[0], c->tev[1]));

@@ -11,6 +11,7 @@
 #include "ctx.hpp"
 #include "fused.hpp"
 #include "lora.hpp"
+#include "moe.hpp"
 
 using namespace hos;
 
@@ -135,6 +136,8 @@ size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 // the device address is looked up once per device with hipGetSymbolAddress and kept per device. Every call
 // on one GPU shares the array and leaves its contents behind; the kernels write every scratch element before
 // reading it, so nothing needs clearing. Calls that overlap on one GPU (two streams or two contexts) race.
+// The cached address is valid for the life of the loaded code object: hipDeviceReset (which frees the module's
+// device globals) is not supported in a process that uses this entry point.
 void* lora_scratch_ptr() {
   static std::mutex mu;
   static void* ptr[64] = {};
@@ -267,6 +270,18 @@ int hos_hip_cross_entropy(hos_ctx* c, const float* logits, size_t rows, size_t V
   return op_guard(c, [&](hipStream_t st) {
     HOS_REQUIRE(logits && targets && row_loss && dlogits, HOS_E_INVALID, "null pointer");
     launch_ce(logits, (int)rows, (int)V, targets, gscale, row_loss, H16{nullptr, nullptr, nullptr}, st, dlogits);
+  });
+}
+
+// The MoE router of src/forward.rs:542-552 on logits [rows, E]: softmax probabilities pfull [rows, E], the top K
+// experts per row by probability (a stable descending sort: ties to the lower expert) with their raw
+// probabilities, sel_e / sel_p [rows, K] in selection order; slot [rows, K] is each selection's rank among its
+// expert's selections and counts [E] the per-expert totals (the grouping the expert GEMMs use).
+int hos_hip_moe_route(hos_ctx* c, const float* logits, size_t rows, int E, int K, float* pfull, int32_t* sel_e,
+                      float* sel_p, int32_t* slot, int32_t* counts) {
+  return op_guard(c, [&](hipStream_t st) {
+    HOS_REQUIRE(logits && pfull && sel_e && sel_p && slot && counts, HOS_E_INVALID, "null pointer");
+    launch_moe_route(logits, (int)rows, E, K, pfull, sel_e, sel_p, slot, counts, st);
   });
 }
 

@@ -665,10 +665,11 @@ struct hos_peft {
       launch_rmsnorm_fwd(xfinal, out_norm, c.rms_eps, M, d, nullptr, hs, invf, st);
     }
     GemmEpi he{};
-    he.rstat = lstat;  // the cross-entropy's softmax statistics come out of the head GEMM's epilogue
-    he.rstat_ld = (V + 63) / 64;
+    if (!need_logits_only) {  // the cross-entropy's softmax statistics come out of the head GEMM's epilogue
+      he.rstat = lstat;
+      he.rstat_ld = (V + 63) / 64;
+    }
     qfwd(out_set ? out : tok, hs, d, M, logits, V, nullptr, nullptr, 0, he, phf);
-    (void)need_logits_only;
   }
 
   // ---------------- loss + backward ----------------

@@ -43,9 +43,9 @@ namespace {
 typedef short s4v __attribute__((ext_vector_type(4)));
 
 
-// e^d for the row statistics of a softmax: hardware exp2 of d·log2 e (one rounding of the product, ~1 ulp exp2;
-// the exponents that matter are small).
-__device__ __forceinline__ float exp_rs(float d) { return __builtin_amdgcn_exp2f(d * 1.4426950408889634f); }
+// e^d for the row statistics of a softmax: expf, the function the cross-entropy pass (fused.hip ce_kernel) applies to
+// the same logits, so the softmax denominator and its numerators come from one exp and each row's p sums to 1.
+__device__ __forceinline__ float exp_rs(float d) { return expf(d); }
 
 // Signed byte i of a word as float (one bit-field extract + one convert).
 __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }

@@ -100,7 +100,8 @@ int hos_hip_qgemm_lora_dev(hos_ctx* ctx, int which, uint64_t key, const float* i
 int hos_hip_time_qgemm(hos_ctx* ctx, int which, uint64_t key, const float* in_dev, size_t t, float* out_dev,
                        int iters, float* avg_ms);
 /* Elapsed time of whatever is enqueued on the context stream between the two calls, from HIP events
- * (timer_end waits for the stream). No counterpart in the reference; measurement only. */
+ * (timer_end waits for the stream; it fails with HOS_E_INVALID unless a timer_begin is open, so each end pairs with
+ * exactly one begin). No counterpart in the reference; measurement only. */
 int hos_hip_timer_begin(hos_ctx* ctx);
 int hos_hip_timer_end(hos_ctx* ctx, float* ms);
 /* quantize(x, ggml_type) of src/gguf_write.rs:41-50 (Q8_0 :178-196, Q4_K :355-416,
@@ -154,6 +155,13 @@ int hos_hip_attention_bwd(hos_ctx* ctx, const float* qkv, size_t ld, size_t kcol
  * dlogits = (p − onehot)·gscale (the reference's g/n: gscale = 1/rows). */
 int hos_hip_cross_entropy(hos_ctx* ctx, const float* logits, size_t rows, size_t V, const int32_t* targets,
                           float gscale, float* row_loss, float* dlogits);
+/* MoE router (src/forward.rs:542-552) on logits [rows, E] (E <= 64, 1 <= K <= E): softmax pfull [rows, E]; the top K
+ * experts of each row by probability, ties to the lower expert (the reference's stable descending sort), with
+ * their raw probabilities: sel_e / sel_p [rows, K] in selection order. slot [rows, K] = rank of the selection among
+ * its expert's selections (token, then slot order); counts [E] = selections per expert. A NaN probability ranks
+ * below every number, so every row still gets K distinct experts in [0, E). */
+int hos_hip_moe_route(hos_ctx* ctx, const float* logits, size_t rows, int E, int K, float* pfull, int32_t* sel_e,
+                      float* sel_p, int32_t* slot, int32_t* counts);
 /* AdamW::step (src/tensor.rs:2952-2975) on n parameters at 1-based step t (bias corrections by f32 powi). */
 int hos_hip_adamw(hos_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, float lr, float beta1,
                   float beta2, float eps, float wd, int step, int decay);
@@ -168,7 +176,8 @@ int hos_hip_lora(hos_ctx* ctx, const float* x, const float* dy, size_t rows, siz
  * Same arguments, kernels and results as hos_hip_lora; its scratch (A transposed, du, split partials) is one
  * 64 MiB device array per GPU, held until the process ends: shapes needing more fail with HOS_E_INVALID before
  * any launch. Every call on one GPU shares that array, so calls that overlap on one GPU (two streams or two
- * contexts) race; calls in one stream order are safe. */
+ * contexts) race; calls in one stream order are safe. The array's device address is looked up once per device,
+ * so hipDeviceReset is not supported in a process that calls this entry point. */
 int hos_hip_lora_noalloc(hos_ctx* ctx, const float* x, const float* dy, size_t rows, size_t in, size_t out, int r,
                          const float* A, const float* B, float scale, float* y, float* u, float* dA, float* dB,
                          float* dx);

@@ -4,6 +4,7 @@
 // call on Linux. OpenMP splits only loops whose iterations write disjoint outputs, each
 // output keeping its serial summation order, so results are identical to one thread.
 #pragma once
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -81,45 +82,99 @@ inline Tensor randn_uniform(std::vector<size_t> shape, uint64_t* seed) {
 
 // ---- ops ----
 
+// C[i][c] += Σ_s A[i][s]·B[s][c] with, for every element, the terms added one at a time in ascending s (one f32
+// rounding per product and per add, no fused multiply-add): exactly the arithmetic of the reference's scalar loops
+// (src/tensor.rs:307-391), whatever order the elements themselves are visited in. The loops are tiled (row and
+// column blocks, chunks of s that carry each element's running sum through C) and the inner 4-row × 16-column
+// block keeps its running sums in SSE registers; none of this changes an element's sequence of roundings.
+typedef float orc_v4 __attribute__((vector_size(16)));
+#ifndef ORC_R
+#define ORC_R 4  // rows of the register block
+#endif
+#ifndef ORC_Q
+#define ORC_Q 2  // 4-float vectors of the register block (8 running sums + 2 B vectors + 1 broadcast in 16 xmm)
+#endif
+inline void ordered_gemm(const float* A, size_t lda, const float* B, size_t ldb, float* C, size_t ldc, size_t M,
+                         size_t S, size_t N) {
+  const size_t MB = 32, NB = 128, SB = 256;
+  const long long nib = (long long)((M + MB - 1) / MB), njb = (long long)((N + NB - 1) / NB);
+#pragma omp parallel for schedule(dynamic)
+  for (long long t = 0; t < nib * njb; t++) {
+    const size_t i0 = (size_t)(t / njb) * MB, c0 = (size_t)(t % njb) * NB;
+    const size_t i1 = std::min(M, i0 + MB), c1 = std::min(N, c0 + NB);
+    for (size_t s0 = 0; s0 < S; s0 += SB) {
+      const size_t s1 = std::min(S, s0 + SB);
+      size_t i = i0;
+      for (; i + ORC_R <= i1; i += ORC_R) {
+        size_t c = c0;
+        for (; c + 4 * ORC_Q <= c1; c += 4 * ORC_Q) {
+          orc_v4 acc[ORC_R][ORC_Q];
+          for (int r = 0; r < ORC_R; r++)
+            for (int q = 0; q < ORC_Q; q++) std::memcpy(&acc[r][q], &C[(i + r) * ldc + c + 4 * q], 16);
+          for (size_t sv = s0; sv < s1; sv++) {
+            orc_v4 bv[ORC_Q];
+            for (int q = 0; q < ORC_Q; q++) std::memcpy(&bv[q], &B[sv * ldb + c + 4 * q], 16);
+            for (int r = 0; r < ORC_R; r++) {
+              const float a = A[(i + r) * lda + sv];
+              const orc_v4 av = {a, a, a, a};
+              for (int q = 0; q < ORC_Q; q++) acc[r][q] = acc[r][q] + av * bv[q];
+            }
+          }
+          for (int r = 0; r < ORC_R; r++)
+            for (int q = 0; q < ORC_Q; q++) std::memcpy(&C[(i + r) * ldc + c + 4 * q], &acc[r][q], 16);
+        }
+        for (; c < c1; c++)
+          for (int r = 0; r < ORC_R; r++) {
+            float acc = C[(i + r) * ldc + c];
+            for (size_t sv = s0; sv < s1; sv++) acc += A[(i + r) * lda + sv] * B[sv * ldb + c];
+            C[(i + r) * ldc + c] = acc;
+          }
+      }
+      for (; i < i1; i++)
+        for (size_t c = c0; c < c1; c++) {
+          float acc = C[i * ldc + c];
+          for (size_t sv = s0; sv < s1; sv++) acc += A[i * lda + sv] * B[sv * ldb + c];
+          C[i * ldc + c] = acc;
+        }
+    }
+  }
+}
+
+// dst[c][r] = src[r][c] for src [R, Cn] (blocked for cache locality).
+inline std::vector<float> transpose_copy(const float* src, size_t R, size_t Cn) {
+  std::vector<float> dst(R * Cn);
+  const size_t TB = 64;
+#pragma omp parallel for schedule(static)
+  for (long long r0 = 0; r0 < (long long)R; r0 += TB)
+    for (size_t c0 = 0; c0 < Cn; c0 += TB)
+      for (size_t r = (size_t)r0; r < std::min(R, (size_t)r0 + TB); r++)
+        for (size_t c = c0; c < std::min(Cn, c0 + TB); c++) dst[c * R + r] = src[r * Cn + c];
+  return dst;
+}
+
 // src/tensor.rs:307-391: fwd i-p-j; dA = g·Bᵀ (i-j-p); dB = Aᵀ·g (i-p-j); frozen B skips dB.
 inline Tensor matmul(const Tensor& A, const Tensor& B) {
   size_t m = A->shape[0], k = A->shape[1], n = B->shape[1];
   std::vector<float> out(m * n, 0.0f);
   const float* a = A->data.data();
   const float* b = B->data.data();
-#pragma omp parallel for schedule(static)
-  for (long long i = 0; i < (long long)m; i++) {
-    float* o = &out[i * n];
-    for (size_t p = 0; p < k; p++) {
-      float av = a[i * k + p];
-      const float* br = b + p * n;
-      for (size_t j = 0; j < n; j++) o[j] += av * br[j];
-    }
-  }
+  ordered_gemm(a, k, b, n, out.data(), n, m, k, n);  // out[i][j]: Σ over p ascending (the i-p-j loop)
   return build(std::move(out), {m, n}, {A, B}, [m, k, n](const std::vector<float>& g, const std::vector<Tensor>& par) {
     bool need_a = par[0]->requires_grad, need_b = par[1]->requires_grad;
     const float* a = par[0]->data.data();
     const float* b = par[1]->data.data();
     if (need_a) {
       std::vector<float> da(m * k, 0.0f);
-#pragma omp parallel for schedule(static)
-      for (long long i = 0; i < (long long)m; i++) {
-        for (size_t j = 0; j < n; j++) {
-          float gv = g[i * n + j];
-          for (size_t p = 0; p < k; p++) da[i * k + p] += gv * b[p * n + j];
-        }
-      }
+      // da[i][p]: Σ over j ascending of g[i][j]·b[p][j] (the i-j-p loop), as a GEMM against Bᵀ
+      const std::vector<float> bt = transpose_copy(b, k, n);
+      ordered_gemm(g.data(), n, bt.data(), k, da.data(), k, m, n, k);
       par[0]->add_grad(da);
     }
     if (need_b) {
       std::vector<float> db(k * n, 0.0f);
-#pragma omp parallel for schedule(static)
-      for (long long p = 0; p < (long long)k; p++) {
-        for (size_t i = 0; i < m; i++) {
-          float av = a[i * k + p];
-          for (size_t j = 0; j < n; j++) db[p * n + j] += av * g[i * n + j];
-        }
-      }
+      // db[p][j]: Σ over i ascending of a[i][p]·g[i][j] (the i-p-j loop), as a GEMM of Aᵀ
+      const std::vector<float> at = transpose_copy(a, m, k);
+      ordered_gemm(at.data(), m, g.data(), n, db.data(), n, k, m, n);
       par[1]->add_grad(db);
     }
   });

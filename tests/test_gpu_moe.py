@@ -118,3 +118,68 @@ def test_moe_graph_replay_matches_eager(gpu):
         a.free()
     for pm in models:
         pm.close()
+
+
+def _route(gpu, logits, K):
+    M, E = logits.shape
+    L = gpu.to_dev(logits)
+    P, SE, SP = gpu.empty_dev((M, E)), gpu.empty_dev((M, K), np.int32), gpu.empty_dev((M, K))
+    SL, CN = gpu.empty_dev((M, K), np.int32), gpu.empty_dev((E,), np.int32)
+    gpu.op("moe_route", L, M, E, K, P, SE, SP, SL, CN)
+    out = tuple(a.get() for a in (P, SE, SP, SL, CN))
+    for a in (L, P, SE, SP, SL, CN):
+        a.free()
+    return out
+
+
+def _check_grouping(sel_e, slot, counts, E):
+    """slot = rank of each selection among its expert's selections in (token, slot) order; counts = totals."""
+    flat, sl = sel_e.ravel(), slot.ravel()
+    seen = np.zeros(E, np.int64)
+    for q, e in enumerate(flat):
+        assert sl[q] == seen[e], f"selection {q}: slot {sl[q]} != {seen[e]}"
+        seen[e] += 1
+    assert np.array_equal(counts, seen)
+
+
+@pytest.mark.parametrize("E,K", [(64, 8), (8, 2), (5, 5)])
+def test_moe_route_matches_stable_sort(gpu, E, K):
+    """The router entry point (src/forward.rs:542-552): softmax within 1e-6 of float64, and the selection equal to
+    a stable descending sort of the kernel's own probabilities (ties to the lower expert), raw probabilities
+    carried. Rows with forced exact ties (duplicated logits) check the tie order."""
+    rng = np.random.default_rng(E * 100 + K)
+    M = 300
+    logits = rng.standard_normal((M, E)).astype(np.float32)
+    logits[::7, 1] = logits[::7, 0]          # exact ties between experts 0 and 1
+    logits[::11, :] = 0.25                   # a whole row tied: experts 0..K-1 in order
+    print(f"moe_route E={E} K={K} M={M}", flush=True)
+    p, sel_e, sel_p, slot, counts = _route(gpu, logits, K)
+    x = logits.astype(np.float64)
+    want = np.exp(x - x.max(1, keepdims=True))
+    want /= want.sum(1, keepdims=True)
+    assert np.abs(p - want).max() <= 1e-6
+    order = np.argsort(-p, axis=1, kind="stable")[:, :K]
+    assert np.array_equal(sel_e, order)
+    assert np.array_equal(sel_p, np.take_along_axis(p, sel_e, 1))
+    _check_grouping(sel_e, slot, counts, E)
+
+
+def test_moe_route_nan_logits_give_distinct_experts(gpu):
+    """Regression test of the router with diverged (NaN) logits: every row still selects K distinct experts in
+    [0, E) (a NaN probability ranks below every number), the grouping stays consistent, and the NaN is carried
+    in the selected probabilities rather than turned into an index."""
+    E, K, M = 64, 8, 64
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((M, E)).astype(np.float32)
+    logits[0, :] = np.nan                    # every logit NaN
+    logits[1, 3] = np.nan                    # one NaN logit: the softmax sum, so the whole row, is NaN
+    logits[2, 10:40] = np.nan
+    print("moe_route NaN logits", flush=True)
+    p, sel_e, sel_p, slot, counts = _route(gpu, logits, K)
+    for t in range(M):
+        assert len(set(sel_e[t].tolist())) == K, f"row {t}: {sel_e[t]}"
+        assert ((sel_e[t] >= 0) & (sel_e[t] < E)).all()
+    assert np.array_equal(sel_e[0], np.arange(K))  # all NaN: ties resolve to the lowest experts
+    assert np.isnan(sel_p[0]).all() and np.isnan(sel_p[1]).all()
+    assert np.isfinite(sel_p[3:]).all()
+    _check_grouping(sel_e, slot, counts, E)

@@ -288,3 +288,44 @@ def test_graph_replay_matches_eager(gpu):
         a.free()
     for pm in models:
         pm.close()
+
+
+def _bench_shape_parity(name, B, T, seed):
+    """The whole training step at a shape the benchmark times, against the oracle on the same seeded inputs, with the
+    default per-site precision policy: the loss and every LoRA dA / dB (every layer, every target) within 1e-3
+    relative L2. At these row counts the tile rule picks the kernels the benchmark runs (the 256-row head tiles
+    with the fused softmax statistics, split contractions whose first split carries the rank-r term, the 64-deep
+    two-plane slabs), which the small-shape parity tests above never reach."""
+    import time
+    from conftest import heartbeat
+    from hos_amd import Gpu
+    from hos_amd.synth import CONFIGS
+    g = Gpu(0)
+    cfg = CONFIGS[name]
+    print(f"peft bench-shape parity {name} B={B} T={T}", flush=True)
+    pm, om, ids, tg, lora, TARGETS = run_pair(g, cfg, B=B, T=T, seed=seed)
+    lg = pm.loss_grad(ids, tg)
+    print(f"gpu loss {lg:.6f}; running the oracle on the host", flush=True)
+    t0 = time.time()
+    with heartbeat(f"oracle {name} B{B}xT{T}"):
+        lo = om.loss_grad(ids, tg)
+    print(f"oracle loss {lo:.6f} in {time.time() - t0:.1f} s", flush=True)
+    assert abs(lg - lo) / abs(lo) <= TOL
+    worst = compare_grads(pm, om, cfg, lora, TARGETS)
+    print(f"{name} B{B}xT{T}: loss gpu {lg:.6f} cpu {lo:.6f}, worst LoRA grad rel L2 {worst:.2e} "
+          f"over {2 * len(lora)} gradients", flush=True)
+    pm.close()
+    g.close()
+
+
+@pytest.mark.timeout(1200)  # the oracle's 4 x 512-token step takes minutes on the host
+def test_qwen25_05b_bench_shape_parity():
+    """configs[2] at the benchmark's own batch: Qwen2.5-0.5B architecture, B4 x T512 (M = 2048 rows)."""
+    _bench_shape_parity("qwen2.5-0.5b", 4, 512, seed=41)
+
+
+@pytest.mark.timeout(1200)
+def test_llama32_1b_long_sequence_parity():
+    """configs[3] architecture with LoRA r32 on all projections at T = 1024 (the benchmark's sequence length;
+    M = 1024 rows, causal attention over the full sequence), B1."""
+    _bench_shape_parity("llama3.2-1b", 1, 1024, seed=43)

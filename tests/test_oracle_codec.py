@@ -358,3 +358,81 @@ def test_qkx_scale_min_branches():  # src/gguf_write.rs:293-351
     assert mn == 0.0 and sc > 0
     # (s <= 0 is not forced: levels are a non-decreasing function of v, so with two or more distinct levels the
     # refit slope is positive in exact arithmetic; the branch is the reference's guard against f32 cancellation.)
+
+
+# ---- qkx_scale_min's candidate search itself (src/gguf_write.rs:311-346) ----
+# The grid blocks above are recovered exactly by many candidates, so they cannot tell a wrong candidate count,
+# step or comparison apart. The blocks below can: each candidate's result is recomputed here independently — the
+# level assignment in f32 exactly as the reference writes it (iscale = (nmax − 1 + 0.1·i)/span, round half away
+# from zero, clamp), the refit as a float64 least-squares solve (numpy lstsq, not the reference's running sums),
+# the error in float64 — and the test asserts that each block's winner is separated from the runner-up and that
+# every plausible mistake (18 or 20 candidates, a 0.09 / 0.11 step, the start at nmax, `<=`) picks a different
+# (scale, min), so the oracle's answer pins those constants.
+
+
+def _qkx_candidates(x, nmax, start=-1, step=0.1, count=19):
+    x32 = np.asarray(x, np.float32)
+    x64 = x32.astype(np.float64)
+    mn32 = np.float32(min(x32.min(), np.float32(0)))
+    span32 = np.float32(x32.max() - mn32)
+    out = []
+    for i in range(count):
+        isc = np.float32(np.float32(nmax + start) + np.float32(np.float32(step) * np.float32(i))) / span32
+        t = (np.float32(isc) * (x32 - mn32)).astype(np.float64)
+        lv = np.clip(np.floor(t + 0.5), 0, nmax)
+        (s, b), *_ = np.linalg.lstsq(np.stack([lv, np.ones_like(lv)], 1), x64, rcond=None)
+        if s > 0:
+            m = max(-b, 0.0)
+        else:
+            s, m = float(span32) / nmax, -float(mn32)
+        l2 = np.clip(np.floor((x64 + m) / s + 0.5), 0, nmax)
+        out.append((float(((s * l2 - m - x64) ** 2).sum()), float(s), float(m)))
+    return out
+
+
+def _qkx_winner(fits, strict=True):
+    e = [f[0] for f in fits]
+    best = min(e)
+    idx = [i for i, v in enumerate(e) if v == best]
+    return idx[0] if strict else idx[-1]
+
+
+_ALL_MISTAKES = ((-1, 0.1, 18), (-1, 0.1, 20), (-1, 0.09, 19), (-1, 0.11, 19), (0, 0.1, 19))
+
+
+@pytest.mark.parametrize("seed,want_i,mistakes", [(75, 18, _ALL_MISTAKES), (561, 18, _ALL_MISTAKES),
+                                                  (736, 18, _ALL_MISTAKES), (1105, 18, _ALL_MISTAKES),
+                                                  (20, 6, _ALL_MISTAKES[2:])])
+def test_qkx_scale_min_candidate_search_pinned(seed, want_i, mistakes):
+    x = np.random.default_rng(seed).standard_normal(32).astype(np.float32)
+    fits = _qkx_candidates(x, 15)
+    i = _qkx_winner(fits)
+    assert i == want_i
+    errs = sorted(f[0] for f in fits)
+    assert errs[1] - errs[0] > 1e-3 * errs[0]  # the winner is not a near-tie that f32 sums could flip
+    s, m = fits[i][1:]
+    # the mistakes this block detects (the test's own discrimination check)
+    for alt in mistakes:
+        af = _qkx_candidates(x, 15, *alt)
+        assert abs(af[_qkx_winner(af)][1] - s) > 1e-3 * s, alt
+    so, mo = o.qkx_scale_min(x, 15)
+    assert abs(so - s) <= 1e-6 * s and abs(mo - m) <= 1e-6 * max(m, 1e-30), (so, s, mo, m)
+
+
+def test_qkx_scale_min_keeps_the_first_of_equal_errors():
+    """Two value clusters {0, a} with a = 14·15·2^-8: candidates 0-4 put a on level 14, candidates 5-18 on level 15,
+    and both refits are exact (error exactly 0 in f32), so only the comparison decides. The strict `<` keeps the
+    first candidate: scale a/14 = 15·2^-8 (with `<=` the last: a/15 = 14·2^-8), min 0."""
+    a = 14 * 15 * 2.0 ** -8
+    x = np.array([0.0] * 20 + [a] * 12, np.float32)
+    fits = _qkx_candidates(x, 15)
+    assert all(f[0] <= 1e-20 for f in fits)  # every candidate's refit is exact
+    assert all(abs(f[1] - 15 * 2.0 ** -8) < 1e-12 for f in fits[:5])
+    assert all(abs(f[1] - 14 * 2.0 ** -8) < 1e-12 for f in fits[5:])
+    assert o.qkx_scale_min(x, 15) == (15 * 2.0 ** -8, 0.0)
+    # the same sub-block inside a Q4_K super-block: scale code and level 14 in the bytes
+    blk = np.zeros(256, np.float32)
+    blk[:32] = x
+    raw = o.quantize(blk, Q4_K).tolist()
+    codes = [raw[16 + i] & 15 for i in range(32)]
+    assert max(codes) == 14 and codes.count(14) == 12
