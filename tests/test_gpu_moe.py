@@ -183,3 +183,38 @@ def test_moe_route_nan_logits_give_distinct_experts(gpu):
     assert np.isnan(sel_p[0]).all() and np.isnan(sel_p[1]).all()
     assert np.isfinite(sel_p[3:]).all()
     _check_grouping(sel_e, slot, counts, E)
+
+
+@pytest.mark.timeout(1500)
+def test_olmoe_full_depth_parity():
+    """configs[4] at full depth (16 layers, d 2048, 64 experts top-8 in Q8_0, QK-norm, LoRA r16 on q/k/v/o) on one
+    512-token sequence — the benchmark's sequence length, so the grouped expert GEMMs run 128-row tiles of experts
+    holding up to hundreds of rows — against the oracle: loss and every LoRA gradient within 1e-3."""
+    import time
+    from conftest import heartbeat
+    from hos_amd import Gpu, synth
+    from hos_amd.peft import PeftModel, TARGETS
+    g = Gpu(0)
+    cfg = synth.CONFIGS["olmoe"]
+    B, T = 1, 512
+    print(f"moe parity olmoe 16 layers B={B} T={T}", flush=True)
+    tensors = synth.build_tensors(g, cfg, seed=71)
+    lora = synth.lora_init(cfg, seed=72, b_std=0.02)
+    ids, tg = synth.tokens(cfg, B, T, seed=73)
+    pm = PeftModel(g, cfg, max_batch=B, max_seq=T)
+    pm.load(tensors)
+    for (l, t), (A, Bm) in lora.items():
+        pm.set_lora(l, t, A, Bm)
+    lg = pm.loss_grad(ids, tg)
+    print(f"gpu loss {lg:.6f}; loading the oracle", flush=True)
+    t0 = time.time()
+    with heartbeat("oracle olmoe B1xT512"):
+        om = oracle_model(cfg, tensors, lora)
+        del tensors
+        lo = om.loss_grad(ids, tg)
+    print(f"oracle loss {lo:.6f} in {time.time() - t0:.1f} s (with loading)", flush=True)
+    assert abs(lg - lo) / abs(lo) <= TOL, (lg, lo)
+    worst = compare_grads(pm, om, cfg, lora, TARGETS)
+    print(f"olmoe 16 layers B1xT512: loss gpu {lg:.6f} cpu {lo:.6f}, worst LoRA grad rel L2 {worst:.2e}", flush=True)
+    pm.close()
+    g.close()
