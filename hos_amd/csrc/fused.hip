@@ -486,12 +486,13 @@ __device__ __forceinline__ void sm_add(float& m, float& s, float x) {
     s += expf(x - m);
   }
 }
-__device__ __forceinline__ void sm_merge(float& m, float& s, float m2, float s2) {
+__device__ __forceinline__ void sm_merge(float& m, float& s, float m2, float s2, bool hw = false) {
+  // hw: the states came from the head GEMM's epilogue, which exponentiates with exp_rs; rescale with it too
   if (m2 > m) {
-    s = s * expf(m - m2) + s2;
+    s = s * (hw ? exp_rs(m - m2) : expf(m - m2)) + s2;
     m = m2;
   } else if (m2 > -INFINITY) {
-    s += s2 * expf(m2 - m);
+    s += s2 * (hw ? exp_rs(m2 - m) : expf(m2 - m));
   }
 }
 
@@ -513,7 +514,7 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
     const float2* rr = rstat + (long long)row * nch;
     for (int c = threadIdx.x; c < nch; c += RB) {
       const float2 x = rr[c];
-      sm_merge(m, sum, x.x, x.y);
+      sm_merge(m, sum, x.x, x.y, true);
     }
   } else if (vec) {
     const float4* l4 = reinterpret_cast<const float4*>(lr);
@@ -534,7 +535,11 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
   } else {
     for (int c = threadIdx.x; c < V; c += RB) sm_add(m, sum, lr[c]);
   }
-  for (int o = 32; o > 0; o >>= 1) sm_merge(m, sum, __shfl_xor(m, o), __shfl_xor(sum, o));
+  // With statistics from the head GEMM's epilogue, every exponential below (merges and numerators) uses the
+  // epilogue's exp_rs, so the denominator and the numerators come from one function; expf when they were computed
+  // here (the op-level entry).
+  const bool hw = rstat != nullptr;
+  for (int o = 32; o > 0; o >>= 1) sm_merge(m, sum, __shfl_xor(m, o), __shfl_xor(sum, o), hw);
   if ((threadIdx.x & 63) == 0) {
     rm[threadIdx.x >> 6] = m;
     rs[threadIdx.x >> 6] = sum;
@@ -543,9 +548,10 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
   m = rm[0];
   sum = rs[0];
 #pragma unroll
-  for (int w = 1; w < RB / 64; w++) sm_merge(m, sum, rm[w], rs[w]);
+  for (int w = 1; w < RB / 64; w++) sm_merge(m, sum, rm[w], rs[w], hw);
   const int t = targets[row];
-  const float pt = expf(lr[t] - m) / sum;
+  auto ex = [hw](float d) { return hw ? exp_rs(d) : expf(d); };
+  const float pt = ex(lr[t] - m) / sum;
   if (threadIdx.x == 0) row_loss[row] = -logf(fmaxf(pt, 1e-12f));
   // max |p − onehot| = max(1/sum, 1 − p_t) (the row max has p = 1/sum)
   const float amax = fmaxf(1.0f / sum, 1.0f - pt) * fabsf(gscale);
@@ -553,7 +559,7 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
   const float sc = ldexpf(1.0f, e), inv = 1.0f / sum;
   if (dl32) {  // plain f32 gradient (the op-level entry point)
     for (int c = threadIdx.x; c < V; c += RB) {
-      float p = expf(lr[c] - m) * inv;
+      float p = ex(lr[c] - m) * inv;
       if (c == t) p -= 1.0f;
       dl32[(long long)row * V + c] = p * gscale;
     }
@@ -565,7 +571,7 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
     const int V4 = V >> 2;
     auto grad4 = [&](float4 x, int c4) {
       const int c = 4 * c4;
-      float4 p = make_float4(expf(x.x - m) * inv, expf(x.y - m) * inv, expf(x.z - m) * inv, expf(x.w - m) * inv);
+      float4 p = make_float4(ex(x.x - m) * inv, ex(x.y - m) * inv, ex(x.z - m) * inv, ex(x.w - m) * inv);
       if (c == t) p.x -= 1.0f;
       if (c + 1 == t) p.y -= 1.0f;
       if (c + 2 == t) p.z -= 1.0f;
@@ -582,7 +588,7 @@ __global__ void __launch_bounds__(RB) ce_kernel(const float* __restrict__ logits
     if (c4 < V4) grad4(l4[c4], c4);
   } else {
     for (int c = threadIdx.x; c < V; c += RB) {
-      float p = expf(lr[c] - m) * inv;
+      float p = ex(lr[c] - m) * inv;
       if (c == t) p -= 1.0f;
       put_h16(p * gscale * sc, dl, dll, (long long)row * V + c);
     }

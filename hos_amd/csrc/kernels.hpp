@@ -30,6 +30,12 @@ inline QWeightView view(const QWeight& w) { return QWeightView{w.type, w.rows, w
 // Correctly rounded f32 division and square root (what Rust's f32 `/` and sqrt give): the f64 operation is
 // correctly rounded, and rounding its result once more to f32 is exact-safe because 53 >= 2·24 + 2. (HIP's
 // __fsqrt_rn is the approximate hardware square root unless OCML rounding mode is enabled.)
+// e^d for the row statistics of a softmax folded into the vocabulary head GEMM's epilogue (qgemm_impl.hpp):
+// hardware exp2 of d·log2 e (one rounding of the product, ~1 ulp exp2; the exponents that matter are small). The
+// cross-entropy pass that consumes those statistics (fused.hip ce_kernel) computes its numerators with the same
+// function, so each row's p sums to 1. (expf in the epilogue instead: the step's forward GEMMs 1.3% slower — the
+// inlined expf of the statistics branch enlarges every forward instantiation.)
+__device__ __forceinline__ float exp_rs(float d) { return __builtin_amdgcn_exp2f(d * 1.4426950408889634f); }
 __device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
 __device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt((double)a); }
 
@@ -129,6 +135,10 @@ struct GemmEpi {
   // (max, Σ e^(y − max)) over the 64-column chunk of that row (set: the launch takes unsplit 128-column tiles).
   float2* rstat = nullptr;
   long long rstat_ld = 0;
+  // Tile order within each XCD's run of workgroups: 0 = output columns fastest (the tiles that run together share
+  // an activation row block), 1 = rows fastest (they share a weight column strip: for outputs many tiles wide,
+  // such as the vocabulary head, each strip is then fetched once instead of once per row block).
+  int rows_fastest = 0;
 };
 // Grouped (mixture-of-experts) GEMM schedule: W holds n_experts stacked [rows, cols] blocks; workgroup row
 // y of the launch computes rows tiles[3y+1] .. +tiles[3y+2] of the operand against expert tiles[3y]

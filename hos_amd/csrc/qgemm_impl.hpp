@@ -43,9 +43,8 @@ namespace {
 typedef short s4v __attribute__((ext_vector_type(4)));
 
 
-// e^d for the row statistics of a softmax: expf, the function the cross-entropy pass (fused.hip ce_kernel) applies to
-// the same logits, so the softmax denominator and its numerators come from one exp and each row's p sums to 1.
-__device__ __forceinline__ float exp_rs(float d) { return expf(d); }
+// (exp_rs, the e^x of the softmax statistics folded in the epilogue, is in kernels.hpp: the cross-entropy pass
+// that consumes them uses it too.)
 
 // Signed byte i of a word as float (one bit-field extract + one convert).
 __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
@@ -289,14 +288,23 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  // Workgroup ids are dispatched round-robin over the 8 XCDs, each with its own L2. Give every XCD a
-  // contiguous run of tiles (columns fastest), so the tiles that share an A row block share one L2.
-  int wid = blockIdx.x + gridDim.x * blockIdx.y;
-  const int nwg = gridDim.x * gridDim.y, full = nwg & ~7;
-  if (wid < full) wid = (wid & 7) * (full >> 3) + (wid >> 3);
-  if (gk.tiles) wid = blockIdx.x;  // grouped: row tile fixed above, no remap
+  // Workgroup ids are dispatched round-robin over the 8 XCDs, each with its own L2. Give every XCD a contiguous
+  // run of tiles — columns fastest, so the tiles that share an A row block share one L2, or rows fastest
+  // (epi.rows_fastest) for outputs many tiles wide, so the tiles that share a weight strip run together. (Runs that
+  // also keep whole splits of a split contraction on one XCD halved the vocabulary head dX's fetched bytes but
+  // made the step's split launches 3% slower on the MI355X: the split index stays blockIdx.z.)
+  int wid;
+  const int zsp = blockIdx.z;
+  if (gk.tiles) {
+    wid = blockIdx.x;  // grouped: row tile fixed above, no remap
+  } else {
+    const int X = gridDim.x, Y = gridDim.y, T = X * Y, full = T & ~7;
+    int t = blockIdx.x + X * blockIdx.y;
+    if (t < full) t = (t & 7) * (full >> 3) + (t >> 3);
+    wid = epi.rows_fastest ? (t % Y) * X + t / Y : t;
+  }
   const int m0 = (wid / gridDim.x) * BM, n0 = (wid % gridDim.x) * BN;
-  const int cbeg = blockIdx.z * c_per_split;
+  const int cbeg = zsp * c_per_split;
   const int cend = min(C, cbeg + c_per_split);
   const int nslab = (cend - cbeg) / BK;
 
@@ -522,7 +530,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
   // over the LDS banks.
   // (split contraction: the first split's workgroups carry the rank-r term in their partial; U is pre-divided by
   // the row's power-of-two rinv, so the reduction's (Σ partials)·rinv is exactly the unsplit result's form)
-  const int rank = (split && blockIdx.z != 0) ? 0 : epi.rank;
+  const int rank = (split && zsp != 0) ? 0 : epi.rank;
   const int rpad = (rank + 15) & ~15;
   const int nch = rpad >> 3, swz = (nch & (nch - 1)) ? 1 : nch - 1;
   auto sidx = [&](int row, int q) { return row * rpad + ((((q >> 3) ^ (row & swz))) << 3) + (q & 7); };
@@ -598,7 +606,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
           if (row >= M || col >= Nout) continue;
           float v[4] = {t4.x, t4.y, t4.z, t4.w};
           if (split) {
-            float* d = ws + ((long long)blockIdx.z * M + row) * Nout + col;
+            float* d = ws + ((long long)zsp * M + row) * Nout + col;
             if (vec) {
               *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
             } else {
@@ -687,7 +695,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
         if (row >= M) continue;
         float v = acc[i][j][r];
         if (split) {
-          ws[((long long)blockIdx.z * M + row) * Nout + col] = v;
+          ws[((long long)zsp * M + row) * Nout + col] = v;
         } else {
           v *= rinv[row];
           if (epi.bias) v += epi.bias[col];
@@ -902,6 +910,8 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
 #endif
   int per = ceil_div(nslab, splits) * bk;
   splits = ceil_div(C, per);
+  // Outputs many tiles wide (the vocabulary head's forward): rows fastest, so each weight strip is fetched once.
+  if (ceil_div(Nout, bn) >= 64 * ceil_div(M, bm)) epi.rows_fastest = 1;
 #define HOS_QG(BM_, BN_, BK_) \
   if (bm == BM_ && bn == BN_ && bk == BK_) launch_shape<QT, DX, BM_, BN_, BK_, NP>(w, a, lda, M, Nout, C, per, splits, epi, ws, st)
   HOS_QG(128, 128, 64);
