@@ -366,25 +366,51 @@ __global__ void __launch_bounds__(RB) swiglu_bwd_reg_kernel(const float* __restr
   if (threadIdx.x == 0) rinv[row] = ldexpf(1.0f, -e);
 }
 
+// Four consecutive elements (offset off = m·n + c) of a row formed from a split qGEMM's deferred partials: summed in
+// split order, times the row's scale, plus the residual — splitk_reduce4's arithmetic for the same output.
+__device__ __forceinline__ float4 split_row4(const SplitSrc& s, long long off, float ri) {
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int z = 0; z < s.splits; z++) {
+    const float4 p = *reinterpret_cast<const float4*>(s.ws + z * s.mn + off);
+    v.x += p.x;
+    v.y += p.y;
+    v.z += p.z;
+    v.w += p.w;
+  }
+  float4 x = make_float4(v.x * ri, v.y * ri, v.z * ri, v.w * ri);
+  if (s.resid) {
+    const float4 a = *reinterpret_cast<const float4*>(s.resid + off);
+    x = make_float4(a.x + x.x, a.y + x.y, a.z + x.z, a.w + x.w);
+  }
+  return x;
+}
+
 // Register-resident RMSNorm forward / backward for d % 4 == 0, d <= 4·RB·NORM_NV (same per-element arithmetic as
 // the kernels above; the row sums are taken over each thread's float4 columns, then across the block).
 constexpr int NORM_NV = 4;
 
-__global__ void __launch_bounds__(RB) rmsnorm_fwd_reg_kernel(const float* __restrict__ x, const float* __restrict__ w,
+// src.splits > 0: the input row is formed from a split GEMM's deferred partials (split_row4) and written to x.
+__global__ void __launch_bounds__(RB) rmsnorm_fwd_reg_kernel(float* __restrict__ x, const float* __restrict__ w,
                                                               float eps, int d, float* __restrict__ xn,
                                                               _Float16* __restrict__ xh, _Float16* __restrict__ xl,
                                                               float* __restrict__ rinv,
-                                                              float* __restrict__ inv_out) {
+                                                              float* __restrict__ inv_out, SplitSrc src) {
   __shared__ float red[8];
   const int row = blockIdx.x, d4 = d >> 2;
-  const float4* xr = reinterpret_cast<const float4*>(x + (long long)row * d);
+  float4* xr = reinterpret_cast<float4*>(x + (long long)row * d);
+  const float sri = src.splits ? src.rinv[row] : 0.0f;
   float4 xv[NORM_NV];
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < NORM_NV; j++) {
     const int i = threadIdx.x + RB * j;
     if (i < d4) {
-      xv[j] = xr[i];
+      if (src.splits) {
+        xv[j] = split_row4(src, (long long)row * d + 4 * i, sri);
+        xr[i] = xv[j];
+      } else {
+        xv[j] = xr[i];
+      }
       ss += xv[j].x * xv[j].x;
       ss += xv[j].y * xv[j].y;
       ss += xv[j].z * xv[j].z;
@@ -420,14 +446,17 @@ __global__ void __launch_bounds__(RB) rmsnorm_fwd_reg_kernel(const float* __rest
   }
 }
 
+// src.splits > 0: the incoming gradient row g is formed from a split GEMM's deferred partials (split_row4).
 __global__ void __launch_bounds__(RB) rmsnorm_bwd_reg_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                               const float* __restrict__ inv_in,
                                                               const float* __restrict__ w, int d,
                                                               float* __restrict__ dx, _Float16* __restrict__ hd,
-                                                              _Float16* __restrict__ hl, float* __restrict__ hr) {
+                                                              _Float16* __restrict__ hl, float* __restrict__ hr,
+                                                              SplitSrc src) {
   __shared__ float red[8];
   const int row = blockIdx.x, d4 = d >> 2;
   const float4* gr = reinterpret_cast<const float4*>(g + (long long)row * d);
+  const float sri = src.splits ? src.rinv[row] : 0.0f;
   const float4* xr = reinterpret_cast<const float4*>(x + (long long)row * d);
   float4* dr = reinterpret_cast<float4*>(dx + (long long)row * d);
   float4 gw[NORM_NV], xv[NORM_NV];
@@ -437,7 +466,7 @@ __global__ void __launch_bounds__(RB) rmsnorm_bwd_reg_kernel(const float* __rest
     const int i = threadIdx.x + RB * j;
     if (i < d4) {
       const float4 wv = reinterpret_cast<const float4*>(w)[i];
-      const float4 gv = gr[i];
+      const float4 gv = src.splits ? split_row4(src, (long long)row * d + 4 * i, sri) : gr[i];
       xv[j] = xr[i];
       gw[j] = make_float4(gv.x * wv.x, gv.y * wv.y, gv.z * wv.z, gv.w * wv.w);
       s += gw[j].x * xv[j].x;
@@ -729,19 +758,40 @@ static bool norm_reg_ok(int d, const void* a, const void* b, const void* c, cons
   auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
   return d % 4 == 0 && d <= 4 * RB * NORM_NV && al(a, 16) && al(b, 16) && al(c, 16) && al(h, 8) && al(l, 8);
 }
-void launch_rmsnorm_fwd(const float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
-                        hipStream_t st) {
-  if (norm_reg_ok(d, x, w, xn, out.data, out.lo))
-    rmsnorm_fwd_reg_kernel<<<M, RB, 0, st>>>(x, w, eps, d, xn, out.data, out.lo, out.rinv, inv);
+// The deferred partials of a split GEMM reduced into dst [M, d] (the general path when a row kernel cannot fuse it).
+static void reduce_split_src(const SplitSrc& s, float* dst, int M, int d, hipStream_t st) {
+  GemmEpi e{};
+  e.out = dst;
+  e.ldo = d;
+  e.resid = s.resid;
+  launch_qgemm_split_reduce(s.ws, s.splits, M, d, s.rinv, e, st);
+}
+static bool split_ok(const SplitSrc& s) {
+  return s.splits > 0 && ((uintptr_t)s.ws & 15) == 0 && ((uintptr_t)s.resid & 15) == 0;
+}
+void launch_rmsnorm_fwd(float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
+                        hipStream_t st, SplitSrc src) {
+  const bool reg = norm_reg_ok(d, x, w, xn, out.data, out.lo);
+  if (src.splits > 0 && !(reg && split_ok(src))) {
+    reduce_split_src(src, x, M, d, st);
+    src = SplitSrc{};
+  }
+  if (reg)
+    rmsnorm_fwd_reg_kernel<<<M, RB, 0, st>>>(x, w, eps, d, xn, out.data, out.lo, out.rinv, inv, src);
   else
     rmsnorm_fwd_kernel<<<M, RB, 0, st>>>(x, w, eps, d, xn, out.data, out.lo, out.rinv, inv);
   HOS_HIP_CHECK(hipGetLastError());
 }
-void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
-                        hipStream_t st, H16 out) {
+void launch_rmsnorm_bwd(float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
+                        hipStream_t st, H16 out, SplitSrc src) {
   auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
-  if (norm_reg_ok(d, g, x, w, out.data, out.lo) && al(dx, 16))
-    rmsnorm_bwd_reg_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv);
+  const bool reg = norm_reg_ok(d, g, x, w, out.data, out.lo) && al(dx, 16);
+  if (src.splits > 0 && !(reg && split_ok(src))) {
+    reduce_split_src(src, g, M, d, st);
+    src = SplitSrc{};
+  }
+  if (reg)
+    rmsnorm_bwd_reg_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv, src);
   else
     rmsnorm_bwd_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());

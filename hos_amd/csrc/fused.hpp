@@ -4,11 +4,13 @@
 
 namespace hos {
 void launch_embed(const QWeight& table, const int32_t* ids, float* x, int M, int d, hipStream_t st);
-void launch_rmsnorm_fwd(const float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
-                        hipStream_t st);
-// out.data != null: also write dx's fp16 GEMM operand (as launch_to_h16 would)
-void launch_rmsnorm_bwd(const float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
-                        hipStream_t st, H16 out = H16{nullptr, nullptr, nullptr});
+// src.splits > 0: x is first formed (and stored) from a split GEMM's deferred partials, as its reduction would.
+void launch_rmsnorm_fwd(float* x, const float* w, float eps, int M, int d, float* xn, H16 out, float* inv,
+                        hipStream_t st, SplitSrc src = SplitSrc{});
+// out.data != null: also write dx's fp16 GEMM operand (as launch_to_h16 would). src.splits > 0: the incoming
+// gradient g is formed from a split GEMM's deferred partials (g is then only written on the general path).
+void launch_rmsnorm_bwd(float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
+                        hipStream_t st, H16 out = H16{nullptr, nullptr, nullptr}, SplitSrc src = SplitSrc{});
 void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,
                  bool inverse, int M, hipStream_t st);
 // RoPE (col0 = 0) fused with the fp16 row operand of the first W columns (row stride W), as launch_rope

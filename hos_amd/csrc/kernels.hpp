@@ -139,7 +139,24 @@ struct GemmEpi {
   // an activation row block), 1 = rows fastest (they share a weight column strip: for outputs many tiles wide,
   // such as the vocabulary head, each strip is then fetched once instead of once per row block).
   int rows_fastest = 0;
+  // Deferred reduction (host pointer, may be null): a launch split over the contraction leaves its partials in the
+  // workspace, stores the split count here and launches no reduction — the consumer reads the partials (SplitSrc);
+  // an unsplit launch writes its output as usual and stores 1.
+  int* defer = nullptr;
 };
+// A row source given as the partials of a split qGEMM whose reduction was deferred to its consumer: row m =
+// (Σ_z ws[z·mn + m·n .. ]) · rinv[m] (+ resid[m]), the partials summed in split order and then scaled, exactly as
+// splitk_reduce4 forms an unbiased, non-accumulating output. splits = 0: no such source.
+struct SplitSrc {
+  const float* ws = nullptr;
+  int splits = 0;
+  long long mn = 0;
+  const float* rinv = nullptr;
+  const float* resid = nullptr;
+};
+// The deterministic split-K reduction of a qGEMM's partials into epi.out (what a launch without epi.defer runs).
+void launch_qgemm_split_reduce(const float* ws, int splits, long long M, int N, const float* rinv, const GemmEpi& epi,
+                               hipStream_t st);
 // Grouped (mixture-of-experts) GEMM schedule: W holds n_experts stacked [rows, cols] blocks; workgroup row
 // y of the launch computes rows tiles[3y+1] .. +tiles[3y+2] of the operand against expert tiles[3y]
 // (−1: nothing to do). Built on the device by the router, so the launch needs no host round trip.

@@ -172,7 +172,7 @@ int hos_hip_rmsnorm_fwd(hos_ctx* c, const float* x, const float* w, size_t rows,
                         float* inv) {
   return op_guard(c, [&](hipStream_t st) {
     HOS_REQUIRE(x && w && y && inv, HOS_E_INVALID, "null pointer");
-    launch_rmsnorm_fwd(x, w, eps, (int)rows, (int)d, y, op_h16(c, rows, d), inv, st);
+    launch_rmsnorm_fwd(const_cast<float*>(x), w, eps, (int)rows, (int)d, y, op_h16(c, rows, d), inv, st);  // x read only
   });
 }
 
@@ -183,7 +183,7 @@ int hos_hip_rmsnorm_bwd(hos_ctx* c, const float* g, const float* x, const float*
   return op_guard(c, [&](hipStream_t st) {
     HOS_REQUIRE(g && x && inv && w && gx, HOS_E_INVALID, "null pointer");
     launch_fill(gx, (long long)(rows * d), 0.0f, st);
-    launch_rmsnorm_bwd(g, x, inv, w, (int)rows, (int)d, gx, st);
+    launch_rmsnorm_bwd(const_cast<float*>(g), x, inv, w, (int)rows, (int)d, gx, st);  // g read only
   });
 }
 

@@ -132,6 +132,11 @@ struct hos_peft {
   std::vector<void*> attn_planes;
   float* ws = nullptr;
   size_t ws_bytes = 0;
+  // Partials of the split GEMMs whose reduction the next row kernel performs (the FFN down projection's forward,
+  // the stacked gate|up dX, the vocabulary head's dX): a workspace of their own, so that launches in between (the
+  // LoRA dA/dB partials) cannot overwrite them.
+  float* ws2 = nullptr;
+  SplitSrc xsrc{};  // the residual row source the next forward RMSNorm forms and stores
   float2* rope_tab = nullptr;
   int32_t *ids = nullptr, *tgts = nullptr;
   std::vector<void*> allocs;
@@ -220,6 +225,37 @@ struct hos_peft {
     e.accumulate = accumulate;
     e.resid = nullptr;
     launch_qgemm_dx(w, a, lda, M, e, ws, ws_bytes, np ? np : pd, st);
+  }
+  // A GEMM whose split-K reduction (if the tile rule splits it) is left to the row kernel that consumes its output:
+  // returns the partials as a SplitSrc (splits = 0 when the launch was not split and wrote out itself). The output
+  // must be dense (ldo = its width), unbiased and not accumulated.
+  SplitSrc deferred(bool dx, const QWeight& w, H16 a, long long lda, int M, float* out, long long ldo,
+                    const float* resid, GemmEpi lo, int np) {
+    const long long N = dx ? w.cols : w.rows;
+    HOS_REQUIRE(ldo == N, HOS_E_INVALID, "peft: a deferred reduction needs a dense output");
+    Scope s(this, dx ? "qgemm_dx" : "qgemm_fwd", 2.0 * M * w.rows * w.cols,
+            2.0 * M * (dx ? w.rows : w.cols) + wbytes(w) + 4.0 * M * N * (resid ? 2 : 1));
+    GemmEpi e = lo;
+    e.out = out;
+    e.ldo = ldo;
+    e.bias = nullptr;
+    e.accumulate = 0;
+    e.resid = resid;
+    int splits = 1;
+    e.defer = &splits;
+    if (dx)
+      launch_qgemm_dx(w, a, lda, M, e, ws2, ws_bytes, np ? np : pd, st);
+    else
+      launch_qgemm_fwd(w, a, lda, M, e, ws2, ws_bytes, np ? np : pf, st);
+    SplitSrc src{};
+    if (splits > 1) {
+      src.ws = ws2;
+      src.splits = splits;
+      src.mn = (long long)M * N;
+      src.rinv = a.rinv;
+      src.resid = resid;
+    }
+    return src;
   }
   void to16(const float* x, long long ldx, int M, int K) {
     Scope s(this, "convert", 0, 6.0 * M * K);
@@ -605,7 +641,8 @@ struct hos_peft {
       const bool lqkv = has(TQ) || has(TK) || has(TV);
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * (lqkv ? 2 : 1) + 2.0 * M * d);
-        launch_rmsnorm_fwd(a.x, w.attn_norm, c.rms_eps, M, d, lqkv ? a.xn1 : nullptr, hs, a.inv1, st);
+        launch_rmsnorm_fwd(a.x, w.attn_norm, c.rms_eps, M, d, lqkv ? a.xn1 : nullptr, hs, a.inv1, st, xsrc);
+        xsrc = SplitSrc{};
       }
       lora_down(l, 0, a.xn1, d, M, hs_in());
       if (w.qkv.q && group_uniform(0) && (!c.attn_bias || w.bias_qkv)) {
@@ -657,12 +694,16 @@ struct hos_peft {
         launch_swiglu_fwd(a.gu, M, F, a.h, hdn, st);
       }
       lora_down(l, 3, a.h, F, M, hdn.lo ? HIn{hdn.data, hdn.lo, hdn.rinv} : HIn{});
-      qfwd(w.w[TD], hdn, F, M, rga ? a.xr : xnext, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
+      if (rga)
+        qfwd(w.w[TD], hdn, F, M, a.xr, d, nullptr, a.x2, 0, up_epi(l, TD), tpf[TD]);
+      else  // x_{l+1} is formed (and stored) by the next RMSNorm from the partials when the launch splits
+        xsrc = deferred(false, w.w[TD], hdn, F, M, xnext, d, a.x2, up_epi(l, TD), tpf[TD]);
       if (rga) rga_forward(l, M, xnext);
     }
     {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d + 2.0 * M * d);
-      launch_rmsnorm_fwd(xfinal, out_norm, c.rms_eps, M, d, nullptr, hs, invf, st);
+      launch_rmsnorm_fwd(xfinal, out_norm, c.rms_eps, M, d, nullptr, hs, invf, st, xsrc);
+      xsrc = SplitSrc{};
     }
     GemmEpi he{};
     if (!need_logits_only) {  // the cross-entropy's softmax statistics come out of the head GEMM's epilogue
@@ -686,18 +727,20 @@ struct hos_peft {
       launch_rga_loss(rgsum, Mmax, L, B, T, Kg, rlambda, rgm, loss, st);
     }
     const QWeight& head = out_set ? out : tok;
-    qdx(head, dl, V, M, dxn, d, 0, GemmEpi{}, phd);
+    const SplitSrc hsrc = deferred(true, head, dl, V, M, dxn, d, nullptr, GemmEpi{}, phd);
     // The RMSNorm backwards also write the fp16 operand of their dx for the GEMMs that follow; not where the
     // RGA backward changes dx in between or a mixture-of-experts FFN takes no such operand.
     const bool fuse16 = !rga && !E;
     {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d * 3 + 4.0 * M * d + (fuse16 ? 6.0 * M * d : 0));
       launch_fill(dx, (long long)M * d, 0.0f, st);
-      launch_rmsnorm_bwd(dxn, xfinal, invf, out_norm, M, d, dx, st, fuse16 ? hs : H16{nullptr, nullptr, nullptr});
+      launch_rmsnorm_bwd(dxn, xfinal, invf, out_norm, M, d, dx, st, fuse16 ? hs : H16{nullptr, nullptr, nullptr},
+                         hsrc);
     }
     for (int l = L - 1; l >= 0; l--) {
       LayerAct& a = act[l];
       LayerW& w = lw[l];
+      SplitSrc gsrc{};  // the stacked gate|up dX's partials, reduced by the FFN RMSNorm backward
       if (rga) rga_backward(l, B, T);  // dx: gradient at x_{l+1} -> at the FFN output
       // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA), or the mixture of experts ----
       if (E) {
@@ -717,7 +760,7 @@ struct hos_peft {
       }
       if (gu_lora) lora_grad_b(l, 2, gu_f32 ? dgu : nullptr, 2LL * F, 2LL * F, M, hs_in());
       if (w.gu.q && group_uniform(2) && gcount(2) * r <= 32) {
-        qdx(w.gu, hs, 2LL * F, M, dxn, d, 0, stacked_down_epi(l, 2), tpd[TG]);
+        gsrc = deferred(true, w.gu, hs, 2LL * F, M, dxn, d, nullptr, stacked_down_epi(l, 2), tpd[TG]);
       } else {
         H16 hu = h16_offset(hs, F);
         qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG), tpd[TG]);
@@ -727,7 +770,7 @@ struct hos_peft {
       }
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4 + 6.0 * M * d);
-        launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st, hs);
+        launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st, hs, gsrc);
       }
       // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
       lora_grad_b(l, 1, dx, d, d, M, hs_in());
@@ -1127,6 +1170,7 @@ struct hos_peft {
       attn_planes[l] = alloc<float>(attn_scratch_bytes(c.max_batch, c.max_seq, c.n_heads, c.n_kv_heads, c.head_dim) / 4);
     ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(d, F) * 4 * 8, 1ull << 30));
     ws = alloc<float>(ws_bytes / 4);
+    ws2 = alloc<float>(ws_bytes / 4);
     cbatch = ColsBatch{};
     cbatch.cap = (64ull << 20) / 4;
     cbatch.base = alloc<float>(cbatch.cap);

@@ -1,24 +1,14 @@
-// Dequant-fused quantized-weight GEMMs on fp16 MFMA (v_mfma_f32_32x32x16_f16, fp32 accumulate).
+// Dequant-fused quantized-weight GEMMs on fp16 MFMA (v_mfma_f32_32x32x16_f16, fp32 accumulate): the launchers and
+// the fp16 operand conversion; the kernel templates and the tile rule are in qgemm_impl.hpp, instantiated per weight
+// layout in qgemm_{q8,q4k,q5k,q6k,f16,bf16,f32}.hip.
 //
 //   fwd: Y[M, N]  = A[M, K] · deq(W)ᵀ   W [N, K]  — the frozen-base forward x·t_const(W)
 //   dx : dX[M, K] = dY[M, N] · deq(W)   W [N, K]  — the frozen-base backward g·Bᵀ
 //        (src/tensor.rs:316-327 and :347-360; src/peft.rs:24-33 transposes W to [in,out])
 //
-// Each 32-wide slab of the contraction streams the packed weight from HBM, dequantizes it in
-// registers with the bit-exact device functions of kernels.hpp and stores it in LDS in the MFMA
-// B-operand layout (contraction-contiguous per output column). The fwd tile is a run of W rows; the
-// dx tile is W transposed on the fly (8 rows × 2 columns per thread). The activation operand arrives
-// as fp16 with an exact power-of-two scale per row; the epilogue multiplies that scale back out.
-//
-// Precision passes (NP): one fp16 product rounds both operands to 11 bits (~3e-4 relative per GEMM).
-//   NP = 1: A·W                            (fp16 × fp16)
-//   NP = 2: A_hi·W + A_lo·W                (activation carried to ~22 bits)
-//   NP = 3: A_hi·W_hi + A_lo·W_hi + A_hi·W_lo  (both operands to ~22 bits; dropped A_lo·W_lo ~2^-22)
-//   NP = 4: A·W_hi + A·W_lo                    (weight to ~22 bits, activation rounded once)
-// where W_hi = fp16(w), W_lo = fp16(w − W_hi) of the f32 dequantized w.
-//
-// Work decomposition: 256 threads = 4 waves (2×2), workgroup tile BM×BN, wave tile (BM/2)×(BN/2)
-// of 32×32 MFMA tiles, double-buffered LDS, optional split-K reduced deterministically.
+// The activation operand arrives as fp16 with an exact power-of-two scale per row (to_h16 below, or the row kernel
+// that produced it); the epilogue multiplies that scale back out. Precision modes 1-5 are described in
+// qgemm_impl.hpp.
 #include "kernels.hpp"
 
 namespace hos {

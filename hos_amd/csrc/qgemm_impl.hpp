@@ -926,7 +926,13 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   else throw Error(HOS_E_INVALID, "qgemm: no kernel for the chosen tile");
 #undef HOS_QG
   HOS_HIP_CHECK(hipGetLastError());
-  if (splits > 1) launch_splitk_reduce(ws, splits, M, Nout, a.rinv, epi, st);
+  if (epi.defer) {
+    HOS_REQUIRE(splits == 1 || (!epi.bias && !epi.accumulate), HOS_E_INVALID,
+                "qgemm: a deferred reduction takes no bias and no accumulation");
+    *epi.defer = splits;
+  } else if (splits > 1) {
+    launch_splitk_reduce(ws, splits, M, Nout, a.rinv, epi, st);
+  }
 }
 
 // Grouped launch (mixture-of-experts): W = n_experts stacked blocks, 128×128 tiles, no split.
