@@ -452,7 +452,7 @@ __global__ void __launch_bounds__(RB) rmsnorm_bwd_reg_kernel(const float* __rest
                                                               const float* __restrict__ w, int d,
                                                               float* __restrict__ dx, _Float16* __restrict__ hd,
                                                               _Float16* __restrict__ hl, float* __restrict__ hr,
-                                                              SplitSrc src) {
+                                                              SplitSrc src, const float* __restrict__ dxin) {
   __shared__ float red[8];
   const int row = blockIdx.x, d4 = d >> 2;
   const float4* gr = reinterpret_cast<const float4*>(g + (long long)row * d);
@@ -483,7 +483,7 @@ __global__ void __launch_bounds__(RB) rmsnorm_bwd_reg_kernel(const float* __rest
   for (int j = 0; j < NORM_NV; j++) {
     const int i = threadIdx.x + RB * j;
     if (i < d4) {
-      float4 o = dr[i];
+      float4 o = dxin ? reinterpret_cast<const float4*>(dxin + (long long)row * d)[i] : dr[i];
       o.x += gw[j].x * inv - xv[j].x * k;
       o.y += gw[j].y * inv - xv[j].y * k;
       o.z += gw[j].z * inv - xv[j].z * k;
@@ -783,15 +783,20 @@ void launch_rmsnorm_fwd(float* x, const float* w, float eps, int M, int d, float
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rmsnorm_bwd(float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
-                        hipStream_t st, H16 out, SplitSrc src) {
+                        hipStream_t st, H16 out, SplitSrc src, const float* dx_in) {
   auto al = [](const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; };
-  const bool reg = norm_reg_ok(d, g, x, w, out.data, out.lo) && al(dx, 16);
+  if (dx_in == dx) dx_in = nullptr;
+  const bool reg = norm_reg_ok(d, g, x, w, out.data, out.lo) && al(dx, 16) && al(dx_in, 16);
+  if (dx_in && !reg) {  // the general kernel updates in place: start from a copy
+    HOS_HIP_CHECK(hipMemcpyAsync(dx, dx_in, (size_t)M * d * sizeof(float), hipMemcpyDeviceToDevice, st));
+    dx_in = nullptr;
+  }
   if (src.splits > 0 && !(reg && split_ok(src))) {
     reduce_split_src(src, g, M, d, st);
     src = SplitSrc{};
   }
   if (reg)
-    rmsnorm_bwd_reg_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv, src);
+    rmsnorm_bwd_reg_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv, src, dx_in);
   else
     rmsnorm_bwd_kernel<<<M, RB, 0, st>>>(g, x, inv, w, d, dx, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());

@@ -9,8 +9,10 @@ void launch_rmsnorm_fwd(float* x, const float* w, float eps, int M, int d, float
                         hipStream_t st, SplitSrc src = SplitSrc{});
 // out.data != null: also write dx's fp16 GEMM operand (as launch_to_h16 would). src.splits > 0: the incoming
 // gradient g is formed from a split GEMM's deferred partials (g is then only written on the general path).
+// dx_in != null: dx = dx_in + the input gradient (dx_in is left as it was) instead of dx += it.
 void launch_rmsnorm_bwd(float* g, const float* x, const float* inv, const float* w, int M, int d, float* dx,
-                        hipStream_t st, H16 out = H16{nullptr, nullptr, nullptr}, SplitSrc src = SplitSrc{});
+                        hipStream_t st, H16 out = H16{nullptr, nullptr, nullptr}, SplitSrc src = SplitSrc{},
+                        const float* dx_in = nullptr);
 void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T, const float2* tab, bool neox,
                  bool inverse, int M, hipStream_t st);
 // RoPE (col0 = 0) fused with the fp16 row operand of the first W columns (row stride W), as launch_rope

@@ -15,6 +15,7 @@
 // split order. Deterministic. (An in-kernel "last workgroup reduces" variant with device-scope fences
 // measured 3-4x slower here: every release fence writes back the XCD's L2.)
 #include <cstdlib>
+#include <vector>
 
 #include "lora.hpp"
 
@@ -398,6 +399,24 @@ __global__ void __launch_bounds__(256) lora_cols_kernel(int M, int mchunk, ColsJ
     cols_body<NSA, GHA, CWA>(a, (int)blockIdx.x, M, mchunk, red, part);
   else
     cols_body<NSB, false>(b, (int)blockIdx.x - b.bx0, M, mchunk, red, part);
+}
+
+// Up to COLS_MULTI independent jobs of one kernel shape (NS row tiles, G as f32 or as the fp16 operand in CW-column
+// runs) in one launch, each over all M rows in one workgroup per column block — no split of M, so no partials and
+// no reduction launch: the training step's dA / dB products of every layer, queued during the backward and run
+// together after it.
+constexpr int COLS_MULTI = 16;
+struct ColsMultiArgs {
+  ColsJobDev jobs[COLS_MULTI];
+  int start[COLS_MULTI + 1];  // first workgroup of each job
+  int n;
+};
+template <int NS, bool GH, int CW>
+__global__ void __launch_bounds__(256) lora_cols_multi_kernel(int M, ColsMultiArgs args) {
+  __shared__ float red[2 * NS * 16 * 16 * CW];
+  int j = 0;
+  while (j + 1 < args.n && (int)blockIdx.x >= args.start[j + 1]) j++;
+  cols_body<NS, GH, CW>(args.jobs[j], (int)blockIdx.x - args.start[j], M, M, red, nullptr);
 }
 
 // Separate-launch reductions of the partials (one thread per output element of every block).
@@ -813,6 +832,52 @@ size_t lora_cols2_ws_bytes(long long M, const ColsJob& ja, const ColsJob* jb) {
   if (jb && a.nsr != b.nsr)  // some width pairs have no combined kernel and run as two launches in turn
     need = std::max({need, lora_cols2_ws_bytes(M, ja, nullptr), lora_cols2_ws_bytes(M, *jb, nullptr)});
   return need;
+}
+
+void launch_lora_cols_multi(long long M, const ColsJob* jobs, int n, hipStream_t st) {
+  if (M <= 0 || n <= 0) return;
+  static_assert(sizeof(ColsMultiArgs) <= 4000, "kernel arguments");
+  // group the jobs by kernel shape, in their order; launch each group in chunks of COLS_MULTI
+  std::vector<ColsJobDev> dev(n);
+  std::vector<int> key(n);
+  for (int i = 0; i < n; i++) {
+    dev[i] = prepare(jobs[i], 0);
+    dev[i].S = 1;
+    dev[i].part_off = 0;
+    const int ns = dev[i].nsr / 16, v = dev[i].gh.hi ? (dev[i].bw == 128 ? 2 : 1) : 0;
+    HOS_REQUIRE(ns >= 1 && ns <= 6, HOS_E_INVALID, "lora_cols_multi: bad width");
+    key[i] = ns * 3 + v;
+  }
+  std::vector<bool> done(n, false);
+  for (int i = 0; i < n; i++) {
+    if (done[i]) continue;
+    ColsMultiArgs args{};
+    int tot = 0;
+    for (int k = i; k < n && args.n < COLS_MULTI; k++) {
+      if (done[k] || key[k] != key[i]) continue;
+      done[k] = true;
+      args.start[args.n] = tot;
+      args.jobs[args.n++] = dev[k];
+      tot += dev[k].gx;
+    }
+    args.start[args.n] = tot;
+    const int ns = key[i] / 3, v = key[i] % 3;
+#define CMULTI(NSV)                                                                                 \
+  case NSV:                                                                                         \
+    if (v == 2)                                                                                     \
+      lora_cols_multi_kernel<NSV, true, 8><<<tot, 256, 0, st>>>((int)M, args);                      \
+    else if (v == 1)                                                                                \
+      lora_cols_multi_kernel<NSV, true, 4><<<tot, 256, 0, st>>>((int)M, args);                      \
+    else                                                                                            \
+      lora_cols_multi_kernel<NSV, false, 4><<<tot, 256, 0, st>>>((int)M, args);                     \
+    break;
+    switch (ns) {
+      CMULTI(1) CMULTI(2) CMULTI(3) CMULTI(4) CMULTI(5) CMULTI(6)
+      default: break;
+    }
+#undef CMULTI
+    HOS_HIP_CHECK(hipGetLastError());
+  }  // (jobs of this shape past a full chunk start a chunk of their own later in the loop)
 }
 
 void launch_lora_cols_flush(ColsBatch& bt, hipStream_t st) {

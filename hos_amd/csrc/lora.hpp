@@ -95,6 +95,9 @@ struct ColsBatch {
   int n = 0;
 };
 void launch_lora_cols_flush(ColsBatch& b, hipStream_t st);
+// Every job in as few launches as their kernel shapes allow, each output block over all M rows in one workgroup
+// (no partials, no reduction launch). Deterministic: each element sums its rows in one fixed order.
+void launch_lora_cols_multi(long long M, const ColsJob* jobs, int n, hipStream_t st);
 // Two independent cols products over the same M in one launch (and one reduction launch); b may be null.
 // Deterministic: the split of M depends only on M and the combined block count, and every output element sums
 // its split partials in split order.

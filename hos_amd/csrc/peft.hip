@@ -82,6 +82,14 @@ struct hos_peft {
   ColsJob pend_db;       // dB of the group whose backward is in progress, launched with its dA
   ColsBatch cbatch;      // a layer's dA/dB partials, reduced in one launch at the end of the layer
   int pend_group = -1;
+  // Whole-backward batching of the LoRA dA / dB products (dense LoRA models with two-plane operands): every layer
+  // keeps the inputs those products read — its du, the q|k|v output gradient, the residual gradients at x2 and at
+  // x_{l+1}, the fp16 d(gate|up) — and the products of all layers run together after the last layer, in a few
+  // launches without a split of M (launch_lora_cols_multi) instead of five small launches per layer.
+  bool gbatch = false;
+  std::vector<float*> du_l, dqkv_l, dxs_l, dx2s_l;  // per layer; dxs_l[l]: gradient at x_{l+1}, dx2s_l[l]: at x2
+  std::vector<H16> dgu16_l;                         // per layer: d(gate|up) as the fp16 operand
+  std::vector<ColsJob> gjobs;                       // the step's queued dA / dB products
   int tpf[7] = {0, 0, 0, 0, 0, 0, 0}, tpd[7] = {0, 0, 0, 0, 0, 0, 0};  // per-target overrides (0 = site mode)
   float lscale = 0.0f;
 
@@ -323,6 +331,7 @@ struct hos_peft {
   // The fp16 operand of the activation the current GEMM reads (when it carries the residual plane) and the
   // factor split of a group's At (a) or Bcat: the LoRA rows products then run on fp16 MFMA.
   HIn hs_in() const { return hs.lo ? HIn{hs.data, hs.lo, hs.rinv} : HIn{}; }
+  float* du_of(int l) const { return gbatch ? du_l[l] : du; }
   B16 fac16(int l, int g, bool a) const {
     const long long off = a ? offAg[l * 4 + g] : offBg[l * 4 + g];
     return B16{P16h + off, P16l + off, psc + (a ? scA : scB)[l * 4 + g]};
@@ -402,7 +411,7 @@ struct hos_peft {
   GemmEpi stacked_down_epi(int l, int g) {
     GemmEpi e{};
     if (gcount(g) == 0) return e;
-    e.U = du + ucol(group_first(g));
+    e.U = du_of(l) + ucol(group_first(g));
     e.ldu = NT * r;
     e.L = P + offAg[l * 4 + g];
     e.slj = in_dim(group_first(g));
@@ -481,7 +490,7 @@ struct hos_peft {
       rs.boff[i] = bcol(t);
     }
     const int w = bw(g);
-    lora_rows("lora_du", M, kspan, lscale, dy, ldy, P + offBg[l * 4 + g], w, rs, du + ucol(first_adapted(g)),
+    lora_rows("lora_du", M, kspan, lscale, dy, ldy, P + offBg[l * 4 + g], w, rs, du_of(l) + ucol(first_adapted(g)),
               NT * r, dyh, dyh.hi ? fac16(l, g, false) : B16{});
     pend_db = ColsJob{r, lscale, act[l].u, NT * r, dy, ldy, cs, G + offBg[l * 4 + g], w, 1, dy ? HIn{} : dyh};
     pend_group = g;
@@ -490,7 +499,7 @@ struct hos_peft {
   GemmEpi down_epi(int l, int t) {
     GemmEpi e{};
     if (!has(t)) return e;
-    e.U = du + ucol(t);
+    e.U = du_of(l) + ucol(t);
     e.ldu = NT * r;
     e.L = P + offA[l * NT + t];
     e.slj = in_dim(t);
@@ -511,7 +520,12 @@ struct hos_peft {
     ColsSeg cs;
     cs.nseg = 1;
     cs.len[0] = in;
-    const ColsJob da{n * r, 1.0f, du + ucol(first), NT * r, x, ldx, cs, G + offAg[l * 4 + g], in, 1, xh};
+    const ColsJob da{n * r, 1.0f, du_of(l) + ucol(first), NT * r, x, ldx, cs, G + offAg[l * 4 + g], in, 1, xh};
+    if (gbatch) {  // both products wait for the end of the backward (their inputs are kept per layer)
+      gjobs.push_back(pend_db);
+      gjobs.push_back(da);
+      return;
+    }
     double fl = 2.0 * M * n * r * in, by = 4.0 * (M * (double)in + (double)M * n * r + (double)n * r * in);
     for (int t = 0; t < pend_db.sg.nseg; t++) {
       fl += 2.0 * M * r * pend_db.sg.len[t];
@@ -527,6 +541,19 @@ struct hos_peft {
   void flush_dab() {
     Scope s(this, "lora_dab", 0, 0);
     launch_lora_cols_flush(cbatch, st);
+  }
+  // The whole backward's queued dA / dB products (gbatch).
+  void run_gjobs(int M) {
+    if (gjobs.empty()) return;
+    double fl = 0.0, by = 0.0;
+    for (const ColsJob& j : gjobs)
+      for (int t = 0; t < j.sg.nseg; t++) {
+        fl += 2.0 * M * j.ns * j.sg.len[t];
+        by += 4.0 * ((double)M * j.sg.len[t] + (double)M * j.ns + (double)j.ns * j.sg.len[t]);
+      }
+    Scope s(this, "lora_dab", fl, by);
+    launch_lora_cols_multi(M, gjobs.data(), (int)gjobs.size(), st);
+    gjobs.clear();
   }
   void check_ready() {
     check_tensors();
@@ -731,6 +758,9 @@ struct hos_peft {
     // The RMSNorm backwards also write the fp16 operand of their dx for the GEMMs that follow; not where the
     // RGA backward changes dx in between or a mixture-of-experts FFN takes no such operand.
     const bool fuse16 = !rga && !E;
+    // gbatch: dx walks the per-layer residual gradients (each RMSNorm backward writes a new one); restored below
+    float* const dx_base = dx;
+    if (gbatch) dx = dxs_l[L - 1];
     {
       Scope s(this, "rmsnorm", 0, 4.0 * M * d * 3 + 4.0 * M * d + (fuse16 ? 6.0 * M * d : 0));
       launch_fill(dx, (long long)M * d, 0.0f, st);
@@ -741,6 +771,8 @@ struct hos_peft {
       LayerAct& a = act[l];
       LayerW& w = lw[l];
       SplitSrc gsrc{};  // the stacked gate|up dX's partials, reduced by the FFN RMSNorm backward
+      // gbatch: this layer's own output-gradient buffers (kept for the dA / dB products after the backward)
+      float* const dq = gbatch ? dqkv_l[l] : dqkv;
       if (rga) rga_backward(l, B, T);  // dx: gradient at x_{l+1} -> at the FFN output
       // ---- FFN branch: x_{l+1} = x2 + h·W_down (+ LoRA), or the mixture of experts ----
       if (E) {
@@ -754,23 +786,28 @@ struct hos_peft {
       // GEMM when it carries the residual plane (the dB pass in 16-byte runs of each plane); an f32 copy only for
       // single-plane precision modes.
       const bool gu_lora = has(TG) || has(TU), gu_f32 = gu_lora && !hs.lo;
+      // d(gate|up) as the fp16 operand: the shared scratch, or (gbatch) this layer's own copy
+      const H16 hg = (gbatch && gu_lora) ? dgu16_l[l] : hs;
       {
         Scope s(this, "swiglu", 0, 4.0 * M * F * 3 + 4.0 * M * F + (gu_f32 ? 8.0 * M * F : 0));
-        launch_swiglu_bwd(a.gu, dh, M, F, gu_f32 ? dgu : nullptr, hs, st);
+        launch_swiglu_bwd(a.gu, dh, M, F, gu_f32 ? dgu : nullptr, hg, st);
       }
-      if (gu_lora) lora_grad_b(l, 2, gu_f32 ? dgu : nullptr, 2LL * F, 2LL * F, M, hs_in());
+      if (gu_lora) lora_grad_b(l, 2, gu_f32 ? dgu : nullptr, 2LL * F, 2LL * F, M, HIn{hg.data, hg.lo, hg.rinv});
       if (w.gu.q && group_uniform(2) && gcount(2) * r <= 32) {
-        gsrc = deferred(true, w.gu, hs, 2LL * F, M, dxn, d, nullptr, stacked_down_epi(l, 2), tpd[TG]);
+        gsrc = deferred(true, w.gu, hg, 2LL * F, M, dxn, d, nullptr, stacked_down_epi(l, 2), tpd[TG]);
       } else {
-        H16 hu = h16_offset(hs, F);
-        qdx(w.w[TG], hs, 2LL * F, M, dxn, d, 0, down_epi(l, TG), tpd[TG]);
+        H16 hu = h16_offset(hg, F);
+        qdx(w.w[TG], hg, 2LL * F, M, dxn, d, 0, down_epi(l, TG), tpd[TG]);
         qdx(w.w[TU], hu, 2LL * F, M, dxn, d, 1, down_epi(l, TU), tpd[TU]);
       }
       lora_grad_a(l, 2, a.xn2, d, M);
       }
       {
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4 + 6.0 * M * d);
-        launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st, hs, gsrc);
+        // gbatch: gradient at x2 into this layer's own buffer (the one at x_{l+1} stays for the down dB)
+        float* const dx_in = dx;
+        if (gbatch) dx = dx2s_l[l];
+        launch_rmsnorm_bwd(dxn, a.x2, a.inv2, w.ffn_norm, M, d, dx, st, hs, gsrc, dx_in);
       }
       // ---- attention branch: x2 = x + attn(x)·W_o (+ LoRA) ----
       lora_grad_b(l, 1, dx, d, d, M, hs_in());
@@ -780,25 +817,25 @@ struct hos_peft {
         Scope s(this, "attn_bwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 5,
                 4.0 * M * (W3 * 2 + qd * 2) + 8.0 * B * c.n_heads * T);
         launch_attn_bwd(a.qkv, W3, qd, qd + kvd, a.o, dout, qd, a.lse, dvec, B, T, c.n_heads, c.n_kv_heads,
-                        c.head_dim, dqkv, W3, attn_part, attn_planes[l], st, true);
+                        c.head_dim, dq, W3, attn_part, attn_planes[l], st, true);
       }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
         // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both; without
         // QK-norm in between it also writes the fp16 operand of the q|k|v dX GEMM
         if (c.qk_norm)
-          launch_rope(dqkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
+          launch_rope(dq, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
         else
-          launch_rope_h16(dqkv, W3, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, W3, hs,
+          launch_rope_h16(dq, W3, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, W3, hs,
                           st);
       }
       if (c.qk_norm) {
         Scope s(this, "rmsnorm", 0, 4.0 * M * (qd + kvd) * 4);
-        launch_qknorm_bwd(dqkv, W3, 0, qd, w.q_norm, a.qk_pre, a.qk_inv, M, st);
-        launch_qknorm_bwd(dqkv, W3, qd, kvd, w.k_norm, a.qk_pre + (size_t)M * qd, a.qk_inv + M, M, st);
+        launch_qknorm_bwd(dq, W3, 0, qd, w.q_norm, a.qk_pre, a.qk_inv, M, st);
+        launch_qknorm_bwd(dq, W3, qd, kvd, w.k_norm, a.qk_pre + (size_t)M * qd, a.qk_inv + M, M, st);
       }
-      if (c.qk_norm) to16(dqkv, W3, M, W3);
-      lora_grad_b(l, 0, dqkv, W3, W3, M, hs_in());
+      if (c.qk_norm) to16(dq, W3, M, W3);
+      lora_grad_b(l, 0, dq, W3, W3, M, hs_in());
       if (w.qkv.q && group_uniform(0) && gcount(0) * r <= 64) {
         // one dX GEMM over the stacked q|k|v contraction, the three LoRA terms as one rank-3r update
         qdx(w.qkv, hs, W3, M, dxn, d, 0, stacked_down_epi(l, 0), tpd[TQ]);
@@ -809,13 +846,18 @@ struct hos_peft {
         qdx(w.w[TV], hv, W3, M, dxn, d, 1, down_epi(l, TV), tpd[TV]);
       }
       lora_grad_a(l, 0, a.xn1, d, M);
-      flush_dab();  // the layer's dA/dB reductions
+      if (!gbatch) flush_dab();  // the layer's dA/dB reductions
       {
         const bool emit = fuse16 && l > 0;
         Scope s(this, "rmsnorm", 0, 4.0 * M * d * 4 + (emit ? 6.0 * M * d : 0));
-        launch_rmsnorm_bwd(dxn, a.x, a.inv1, w.attn_norm, M, d, dx, st, emit ? hs : H16{nullptr, nullptr, nullptr});
+        float* const dx_in = dx;
+        if (gbatch) dx = l > 0 ? dxs_l[l - 1] : dx_base;
+        launch_rmsnorm_bwd(dxn, a.x, a.inv1, w.attn_norm, M, d, dx, st, emit ? hs : H16{nullptr, nullptr, nullptr},
+                           SplitSrc{}, dx_in);
       }
     }
+    dx = dx_base;
+    if (gbatch) run_gjobs(M);  // every layer's LoRA dA / dB
     if (rga) {
       Scope s(this, "rga", 0, 4.0 * (L * Kg + 32.0 * Kg));
       launch_rga_genome_grad(P + offGen, P + offWg, rdgb, L, Kg, G + offWg, G + offGen, st);
@@ -1163,6 +1205,27 @@ struct hos_peft {
     dh = E ? nullptr : alloc<float>(M * F);
     dgu = (has(TG) || has(TU)) ? alloc<float>(M * 2 * F) : nullptr;
     du = alloc<float>(M * NT * r);
+    // whole-backward batching of the LoRA dA / dB products: dense LoRA models with the two-plane fp16 operand
+    gbatch = !rga && !E && c.lora_targets != 0 && hs.lo != nullptr;
+    if (const char* e = getenv("HOS_LORA_GBATCH")) gbatch = gbatch && atoi(e) != 0;
+    if (gbatch) {
+      du_l.resize(L);
+      dqkv_l.resize(L);
+      dxs_l.resize(L);
+      dx2s_l.resize(L);
+      dgu16_l.resize(L);
+      for (int l = 0; l < L; l++) {
+        du_l[l] = alloc<float>(M * NT * r);
+        dqkv_l[l] = alloc<float>(M * W3);
+        dxs_l[l] = alloc<float>(M * d);
+        dx2s_l[l] = alloc<float>(M * d);
+        if (has(TG) || has(TU)) {
+          dgu16_l[l].data = alloc<half_t>(M * 2 * F);
+          dgu16_l[l].lo = alloc<half_t>(M * 2 * F);
+          dgu16_l[l].rinv = alloc<float>(M);
+        }
+      }
+    }
     dvec = alloc<float>(M * c.n_heads);
     if (c.n_heads != c.n_kv_heads) attn_part = alloc<float>(M * c.n_heads * 2 * c.head_dim);
     attn_planes.resize(L);
