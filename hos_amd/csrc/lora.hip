@@ -14,6 +14,7 @@
 // waves in LDS in a fixed order and writes its partial block; a reduce launch sums the partials in
 // split order. Deterministic. (An in-kernel "last workgroup reduces" variant with device-scope fences
 // measured 3-4x slower here: every release fence writes back the XCD's L2.)
+#include <algorithm>
 #include <cstdlib>
 #include <vector>
 
@@ -401,22 +402,22 @@ __global__ void __launch_bounds__(256) lora_cols_kernel(int M, int mchunk, ColsJ
     cols_body<NSB, false>(b, (int)blockIdx.x - b.bx0, M, mchunk, red, part);
 }
 
-// Up to COLS_MULTI independent jobs of one kernel shape (NS row tiles, G as f32 or as the fp16 operand in CW-column
-// runs) in one launch, each over all M rows in one workgroup per column block — no split of M, so no partials and
-// no reduction launch: the training step's dA / dB products of every layer, queued during the backward and run
-// together after it.
-constexpr int COLS_MULTI = 16;
-struct ColsMultiArgs {
-  ColsJobDev jobs[COLS_MULTI];
-  int start[COLS_MULTI + 1];  // first workgroup of each job
-  int n;
-};
+// Independent jobs of one kernel shape (NS row tiles, G as f32 or as the fp16 operand in CW-column runs) from a
+// device-resident table in one launch, each over all M rows in one workgroup per column block — no split of M, so no
+// partials and no reduction launch: the training step's dA / dB products of every layer, queued during the backward
+// and run together after it. Workgroup b runs job j with start[j] <= b < start[j + 1] (binary search).
 template <int NS, bool GH, int CW>
-__global__ void __launch_bounds__(256) lora_cols_multi_kernel(int M, ColsMultiArgs args) {
+__global__ void __launch_bounds__(256) lora_cols_table_kernel(int M, const ColsJobDev* __restrict__ jobs,
+                                                              const int* __restrict__ start, int n) {
   __shared__ float red[2 * NS * 16 * 16 * CW];
-  int j = 0;
-  while (j + 1 < args.n && (int)blockIdx.x >= args.start[j + 1]) j++;
-  cols_body<NS, GH, CW>(args.jobs[j], (int)blockIdx.x - args.start[j], M, M, red, nullptr);
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int)blockIdx.x >= start[mid]) lo = mid;
+    else hi = mid - 1;
+  }
+  const ColsJobDev jb = jobs[lo];
+  cols_body<NS, GH, CW>(jb, (int)blockIdx.x - start[lo], M, M, red, nullptr);
 }
 
 // Separate-launch reductions of the partials (one thread per output element of every block).
@@ -834,51 +835,65 @@ size_t lora_cols2_ws_bytes(long long M, const ColsJob& ja, const ColsJob* jb) {
   return need;
 }
 
-void launch_lora_cols_multi(long long M, const ColsJob* jobs, int n, hipStream_t st) {
+void launch_lora_cols_table(long long M, const ColsJob* jobs, int n, ColsTable& tab, hipStream_t st) {
   if (M <= 0 || n <= 0) return;
-  static_assert(sizeof(ColsMultiArgs) <= 4000, "kernel arguments");
-  // group the jobs by kernel shape, in their order; launch each group in chunks of COLS_MULTI
+  HOS_REQUIRE(n <= tab.cap, HOS_E_INVALID, "lora_cols_table: more jobs than the table holds");
+  // jobs grouped by kernel shape (stable), each group's jobs and block starts contiguous in the table
+  std::vector<int> key(n), order(n);
   std::vector<ColsJobDev> dev(n);
-  std::vector<int> key(n);
   for (int i = 0; i < n; i++) {
     dev[i] = prepare(jobs[i], 0);
     dev[i].S = 1;
     dev[i].part_off = 0;
     const int ns = dev[i].nsr / 16, v = dev[i].gh.hi ? (dev[i].bw == 128 ? 2 : 1) : 0;
-    HOS_REQUIRE(ns >= 1 && ns <= 6, HOS_E_INVALID, "lora_cols_multi: bad width");
+    HOS_REQUIRE(ns >= 1 && ns <= 6, HOS_E_INVALID, "lora_cols_table: bad width");
     key[i] = ns * 3 + v;
+    order[i] = i;
   }
-  std::vector<bool> done(n, false);
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key[a] < key[b]; });
+  struct Group {
+    int key, first, n, blocks;
+  };
+  std::vector<Group> groups;
+  int* hstart = reinterpret_cast<int*>(tab.host + tab.cap);
   for (int i = 0; i < n; i++) {
-    if (done[i]) continue;
-    ColsMultiArgs args{};
-    int tot = 0;
-    for (int k = i; k < n && args.n < COLS_MULTI; k++) {
-      if (done[k] || key[k] != key[i]) continue;
-      done[k] = true;
-      args.start[args.n] = tot;
-      args.jobs[args.n++] = dev[k];
-      tot += dev[k].gx;
-    }
-    args.start[args.n] = tot;
-    const int ns = key[i] / 3, v = key[i] % 3;
-#define CMULTI(NSV)                                                                                 \
-  case NSV:                                                                                         \
-    if (v == 2)                                                                                     \
-      lora_cols_multi_kernel<NSV, true, 8><<<tot, 256, 0, st>>>((int)M, args);                      \
-    else if (v == 1)                                                                                \
-      lora_cols_multi_kernel<NSV, true, 4><<<tot, 256, 0, st>>>((int)M, args);                      \
-    else                                                                                            \
-      lora_cols_multi_kernel<NSV, false, 4><<<tot, 256, 0, st>>>((int)M, args);                     \
+    const int k = key[order[i]];
+    if (groups.empty() || groups.back().key != k) groups.push_back(Group{k, i, 0, 0});
+    Group& g = groups.back();
+    tab.host[i] = dev[order[i]];
+    hstart[i + (int)groups.size() - 1] = g.blocks;  // a group of n jobs takes n + 1 starts
+    g.blocks += dev[order[i]].gx;
+    g.n++;
+  }
+  // each group's closing start
+  for (size_t gi = 0; gi < groups.size(); gi++) hstart[groups[gi].first + groups[gi].n + (int)gi] = groups[gi].blocks;
+  const size_t bytes = (size_t)tab.cap * sizeof(ColsJobDev) + (size_t)(n + groups.size()) * sizeof(int);
+  HOS_HIP_CHECK(hipMemcpyAsync(tab.dev, tab.host, bytes, hipMemcpyHostToDevice, st));
+  const int* dstart = reinterpret_cast<const int*>(tab.dev + tab.cap);
+  for (size_t gi = 0; gi < groups.size(); gi++) {
+    const Group& g = groups[gi];
+    const ColsJobDev* dj = tab.dev + g.first;
+    const int* ds = dstart + g.first + (int)gi;
+    const int ns = g.key / 3, v = g.key % 3;
+#define CTAB(NSV)                                                                                               \
+  case NSV:                                                                                                     \
+    if (v == 2)                                                                                                 \
+      lora_cols_table_kernel<NSV, true, 8><<<g.blocks, 256, 0, st>>>((int)M, dj, ds, g.n);                      \
+    else if (v == 1)                                                                                            \
+      lora_cols_table_kernel<NSV, true, 4><<<g.blocks, 256, 0, st>>>((int)M, dj, ds, g.n);                      \
+    else                                                                                                        \
+      lora_cols_table_kernel<NSV, false, 4><<<g.blocks, 256, 0, st>>>((int)M, dj, ds, g.n);                     \
     break;
     switch (ns) {
-      CMULTI(1) CMULTI(2) CMULTI(3) CMULTI(4) CMULTI(5) CMULTI(6)
+      CTAB(1) CTAB(2) CTAB(3) CTAB(4) CTAB(5) CTAB(6)
       default: break;
     }
-#undef CMULTI
+#undef CTAB
     HOS_HIP_CHECK(hipGetLastError());
-  }  // (jobs of this shape past a full chunk start a chunk of their own later in the loop)
+  }
 }
+
+size_t lora_cols_table_bytes(int cap) { return (size_t)cap * sizeof(ColsJobDev) + (size_t)2 * cap * sizeof(int); }
 
 void launch_lora_cols_flush(ColsBatch& bt, hipStream_t st) {
   if (bt.n > 0) {

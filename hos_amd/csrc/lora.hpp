@@ -95,9 +95,19 @@ struct ColsBatch {
   int n = 0;
 };
 void launch_lora_cols_flush(ColsBatch& b, hipStream_t st);
-// Every job in as few launches as their kernel shapes allow, each output block over all M rows in one workgroup
-// (no partials, no reduction launch). Deterministic: each element sums its rows in one fixed order.
-void launch_lora_cols_multi(long long M, const ColsJob* jobs, int n, hipStream_t st);
+// A job table for launch_lora_cols_table: cap jobs plus 2·cap block starts, a pinned host copy and a device copy
+// (lora_cols_table_bytes(cap) bytes each, allocated by the owner before any graph capture). The host copy is
+// rewritten and sent with each launch — identical content for the same jobs, so a captured copy of it stays valid.
+struct ColsTable {
+  ColsJobDev* host = nullptr;
+  ColsJobDev* dev = nullptr;
+  int cap = 0;
+};
+size_t lora_cols_table_bytes(int cap);
+// Every job, one launch per kernel shape whatever the job count (the jobs go through tab), each output block over all
+// M rows in one workgroup (no partials, no reduction launch). Deterministic: each element sums its rows in one fixed
+// order.
+void launch_lora_cols_table(long long M, const ColsJob* jobs, int n, ColsTable& tab, hipStream_t st);
 // Two independent cols products over the same M in one launch (and one reduction launch); b may be null.
 // Deterministic: the split of M depends only on M and the combined block count, and every output element sums
 // its split partials in split order.

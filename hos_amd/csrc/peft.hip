@@ -85,11 +85,12 @@ struct hos_peft {
   // Whole-backward batching of the LoRA dA / dB products (dense LoRA models with two-plane operands): every layer
   // keeps the inputs those products read — its du, the q|k|v output gradient, the residual gradients at x2 and at
   // x_{l+1}, the fp16 d(gate|up) — and the products of all layers run together after the last layer, in a few
-  // launches without a split of M (launch_lora_cols_multi) instead of five small launches per layer.
+  // launches without a split of M (launch_lora_cols_table) instead of five small launches per layer.
   bool gbatch = false;
   std::vector<float*> du_l, dqkv_l, dxs_l, dx2s_l;  // per layer; dxs_l[l]: gradient at x_{l+1}, dx2s_l[l]: at x2
   std::vector<H16> dgu16_l;                         // per layer: d(gate|up) as the fp16 operand
   std::vector<ColsJob> gjobs;                       // the step's queued dA / dB products
+  ColsTable gtab;                                   // their device table (launch_lora_cols_table)
   int tpf[7] = {0, 0, 0, 0, 0, 0, 0}, tpd[7] = {0, 0, 0, 0, 0, 0, 0};  // per-target overrides (0 = site mode)
   float lscale = 0.0f;
 
@@ -552,7 +553,7 @@ struct hos_peft {
         by += 4.0 * ((double)M * j.sg.len[t] + (double)M * j.ns + (double)j.ns * j.sg.len[t]);
       }
     Scope s(this, "lora_dab", fl, by);
-    launch_lora_cols_multi(M, gjobs.data(), (int)gjobs.size(), st);
+    launch_lora_cols_table(M, gjobs.data(), (int)gjobs.size(), gtab, st);
     gjobs.clear();
   }
   void check_ready() {
@@ -1209,6 +1210,11 @@ struct hos_peft {
     gbatch = !rga && !E && c.lora_targets != 0 && hs.lo != nullptr;
     if (const char* e = getenv("HOS_LORA_GBATCH")) gbatch = gbatch && atoi(e) != 0;
     if (gbatch) {
+      gtab.cap = 8 * L;  // a dA and a dB per adapted group of each layer
+      void* hp = nullptr;
+      HOS_HIP_CHECK(hipHostMalloc(&hp, lora_cols_table_bytes(gtab.cap), hipHostMallocDefault));
+      gtab.host = (ColsJobDev*)hp;
+      gtab.dev = (ColsJobDev*)alloc<unsigned char>(lora_cols_table_bytes(gtab.cap));
       du_l.resize(L);
       dqkv_l.resize(L);
       dxs_l.resize(L);
@@ -1257,6 +1263,8 @@ struct hos_peft {
 
   void release() {
     (void)hipStreamSynchronize(st);
+    if (gtab.host) (void)hipHostFree(gtab.host);
+    gtab.host = nullptr;
     for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
     graphs.clear();
     for (auto& rc : recs) {
