@@ -130,10 +130,15 @@ __device__ __forceinline__ Work work_item() {
 
 // ---- split kernels ----
 // q (scaled), k, v of rows [M, ld] into head-major hi/lo planes; one thread per 8 columns.
+// tab set: q and k are rotated first (RoPE, the forward rotation of rope_kernel in fused.hip with the same
+// separately rounded products and sums; tab holds (sin, cos) per (position, pair)), so the planes hold what
+// splitting the rotated rows would give, while qkv itself is left unrotated.
 template <int HD>
 __global__ void attn_split_qkv(const float* __restrict__ qkv, long long ld, int kcol, int vcol, int T, int nh, int nkv,
                                long long M, __bf16* __restrict__ qh, __bf16* __restrict__ ql, __bf16* __restrict__ kh,
-                               __bf16* __restrict__ kl, __bf16* __restrict__ vh, __bf16* __restrict__ vl) {
+                               __bf16* __restrict__ kl, __bf16* __restrict__ vh, __bf16* __restrict__ vl,
+                               const float2* __restrict__ tab, int neox) {
+#pragma clang fp contract(off)
   const int per_row = (nh + 2 * nkv) * AC<HD>::CH;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M * per_row) return;
@@ -163,7 +168,35 @@ __global__ void attn_split_qkv(const float* __restrict__ qkv, long long ld, int 
     hrow = ((long long)b * nkv + c / HD) * T + t;
   }
   const float4 a0 = reinterpret_cast<const float4*>(src)[0], a1 = reinterpret_cast<const float4*>(src)[1];
-  const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  if (tab && c8 < (nh + nkv) * HD) {
+    constexpr int half = HD / 2;
+    const int cc = c8 % HD;  // first head dim of this thread's 8
+    const float2* tr = tab + (long long)t * half;
+    float r[8];
+    if (neox) {
+      // pairs (i, i + half): the partner run is the 8 dims half away
+      const bool lo_half = cc < half;
+      const float* ps = lo_half ? src + half : src - half;
+      const float4 b0 = reinterpret_cast<const float4*>(ps)[0], b1 = reinterpret_cast<const float4*>(ps)[1];
+      const float w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float2 sc = tr[(lo_half ? cc : cc - half) + e];
+        r[e] = lo_half ? v[e] * sc.y - w[e] * sc.x : w[e] * sc.x + v[e] * sc.y;
+      }
+    } else {
+      // adjacent pairs (2i, 2i + 1), all inside this thread's 8
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float2 sc = tr[(cc + e) / 2];
+        r[e] = v[e] * sc.y - v[e + 1] * sc.x;
+        r[e + 1] = v[e] * sc.x + v[e + 1] * sc.y;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = r[e];
+  }
   bf8 H, L;
   split8(v, mul, H, L);
   const long long o = hrow * HD + (c8 % HD);
@@ -667,18 +700,18 @@ void check_layout(long long ld, int kcol, int vcol, int hd, const void* scratch)
 
 template <int HD>
 void split_qkv(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, const Planes& P,
-               hipStream_t st) {
+               hipStream_t st, const float2* rope_tab = nullptr, bool rope_neox = false) {
   const long long M = (long long)B * T, n = M * (nh + 2 * nkv) * AC<HD>::CH;
   attn_split_qkv<HD><<<ceil_div(n, 256), 256, 0, st>>>(qkv, ld, kcol, vcol, T, nh, nkv, M, P.qh, P.ql, P.kh, P.kl,
-                                                       P.vh, P.vl);
+                                                       P.vh, P.vl, rope_tab, rope_neox ? 1 : 0);
   HOS_HIP_CHECK(hipGetLastError());
 }
 
 template <int HD>
 void attn_fwd_hd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, float* o,
-                 long long ldo, float* lse, void* scratch, hipStream_t st) {
+                 long long ldo, float* lse, void* scratch, hipStream_t st, const float2* rope_tab, bool rope_neox) {
   const Planes P = planes_of(scratch, B, T, nh, nkv, HD);
-  split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
+  split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st, rope_tab, rope_neox);
   dim3 grid(ceil_div(T, BR), nh, B);
   constexpr int NGF = fwd_groups<HD>();
   attn_fwd_kernel<HD, NGF><<<grid, 256 * NGF, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, T, nh, nh / nkv, o,
@@ -717,14 +750,15 @@ size_t attn_scratch_bytes(int B, int T, int nh, int nkv, int hd) {
 }
 
 void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,
-                     float* o, long long ldo, float* lse, void* scratch, hipStream_t st) {
+                     float* o, long long ldo, float* lse, void* scratch, hipStream_t st, const float2* rope_tab,
+                     bool rope_neox) {
   check_layout(ld, kcol, vcol, hd, scratch);
   HOS_REQUIRE(ldo % 4 == 0 && nkv > 0 && nh % nkv == 0, HOS_E_INVALID, "attention: bad output layout or heads");
   if (B <= 0 || T <= 0) return;
   if (hd == 64)
-    attn_fwd_hd<64>(qkv, ld, kcol, vcol, B, T, nh, nkv, o, ldo, lse, scratch, st);
+    attn_fwd_hd<64>(qkv, ld, kcol, vcol, B, T, nh, nkv, o, ldo, lse, scratch, st, rope_tab, rope_neox);
   else
-    attn_fwd_hd<128>(qkv, ld, kcol, vcol, B, T, nh, nkv, o, ldo, lse, scratch, st);
+    attn_fwd_hd<128>(qkv, ld, kcol, vcol, B, T, nh, nkv, o, ldo, lse, scratch, st, rope_tab, rope_neox);
 }
 
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,

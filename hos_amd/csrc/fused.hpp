@@ -43,8 +43,10 @@ void launch_copy_rows(const float* src, long long lds, float* dst, long long ldd
 // bytes, 16-byte aligned; its contents need not survive between the calls — except that a backward with
 // qkv_planes = true reuses the q, k, v planes the forward of the same qkv left in the same scratch.
 size_t attn_scratch_bytes(int B, int T, int nh, int nkv, int hd);
+// rope_tab set: q and k are rotated (RoPE, forward) on their way into the planes; qkv stays unrotated.
 void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,
-                     float* o, long long ldo, float* lse, void* scratch, hipStream_t st);
+                     float* o, long long ldo, float* lse, void* scratch, hipStream_t st,
+                     const float2* rope_tab = nullptr, bool rope_neox = false);
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
                      long long ldd, float* part, void* scratch, hipStream_t st, bool qkv_planes = false);

@@ -687,15 +687,12 @@ struct hos_peft {
         launch_qknorm_fwd(a.qkv, W3, qd, kvd, w.k_norm, c.rms_eps, M, a.qk_pre + (size_t)M * qd, a.qk_inv + M, st);
       }
       {
-        Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
-        // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both
-        launch_rope(a.qkv, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, false, M, st);
-      }
-      {
+        // RoPE on q and k is applied as they are split into the attention's planes (a.qkv stays unrotated: the
+        // backward reads only the planes)
         Scope s(this, "attn_fwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 2,
                 4.0 * M * (W3 + qd) + 4.0 * B * c.n_heads * T);
         launch_attn_fwd(a.qkv, W3, qd, qd + kvd, B, T, c.n_heads, c.n_kv_heads, c.head_dim, a.o, qd, a.lse,
-                        attn_planes[l], st);
+                        attn_planes[l], st, rope_tab, c.rope_neox);
       }
       to16(a.o, qd, M, qd);
       lora_down(l, 1, a.o, qd, M, hs_in());
