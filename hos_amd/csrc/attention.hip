@@ -10,9 +10,10 @@
 // log-sum-exp, dS = P∘(dP − rowsum(dO∘O)), and GQA gradients are summed over the group in head order.
 // The scale 1/√hd is folded into q (exactly 2^-3 for hd = 64; the f32 value of 1/√128 for hd = 128).
 //
-// Data path. One split kernel per direction turns the f32 operands into bf16 hi/lo planes, head-major
-// ([b][head][t][d], so a 32-row tile of one head is one contiguous 32·hd run): q (pre-scaled), k, v, and for
-// the backward dO with D = rowsum(dO∘O) fused in. Every attention kernel is a workgroup of 4 waves over 128
+// Data path. A split kernel turns the f32 q (pre-scaled, optionally rotated), k, v into bf16 hi/lo planes,
+// head-major ([b][head][t][d], so a 32-row tile of one head is one contiguous 32·hd run); the backward reads
+// dO from its f32 rows and splits it as it loads it, the dQ kernel forming D = rowsum(dO∘O) for the dK/dV
+// kernel on the way. Every attention kernel is a workgroup of 4 waves over 128
 // rows of one (head, sequence) — queries for the forward and dQ, keys for dK/dV — each wave owning 32 of them
 // for the whole loop (its accumulators never leave registers, no cross-wave merge). The other axis streams
 // through LDS in 32-row tiles, loaded once per workgroup with 16-byte loads and double-buffered (one barrier
@@ -204,36 +205,6 @@ __global__ void attn_split_qkv(const float* __restrict__ qkv, long long ld, int 
   *reinterpret_cast<bf8*>(dl + o) = L;
 }
 
-// dO into hi/lo planes and D = Σ_d dO·O per (row, head); HD/8 consecutive threads per (row, head).
-template <int HD>
-__global__ void attn_split_do(const float* __restrict__ o, const float* __restrict__ dout, long long ldo, int T, int nh,
-                              long long M, __bf16* __restrict__ dh, __bf16* __restrict__ dl, float* __restrict__ dvec) {
-  constexpr int CH = AC<HD>::CH;
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool ok = i < M * nh * CH;
-  const long long mh = ok ? i / CH : 0;
-  const int ch = (int)(i % CH);
-  const long long m = mh / nh;
-  const int h = (int)(mh % nh), b = (int)(m / T), t = (int)(m % T);
-  float s = 0.0f;
-  if (ok) {
-    const float* dp = dout + m * ldo + h * HD + 8 * ch;
-    const float* op = o + m * ldo + h * HD + 8 * ch;
-    const float4 d0 = reinterpret_cast<const float4*>(dp)[0], d1 = reinterpret_cast<const float4*>(dp)[1];
-    const float4 o0 = reinterpret_cast<const float4*>(op)[0], o1 = reinterpret_cast<const float4*>(op)[1];
-    const float v[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-    s = d0.x * o0.x + d0.y * o0.y + d0.z * o0.z + d0.w * o0.w + d1.x * o1.x + d1.y * o1.y + d1.z * o1.z + d1.w * o1.w;
-    bf8 H, L;
-    split8(v, 1.0f, H, L);
-    const long long off = (((long long)b * nh + h) * T + t) * HD + 8 * ch;
-    *reinterpret_cast<bf8*>(dh + off) = H;
-    *reinterpret_cast<bf8*>(dl + off) = L;
-  }
-#pragma unroll
-  for (int k = CH / 2; k > 0; k >>= 1) s += __shfl_xor(s, k);
-  if (ok && ch == 0) dvec[((long long)b * nh + h) * T + t] = s;
-}
-
 // Cooperative load of 4 planes' 32-row tiles (rows r0 .. r0+31 of head-major planes, clamped to T-1) into
 // registers, then into LDS tiles of stride LD. Thread tid moves chunk tid + 256·v of the tile set, so the plane
 // and row of every chunk are compile-time functions of v plus tid.
@@ -260,6 +231,44 @@ struct TileLoader {
     for (int v = 0; v < NL; v++) {
       const int rem = (v % VPP) * NW * 64 + tid, row = rem / AC<HD>::CH, ch = rem % AC<HD>::CH;
       *reinterpret_cast<u32x4*>(lds + (v / VPP) * AC<HD>::TILE + row * AC<HD>::LD + 8 * ch) = reg[v];
+    }
+  }
+};
+
+// The same for the dK/dV kernel's stream: q hi/lo from their head-major planes, dO from its f32 rows ([B·T, ldo],
+// head h at column h·HD), split into hi/lo on the way into LDS (split8, the split the planes would hold).
+template <int HD>
+struct TileLoaderQD {
+  static constexpr int PER = TB * AC<HD>::CH;
+  static constexpr int VPP = PER / (NW * 64);
+  u32x4 q[2 * VPP];
+  float4 d[2 * VPP];  // 8 floats of dO per chunk
+  __device__ __forceinline__ void load(const __bf16* qh, const __bf16* ql, const float* dout, long long ldo,
+                                       long long hbase, long long rbase, int r0, int T, int tid) {
+#pragma unroll
+    for (int v = 0; v < VPP; v++) {
+      const int rem = v * NW * 64 + tid, row = rem / AC<HD>::CH, ch = rem % AC<HD>::CH;
+      const int t = min(r0 + row, T - 1);
+      q[v] = *reinterpret_cast<const u32x4*>(qh + (hbase + t) * HD + 8 * ch);
+      q[VPP + v] = *reinterpret_cast<const u32x4*>(ql + (hbase + t) * HD + 8 * ch);
+      const float4* src = reinterpret_cast<const float4*>(dout + (rbase + t) * ldo + 8 * ch);
+      d[2 * v] = src[0];
+      d[2 * v + 1] = src[1];
+    }
+  }
+  __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+#pragma unroll
+    for (int v = 0; v < VPP; v++) {
+      const int rem = v * NW * 64 + tid, row = rem / AC<HD>::CH, ch = rem % AC<HD>::CH;
+      const int o = row * AC<HD>::LD + 8 * ch;
+      *reinterpret_cast<u32x4*>(lds + o) = q[v];
+      *reinterpret_cast<u32x4*>(lds + AC<HD>::TILE + o) = q[VPP + v];
+      const float4 a = d[2 * v], b = d[2 * v + 1];
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      bf8 H, L;
+      split8(x, 1.0f, H, L);
+      *reinterpret_cast<bf8*>(lds + 2 * AC<HD>::TILE + o) = H;
+      *reinterpret_cast<bf8*>(lds + 3 * AC<HD>::TILE + o) = L;
     }
   }
 };
@@ -408,10 +417,10 @@ template <int HD, int NG>
 __global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
                                                       const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
                                                       const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
-                                                      const __bf16* __restrict__ doh, const __bf16* __restrict__ dol,
-                                                      const float* __restrict__ lse, const float* __restrict__ dvec,
-                                                      int T, int nh, int group, float* __restrict__ dq,
-                                                      long long ldq) {
+                                                      const float* __restrict__ o, const float* __restrict__ dout,
+                                                      long long ldo, const float* __restrict__ lse,
+                                                      float* __restrict__ dvec, int T, int nh, int group,
+                                                      float* __restrict__ dq, long long ldq) {
   using C = AC<HD>;
   __shared__ __attribute__((aligned(16))) __bf16 sm[NG][2][4 * C::TILE];  // per group, stage: Kh, Kl, Vh, Vl
   const int nqb = (T + BR - 1) / BR;
@@ -426,8 +435,26 @@ __global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restr
   const long long qr = qrow0 + min(myq, T - 1);
   bf8 Qh[C::NS], Ql[C::NS], Dh[C::NS], Dl[C::NS];
   own_frags<HD>(qh, ql, qr, hl, Qh, Ql);
-  own_frags<HD>(doh, dol, qr, hl, Dh, Dl);
-  const float Lq2 = lse[qr] * LOG2E, Dq = dvec[qr];
+  // this lane's half of its query's dO row (head dims 16t + 8·hl .. +7) from the f32 rows, split to hi/lo, and
+  // D = Σ_d dO·O over the row (the two half-rows of lanes c and c + 32 added)
+  float Dq = 0.0f;
+  {
+    const long long rr = ((long long)b * T + min(myq, T - 1)) * ldo + h * HD + 8 * hl;
+#pragma unroll
+    for (int t = 0; t < C::NS; t++) {
+      const float4* dp = reinterpret_cast<const float4*>(dout + rr + 16 * t);
+      const float4* op = reinterpret_cast<const float4*>(o + rr + 16 * t);
+      const float4 d0 = dp[0], d1 = dp[1], o0 = op[0], o1 = op[1];
+      const float v[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+      split8(v, 1.0f, Dh[t], Dl[t]);
+#pragma unroll
+      for (int e = 0; e < 8; e++) Dq = __builtin_fmaf(v[e], ov[e], Dq);
+    }
+    Dq += __shfl_xor(Dq, 32);
+    if (grp == 0 && hl == 0 && active && myq < T) dvec[qr] = Dq;  // for the dK/dV launch that follows
+  }
+  const float Lq2 = lse[qr] * LOG2E;
   f16v A[C::NC];
 #pragma unroll
   for (int i = 0; i < C::NC; i++)
@@ -519,7 +546,7 @@ template <int HD, int NG>
 __global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __restrict__ qh, const __bf16* __restrict__ ql,
                                                         const __bf16* __restrict__ kh, const __bf16* __restrict__ kl,
                                                         const __bf16* __restrict__ vh, const __bf16* __restrict__ vl,
-                                                        const __bf16* __restrict__ doh, const __bf16* __restrict__ dol,
+                                                        const float* __restrict__ dout, long long ldo,
                                                         const float* __restrict__ lse, const float* __restrict__ dvec,
                                                         int T, int nh, int group, float* __restrict__ dkv,
                                                         long long ldk, int kcol, int vcol, float* __restrict__ part) {
@@ -546,11 +573,12 @@ __global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __res
   const int qt0 = (wk.xb * BR) / TB;                 // the first one that sees any of the workgroup's keys
   const int my_first = active ? kw0 / TB : nqt;      // this wave's first (diagonal) query tile
   const int per = (nqt - qt0 + NG - 1) / NG, qbeg = qt0 + grp * per, qend = min(nqt, qbeg + per);  // group range
-  const Planes4 planes{{qh, ql, doh, dol}};
-  TileLoader<HD> ld;
+  TileLoaderQD<HD> ld;
+  const float* dhead = dout + h * HD;
+  const long long rrow0 = (long long)b * T;
   float ldv = 0.0f;
   auto load = [&](int qt) {
-    ld.load(planes, qrow0, qt * TB, T, gt);
+    ld.load(qh, ql, dhead, ldo, qrow0, rrow0, qt * TB, T, gt);
     if (gt < 2 * TB) {
       const long long r = qrow0 + min(qt * TB + (gt & (TB - 1)), T - 1);
       ldv = gt < TB ? lse[r] * LOG2E : dvec[r];
@@ -673,9 +701,9 @@ __global__ void attn_group_sum(const float* __restrict__ part, int M, int nh, in
   dkv[m * ldk + col] = s;
 }
 
-// Plane pointers inside the caller's scratch: q, k, v, dO, each hi then lo.
+// Plane pointers inside the caller's scratch: q, k, v, each hi then lo.
 struct Planes {
-  __bf16 *qh, *ql, *kh, *kl, *vh, *vl, *dh, *dl;
+  __bf16 *qh, *ql, *kh, *kl, *vh, *vl;
 };
 Planes planes_of(void* scratch, int B, int T, int nh, int nkv, int hd) {
   const long long nq = (long long)B * nh * T * hd, nk = (long long)B * nkv * T * hd;
@@ -687,8 +715,6 @@ Planes planes_of(void* scratch, int B, int T, int nh, int nkv, int hd) {
   P.kl = P.kh + nk;
   P.vh = P.kl + nk;
   P.vl = P.vh + nk;
-  P.dh = P.vl + nk;
-  P.dl = P.dh + nq;
   return P;
 }
 
@@ -725,15 +751,14 @@ void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float
                  void* scratch, hipStream_t st, bool qkv_planes) {
   const Planes P = planes_of(scratch, B, T, nh, nkv, HD);
   if (!qkv_planes) split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
-  const long long M = (long long)B * T, n = M * nh * AC<HD>::CH;
-  attn_split_do<HD><<<ceil_div(n, 256), 256, 0, st>>>(o, dout, ldo, T, nh, M, P.dh, P.dl, dvec);
-  HOS_HIP_CHECK(hipGetLastError());
+  // dO is read from its f32 rows by both kernels (split to hi/lo as it is loaded); the dQ launch also forms
+  // D = rowsum(dO∘O) for its queries and leaves it in dvec for the dK/dV launch
   dim3 grid(ceil_div(T, BR), nh, B);
   constexpr int NGB = bwd_groups<HD>();
-  attn_dq_kernel<HD, NGB><<<grid, 256 * NGB, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse, dvec,
+  attn_dq_kernel<HD, NGB><<<grid, 256 * NGB, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, o, dout, ldo, lse, dvec,
                                                             T, nh, nh / nkv, dqkv, ldd);
   HOS_HIP_CHECK(hipGetLastError());
-  attn_dkdv_kernel<HD, NGB><<<grid, 256 * NGB, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, P.dh, P.dl, lse,
+  attn_dkdv_kernel<HD, NGB><<<grid, 256 * NGB, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, dout, ldo, lse,
                                                               dvec, T, nh, nh / nkv, dqkv, ldd, kcol, vcol, part);
   HOS_HIP_CHECK(hipGetLastError());
   if (nh != nkv) {
@@ -746,7 +771,7 @@ void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float
 }  // namespace
 
 size_t attn_scratch_bytes(int B, int T, int nh, int nkv, int hd) {
-  return (size_t)B * T * hd * (2 * (size_t)nh + 2 * (size_t)nkv) * 2 * sizeof(__bf16);
+  return (size_t)B * T * hd * ((size_t)nh + 2 * (size_t)nkv) * 2 * sizeof(__bf16);
 }
 
 void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, int T, int nh, int nkv, int hd,

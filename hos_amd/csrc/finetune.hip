@@ -96,7 +96,7 @@ struct hos_ft {
   float *xf = nullptr, *xfn = nullptr, *invf = nullptr, *logits = nullptr, *dl = nullptr, *row_loss = nullptr,
         *loss = nullptr, *dx = nullptr, *dxn = nullptr, *dqkv = nullptr, *dout = nullptr, *dh = nullptr,
         *dgu = nullptr, *dvec = nullptr, *part = nullptr, *ws = nullptr;
-  void* attn_planes = nullptr;  // bf16 hi/lo planes of q, k, v, dO (attention scratch)
+  void* attn_planes = nullptr;  // bf16 hi/lo planes of q, k, v (attention scratch)
   size_t ws_bytes = 0;
   H16 hs{};
   float2* rope_tab = nullptr;

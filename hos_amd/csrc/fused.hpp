@@ -39,7 +39,7 @@ void launch_adamw_dev(float* p, const float* g, float* m, float* v, long long n,
 void launch_fill(float* p, long long n, float v, hipStream_t st);
 void launch_copy_rows(const float* src, long long lds, float* dst, long long ldd, int rows, int cols,
                       hipStream_t st);
-// Attention (attention.hip). `scratch` holds the bf16 hi/lo planes of q, k, v and dO: attn_scratch_bytes(...)
+// Attention (attention.hip). `scratch` holds the bf16 hi/lo planes of q, k and v: attn_scratch_bytes(...)
 // bytes, 16-byte aligned; its contents need not survive between the calls — except that a backward with
 // qkv_planes = true reuses the q, k, v planes the forward of the same qkv left in the same scratch.
 size_t attn_scratch_bytes(int B, int T, int nh, int nkv, int hd);

@@ -234,7 +234,7 @@ int hos_hip_attention_fwd(hos_ctx* c, const float* qkv, size_t ld, size_t kcol, 
   return op_guard(c, [&](hipStream_t st) {
     HOS_REQUIRE(qkv && o && lse && B > 0 && T > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, HOS_E_INVALID,
                 "attention: bad arguments");
-    DevMem& pl = internal_scratch(c, 7);  // bf16 planes of q, k, v, dO
+    DevMem& pl = internal_scratch(c, 7);  // bf16 planes of q, k, v
     pl.ensure(attn_scratch_bytes(B, T, n_heads, n_kv_heads, head_dim));
     launch_attn_fwd(qkv, (long long)ld, (int)kcol, (int)vcol, B, T, n_heads, n_kv_heads, head_dim, o, (long long)ldo,
                     lse, pl.p, st);
@@ -256,7 +256,7 @@ int hos_hip_attention_bwd(hos_ctx* c, const float* qkv, size_t ld, size_t kcol, 
       pm.ensure(M * n_heads * 2 * head_dim * 4);
       part = (float*)pm.p;
     }
-    DevMem& pl = internal_scratch(c, 7);  // bf16 planes of q, k, v, dO
+    DevMem& pl = internal_scratch(c, 7);  // bf16 planes of q, k, v
     pl.ensure(attn_scratch_bytes(B, T, n_heads, n_kv_heads, head_dim));
     launch_attn_bwd(qkv, (long long)ld, (int)kcol, (int)vcol, o, dout, (long long)ldo, lse, (float*)dv.p, B, T,
                     n_heads, n_kv_heads, head_dim, dqkv, (long long)ldd, part, pl.p, st);

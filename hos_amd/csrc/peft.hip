@@ -136,7 +136,7 @@ struct hos_peft {
   float *row_loss = nullptr, *loss = nullptr;
   float *dx = nullptr, *dxn = nullptr, *dqkv = nullptr, *dout = nullptr, *dh = nullptr, *dgu = nullptr,
         *du = nullptr, *dvec = nullptr, *attn_part = nullptr;
-  // bf16 hi/lo planes of q, k, v, dO (attention scratch), one per layer: the backward reuses the q, k, v planes
+  // bf16 hi/lo planes of q, k, v (attention scratch), one per layer: the backward reuses the q, k, v planes
   // its layer's forward made
   std::vector<void*> attn_planes;
   float* ws = nullptr;
