@@ -77,9 +77,9 @@ void lora_check(const float* x, const float* dy, size_t in, size_t out, int r, c
   HOS_REQUIRE(in % 4 == 0 && out % 4 == 0, HOS_E_INVALID, "lora: in and out must be multiples of 4");
 }
 
-// The two cols jobs of the branch: dB = s·uᵀ·dy [r, out] and dAᵀ = duᵀ·x [r, in] (into at).
+// The two cols jobs of the branch: dB = s·uᵀ·dy [r, out] and dA = (duᵀ·x)ᵀ [in, r] (strided stores).
 void lora_cols_jobs(const float* dy, const float* x, size_t rows, size_t in, size_t out, int r, float scale,
-                    const float* u, const float* du, float* dB, float* at, ColsJob* jdb, ColsJob* jda) {
+                    const float* u, const float* du, float* dB, float* dA, ColsJob* jdb, ColsJob* jda) {
   (void)rows;
   ColsSeg cb;
   cb.nseg = 1;
@@ -88,10 +88,10 @@ void lora_cols_jobs(const float* dy, const float* x, size_t rows, size_t in, siz
   ca.nseg = 1;
   ca.len[0] = (int)in;
   *jdb = ColsJob{r, scale, u, r, dy, (long long)out, cb, dB, (long long)out, 1};
-  *jda = ColsJob{r, 1.0f, du, r, x, (long long)in, ca, at, (long long)in, 1};
+  *jda = ColsJob{r, 1.0f, du, r, x, (long long)in, ca, dA, 1, (long long)r};  // dA(c, j): written as [in, r]
 }
 
-// The LoRA branch on caller-provided scratch: at [r, in] (Aᵀ, then dAᵀ), du [rows, r], ws the split partials.
+// The LoRA branch on caller-provided scratch: at [r, in] (Aᵀ), du [rows, r], ws the split partials.
 void lora_run(const float* x, const float* dy, size_t rows, size_t in, size_t out, int r, const float* A,
               const float* B, float scale, float* y, float* u, float* dA, float* dB, float* dx, float* at, float* du,
               float* ws, size_t wsb, hipStream_t st) {
@@ -111,11 +111,10 @@ void lora_run(const float* x, const float* dy, size_t rows, size_t in, size_t ou
   up.kend[0] = (int)out;
   launch_lora_rows((long long)rows, (long long)out, scale, dy, (long long)out, B, (long long)out, up, du, r, ws, wsb,
                    st);
-  // dB = s·uᵀ·dy and dAᵀ = duᵀ·x in one launch
+  // dB = s·uᵀ·dy and dA = (duᵀ·x)ᵀ in one launch
   ColsJob jdb, jda;
-  lora_cols_jobs(dy, x, rows, in, out, r, scale, u, du, dB, at, &jdb, &jda);
+  lora_cols_jobs(dy, x, rows, in, out, r, scale, u, du, dB, dA, &jdb, &jda);
   launch_lora_cols2((long long)rows, jdb, &jda, ws, wsb, st);
-  transpose(at, r, (int)in, dA, st);
   if (dx)
     launch_gemm_f32((long long)rows, (long long)in, r, 1.0f, du, r, 1, A, 1, r, 1.0f, dx, (long long)in, ws, wsb, st);
 }
@@ -305,7 +304,7 @@ int hos_hip_lora(hos_ctx* c, const float* x, const float* dy, size_t rows, size_
   return op_guard(c, [&](hipStream_t st) {
     lora_check(x, dy, in, out, r, A, B, u, dA, dB);
     DevMem& wsm = internal_ws(c);
-    DevMem& at = internal_scratch(c, 5);  // Aᵀ [r, in], then dAᵀ
+    DevMem& at = internal_scratch(c, 5);  // Aᵀ [r, in]
     at.ensure((size_t)r * in * 4);
     DevMem& dub = internal_scratch(c, 6);  // du [rows, r]
     dub.ensure(rows * r * 4 + 4);
