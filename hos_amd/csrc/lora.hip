@@ -79,18 +79,6 @@ __device__ __forceinline__ float sum_parts(const float* part, int S, int gx, int
   return v;
 }
 
-// Block result in red[0..E): write it (no split) or store this split's partial for the reduce launch.
-// store(e, value) writes one finished element of the output.
-template <class Store>
-__device__ __forceinline__ void finish_block(const float* red, int E, float* part, Store store) {
-  if (gridDim.y == 1) {
-    for (int e = threadIdx.x; e < E; e += 256) store(e, red[e]);
-    return;
-  }
-  float* mine = part + ((long long)blockIdx.y * gridDim.x + blockIdx.x) * E;
-  for (int e = threadIdx.x; e < E; e += 256) mine[e] = red[e];
-}
-
 // ---------------- rows: C[M, n] = α·X·Bᵀ ----------------
 // Workgroup: 16·RT rows × all n columns × a k-chunk; wave w takes the chunk's 16-wide k steps w, w+4, …
 // Lane (q = lane/16, p = lane%16): rows m0+16t+p, k-slot q (k = step + 4q .. +3 as one float4).
@@ -100,11 +88,29 @@ __device__ __forceinline__ void finish_block(const float* red, int E, float* par
 #ifndef HOS_COLS_UNROLL
 #define HOS_COLS_UNROLL 4
 #endif
+// One rows product of a launch (a launch takes one or two: blockIdx.z picks the job; a job split into S
+// contraction chunks writes its partials to part, [chunk][row block][E], for lora_rows_reduce).
+struct RowsJobK {
+  int K, kchunk, S;
+  float alpha;
+  const float* X;
+  long long ldx;
+  const float* Bt;
+  long long ldb;
+  RowsSeg sg;
+  float* C;
+  long long ldc;
+  float* part;
+};
 template <int NJ, int RT = 2>
-__global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk, float alpha,
-                                                        const float* __restrict__ X, long long ldx,
-                                                        const float* __restrict__ Bt, long long ldb, RowsSeg sg,
-                                                        float* __restrict__ C, long long ldc, float* part, HIn xh) {
+__global__ void __launch_bounds__(256) lora_rows_kernel(int M, RowsJobK j0, RowsJobK j1, HIn xh) {
+  const RowsJobK& jb = blockIdx.z ? j1 : j0;
+  if ((int)blockIdx.y >= jb.S) return;
+  const int K = jb.K, kchunk = jb.kchunk;
+  const float* __restrict__ X = jb.X;
+  const float* __restrict__ Bt = jb.Bt;
+  const long long ldx = jb.ldx, ldb = jb.ldb;
+  const RowsSeg& sg = jb.sg;
   constexpr int NC = NJ * 16, E = 16 * RT * NC;
   __shared__ float red[2 * E];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
@@ -197,10 +203,15 @@ __global__ void __launch_bounds__(256) lora_rows_kernel(int M, int K, int kchunk
     const int i = idx & 3, tj = idx >> 2, t = tj / NJ, jt = tj % NJ;
     return (16 * t + 4 * q + i) * NC + 16 * jt + p;
   });
-  finish_block(red, E, part, [&](int e, float val) {
-    const int rr = e / NC, c = e % NC, row = m0 + rr;
-    if (row < M && c < n) C[(long long)row * ldc + c] = alpha * val;
-  });
+  if (jb.S == 1) {
+    for (int e = threadIdx.x; e < E; e += 256) {
+      const int rr = e / NC, c = e % NC, row = m0 + rr;
+      if (row < M && c < n) jb.C[(long long)row * jb.ldc + c] = jb.alpha * red[e];
+    }
+    return;
+  }
+  float* mine = jb.part + ((long long)blockIdx.y * gridDim.x + blockIdx.x) * E;
+  for (int e = threadIdx.x; e < E; e += 256) mine[e] = red[e];
 }
 
 // Short contractions (K <= ROWS_WIDE_KMAX): one 16-row × 16·NJ-column block per workgroup of 16 waves, the waves
@@ -420,15 +431,24 @@ __global__ void __launch_bounds__(256) lora_cols_table_kernel(int M, const ColsJ
   cols_body<NS, GH, CW>(jb, (int)blockIdx.x - start[lo], M, M, red, nullptr);
 }
 
-// Separate-launch reductions of the partials (one thread per output element of every block).
-__global__ void lora_rows_reduce(const float* __restrict__ part, int S, int gx, int RB, int NC, int M, int n,
-                                 float alpha, float* __restrict__ C, long long ldc) {
+// Separate-launch reductions of the partials (one thread per output element of every block); blockIdx.y picks
+// the job of a two-job rows launch, a job with S = 1 wrote its output itself.
+struct RowsRed {
+  const float* part;
+  int S;
+  float alpha;
+  float* C;
+  long long ldc;
+};
+__global__ void lora_rows_reduce(int gx, int RB, int NC, int M, int n, RowsRed r0, RowsRed r1) {
+  const RowsRed& rd = blockIdx.y ? r1 : r0;
+  if (rd.S <= 1) return;
   const int E = RB * NC;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long long)gx * E) return;
   const int bx = (int)(i / E), e = (int)(i % E), rr = e / NC, c = e % NC, row = bx * RB + rr;
   if (row >= M || c >= n) return;
-  C[(long long)row * ldc + c] = alpha * sum_parts(part, S, gx, bx, E, e);
+  rd.C[(long long)row * rd.ldc + c] = rd.alpha * sum_parts(rd.part, rd.S, gx, bx, E, e);
 }
 // One thread per output element of every block of both jobs (job a's elements first).
 __device__ __forceinline__ void cols_reduce_one(const ColsJobDev& jb, const float* part, int S, long long i) {
@@ -640,6 +660,33 @@ void launch_split_rows16(const SplitRow* rows, int nrows, const float* src, _Flo
   HOS_HIP_CHECK(hipGetLastError());
 }
 
+namespace {
+bool rows_short(long long K) { return K <= ROWS_WIDE_KMAX; }
+// One launch of the f32 rows kernel over njobs jobs (j1 unused for one), then one reduction launch for the split ones.
+void launch_rows_jobs(long long M, int NJ, int n, const RowsJobK& j0, const RowsJobK& j1, int njobs, HIn xh,
+                      hipStream_t st) {
+  const int gx = ceil_div_i(M, 32);
+  dim3 grid(gx, std::max(j0.S, njobs > 1 ? j1.S : 1), njobs);
+#define ROWS(NJV)                                                                        \
+  case NJV:                                                                              \
+    lora_rows_kernel<NJV><<<grid, 256, 0, st>>>((int)M, j0, njobs > 1 ? j1 : j0, xh);    \
+    break;
+  switch (NJ) {
+    ROWS(1) ROWS(2) ROWS(3) ROWS(4) ROWS(5) ROWS(6)
+    default: throw Error(HOS_E_INVALID, "lora_rows: bad width");
+  }
+#undef ROWS
+  HOS_HIP_CHECK(hipGetLastError());
+  if (j0.S > 1 || (njobs > 1 && j1.S > 1)) {
+    const long long tot = (long long)gx * 32 * NJ * 16;
+    const RowsRed r0{j0.part, j0.S, j0.alpha, j0.C, j0.ldc};
+    const RowsRed r1 = njobs > 1 ? RowsRed{j1.part, j1.S, j1.alpha, j1.C, j1.ldc} : r0;
+    lora_rows_reduce<<<dim3(ceil_div_i(tot, 256), njobs), 256, 0, st>>>(gx, 32, NJ * 16, (int)M, n, r0, r1);
+    HOS_HIP_CHECK(hipGetLastError());
+  }
+}
+}  // namespace
+
 void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
                       long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
                       hipStream_t st, HIn xh, B16 b16) {
@@ -673,7 +720,8 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
     HOS_HIP_CHECK(hipGetLastError());
     if (S > 1) {
       const long long tot = (long long)gx * 16 * NJ * 16;
-      lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, 16, NJ * 16, (int)M, n, alpha, C, ldc);
+      const RowsRed rd{ws, S, alpha, C, ldc};
+      lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(gx, 16, NJ * 16, (int)M, n, rd, rd);
       HOS_HIP_CHECK(hipGetLastError());
     }
     return;
@@ -686,7 +734,7 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
     HOS_REQUIRE(sg.kbeg[t] % 4 == 0 && sg.kend[t] % 4 == 0 && sg.boff[t] % 4 == 0 && sg.kbeg[t] >= 0 &&
                     sg.kend[t] <= K,
                 HOS_E_INVALID, "lora_rows: segment bounds must be multiples of 4 within K");
-  if (K <= ROWS_WIDE_KMAX && n <= 96) {
+  if (rows_short(K) && n <= 96) {
     // one 16-column tile per workgroup (grid.y = tiles): 128-row-block grids alone leave half the CUs idle
     const dim3 gw((unsigned)ceil_div_i(M, 16), (unsigned)((n + 15) / 16));
     lora_rows_wide_kernel<1><<<gw, 64 * ROWS_WIDE_NW, 0, st>>>((int)M, (int)K, alpha, X, ldx, Bt, ldb, sg, C, ldc, xh);
@@ -698,23 +746,37 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
   rows_split(M, K, &S, &kchunk);
   const int NJ = (n + 15) / 16;
   HOS_REQUIRE(S == 1 || (size_t)S * gx * 32 * NJ * 16 * 4 <= ws_bytes, HOS_E_INVALID, "lora_rows: workspace too small");
-  dim3 grid(gx, S);
-#define ROWS(NJV)                                                                                         \
-  case NJV:                                                                                               \
-    lora_rows_kernel<NJV><<<grid, 256, 0, st>>>((int)M, (int)K, kchunk, alpha, X, ldx, Bt, ldb, sg, C, ldc, \
-                                                ws, xh);                                         \
-    break;
-  switch (NJ) {
-    ROWS(1) ROWS(2) ROWS(3) ROWS(4) ROWS(5) ROWS(6)
-    default: throw Error(HOS_E_INVALID, "lora_rows: bad width");
+  const RowsJobK jb{(int)K, kchunk, S, alpha, X, ldx, Bt, ldb, sg, C, ldc, ws};
+  launch_rows_jobs(M, NJ, n, jb, jb, 1, xh, st);
+}
+
+// Two independent f32 rows products over the same rows (u = x·A and du = s·dy·Bᵀ of the LoRA branch op) in one
+// launch and one reduction launch, each job's partials in its own part of ws; shapes the one-job launcher would
+// give another kernel (short contractions, other widths) or a too small ws run as two launches.
+void launch_lora_rows2(long long M, const RowsCall& a, const RowsCall& b, float* ws, size_t ws_bytes,
+                       hipStream_t st) {
+  const int n = a.sg.nt * a.sg.r, NJ = (n + 15) / 16, gx = ceil_div_i(M, 32);
+  auto plain = [&](const RowsCall& c) {
+    bool ok = c.sg.nt * c.sg.r == n && !rows_short(c.K) && n <= 96 && c.sg.nt >= 1 && c.sg.nt <= 4 &&
+              c.K % 4 == 0 && c.ldx % 4 == 0 && c.ldb % 4 == 0 && ((uintptr_t)c.Bt & 15) == 0 &&
+              ((uintptr_t)c.X & 15) == 0;
+    for (int t = 0; t < c.sg.nt; t++)
+      ok = ok && c.sg.kbeg[t] % 4 == 0 && c.sg.kend[t] % 4 == 0 && c.sg.boff[t] % 4 == 0 && c.sg.kbeg[t] >= 0 &&
+           c.sg.kend[t] <= c.K;
+    return ok;
+  };
+  int Sa = 0, ka = 0, Sb = 0, kb = 0;
+  rows_split(M, a.K, &Sa, &ka);
+  rows_split(M, b.K, &Sb, &kb);
+  const size_t pa = Sa > 1 ? (size_t)Sa * gx * 32 * NJ * 16 : 0, pb = Sb > 1 ? (size_t)Sb * gx * 32 * NJ * 16 : 0;
+  if (M <= 0 || n <= 0 || !plain(a) || !plain(b) || (pa + pb) * 4 > ws_bytes) {
+    launch_lora_rows(M, a.K, a.alpha, a.X, a.ldx, a.Bt, a.ldb, a.sg, a.C, a.ldc, ws, ws_bytes, st);
+    launch_lora_rows(M, b.K, b.alpha, b.X, b.ldx, b.Bt, b.ldb, b.sg, b.C, b.ldc, ws, ws_bytes, st);
+    return;
   }
-#undef ROWS
-  HOS_HIP_CHECK(hipGetLastError());
-  if (S > 1) {
-    const long long tot = (long long)gx * 32 * NJ * 16;
-    lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(ws, S, gx, 32, NJ * 16, (int)M, n, alpha, C, ldc);
-    HOS_HIP_CHECK(hipGetLastError());
-  }
+  const RowsJobK ja{(int)a.K, ka, Sa, a.alpha, a.X, a.ldx, a.Bt, a.ldb, a.sg, a.C, a.ldc, ws};
+  const RowsJobK jb{(int)b.K, kb, Sb, b.alpha, b.X, b.ldx, b.Bt, b.ldb, b.sg, b.C, b.ldc, ws + pa};
+  launch_rows_jobs(M, NJ, n, ja, jb, 2, HIn{}, st);
 }
 
 namespace {

@@ -35,6 +35,22 @@ struct RowsSeg {
 void launch_lora_rows(long long M, long long K, float alpha, const float* X, long long ldx, const float* Bt,
                       long long ldb, const RowsSeg& sg, float* C, long long ldc, float* ws, size_t ws_bytes,
                       hipStream_t st, HIn xh = HIn{}, B16 b16 = B16{});
+// The arguments of one f32 launch_lora_rows product.
+struct RowsCall {
+  long long K;
+  float alpha;
+  const float* X;
+  long long ldx;
+  const float* Bt;
+  long long ldb;
+  RowsSeg sg;
+  float* C;
+  long long ldc;
+};
+// Two independent f32 rows products over the same M rows in one launch (falls back to two launch_lora_rows calls
+// where one launch does not fit); ws holds both jobs' split partials (lora_rows_ws_bytes of each, summed).
+void launch_lora_rows2(long long M, const RowsCall& a, const RowsCall& b, float* ws, size_t ws_bytes,
+                       hipStream_t st);
 // With both xh and b16 given the product runs on fp16 MFMA (three products, hi·hi + lo·hi + hi·lo: ~2^-22 relative
 // to the f32 one) — the rows kernel's fp32 MFMA rate bounds the long contractions otherwise.
 

@@ -100,17 +100,16 @@ void lora_run(const float* x, const float* dy, size_t rows, size_t in, size_t ou
   down.nt = 1;
   down.r = r;
   down.kend[0] = (int)in;
-  launch_lora_rows((long long)rows, (long long)in, 1.0f, x, (long long)in, at, (long long)in, down, u, r, ws, wsb,
-                   st);
-  if (y)
-    launch_gemm_f32((long long)rows, (long long)out, r, scale, u, r, 1, B, (long long)out, 1, 1.0f, y, (long long)out,
-                    ws, wsb, st);
   RowsSeg up;
   up.nt = 1;
   up.r = r;
   up.kend[0] = (int)out;
-  launch_lora_rows((long long)rows, (long long)out, scale, dy, (long long)out, B, (long long)out, up, du, r, ws, wsb,
-                   st);
+  // u = x·A and du = s·dy·Bᵀ (independent) in one launch
+  launch_lora_rows2((long long)rows, RowsCall{(long long)in, 1.0f, x, (long long)in, at, (long long)in, down, u, r},
+                    RowsCall{(long long)out, scale, dy, (long long)out, B, (long long)out, up, du, r}, ws, wsb, st);
+  if (y)
+    launch_gemm_f32((long long)rows, (long long)out, r, scale, u, r, 1, B, (long long)out, 1, 1.0f, y, (long long)out,
+                    ws, wsb, st);
   // dB = s·uᵀ·dy and dA = (duᵀ·x)ᵀ in one launch
   ColsJob jdb, jda;
   lora_cols_jobs(dy, x, rows, in, out, r, scale, u, du, dB, dA, &jdb, &jda);
@@ -123,9 +122,9 @@ void lora_run(const float* x, const float* dy, size_t rows, size_t in, size_t ou
 size_t lora_ws_need(size_t rows, size_t in, size_t out, int r) {
   ColsJob jdb, jda;
   lora_cols_jobs(nullptr, nullptr, rows, in, out, r, 1.0f, nullptr, nullptr, nullptr, nullptr, &jdb, &jda);
-  return std::max({lora_rows_ws_bytes((long long)rows, (long long)in, r),
-                   lora_rows_ws_bytes((long long)rows, (long long)out, r),
-                   lora_cols2_ws_bytes((long long)rows, jdb, &jda)});
+  return std::max(lora_rows_ws_bytes((long long)rows, (long long)in, r) +
+                      lora_rows_ws_bytes((long long)rows, (long long)out, r),
+                  lora_cols2_ws_bytes((long long)rows, jdb, &jda));
 }
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
