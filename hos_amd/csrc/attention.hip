@@ -748,7 +748,7 @@ void attn_fwd_hd(const float* qkv, long long ld, int kcol, int vcol, int B, int 
 template <int HD>
 void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout, long long ldo,
                  const float* lse, float* dvec, int B, int T, int nh, int nkv, float* dqkv, long long ldd, float* part,
-                 void* scratch, hipStream_t st, bool qkv_planes) {
+                 void* scratch, hipStream_t st, bool qkv_planes, bool defer_group_sum) {
   const Planes P = planes_of(scratch, B, T, nh, nkv, HD);
   if (!qkv_planes) split_qkv<HD>(qkv, ld, kcol, vcol, B, T, nh, nkv, P, st);
   // dO is read from its f32 rows by both kernels (split to hi/lo as it is loaded); the dQ launch also forms
@@ -761,7 +761,7 @@ void attn_bwd_hd(const float* qkv, long long ld, int kcol, int vcol, const float
   attn_dkdv_kernel<HD, NGB><<<grid, 256 * NGB, 0, st>>>(P.qh, P.ql, P.kh, P.kl, P.vh, P.vl, dout, ldo, lse,
                                                               dvec, T, nh, nh / nkv, dqkv, ldd, kcol, vcol, part);
   HOS_HIP_CHECK(hipGetLastError());
-  if (nh != nkv) {
+  if (nh != nkv && !defer_group_sum) {
     long long ne = (long long)B * T * nkv * 2 * HD;
     attn_group_sum<HD><<<ceil_div(ne, 256), 256, 0, st>>>(part, B * T, nh, nkv, nh / nkv, dqkv, ldd, kcol, vcol);
     HOS_HIP_CHECK(hipGetLastError());
@@ -788,17 +788,18 @@ void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, 
 
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
-                     long long ldd, float* part, void* scratch, hipStream_t st, bool qkv_planes) {
+                     long long ldd, float* part, void* scratch, hipStream_t st, bool qkv_planes,
+                     bool defer_group_sum) {
   check_layout(ld, kcol, vcol, hd, scratch);
   HOS_REQUIRE(nh == nkv || part != nullptr, HOS_E_INVALID, "attention: GQA backward needs a partial buffer");
   HOS_REQUIRE(ldo % 4 == 0 && ldd % 4 == 0 && nkv > 0 && nh % nkv == 0, HOS_E_INVALID, "attention: unaligned layout");
   if (B <= 0 || T <= 0) return;
   if (hd == 64)
     attn_bwd_hd<64>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st,
-                    qkv_planes);
+                    qkv_planes, defer_group_sum);
   else
     attn_bwd_hd<128>(qkv, ld, kcol, vcol, o, dout, ldo, lse, dvec, B, T, nh, nkv, dqkv, ldd, part, scratch, st,
-                     qkv_planes);
+                     qkv_planes, defer_group_sum);
 }
 
 }  // namespace hos

@@ -181,6 +181,80 @@ __global__ void __launch_bounds__(256) rope_h16_kernel(float* __restrict__ buf, 
   if (threadIdx.x == 0) orinv[m] = ldexpf(1.0f, -e);
 }
 
+// The row pass after the training step's attention backward, per row m of dqkv [M, ld] (q heads at 0, k heads at
+// kcol = nh·hd right after them, v heads at vcol): the k and v columns formed from the per-query-head partials
+// part[(m·nh + head)·2·hd + (0 | hd) + i] by summing each GQA group in head order (as attn_group_sum; group == 1:
+// dqkv already holds them), the q and k heads rotated back (inverse RoPE with rope_kernel's arithmetic), the row
+// stored back in f32 and written as the fp16 operand of its first W columns (the f32 -> fp16 row conversion).
+// One workgroup per row; the formed row is staged in LDS for the rotation's partner reads; W <= RB·ROWS_NV.
+constexpr int ROWS_NV = 16;
+static_assert(RB * ROWS_NV == kAttnRowsMax, "row pass capacity");
+__global__ void __launch_bounds__(RB) attn_bwd_rows_kernel(float* __restrict__ dqkv, long long ld, int hd, int nh,
+                                                           int nkv, int group, int vcol,
+                                                           const float* __restrict__ part, int T,
+                                                           const float2* __restrict__ tab, int neox, int W,
+                                                           _Float16* __restrict__ oh, _Float16* __restrict__ ol,
+                                                           float* __restrict__ orinv) {
+#pragma clang fp contract(off)
+  extern __shared__ float rowbuf[];
+  __shared__ float red[8];
+  const int m = blockIdx.x, half = hd >> 1, kcol = nh * hd, nrotc = (nh + nkv) * hd;
+  float* row = dqkv + (long long)m * ld;
+  for (int c = threadIdx.x; c < W; c += RB) {
+    float v;
+    if (group > 1 && c >= kcol && c < vcol + nkv * hd && (c < kcol + nkv * hd || c >= vcol)) {
+      const bool isv = c >= vcol;
+      const int cc = isv ? c - vcol : c - kcol, g = cc / hd, i = cc % hd;
+      const float* pp = part + ((long long)m * nh + (long long)g * group) * 2 * hd + (isv ? hd : 0) + i;
+      v = 0.0f;
+      for (int hh = 0; hh < group; hh++) v += pp[(long long)hh * 2 * hd];
+    } else {
+      v = row[c];
+    }
+    rowbuf[c] = v;
+  }
+  __syncthreads();
+  const float2* tr = tab + (long long)(m % T) * half;
+  float rv[ROWS_NV];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < ROWS_NV; j++) {
+    const int c = threadIdx.x + RB * j;
+    if (c >= W) break;
+    float r = rowbuf[c];
+    if (c < nrotc) {
+      const int hb = c - c % hd, i = c % hd;
+      int p, ia, ib;
+      if (neox) {
+        p = i < half ? i : i - half;
+        ia = p;
+        ib = p + half;
+      } else {
+        p = i >> 1;
+        ia = 2 * p;
+        ib = 2 * p + 1;
+      }
+      const float a = rowbuf[hb + ia], b = rowbuf[hb + ib];
+      const float2 sc2 = tr[p];
+      const float sn = sc2.x, cs = sc2.y;
+      r = (i == ia) ? a * cs + b * sn : -a * sn + b * cs;
+    }
+    rv[j] = r;
+    row[c] = r;
+    amax = fmaxf(amax, fabsf(r));
+  }
+  amax = block_max(amax, red);
+  const int e = row_exp(amax);
+  const float sc = ldexpf(1.0f, e);
+#pragma unroll
+  for (int j = 0; j < ROWS_NV; j++) {
+    const int c = threadIdx.x + RB * j;
+    if (c >= W) break;
+    put_h16(rv[j] * sc, oh, ol, (long long)m * W + c);
+  }
+  if (threadIdx.x == 0) orinv[m] = ldexpf(1.0f, -e);
+}
+
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
 // gu rows = [gate (F) | up (F)] -> h = silu(gate)·up: f32 (optional) + fp16 operand.
@@ -805,6 +879,16 @@ void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T,
                  bool inverse, int M, hipStream_t st) {
   long long n = (long long)M * n_heads * (hd / 2);
   rope_kernel<<<ceil_div(n, 256), 256, 0, st>>>(buf, ld, col0, n_heads, hd, T, tab, neox, inverse, M);
+  HOS_HIP_CHECK(hipGetLastError());
+}
+void launch_attn_bwd_rows(float* dqkv, long long ld, int hd, int nh, int nkv, int vcol, const float* part, int T,
+                          const float2* tab, bool neox, int M, int W, H16 out, hipStream_t st) {
+  HOS_REQUIRE(nkv > 0 && nh % nkv == 0 && W <= ld && W <= RB * ROWS_NV && vcol >= (nh + nkv) * hd &&
+                  vcol + nkv * hd <= W && (nh == nkv || part != nullptr),
+              HOS_E_INVALID, "attention rows pass: bad layout");
+  if (M <= 0) return;
+  attn_bwd_rows_kernel<<<M, RB, (size_t)W * sizeof(float), st>>>(dqkv, ld, hd, nh, nkv, nh / nkv, vcol, part, T, tab,
+                                                                  neox, W, out.data, out.lo, out.rinv);
   HOS_HIP_CHECK(hipGetLastError());
 }
 void launch_rope_h16(float* buf, long long ld, int n_heads, int hd, int T, const float2* tab, bool neox, bool inverse,

@@ -17,6 +17,12 @@ void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T,
                  bool inverse, int M, hipStream_t st);
 // RoPE (col0 = 0) fused with the fp16 row operand of the first W columns (row stride W), as launch_rope
 // followed by the f32 -> fp16 row conversion.
+// After a launch_attn_bwd with defer_group_sum: per row of dqkv, dK/dV summed over each GQA group from `part`, the
+// inverse RoPE of the q and k heads (k right after q), the row stored back and written as the fp16 operand of its
+// first W columns (W <= kAttnRowsMax). Equal to attn_group_sum + launch_rope_h16 (inverse) element for element.
+constexpr int kAttnRowsMax = 4096;
+void launch_attn_bwd_rows(float* dqkv, long long ld, int hd, int nh, int nkv, int vcol, const float* part, int T,
+                          const float2* tab, bool neox, int M, int W, H16 out, hipStream_t st);
 void launch_rope_h16(float* buf, long long ld, int n_heads, int hd, int T, const float2* tab, bool neox, bool inverse,
                      int M, int W, H16 out, hipStream_t st);
 void launch_swiglu_fwd(const float* gu, int M, int F, float* h, H16 out, hipStream_t st);
@@ -49,5 +55,6 @@ void launch_attn_fwd(const float* qkv, long long ld, int kcol, int vcol, int B, 
                      const float2* rope_tab = nullptr, bool rope_neox = false);
 void launch_attn_bwd(const float* qkv, long long ld, int kcol, int vcol, const float* o, const float* dout,
                      long long ldo, const float* lse, float* dvec, int B, int T, int nh, int nkv, int hd, float* dqkv,
-                     long long ldd, float* part, void* scratch, hipStream_t st, bool qkv_planes = false);
+                     long long ldd, float* part, void* scratch, hipStream_t st, bool qkv_planes = false,
+                     bool defer_group_sum = false);
 }  // namespace hos

@@ -811,21 +811,27 @@ struct hos_peft {
       lora_grad_b(l, 1, dx, d, d, M, hs_in());
       qdx(w.w[TO], hs, d, M, dout, qd, 0, down_epi(l, TO), tpd[TO]);
       lora_grad_a(l, 1, a.o, qd, M);
+      const bool rows_pass = !c.qk_norm && W3 <= kAttnRowsMax;
       {
         Scope s(this, "attn_bwd", 2.0 * B * c.n_heads * (double)T * (T + 1) / 2 * c.head_dim * 5,
                 4.0 * M * (W3 * 2 + qd * 2) + 8.0 * B * c.n_heads * T);
+        // without QK-norm the GQA group sum of dK/dV is left to the row pass below
         launch_attn_bwd(a.qkv, W3, qd, qd + kvd, a.o, dout, qd, a.lse, dvec, B, T, c.n_heads, c.n_kv_heads,
-                        c.head_dim, dq, W3, attn_part, attn_planes[l], st, true);
+                        c.head_dim, dq, W3, attn_part, attn_planes[l], st, true, rows_pass);
       }
       {
         Scope s(this, "rope", 0, 8.0 * M * (qd + kvd));
         // the k heads follow the q heads in the row (qd = n_heads·head_dim): one launch rotates both; without
-        // QK-norm in between it also writes the fp16 operand of the q|k|v dX GEMM
+        // QK-norm in between the same row pass also sums dK/dV over each GQA group and writes the fp16 operand of
+        // the q|k|v dX GEMM
         if (c.qk_norm)
           launch_rope(dq, W3, 0, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, st);
-        else
+        else if (!rows_pass)
           launch_rope_h16(dq, W3, c.n_heads + c.n_kv_heads, c.head_dim, T, rope_tab, c.rope_neox, true, M, W3, hs,
                           st);
+        else
+          launch_attn_bwd_rows(dq, W3, c.head_dim, c.n_heads, c.n_kv_heads, qd + kvd, attn_part, T, rope_tab,
+                               c.rope_neox, M, W3, hs, st);
       }
       if (c.qk_norm) {
         Scope s(this, "rmsnorm", 0, 4.0 * M * (qd + kvd) * 4);
