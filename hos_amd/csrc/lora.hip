@@ -492,14 +492,14 @@ __global__ void lora_cols_reduce(const float* __restrict__ part, int S, ColsJobD
 // workgroups (partials reduced by lora_rows_reduce). Lane (q = lane/16, p = lane%16): A row p, B column p, k 8q .. +7.
 constexpr int R16_NW = 16;
 typedef _Float16 h8l __attribute__((ext_vector_type(8)));
-template <int NJ>
+template <int NJ, int RT>
 __global__ void __launch_bounds__(64 * R16_NW) lora_rows16_kernel(int M, int K, int kchunk, float alpha, HIn xh,
                                                                   long long ldx, B16 bt, long long ldb, RowsSeg sg,
                                                                   float* __restrict__ C, long long ldc, float* part) {
-  constexpr int NC = NJ * 16, E = 16 * NC;
+  constexpr int NC = NJ * 16, E = 16 * RT * NC;
   __shared__ float red[R16_NW * E];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, p = lane & 15;
-  const int m0 = blockIdx.x * 16, n = sg.nt * sg.r;
+  const int m0 = blockIdx.x * 16 * RT, n = sg.nt * sg.r;
   const int kb = blockIdx.y * kchunk, ke = min(K, kb + kchunk);
   long long bbase[NJ];
   int klo[NJ], khi[NJ];
@@ -519,22 +519,32 @@ __global__ void __launch_bounds__(64 * R16_NW) lora_rows16_kernel(int M, int K, 
       bsc[jt] = 0.0f;
     }
   }
-  const int row = m0 + p;
-  const bool rv = row < M;
-  const long long xr = (long long)(rv ? row : 0) * ldx;
-  f4v acc[NJ];
+  bool rv[RT];
+  long long xr[RT];
 #pragma unroll
-  for (int jt = 0; jt < NJ; jt++) acc[jt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = 0; t < RT; t++) {
+    const int row = m0 + 16 * t + p;
+    rv[t] = row < M;
+    xr[t] = (long long)(rv[t] ? row : 0) * ldx;
+  }
+  f4v acc[RT][NJ];
+#pragma unroll
+  for (int t = 0; t < RT; t++)
+#pragma unroll
+    for (int jt = 0; jt < NJ; jt++) acc[t][jt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
   const h8l z8 = {};
-  constexpr int U = NJ <= 2 ? 2 : 1;  // steps per trip, loads first (steps past the end add exact zeros)
+  constexpr int U = NJ * RT <= 2 ? 2 : 1;  // steps per trip, loads first (steps past the end add exact zeros)
   for (int k0 = kb + 32 * wave; k0 < ke; k0 += 32 * R16_NW * U) {
-    h8l ah[U], al[U], bh[U][NJ], bl[U][NJ];
+    h8l ah[U][RT], al[U][RT], bh[U][NJ], bl[U][NJ];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int kk = k0 + 32 * R16_NW * u + 8 * q;
       const bool kin = kk < ke;
-      ah[u] = (rv && kin) ? *reinterpret_cast<const h8l*>(xh.hi + xr + kk) : z8;
-      al[u] = (rv && kin) ? *reinterpret_cast<const h8l*>(xh.lo + xr + kk) : z8;
+#pragma unroll
+      for (int t = 0; t < RT; t++) {
+        ah[u][t] = (rv[t] && kin) ? *reinterpret_cast<const h8l*>(xh.hi + xr[t] + kk) : z8;
+        al[u][t] = (rv[t] && kin) ? *reinterpret_cast<const h8l*>(xh.lo + xr[t] + kk) : z8;
+      }
 #pragma unroll
       for (int jt = 0; jt < NJ; jt++) {
         const bool in = kin && kk >= klo[jt] && kk < khi[jt];
@@ -545,20 +555,25 @@ __global__ void __launch_bounds__(64 * R16_NW) lora_rows16_kernel(int M, int K, 
 #pragma unroll
     for (int u = 0; u < U; u++)
 #pragma unroll
-      for (int jt = 0; jt < NJ; jt++) {
-        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[u], bh[u][jt], acc[jt], 0, 0, 0);
-        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u], bl[u][jt], acc[jt], 0, 0, 0);
-        acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u], bh[u][jt], acc[jt], 0, 0, 0);
-      }
-  }
-  // element (row 4q+i, col 16jt+p): the operand's row scale and the factor row's scale
+      for (int t = 0; t < RT; t++)
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r2 = m0 + 4 * q + i;
-    const float ri = r2 < M ? xh.rinv[r2] : 0.0f;
-#pragma unroll
-    for (int jt = 0; jt < NJ; jt++) red[wave * E + (4 * q + i) * NC + 16 * jt + p] = acc[jt][i] * ri * bsc[jt];
+        for (int jt = 0; jt < NJ; jt++) {
+          acc[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[u][t], bh[u][jt], acc[t][jt], 0, 0, 0);
+          acc[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u][t], bl[u][jt], acc[t][jt], 0, 0, 0);
+          acc[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u][t], bh[u][jt], acc[t][jt], 0, 0, 0);
+        }
   }
+  // element (row 16t+4q+i, col 16jt+p): the operand's row scale and the factor row's scale
+#pragma unroll
+  for (int t = 0; t < RT; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r2 = m0 + 16 * t + 4 * q + i;
+      const float ri = r2 < M ? xh.rinv[r2] : 0.0f;
+#pragma unroll
+      for (int jt = 0; jt < NJ; jt++)
+        red[wave * E + (16 * t + 4 * q + i) * NC + 16 * jt + p] = acc[t][jt][i] * ri * bsc[jt];
+    }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += 64 * R16_NW) {
     float v = 0.0f;
@@ -635,8 +650,19 @@ void cols_split(long long M, int gx, int* S, int* mchunk) {
 #ifndef HOS_R16_MINROUNDS
 #define HOS_R16_MINROUNDS 4
 #endif
-void rows16_split(long long M, long long K, int* S, int* kchunk) {
-  const int gx = ceil_div_i(M, 16), round = 32 * R16_NW;
+// Row tiles of 16 per fp16 rows workgroup: two when the 32-row blocks alone reach the split target and n <= 64 (each
+// factor fragment loaded from L2 then feeds two row tiles; at one tile the factors' L2 bytes per workgroup are
+// 2·n/16 times the activation's: Llama-3.2-1B's step, M 8192, +1.1%), else one (with fewer row blocks, two tiles per
+// workgroup would need more contraction splits: Qwen2.5-0.5B at M 2048 −1.3% with two; above 64 columns the 16
+// waves' LDS partial tiles would not fit).
+#ifndef HOS_R16_RT
+#define HOS_R16_RT 2
+#endif
+int rows16_rt(long long M, int n) {
+  return (n <= 64 && (M + 31) / 32 >= HOS_R16_TARGET) ? HOS_R16_RT : 1;
+}
+void rows16_split(long long M, long long K, int* S, int* kchunk, int rb = 16) {
+  const int gx = ceil_div_i(M, rb), round = 32 * R16_NW;
   int s = std::max(1, std::min(ceil_div_i(HOS_R16_TARGET, gx), (int)(K / ((long long)round * HOS_R16_MINROUNDS))));
   *kchunk = ceil_div_i(ceil_div_i(K, s), round) * round;
   *S = std::max(1, ceil_div_i(K, *kchunk));
@@ -645,8 +671,9 @@ void rows16_split(long long M, long long K, int* S, int* kchunk) {
 size_t lora_rows_ws_bytes(long long M, long long K, int n) {
   if (M <= 0 || n <= 0) return 0;
   int S16 = 0, kc16 = 0;
-  rows16_split(M, K, &S16, &kc16);
-  const size_t w16 = S16 > 1 ? (size_t)S16 * ceil_div_i(M, 16) * 16 * ((n + 15) / 16) * 16 * 4 : 0;
+  const int rb16 = 16 * rows16_rt(M, n);
+  rows16_split(M, K, &S16, &kc16, rb16);
+  const size_t w16 = S16 > 1 ? (size_t)S16 * ceil_div_i(M, rb16) * rb16 * ((n + 15) / 16) * 16 * 4 : 0;
   if (K <= ROWS_WIDE_KMAX) return w16;
   int S = 0, kchunk = 0;
   rows_split(M, K, &S, &kchunk);
@@ -702,26 +729,29 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
           sg.kend[t] <= K;
   if (f16) {
     HOS_REQUIRE(xh.rinv, HOS_E_INVALID, "lora_rows: the fp16 operand needs its row scales");
-    const int gx = ceil_div_i(M, 16), NJ = (n + 15) / 16;
+    const int RT = rows16_rt(M, n), rb = 16 * RT, gx = ceil_div_i(M, rb), NJ = (n + 15) / 16;
     int S = 0, kchunk = 0;
-    rows16_split(M, K, &S, &kchunk);
-    HOS_REQUIRE(S == 1 || (size_t)S * gx * 16 * NJ * 16 * 4 <= ws_bytes, HOS_E_INVALID, "lora_rows: workspace too small");
+    rows16_split(M, K, &S, &kchunk, rb);
+    HOS_REQUIRE(S == 1 || (size_t)S * gx * rb * NJ * 16 * 4 <= ws_bytes, HOS_E_INVALID, "lora_rows: workspace too small");
     dim3 grid(gx, S);
-#define ROWS16(NJV)                                                                                                  \
-  case NJV:                                                                                                          \
-    lora_rows16_kernel<NJV><<<grid, 64 * R16_NW, 0, st>>>((int)M, (int)K, kchunk, alpha, xh, ldx, b16, ldb, sg, C, ldc, \
-                                                         ws);                                                        \
+#define ROWS16(NJV, RTV)                                                                                   \
+  case NJV * 8 + RTV:                                                                                      \
+    lora_rows16_kernel<NJV, RTV><<<grid, 64 * R16_NW, 0, st>>>((int)M, (int)K, kchunk, alpha, xh, ldx, b16, ldb, sg, \
+                                                               C, ldc, ws);                                \
     break;
-    switch (NJ) {
-      ROWS16(1) ROWS16(2) ROWS16(3) ROWS16(4) ROWS16(5) ROWS16(6)
+    switch (NJ * 8 + RT) {
+      ROWS16(1, 1) ROWS16(2, 1) ROWS16(3, 1) ROWS16(4, 1) ROWS16(5, 1) ROWS16(6, 1)
+#if HOS_R16_RT == 2
+      ROWS16(1, 2) ROWS16(2, 2) ROWS16(3, 2) ROWS16(4, 2)
+#endif
       default: throw Error(HOS_E_INVALID, "lora_rows: bad width");
     }
 #undef ROWS16
     HOS_HIP_CHECK(hipGetLastError());
     if (S > 1) {
-      const long long tot = (long long)gx * 16 * NJ * 16;
+      const long long tot = (long long)gx * rb * NJ * 16;
       const RowsRed rd{ws, S, alpha, C, ldc};
-      lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(gx, 16, NJ * 16, (int)M, n, rd, rd);
+      lora_rows_reduce<<<ceil_div_i(tot, 256), 256, 0, st>>>(gx, rb, NJ * 16, (int)M, n, rd, rd);
       HOS_HIP_CHECK(hipGetLastError());
     }
     return;

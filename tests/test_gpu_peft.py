@@ -103,6 +103,21 @@ def test_step_llama_layout_ragged(gpu):
     compare_grads(pm, om, cfg, lora, TARGETS)
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("rank", [16, 32])
+def test_step_many_rows(gpu, rank):
+    """M = 8192 token rows, as in Llama-3.2-1B's B8×T1024 step: the fp16 LoRA rows products then take two 16-row
+    tiles per workgroup wherever their width allows (r16: q|k|v 48, gate|up 32, o and down 16 columns; r32: gate|up
+    64, o and down 32 — q|k|v at 96 stays at one tile), which the smaller steps above never reach."""
+    cfg = tiny(12, lora_rank=rank, lora_alpha=2.0 * rank, n_layers=2)
+    print(f"peft tiny Q4_K r{rank} B=16 T=512", flush=True)
+    pm, om, ids, tg, lora, TARGETS = run_pair(gpu, cfg, B=16, T=512, seed=11)
+    lg = pm.loss_grad(ids, tg)
+    lo = om.loss_grad(ids, tg)
+    assert abs(lg - lo) / abs(lo) <= TOL
+    compare_grads(pm, om, cfg, lora, TARGETS)
+
+
 def test_reference_faithful_qv_b_zero(gpu):
     """The reference's own setting: LoRA on q and v only, B = 0 (src/peft.rs:187-199). dA must be exactly 0,
     and the adapted logits equal the base (the init-parity check of src/main.rs:2497-2534)."""
