@@ -48,6 +48,22 @@ __device__ __forceinline__ void put_h16(float v, _Float16* hi, _Float16* lo, lon
   if (lo) lo[i] = (_Float16)(v - (float)h);
 }
 
+// Four consecutive elements of the fp16 operand at once.
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void put_h16x4(float4 v, _Float16* hi, _Float16* lo, long long i) {
+  h16x4 h{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  *reinterpret_cast<h16x4*>(hi + i) = h;
+  if (lo) {
+    h16x4 l{(_Float16)(v.x - (float)h.x), (_Float16)(v.y - (float)h.y), (_Float16)(v.z - (float)h.z),
+            (_Float16)(v.w - (float)h.w)};
+    *reinterpret_cast<h16x4*>(lo + i) = l;
+  }
+}
+__device__ __forceinline__ float4 scale4(float4 v, float s) { return make_float4(v.x * s, v.y * s, v.z * s, v.w * s); }
+__device__ __forceinline__ float amax4(float a, float4 v) {
+  return fmaxf(fmaxf(a, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
 // Power-of-two scale that maps a row max-abs into [2^14, 2^15) (exact in fp16 and f32).
 __device__ __forceinline__ int row_exp(float amax) {
   if (!(amax > 0.0f) || amax >= 3.0e38f) return 0;
@@ -186,9 +202,10 @@ __global__ void __launch_bounds__(256) rope_h16_kernel(float* __restrict__ buf, 
 // part[(m·nh + head)·2·hd + (0 | hd) + i] by summing each GQA group in head order (as attn_group_sum; group == 1:
 // dqkv already holds them), the q and k heads rotated back (inverse RoPE with rope_kernel's arithmetic), the row
 // stored back in f32 and written as the fp16 operand of its first W columns (the f32 -> fp16 row conversion).
-// One workgroup per row; the formed row is staged in LDS for the rotation's partner reads; W <= RB·ROWS_NV.
-constexpr int ROWS_NV = 16;
-static_assert(RB * ROWS_NV == kAttnRowsMax, "row pass capacity");
+// One workgroup per row, 16-byte accesses (every head dim and W a multiple of 4); the formed row is staged in LDS for
+// the rotation's partner reads; W <= 4·RB·ROWS_NV.
+constexpr int ROWS_NV = 4;
+static_assert(4 * RB * ROWS_NV == kAttnRowsMax, "row pass capacity");
 __global__ void __launch_bounds__(RB) attn_bwd_rows_kernel(float* __restrict__ dqkv, long long ld, int hd, int nh,
                                                            int nkv, int group, int vcol,
                                                            const float* __restrict__ part, int T,
@@ -198,61 +215,73 @@ __global__ void __launch_bounds__(RB) attn_bwd_rows_kernel(float* __restrict__ d
 #pragma clang fp contract(off)
   extern __shared__ float rowbuf[];
   __shared__ float red[8];
-  const int m = blockIdx.x, half = hd >> 1, kcol = nh * hd, nrotc = (nh + nkv) * hd;
+  const int m = blockIdx.x, half = hd >> 1, kcol = nh * hd, nrotc = (nh + nkv) * hd, W4 = W >> 2;
   float* row = dqkv + (long long)m * ld;
-  for (int c = threadIdx.x; c < W; c += RB) {
-    float v;
+  for (int c4 = threadIdx.x; c4 < W4; c4 += RB) {
+    const int c = 4 * c4;
+    float4 v;
     if (group > 1 && c >= kcol && c < vcol + nkv * hd && (c < kcol + nkv * hd || c >= vcol)) {
       const bool isv = c >= vcol;
       const int cc = isv ? c - vcol : c - kcol, g = cc / hd, i = cc % hd;
       const float* pp = part + ((long long)m * nh + (long long)g * group) * 2 * hd + (isv ? hd : 0) + i;
-      v = 0.0f;
-      for (int hh = 0; hh < group; hh++) v += pp[(long long)hh * 2 * hd];
+      v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int hh = 0; hh < group; hh++) {
+        const float4 t = *reinterpret_cast<const float4*>(pp + (long long)hh * 2 * hd);
+        v.x += t.x;
+        v.y += t.y;
+        v.z += t.z;
+        v.w += t.w;
+      }
     } else {
-      v = row[c];
+      v = reinterpret_cast<const float4*>(row)[c4];
     }
-    rowbuf[c] = v;
+    reinterpret_cast<float4*>(rowbuf)[c4] = v;
   }
   __syncthreads();
   const float2* tr = tab + (long long)(m % T) * half;
-  float rv[ROWS_NV];
+  float4 rv[ROWS_NV];
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < ROWS_NV; j++) {
-    const int c = threadIdx.x + RB * j;
-    if (c >= W) break;
-    float r = rowbuf[c];
-    if (c < nrotc) {
-      const int hb = c - c % hd, i = c % hd;
-      int p, ia, ib;
-      if (neox) {
-        p = i < half ? i : i - half;
-        ia = p;
-        ib = p + half;
-      } else {
-        p = i >> 1;
-        ia = 2 * p;
-        ib = 2 * p + 1;
+    const int c4 = threadIdx.x + RB * j;
+    if (c4 >= W4) break;
+    float r[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int c = 4 * c4 + e;
+      r[e] = rowbuf[c];
+      if (c < nrotc) {
+        const int hb = c - c % hd, i = c % hd;
+        int p, ia, ib;
+        if (neox) {
+          p = i < half ? i : i - half;
+          ia = p;
+          ib = p + half;
+        } else {
+          p = i >> 1;
+          ia = 2 * p;
+          ib = 2 * p + 1;
+        }
+        const float a = rowbuf[hb + ia], b = rowbuf[hb + ib];
+        const float2 sc2 = tr[p];
+        const float sn = sc2.x, cs = sc2.y;
+        r[e] = (i == ia) ? a * cs + b * sn : -a * sn + b * cs;
       }
-      const float a = rowbuf[hb + ia], b = rowbuf[hb + ib];
-      const float2 sc2 = tr[p];
-      const float sn = sc2.x, cs = sc2.y;
-      r = (i == ia) ? a * cs + b * sn : -a * sn + b * cs;
+      amax = fmaxf(amax, fabsf(r[e]));
     }
-    rv[j] = r;
-    row[c] = r;
-    amax = fmaxf(amax, fabsf(r));
+    rv[j] = make_float4(r[0], r[1], r[2], r[3]);
+    reinterpret_cast<float4*>(row)[c4] = rv[j];
   }
   amax = block_max(amax, red);
-  const int e = row_exp(amax);
-  const float sc = ldexpf(1.0f, e);
+  const int ex = row_exp(amax);
+  const float sc = ldexpf(1.0f, ex);
 #pragma unroll
   for (int j = 0; j < ROWS_NV; j++) {
-    const int c = threadIdx.x + RB * j;
-    if (c >= W) break;
-    put_h16(rv[j] * sc, oh, ol, (long long)m * W + c);
+    const int c4 = threadIdx.x + RB * j;
+    if (c4 >= W4) break;
+    put_h16x4(make_float4(rv[j].x * sc, rv[j].y * sc, rv[j].z * sc, rv[j].w * sc), oh, ol, (long long)m * W + 4 * c4);
   }
-  if (threadIdx.x == 0) orinv[m] = ldexpf(1.0f, -e);
+  if (threadIdx.x == 0) orinv[m] = ldexpf(1.0f, -ex);
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
@@ -316,21 +345,6 @@ __global__ void __launch_bounds__(RB) swiglu_bwd_kernel(const float* __restrict_
 // Register-resident variants of the two kernels above for F % 4 == 0, F <= 4·RB·NV: each thread loads its
 // float4 columns once (i = tid + RB·j), so the row is read from HBM once and the fp16 pass works from
 // registers; the same per-element arithmetic and the same row max, hence the same outputs.
-typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void put_h16x4(float4 v, _Float16* hi, _Float16* lo, long long i) {
-  h16x4 h{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-  *reinterpret_cast<h16x4*>(hi + i) = h;
-  if (lo) {
-    h16x4 l{(_Float16)(v.x - (float)h.x), (_Float16)(v.y - (float)h.y), (_Float16)(v.z - (float)h.z),
-            (_Float16)(v.w - (float)h.w)};
-    *reinterpret_cast<h16x4*>(lo + i) = l;
-  }
-}
-__device__ __forceinline__ float4 scale4(float4 v, float s) { return make_float4(v.x * s, v.y * s, v.z * s, v.w * s); }
-__device__ __forceinline__ float amax4(float a, float4 v) {
-  return fmaxf(fmaxf(a, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
-}
-
 constexpr int SWIGLU_NV = 8;
 
 __global__ void __launch_bounds__(RB) swiglu_fwd_reg_kernel(const float* __restrict__ gu, int F,
@@ -883,8 +897,10 @@ void launch_rope(float* buf, long long ld, int col0, int n_heads, int hd, int T,
 }
 void launch_attn_bwd_rows(float* dqkv, long long ld, int hd, int nh, int nkv, int vcol, const float* part, int T,
                           const float2* tab, bool neox, int M, int W, H16 out, hipStream_t st) {
-  HOS_REQUIRE(nkv > 0 && nh % nkv == 0 && W <= ld && W <= RB * ROWS_NV && vcol >= (nh + nkv) * hd &&
-                  vcol + nkv * hd <= W && (nh == nkv || part != nullptr),
+  HOS_REQUIRE(nkv > 0 && nh % nkv == 0 && W <= ld && W <= kAttnRowsMax && W % 4 == 0 && ld % 4 == 0 && hd % 4 == 0 &&
+                  vcol % 4 == 0 && vcol >= (nh + nkv) * hd && vcol + nkv * hd <= W && (nh == nkv || part != nullptr) &&
+                  ((uintptr_t)dqkv & 15) == 0 && ((uintptr_t)part & 15) == 0 && ((uintptr_t)out.data & 7) == 0 &&
+                  ((uintptr_t)out.lo & 7) == 0,
               HOS_E_INVALID, "attention rows pass: bad layout");
   if (M <= 0) return;
   attn_bwd_rows_kernel<<<M, RB, (size_t)W * sizeof(float), st>>>(dqkv, ld, hd, nh, nkv, nh / nkv, vcol, part, T, tab,
