@@ -868,11 +868,19 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bn = 128;
     bk = 32;
   }
-  // A fused rank above 32 (stacked q|k|v dX): 64×64 tiles, whose LDS holds the rank-64 staging, and no split.
+  // A fused rank above 32 (stacked q|k|v dX): no split, and a tile whose LDS holds the rank staging — 128×128×64
+  // where its tiles alone give every CU one (their staging holds rank 64 in the two-plane modes; OLMoE's q|k|v dX,
+  // 2048 × 2048 × 6144 at rank 48: 254 µs on 64×64 tiles), else 64×64.
   if (epi.rank > 32) {
-    bm = 64;
-    bn = 64;
-    bk = C % 64 == 0 ? 64 : 32;
+    if (C % 64 == 0 && epi.rank <= Geo<128, 128, 64, DX, NP>::RCAP && ntiles(128, 128) >= 256) {
+      bm = 128;
+      bn = 128;
+      bk = 64;
+    } else {
+      bm = 64;
+      bn = 64;
+      bk = C % 64 == 0 ? 64 : 32;
+    }
   }
   // Column-segmented U (stacked projections): tiles must not straddle a segment boundary, and the split-K
   // reduction (which stages one U block for all its columns) is not used.

@@ -8,7 +8,8 @@ term); the test makes it as large as the base term, so a dropped or misplaced ra
 1e-5 bar by orders of magnitude.
 
 Cases: ragged row counts (not a multiple of any tile), an output width that is not a multiple of the tile
-(forward), ranks 16 / 20 (zero-padded to 32) / 48 / 64 (the stacked q|k|v dX), L read through both stride
+(forward), ranks 16 / 20 (zero-padded to 32) / 48 / 64 (the stacked q|k|v dX, on 64×64 and, with 256 output tiles,
+128×128×64 tiles), L read through both stride
 orders (B [r, N] rows, A [N, r] transposed), a narrow output with a long contraction (split over the contraction:
 the first split's workgroups carry the term in their partial), rows whose magnitudes span 1e-20 .. 1e6 (the activation row
 scale the term is divided by before it joins the accumulator), and 1 and 3 precision passes.
@@ -64,6 +65,8 @@ CASES = [
     (1, 300, 512, 768, 16, 3),
     (1, 200, 512, 768, 48, 3),
     (1, 130, 256, 1024, 64, 1),
+    (1, 2048, 2048, 2048, 48, 3),  # rank above 32 on 128x128x64 tiles (256 of them)
+    (1, 2048, 2048, 2048, 64, 1),  # one-plane staging holds 32: back to 64x64
     (1, 64, 4096, 256, 16, 3),  # narrow output, long contraction: split-K
     (1, 64, 4096, 256, 32, 1),
 ]
