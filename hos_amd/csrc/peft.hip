@@ -40,6 +40,7 @@ struct LayerW {
   float *q_norm = nullptr, *k_norm = nullptr;     // OLMoE QK-norm weights [qd], [kvd]
   float* router = nullptr;                        // MoE router [E][d] (f32, ffn_gate_inp.weight)
   QWeight xg, xu, xd;                             // MoE experts, stacked [E·F][d], [E·F][d], [E·d][F]
+  QWeight xgu;  // MoE gate|up interleaved per expert, [E·2F][d]: expert e's gate rows then its up rows
   // q|k|v and gate|up stacked row-wise (same encoding and width), each group one GEMM; the q|k|v biases
   // concatenated. Absent when the parts differ in encoding.
   QWeight qkv, gu;
@@ -431,8 +432,10 @@ struct hos_peft {
       LayerW& w = lw[l];
       free_qweight(w.qkv);
       free_qweight(w.gu);
+      free_qweight(w.xgu);
       stack(w.qkv, {&w.w[TQ], &w.w[TK], &w.w[TV]});
       if (!E) stack(w.gu, {&w.w[TG], &w.w[TU]});
+      if (E) stack_experts(w.xgu, w.xg, w.xu);
       if (c.attn_bias && w.bias[0] && w.bias[1] && w.bias[2]) {
         if (!w.bias_qkv) w.bias_qkv = alloc<float>((size_t)W3);
         HOS_HIP_CHECK(hipMemcpyAsync(w.bias_qkv, w.bias[0], (size_t)qd * 4, hipMemcpyDeviceToDevice, st));
@@ -442,6 +445,28 @@ struct hos_peft {
     }
     HOS_HIP_CHECK(hipStreamSynchronize(st));
     stacks_dirty = false;
+  }
+  // Per-expert row interleave of two expert stacks of one encoding and width ([E·F][d] each): expert e's rows of a,
+  // then its rows of b (the q and s arrays are row-major, so each expert's block of rows is one contiguous run of
+  // each array); left empty unless both are present and alike.
+  void stack_experts(QWeight& out, const QWeight& a, const QWeight& b) {
+    if (!a.q || !b.q || a.type != b.type || a.cols != b.cols || a.rows != b.rows || a.rows % E != 0) return;
+    out.type = a.type;
+    out.rows = 2 * a.rows;
+    out.cols = a.cols;
+    qweight_sizes(out.type, out.rows, out.cols, &out.q_bytes, &out.s_bytes);
+    HOS_HIP_CHECK(hipMalloc(&out.q, out.q_bytes));
+    HOS_HIP_CHECK(hipMalloc((void**)&out.s, out.s_bytes > 0 ? out.s_bytes : 256));
+    const size_t qe = a.q_bytes / E, se = a.s_bytes / E;  // one expert's bytes of each array
+    for (int e = 0; e < E; e++)
+      for (int h = 0; h < 2; h++) {
+        const QWeight& src = h ? b : a;
+        HOS_HIP_CHECK(hipMemcpyAsync((uint8_t*)out.q + (2 * e + h) * qe, (const uint8_t*)src.q + e * qe, qe,
+                                     hipMemcpyDeviceToDevice, st));
+        if (se > 0)
+          HOS_HIP_CHECK(hipMemcpyAsync((uint8_t*)out.s + (2 * e + h) * se, (const uint8_t*)src.s + e * se, se,
+                                       hipMemcpyDeviceToDevice, st));
+      }
   }
   // Row-wise concatenation of repacked weights (their q and s arrays are row-major, so the stack is the
   // concatenation of each array); left empty unless every part is present with one encoding and width.
@@ -607,8 +632,12 @@ struct hos_peft {
       launch_moe_plan(a.counts, E, a.offsets, a.tiles, max_tiles, st);
       launch_moe_gather(hs, d, a.sel_e, a.slot, a.offsets, M, K, d, a.pos, hx, d, st);
     }
-    grouped(false, w.xg, hx, d, a.tiles, a.gug, 2LL * F, 0, M, pf);
-    grouped(false, w.xu, hx, d, a.tiles, a.gug + F, 2LL * F, 0, M, pf);
+    if (w.xgu.q) {  // gate|up of every expert in one launch
+      grouped(false, w.xgu, hx, d, a.tiles, a.gug, 2LL * F, 0, M, pf);
+    } else {
+      grouped(false, w.xg, hx, d, a.tiles, a.gug, 2LL * F, 0, M, pf);
+      grouped(false, w.xu, hx, d, a.tiles, a.gug + F, 2LL * F, 0, M, pf);
+    }
     {
       Scope s(this, "swiglu", 0, 8.0 * P * F + 2.0 * P * F);
       launch_swiglu_fwd(a.gug, (int)P, F, nullptr, hx, st);
@@ -640,8 +669,12 @@ struct hos_peft {
       Scope s(this, "swiglu", 0, 4.0 * P * F * 3 + 4.0 * P * F);
       launch_swiglu_bwd(a.gug, mdH, (int)P, F, nullptr, hx, st);
     }
-    grouped(true, w.xg, hx, 2LL * F, a.tiles, mdX, d, 0, M, pd);
-    grouped(true, w.xu, h16_offset(hx, F), 2LL * F, a.tiles, mdX, d, 1, M, pd);
+    if (w.xgu.q) {  // d(gate|up) against the interleaved stack: one contraction over 2F
+      grouped(true, w.xgu, hx, 2LL * F, a.tiles, mdX, d, 0, M, pd);
+    } else {
+      grouped(true, w.xg, hx, 2LL * F, a.tiles, mdX, d, 0, M, pd);
+      grouped(true, w.xu, h16_offset(hx, F), 2LL * F, a.tiles, mdX, d, 1, M, pd);
+    }
     {
       Scope s(this, "moe_route", 2.0 * M * d * E, 4.0 * (P * d + 2.0 * M * d + (double)E * d + 3.0 * M * E));
       launch_moe_router_bwd(a.pfull, mdp, a.sel_e, M, E, K, mdl, st);
@@ -1279,6 +1312,7 @@ struct hos_peft {
       for (auto& w : l.w) free_qweight(w);
       free_qweight(l.xg);
       free_qweight(l.xu);
+      free_qweight(l.xgu);
       free_qweight(l.xd);
       free_qweight(l.qkv);
       free_qweight(l.gu);
