@@ -873,7 +873,7 @@ struct hos_peft {
       }
       if (c.qk_norm) to16(dq, W3, M, W3);
       lora_grad_b(l, 0, dq, W3, W3, M, hs_in());
-      if (w.qkv.q && group_uniform(0) && gcount(0) * r <= 64) {
+      if (w.qkv.q && group_uniform(0) && gcount(0) * r <= 128) {
         // one dX GEMM over the stacked q|k|v contraction, the three LoRA terms as one rank-3r update
         qdx(w.qkv, hs, W3, M, dxn, d, 0, stacked_down_epi(l, 0), tpd[TQ]);
       } else {

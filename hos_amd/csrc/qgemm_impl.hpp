@@ -530,20 +530,24 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
   // over the LDS banks.
   // (split contraction: the first split's workgroups carry the rank-r term in their partial; U is pre-divided by
   // the row's power-of-two rinv, so the reduction's (Σ partials)·rinv is exactly the unsplit result's form)
+  // Ranks above the staging's capacity (G::RCAP) run in chunks of that many ranks, one staging and product per chunk.
   const int rank = (split && zsp != 0) ? 0 : epi.rank;
-  const int rpad = (rank + 15) & ~15;
-  const int nch = rpad >> 3, swz = (nch & (nch - 1)) ? 1 : nch - 1;
-  auto sidx = [&](int row, int q) { return row * rpad + ((((q >> 3) ^ (row & swz))) << 3) + (q & 7); };
-  __bf16* Uh = (__bf16*)smem;
-  __bf16* Ul = Uh + BM * rpad;
-  __bf16* Lh = Ul + BM * rpad;
-  __bf16* Ll = Lh + BN * rpad;
-  if (rank > 0) {
+  for (int rc0 = 0; rc0 < rank; rc0 += G::RCAP) {
+    const int rn = min(G::RCAP, rank - rc0);
+    const int rpad = (rn + 15) & ~15;
+    const int nch = rpad >> 3, swz = (nch & (nch - 1)) ? 1 : nch - 1;
+    auto sidx = [&](int row, int q) { return row * rpad + ((((q >> 3) ^ (row & swz))) << 3) + (q & 7); };
+    __bf16* Uh = (__bf16*)smem;
+    __bf16* Ul = Uh + BM * rpad;
+    __bf16* Lh = Ul + BM * rpad;
+    __bf16* Ll = Lh + BN * rpad;
+    if (rc0 > 0) __syncthreads();  // every wave is done reading the previous chunk
     // a tile never straddles a column segment (the launcher picks BN to divide the boundaries)
-    const float* Ub = epi.U + (epi.ustep ? epi.ustep * ((n0 >= epi.ub0) + (n0 >= epi.ub1)) : 0);
+    const float* Ub = epi.U + (epi.ustep ? epi.ustep * ((n0 >= epi.ub0) + (n0 >= epi.ub1)) : 0) + rc0;
+    const float* Lb = epi.L + (long long)rc0 * epi.slj;
     for (int e = tid; e < BM * rpad; e += G::NT) {
       const int rr = e / rpad, jj = e % rpad, row = m0 + rr;
-      const float x = (row < M && jj < rank) ? Ub[(long long)row * epi.ldu + jj] / rinv[row] : 0.0f;
+      const float x = (row < M && jj < rn) ? Ub[(long long)row * epi.ldu + jj] / rinv[row] : 0.0f;
       const __bf16 h = (__bf16)x;
       Uh[sidx(rr, jj)] = h;
       Ul[sidx(rr, jj)] = (__bf16)(x - (float)h);
@@ -551,7 +555,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
     for (int e = tid; e < rpad * BN; e += G::NT) {
       const int jj = e / BN, cc = e % BN, col = n0 + cc;
       const float x =
-          (col < Nout && jj < rank) ? epi.L[(long long)jj * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
+          (col < Nout && jj < rn) ? Lb[(long long)jj * epi.slj + (long long)col * epi.sln] * epi.scale : 0.0f;
       const __bf16 h = (__bf16)x;
       Lh[sidx(cc, jj)] = h;
       Ll[sidx(cc, jj)] = (__bf16)(x - (float)h);
@@ -801,8 +805,6 @@ void launch_splitk_reduce(const float* ws, int splits, long long M, int N, const
 template <uint32_t QT, bool DX, int BM, int BN, int BK, int NP>
 void launch_shape(const QWeight& w, H16 a, long long lda, long long M, int Nout, int C, int per, int splits,
                   GemmEpi epi, float* ws, hipStream_t st) {
-  constexpr int rcap = Geo<BM, BN, BK, DX, NP>::RCAP;
-  HOS_REQUIRE(epi.rank <= rcap, HOS_E_INVALID, "qgemm: fused rank exceeds the tile's staging");
   HOS_REQUIRE(!epi.rstat || (BN == 128 && splits == 1 &&
                              Geo<BM, BN, BK, DX, NP>::SMEM * 2 >= Geo<BM, BN, BK, DX, NP>::NT / 64 * 32 * 40 * 4),
               HOS_E_INVALID, "qgemm: row statistics need the staged epilogue on unsplit 128-column tiles");
@@ -821,7 +823,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   HOS_REQUIRE((lda % 8) == 0, HOS_E_INVALID, "qgemm: activation row stride must be a multiple of 8");
   HOS_REQUIRE((NP != 2 && NP != 3 && NP != 5) || a.lo != nullptr, HOS_E_INVALID,
               "qgemm: activation-split precision needs the operand residual");
-  HOS_REQUIRE(epi.rank >= 0 && epi.rank <= 64, HOS_E_INVALID, "qgemm: fused rank-r update supports r <= 64");
+  HOS_REQUIRE(epi.rank >= 0 && epi.rank <= 128, HOS_E_INVALID, "qgemm: fused rank-r update supports r <= 128");
   // Tile choice: the largest tile that still gives ~1.25 waves of workgroups over the 256 CUs; only when
   // even 64×64 tiles leave the chip idle is the contraction split (deterministic reduction after).
   auto ntiles = [&](int bm, int bn) { return ceil_div(M, bm) * ceil_div(Nout, bn); };
@@ -868,11 +870,11 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bn = 128;
     bk = 32;
   }
-  // A fused rank above 32 (stacked q|k|v dX): no split, and a tile whose LDS holds the rank staging — 128×128×64
-  // where its tiles alone give every CU one (their staging holds rank 64 in the two-plane modes; OLMoE's q|k|v dX,
-  // 2048 × 2048 × 6144 at rank 48: 254 µs on 64×64 tiles), else 64×64.
+  // A fused rank above 32 (stacked q|k|v dX): no split, and 128×128×64 tiles where they alone give every CU one
+  // (OLMoE's q|k|v dX, 2048 × 2048 × 6144 at rank 48: 254 µs on 64×64 tiles), else 64×64 (whose staging holds rank 64
+  // in one chunk).
   if (epi.rank > 32) {
-    if (C % 64 == 0 && epi.rank <= Geo<128, 128, 64, DX, NP>::RCAP && ntiles(128, 128) >= 256) {
+    if (C % 64 == 0 && ntiles(128, 128) >= 256) {
       bm = 128;
       bn = 128;
       bk = 64;

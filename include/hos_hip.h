@@ -89,8 +89,7 @@ int hos_hip_qgemm_dx_dev(hos_ctx* ctx, uint64_t key, const float* dy_dev, size_t
 /* A frozen-base GEMM with its LoRA term fused in the epilogue — the adapted linear of src/peft.rs:508-512
  * (base + s·(x·A)·B) and its input gradient (dY·W + du·Aᵀ): out[t, N] = op(in, deq(W)) + scale·U·L with
  * which 0: op = in·deq(W)ᵀ (N = rows), 1: op = in·deq(W) (N = cols); U [t, rank] with row stride ldu,
- * L(j, n) = l[j·slj + n·sln]. Device pointers; rank <= 64, and a rank above 32 needs a contraction that is a
- * multiple of 64. */
+ * L(j, n) = l[j·slj + n·sln]. Device pointers; 1 <= rank <= 128. */
 int hos_hip_qgemm_lora_dev(hos_ctx* ctx, int which, uint64_t key, const float* in_dev, size_t t, const float* u_dev,
                            size_t ldu, const float* l_dev, size_t slj, size_t sln, int rank, float scale,
                            float* out_dev);

@@ -8,8 +8,8 @@ term); the test makes it as large as the base term, so a dropped or misplaced ra
 1e-5 bar by orders of magnitude.
 
 Cases: ragged row counts (not a multiple of any tile), an output width that is not a multiple of the tile
-(forward), ranks 16 / 20 (zero-padded to 32) / 48 / 64 (the stacked q|k|v dX, on 64×64 and, with 256 output tiles,
-128×128×64 tiles), L read through both stride
+(forward), ranks 16 / 20 (zero-padded to 32) / 48 / 64 / 96 (the stacked q|k|v dX, on 64×64 and, with 256 output
+tiles, 128×128×64 tiles; ranks above a tile's LDS staging in chunks), L read through both stride
 orders (B [r, N] rows, A [N, r] transposed), a narrow output with a long contraction (split over the contraction:
 the first split's workgroups carry the term in their partial), rows whose magnitudes span 1e-20 .. 1e6 (the activation row
 scale the term is divided by before it joins the accumulator), and 1 and 3 precision passes.
@@ -66,7 +66,10 @@ CASES = [
     (1, 200, 512, 768, 48, 3),
     (1, 130, 256, 1024, 64, 1),
     (1, 2048, 2048, 2048, 48, 3),  # rank above 32 on 128x128x64 tiles (256 of them)
-    (1, 2048, 2048, 2048, 64, 1),  # one-plane staging holds 32: back to 64x64
+    (1, 2048, 2048, 2048, 64, 1),  # rank 64 in two staged chunks of 32 (one-plane 128x128x64 staging)
+    (1, 300, 768, 512, 96, 3),  # rank 96 (Llama-3.2-1B's stacked q|k|v dX): chunks of 64 + 32 on 64x64 tiles
+    (1, 2048, 3072, 2048, 96, 3),  # ... and on 128x128x64 tiles
+    (1, 100, 544, 512, 48, 3),  # contraction not a multiple of 64: 32-deep slabs, chunks of 32 + 16
     (1, 64, 4096, 256, 16, 3),  # narrow output, long contraction: split-K
     (1, 64, 4096, 256, 32, 1),
 ]
@@ -126,12 +129,12 @@ def test_qgemm_lora_term_alone(gpu):
 def test_qgemm_lora_rejects_bad_rank(gpu):
     g = gpu
     g.upload_quant(0x1C00, o.quantize(np.zeros((64, 256), np.float32), Q8_0), Q8_0, 64, 256)
-    X, U, L = g.to_dev(np.zeros((4, 256), np.float32)), g.to_dev(np.zeros((4, 80), np.float32)), \
-        g.to_dev(np.zeros((80, 64), np.float32))
+    X, U, L = g.to_dev(np.zeros((4, 256), np.float32)), g.to_dev(np.zeros((4, 140), np.float32)), \
+        g.to_dev(np.zeros((140, 64), np.float32))
     OUT = g.empty_dev((4, 64), fill=0.0)
-    for rank in (0, 65):
+    for rank in (0, 129):
         with pytest.raises(Exception):
-            g.op("qgemm_lora_dev", 0, 0x1C00, X, 4, U, 80, L, 64, 1, rank, 1.0, OUT)
+            g.op("qgemm_lora_dev", 0, 0x1C00, X, 4, U, 140, L, 64, 1, rank, 1.0, OUT)
     for a in (X, U, L, OUT):
         a.free()
     g.evict(0x1C00)
