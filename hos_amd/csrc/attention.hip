@@ -360,9 +360,10 @@ __global__ void __launch_bounds__(256 * NG) attn_fwd_kernel(const __bf16* __rest
         bf8 ph, pl;
         split8(p + 8 * t, 1.0f, ph, pl);
 #pragma unroll
-        for (int i = 0; i < C::NC; i++)
-          O[i] = mma3_bf16(tr_frag<HD>(st + 2 * C::TILE, t, i, lane), tr_frag<HD>(st + 3 * C::TILE, t, i, lane), ph,
-                           pl, O[i]);
+        for (int i = 0; i < C::NC; i += 2)
+          mma3_bf16_x2(tr_frag<HD>(st + 2 * C::TILE, t, i, lane), tr_frag<HD>(st + 3 * C::TILE, t, i, lane), ph, pl,
+                       O[i], tr_frag<HD>(st + 2 * C::TILE, t, i + 1, lane), tr_frag<HD>(st + 3 * C::TILE, t, i + 1, lane),
+                       ph, pl, O[i + 1]);
       }
     }
     if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(0);
@@ -478,11 +479,9 @@ __global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restr
 #pragma unroll
       for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
 #pragma unroll
-      for (int t = 0; t < C::NS; t++) {
-        S = mma3_bf16(row_frag<HD>(st, t, lane), row_frag<HD>(st + C::TILE, t, lane), Qh[t], Ql[t], S);
-        dP = mma3_bf16(row_frag<HD>(st + 2 * C::TILE, t, lane), row_frag<HD>(st + 3 * C::TILE, t, lane), Dh[t], Dl[t],
-                       dP);
-      }
+      for (int t = 0; t < C::NS; t++)
+        mma3_bf16_x2(row_frag<HD>(st, t, lane), row_frag<HD>(st + C::TILE, t, lane), Qh[t], Ql[t], S,
+                     row_frag<HD>(st + 2 * C::TILE, t, lane), row_frag<HD>(st + 3 * C::TILE, t, lane), Dh[t], Dl[t], dP);
       const int k0 = kb * TB;
       float ds[16];
 #pragma unroll
@@ -497,8 +496,9 @@ __global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restr
         bf8 sh, sl;
         split8(ds + 8 * t, 1.0f, sh, sl);
 #pragma unroll
-        for (int i = 0; i < C::NC; i++)
-          A[i] = mma3_bf16(tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, A[i]);
+        for (int i = 0; i < C::NC; i += 2)
+          mma3_bf16_x2(tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, A[i],
+                       tr_frag<HD>(st, t, i + 1, lane), tr_frag<HD>(st + C::TILE, t, i + 1, lane), sh, sl, A[i + 1]);
       }
     }
     if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(0);
@@ -602,11 +602,9 @@ __global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __res
 #pragma unroll
       for (int r = 0; r < 16; r++) S[r] = dP[r] = 0.0f;
 #pragma unroll
-      for (int t = 0; t < C::NS; t++) {
-        S = mma3_bf16(row_frag<HD>(st, t, lane), row_frag<HD>(st + C::TILE, t, lane), Kh[t], Kl[t], S);
-        dP = mma3_bf16(row_frag<HD>(st + 2 * C::TILE, t, lane), row_frag<HD>(st + 3 * C::TILE, t, lane), Vh[t], Vl[t],
-                       dP);
-      }
+      for (int t = 0; t < C::NS; t++)
+        mma3_bf16_x2(row_frag<HD>(st, t, lane), row_frag<HD>(st + C::TILE, t, lane), Kh[t], Kl[t], S,
+                     row_frag<HD>(st + 2 * C::TILE, t, lane), row_frag<HD>(st + 3 * C::TILE, t, lane), Vh[t], Vl[t], dP);
       // S[r] = score(query q0 + κ(r, hl), key mykey); LSE and D of those queries from LDS (4 runs of 4)
       const int q0 = qt * TB;
       float Lr[16], Dr[16];
@@ -632,11 +630,9 @@ __global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __res
         split8(p + 8 * t, 1.0f, ph, pl);
         split8(ds + 8 * t, 1.0f, sh, sl);
 #pragma unroll
-        for (int i = 0; i < C::NC; i++) {
-          dV[i] = mma3_bf16(tr_frag<HD>(st + 2 * C::TILE, t, i, lane), tr_frag<HD>(st + 3 * C::TILE, t, i, lane), ph, pl,
-                            dV[i]);
-          dK[i] = mma3_bf16(tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, dK[i]);
-        }
+        for (int i = 0; i < C::NC; i++)
+          mma3_bf16_x2(tr_frag<HD>(st + 2 * C::TILE, t, i, lane), tr_frag<HD>(st + 3 * C::TILE, t, i, lane), ph, pl,
+                       dV[i], tr_frag<HD>(st, t, i, lane), tr_frag<HD>(st + C::TILE, t, i, lane), sh, sl, dK[i]);
       }
     }
     if constexpr (ATT_PRIO) __builtin_amdgcn_s_setprio(0);

@@ -32,6 +32,18 @@ __device__ __forceinline__ f16v mma3_bf16(const bf8& ah, const bf8& al, const bf
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, c, 0, 0, 0);
 }
 
+// Two independent three-product updates with their passes interleaved, so consecutive MFMAs never depend on each
+// other; each accumulator receives the same products in the same order as two mma3_bf16 calls.
+__device__ __forceinline__ void mma3_bf16_x2(const bf8& ah0, const bf8& al0, const bf8& bh0, const bf8& bl0, f16v& c0,
+                                             const bf8& ah1, const bf8& al1, const bf8& bh1, const bf8& bl1, f16v& c1) {
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al0, bh0, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al1, bh1, c1, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bl0, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bl1, c1, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bh0, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bh1, c1, 0, 0, 0);
+}
+
 // Host-side error carrying a HOS_E_* status code across the C ABI.
 struct Error : std::runtime_error {
   int code;
