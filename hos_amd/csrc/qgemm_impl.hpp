@@ -571,19 +571,36 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
       Ll[sidx(cc, jj)] = (__bf16)(x - (float)h);
     }
     __syncthreads();
+    // per 16 ranks: each tile's three products (lo·hi, hi·lo, hi·hi, as mma3_bf16) issued pass by pass across the
+    // tiles, the fragments read once for all tiles of their row or column
+    for (int k0 = 0; k0 < rpad; k0 += 16) {
+      const int k = k0 + 8 * (lane >> 5);
+      bf8 ah[G::TM], al[G::TM], bh[G::TN], bl[G::TN];
 #pragma unroll
-    for (int i = 0; i < G::TM; i++)
+      for (int i = 0; i < G::TM; i++) {
+        const int ra = wm * (BM / G::WGM) + 32 * i + (lane & 31);
+        ah[i] = *(const bf8*)(Uh + sidx(ra, k));
+        al[i] = *(const bf8*)(Ul + sidx(ra, k));
+      }
 #pragma unroll
       for (int j = 0; j < G::TN; j++) {
-        const int ra = wm * (BM / G::WGM) + 32 * i + (lane & 31);
         const int rb = wn * (BN / 2) + 32 * j + (lane & 31);
-        for (int k0 = 0; k0 < rpad; k0 += 16) {
-          const int k = k0 + 8 * (lane >> 5);
-          const bf8 ah = *(const bf8*)(Uh + sidx(ra, k)), al = *(const bf8*)(Ul + sidx(ra, k));
-          const bf8 bh = *(const bf8*)(Lh + sidx(rb, k)), bl = *(const bf8*)(Ll + sidx(rb, k));
-          acc[i][j] = mma3_bf16(ah, al, bh, bl, acc[i][j]);
-        }
+        bh[j] = *(const bf8*)(Lh + sidx(rb, k));
+        bl[j] = *(const bf8*)(Ll + sidx(rb, k));
       }
+#pragma unroll
+      for (int i = 0; i < G::TM; i++)
+#pragma unroll
+        for (int j = 0; j < G::TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < G::TM; i++)
+#pragma unroll
+        for (int j = 0; j < G::TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < G::TM; i++)
+#pragma unroll
+        for (int j = 0; j < G::TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+    }
   }
   // Output stores. Each 32×32 tile goes through a per-wave LDS transpose and leaves as row-major float4 runs
   // (8 lanes per 128-byte row piece): a quarter of the store instructions of the MFMA layout's one-float-per-lane
