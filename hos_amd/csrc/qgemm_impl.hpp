@@ -488,29 +488,47 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
       // different tiles (each accumulator receives the same products in the same order as tile-major issue, which
       // put a tile's three dependent passes back to back: the step +0.9%, 4096³ 3-pass dX −2%)
       const int cb = NPASS * (kk / 16);
-      if constexpr (BLO)
+      auto pass_blo = [&]() {
+        if constexpr (BLO)
+#pragma unroll
+          for (int i = 0; i < G::TM; i++)
+#pragma unroll
+            for (int j = 0; j < G::TN; j++) {
+              f16v& t = accs[(cb + 2) % NACC][i][j];
+              t = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], t, 0, 0, 0);
+            }
+      };
+      auto pass_alo = [&]() {
+        if constexpr (ALO)
+#pragma unroll
+          for (int i = 0; i < G::TM; i++)
+#pragma unroll
+            for (int j = 0; j < G::TN; j++) {
+              f16v& t = accs[(cb + 1) % NACC][i][j];
+              t = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], t, 0, 0, 0);
+            }
+      };
+      auto pass_hi = [&]() {
 #pragma unroll
         for (int i = 0; i < G::TM; i++)
 #pragma unroll
           for (int j = 0; j < G::TN; j++) {
-            f16v& t = accs[(cb + 2) % NACC][i][j];
-            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], t, 0, 0, 0);
+            f16v& t = accs[cb % NACC][i][j];
+            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], t, 0, 0, 0);
           }
-      if constexpr (ALO)
-#pragma unroll
-        for (int i = 0; i < G::TM; i++)
-#pragma unroll
-          for (int j = 0; j < G::TN; j++) {
-            f16v& t = accs[(cb + 1) % NACC][i][j];
-            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], t, 0, 0, 0);
-          }
-#pragma unroll
-      for (int i = 0; i < G::TM; i++)
-#pragma unroll
-        for (int j = 0; j < G::TN; j++) {
-          f16v& t = accs[cb % NACC][i][j];
-          t = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], t, 0, 0, 0);
-        }
+      };
+      if constexpr (NACC == 4) {
+        // the passes of a k-step go to chains cb, cb + 1, cb + 2 (mod 4), all distinct: issued in that order they
+        // cycle through the four sets (the longest distance between dependent MFMAs; the same products per set in
+        // the same order either way)
+        pass_hi();
+        pass_alo();
+        pass_blo();
+      } else {
+        pass_blo();
+        pass_alo();
+        pass_hi();
+      }
     }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     if (more) {
