@@ -553,16 +553,25 @@ __global__ void __launch_bounds__(64 * R16_NW) lora_rows16_kernel(int M, int K, 
         bl[u][jt] = in ? *reinterpret_cast<const h8l*>(bt.lo + bbase[jt] + kk) : z8;
       }
     }
+    // the three products of each tile issued pass by pass across the tiles (consecutive MFMAs independent)
 #pragma unroll
-    for (int u = 0; u < U; u++)
+    for (int u = 0; u < U; u++) {
 #pragma unroll
       for (int t = 0; t < RT; t++)
 #pragma unroll
-        for (int jt = 0; jt < NJ; jt++) {
+        for (int jt = 0; jt < NJ; jt++)
           acc[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[u][t], bh[u][jt], acc[t][jt], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int jt = 0; jt < NJ; jt++)
           acc[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u][t], bl[u][jt], acc[t][jt], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int jt = 0; jt < NJ; jt++)
           acc[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u][t], bh[u][jt], acc[t][jt], 0, 0, 0);
-        }
+    }
   }
   // element (row 16t+4q+i, col 16jt+p): the operand's row scale and the factor row's scale
 #pragma unroll
