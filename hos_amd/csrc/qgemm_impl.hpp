@@ -90,15 +90,25 @@ struct Run {
   bool ok;
 };
 
+// Where the run starting at element e (row-major over W) lives: its byte offset in q and its float offset in s.
+// Both are linear in e, so a run's address splits into a per-thread part and a slab part (e a multiple of 32 there).
+template <uint32_t QT>
+__device__ __forceinline__ long long run_qoff(long long e) {
+  return QT == GGUF_Q4_K ? (e >> 1) : e * elem_bytes<QT>();
+}
+template <uint32_t QT>
+__device__ __forceinline__ long long run_soff(long long e) {
+  if constexpr (QT == GGUF_Q4_K || QT == GGUF_Q5_K) return 2 * (e >> 5);  // a float2 per 32 values
+  else if constexpr (QT == GGUF_Q8_0) return e >> 5;
+  else if constexpr (QT == GGUF_Q6_K) return e >> 4;
+  else return 0;  // unscaled types
+}
+
+// Load the run at q bytes qp and scales sp (as run_qoff / run_soff place them).
 template <uint32_t QT, int E>
-__device__ __forceinline__ void run_load(const QWeightView& w, long long row, int col, bool ok, Run<QT, E>& r) {
-  r.ok = ok;
-  if (!ok) {
-    row = 0;
-    col = 0;
-  }
-  const long long e = row * w.cols + col;
-  const uint32_t* src = (const uint32_t*)((const uint8_t*)w.q + (QT == GGUF_Q4_K ? (e >> 1) : e * elem_bytes<QT>()));
+__device__ __forceinline__ void run_load(const uint8_t* qp, const float* sp, Run<QT, E>& r) {
+  r.ok = true;
+  const uint32_t* src = (const uint32_t*)qp;
   if constexpr (Run<QT, E>::NW == 1) {
     r.q[0] = src[0];
   } else if constexpr (Run<QT, E>::NW == 2) {
@@ -116,14 +126,14 @@ __device__ __forceinline__ void run_load(const QWeightView& w, long long row, in
     }
   }
   if constexpr (QT == GGUF_Q4_K || QT == GGUF_Q5_K) {
-    r.s[0] = ((const float2*)w.s)[e >> 5];
+    r.s[0] = *(const float2*)sp;
   } else if constexpr (QT == GGUF_F16 || QT == GGUF_BF16 || QT == GGUF_F32) {
     // unscaled: the stored value is the weight
   } else if constexpr (QT == GGUF_Q8_0) {
-    r.s[0].x = w.s[e >> 5];
+    r.s[0].x = sp[0];
   } else {
-    r.s[0].x = w.s[e >> 4];
-    if constexpr (E > 16) r.s[1].x = w.s[(e >> 4) + 1];
+    r.s[0].x = sp[0];
+    if constexpr (E > 16) r.s[1].x = sp[1];
   }
 }
 
@@ -336,8 +346,19 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
   };
   float scur[ICODE ? G::TN * G::NSB : 1];  // the scales of the slab in LDS
   Regs R0, R1;
-  // this thread's B run: tile row br, first column bc
+  // this thread's B run: tile row br, first column bc. Its element index at slab 0, e0, is fixed for the launch; a
+  // run past the last output column is clamped into the weight (it only feeds columns that are never stored).
   const int br = tid / G::TPR, bc = G::E * (tid % G::TPR);
+  long long e0;
+  if constexpr (DX) {
+    const int col = n0 + bc;  // output column run; rows are the contraction
+    e0 = (long long)br * w.cols + (col < w.cols ? col : 0);
+  } else {
+    const long long row = n0 + br;  // W row = output column; run along the contraction
+    e0 = (row < w.rows ? row : 0) * w.cols + bc;
+  }
+  const uint8_t* const bq = (const uint8_t*)w.q + run_qoff<QT>(e0);
+  const float* const bs_ = w.s + run_soff<QT>(e0);
 
   auto load = [&](Regs& R, int c0) {
 #pragma unroll
@@ -352,12 +373,10 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
       R.a[v] = *(const h8*)(A + offc);
       if constexpr (ALO) R.al[v] = *(const h8*)(Alo + offc);
     }
-    if constexpr (DX) {
-      const int col = n0 + bc;  // output column run; rows are the contraction
-      run_load<QT, G::E>(w, c0 + br, col, col < w.cols, R.b);
-    } else {
-      const long long row = n0 + br;  // W row = output column; run along the contraction
-      run_load<QT, G::E>(w, row, c0 + bc, row < w.rows, R.b);
+    {
+      // the slab part of the run's element index: c0 rows further (dX) or c0 columns further (forward)
+      const long long se = DX ? (long long)c0 * w.cols : (long long)c0;
+      run_load<QT, G::E>(bq + run_qoff<QT>(se), bs_ + run_soff<QT>(se), R.b);
     }
     if constexpr (ICODE) {
 #pragma unroll
