@@ -5,8 +5,9 @@
 //   dx : dX[M, K] = dY[M, N] · deq(W)   W [N, K]  — the frozen-base backward g·Bᵀ
 //        (src/tensor.rs:316-327 and :347-360; src/peft.rs:24-33 transposes W to [in,out])
 //
-// Each BK-deep slab of the contraction streams the packed weight from HBM, dequantizes it in registers
-// with the bit-exact device functions of kernels.hpp and stores it row-major in LDS exactly as the rows
+// Each BK-deep slab of the contraction streams the packed weight from HBM, dequantizes it in registers to
+// the same f32 values as the device functions of kernels.hpp (run_store: codes as fp16 subnormals into
+// mixed-precision fmas, or packed fp16 for Q8_0) and stores it row-major in LDS exactly as the rows
 // arrive (a run of E consecutive values per thread, one coalesced load, one vector LDS store):
 //   fwd: W rows are output columns, runs go along the contraction → B fragments are plain 128-bit reads;
 //   dx:  W rows are the contraction, runs go along the output → B fragments are read transposed with
@@ -45,33 +46,6 @@ typedef short s4v __attribute__((ext_vector_type(4)));
 
 // (exp_rs, the e^x of the softmax statistics folded in the epilogue, is in kernels.hpp: the cross-entropy pass
 // that consumes them uses it too.)
-
-// Signed byte i of a word as float (one bit-field extract + one convert).
-__device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
-// Unsigned byte i as float (maps to v_cvt_f32_ubyte<i>).
-__device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
-
-// Four consecutive dequantized values from one packed source: Q4_K a 16-bit half-word (4 nibbles),
-// Q8_0/Q6_K/Q5_K a 32-bit word (4 int8 / 4 uint8 codes). Same arithmetic as deq_q4k / deq_q8 / deq_q6k.
-template <uint32_t QT>
-__device__ __forceinline__ void deq4(uint32_t src, float2 s, float* v) {
-  if constexpr (QT == GGUF_Q4_K) {
-    const uint32_t lo = src & 0x0F0Fu, hi = (src >> 4) & 0x0F0Fu;  // nibbles of cols 0,2 | 1,3
-    v[0] = deq_q4k_f(ubyte(lo, 0), s);
-    v[1] = deq_q4k_f(ubyte(hi, 0), s);
-    v[2] = deq_q4k_f(ubyte(lo, 1), s);
-    v[3] = deq_q4k_f(ubyte(hi, 1), s);
-  } else if constexpr (QT == GGUF_Q5_K) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = deq_q4k_f(ubyte(src, i), s);
-  } else if constexpr (QT == GGUF_Q8_0) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = __fmul_rn(sbyte(src, i), s.x);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = __fmul_rn(s.x, sbyte(src, i));
-  }
-}
 
 // Bytes per element of a device weight layout (Q4_K: two per byte).
 template <uint32_t QT>
@@ -204,18 +178,57 @@ __device__ __forceinline__ void run_store(const Run<QT, E>& r, _Float16* dst, in
       } else {
         const float2 sc = (QT == GGUF_Q6_K && v >= 2) ? r.s[1] : r.s[0];
         if constexpr (QT == GGUF_Q4_K) {
-          deq4<QT>(r.q[v] & 0xffffu, sc, f);
-          deq4<QT>(r.q[v] >> 16, sc, f + 4);
+          // Value j of the word sits in bits 4j..4j+3. Masked into the low bits of an fp16 half, a code q is
+          // the subnormal q·2^-24 (exact), and (float) of it is exact too, so with d' = d·2^24 (exact)
+          // fma(d', q·2^-24, -m) rounds the same real number as fma(d, q, -m): the identical f32 value,
+          // from one mixed-precision fma per value and four masks per eight.
+          const uint32_t w = r.q[v];
+          const float dd = sc.x * 16777216.0f;
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const uint32_t p = (w >> (4 * j)) & 0x000F000Fu;
+            h2 x;
+            __builtin_memcpy(&x, &p, 4);
+            f[j] = __builtin_fmaf(dd, (float)x[0], -sc.y);
+            f[j + 4] = __builtin_fmaf(dd, (float)x[1], -sc.y);
+          }
         } else {
-          deq4<QT>(r.q[2 * v], sc, f);
-          deq4<QT>(r.q[2 * v + 1], sc, f + 4);
+          // Byte codes, the same way: Q5_K's 0..31 with fma(d', q·2^-24, -m); Q6_K's signed q (-32..31) as
+          // u = q + 32 = (byte ^ 0x20) & 0x3F with fma(d', u·2^-24, -32·d), which rounds the real d·q once,
+          // as d·q itself does (-32·d is exact).
+          const float dd = sc.x * 16777216.0f;
+          const float c = QT == GGUF_Q5_K ? -sc.y : -32.0f * sc.x;
+#pragma unroll
+          for (int wv = 0; wv < 2; wv++) {
+            uint32_t w = r.q[2 * v + wv];
+            if constexpr (QT == GGUF_Q6_K) w = (w ^ 0x20202020u) & 0x3F3F3F3Fu;
+            const uint32_t p0 = w & 0x00FF00FFu, p1 = (w >> 8) & 0x00FF00FFu;  // bytes 0, 2 | 1, 3
+            h2 x0, x1;
+            __builtin_memcpy(&x0, &p0, 4);
+            __builtin_memcpy(&x1, &p1, 4);
+            f[4 * wv] = __builtin_fmaf(dd, (float)x0[0], c);
+            f[4 * wv + 1] = __builtin_fmaf(dd, (float)x1[0], c);
+            f[4 * wv + 2] = __builtin_fmaf(dd, (float)x0[1], c);
+            f[4 * wv + 3] = __builtin_fmaf(dd, (float)x1[1], c);
+          }
         }
       }
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        _Float16 h = (_Float16)f[i];
-        hv[i] = h;
-        if constexpr (SPLIT) lv[i] = (_Float16)(f[i] - (float)h);
+      for (int i = 0; i < 8; i += 2) {
+        const h2 hp = {(_Float16)f[i], (_Float16)f[i + 1]};
+        hv[i] = hp[0];
+        hv[i + 1] = hp[1];
+        if constexpr (SPLIT) {
+          // lo = fp16(f - hi), formed as fma(hi, -1, f) (f - hi is exact in f32, so the same value) by one
+          // mixed-precision fma per value that reads hi straight from its half of the packed pair
+          uint32_t lp;
+          asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lp) : "v"(hp), "v"(f[i]));
+          asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lp) : "v"(hp), "v"(f[i + 1]));
+          h2 l2;
+          __builtin_memcpy(&l2, &lp, 4);
+          lv[i] = l2[0];
+          lv[i + 1] = l2[1];
+        }
       }
     }
     *(h8*)(dst + 8 * v) = hv;
