@@ -186,3 +186,39 @@ def test_qgemm_other_encodings(gpu, t, shape, passes):
         tol = 5e-4  # the weight is exact in fp16: only the activation rounds
     assert rel_l2(y, ref_y) < tol
     assert rel_l2(dx, ref_dx) < tol
+
+
+def planes(w):
+    """The GEMM's weight planes of the f32 dequantized w: hi = fp16(w), lo = fp16(w - hi)."""
+    hi = w.astype(np.float16)
+    lo = (w - hi.astype(np.float32)).astype(np.float16)
+    return hi.astype(np.float32), lo.astype(np.float32)
+
+
+@pytest.mark.parametrize("passes", [1, 3, 4])
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K] + OTHER + ["q5k_random"])
+@pytest.mark.parametrize("shape", [(576, 768), (2048, 2048)])
+def test_qgemm_weight_planes_bit_exact(gpu, t, shape, passes):
+    """The weight as the qGEMM dequantizes it in registers (not the standalone dequant kernel): with one-hot
+    activation rows every output element is one product 1·w_hi (+ 1·w_lo), exact in the fp32 accumulators, so
+    the forward returns deq(W)ᵀ's hi plane (1 pass) or hi + lo (3 and 4 passes) bit for bit, and the dX returns
+    deq(W)'s, both on the tiles the rule picks at these sizes."""
+    N, K = shape
+    print(f"qgemm weight planes type {t} N={N} K={K} passes={passes}", flush=True)
+    raw = random_q5k(N, K, 9) if t == "q5k_random" else encoded(N, K, t, 60)
+    t = Q5_K if t == "q5k_random" else t
+    key = 400 + t
+    gpu.upload_quant(key, raw, t, N, K)
+    w = o.dequant(raw, t, N * K).reshape(N, K)
+    hi, lo = planes(w)
+    # the f32 sum of the two planes is exact; + 0 turns a -0 weight into the +0 that 0 + (-0) accumulates to
+    want = (hi if passes == 1 else hi + lo) + np.float32(0.0)
+    gpu.set_gemm_passes(passes)
+    try:
+        y = gpu.qgemm_fwd(key, np.eye(K, dtype=np.float32), N)  # y[k, n] = w[n, k]
+        dx = gpu.qgemm_dx(key, np.eye(N, dtype=np.float32), K)  # dx[n, k] = w[n, k]
+    finally:
+        gpu.set_gemm_passes(1)
+        gpu.evict(key)
+    assert np.array_equal(y.view(np.uint32), np.ascontiguousarray(want.T).view(np.uint32))
+    assert np.array_equal(dx.view(np.uint32), want.view(np.uint32))
