@@ -38,6 +38,9 @@ constexpr int BR = TB * NW;   // rows a workgroup owns
 // Wave groups splitting the streamed axis of a workgroup. Forward: three at head dim 64 (a third of the key range
 // each, 110 KB of LDS; measured 3-6% faster than two), two at 128 (three would need 204 KB). Backward: two, except
 // for head dim 128, whose accumulators need more than the 256 registers two waves per SIMD leave (they spill).
+#ifndef HOS_ATT_LPT
+#define HOS_ATT_LPT 1
+#endif
 #ifndef HOS_ATT_PRIO
 #define HOS_ATT_PRIO 1
 #endif
@@ -121,12 +124,26 @@ __device__ __forceinline__ void split8(const float* v, float mul, bf8& H, bf8& L
 struct Work {
   int xb, h, b;
 };
+
+// The causal mask makes a row block's work linear in its index (the forward and dQ visit xb + 1 key blocks, dK/dV
+// nb - xb query blocks). Where the grid is dealt in several rounds per CU, a round's free CUs take the next items in
+// order, so the run is ordered heaviest first (row-block-major over its heads): the last items dispatched are the
+// lightest and the launch does not end on a heavy block started late. HEAVY_HIGH: the heavy blocks are the high xb.
+template <bool HEAVY_HIGH>
 __device__ __forceinline__ Work work_item() {
-  const int nwg = gridDim.x * gridDim.y * gridDim.z, full = nwg & ~7;
+  const int nwg = gridDim.x * gridDim.y * gridDim.z, full = nwg & ~7, nb = gridDim.x;
   int L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  if (L < full) L = (L & 7) * (full >> 3) + (L >> 3);
-  const int rest = L / gridDim.x;
-  return Work{L % (int)gridDim.x, rest % (int)gridDim.y, rest / (int)gridDim.y};
+  if (L < full) {
+    const int per = full >> 3, x = L & 7, j = L >> 3;  // XCD x, position j in its run
+    if (HOS_ATT_LPT && per % nb == 0) {
+      // the run covers the same (head, sequence) items as the row-major order below: rest in [x·hper, (x+1)·hper)
+      const int hper = per / nb, rank = j / hper, rest = x * hper + j % hper;
+      return Work{HEAVY_HIGH ? nb - 1 - rank : rank, rest % (int)gridDim.y, rest / (int)gridDim.y};
+    }
+    L = x * per + j;
+  }
+  const int rest = L / nb;
+  return Work{L % nb, rest % (int)gridDim.y, rest / (int)gridDim.y};
 }
 
 // ---- split kernels ----
@@ -287,7 +304,7 @@ __global__ void __launch_bounds__(256 * NG) attn_fwd_kernel(const __bf16* __rest
   using C = AC<HD>;
   __shared__ __attribute__((aligned(16))) __bf16 sm[NG][2][4 * C::TILE];  // per group, stage: Kh, Kl, Vh, Vl
   const int nqb = (T + BR - 1) / BR;
-  const Work wk = work_item();
+  const Work wk = work_item<true>();
   const int qb = nqb - 1 - wk.xb, h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
   const int tid = threadIdx.x, gt = tid & (NW * 64 - 1), grp = __builtin_amdgcn_readfirstlane(tid >> 8);
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane((tid >> 6) & (NW - 1)), hl = lane >> 5,
@@ -425,7 +442,7 @@ __global__ void __launch_bounds__(256 * NG) attn_dq_kernel(const __bf16* __restr
   using C = AC<HD>;
   __shared__ __attribute__((aligned(16))) __bf16 sm[NG][2][4 * C::TILE];  // per group, stage: Kh, Kl, Vh, Vl
   const int nqb = (T + BR - 1) / BR;
-  const Work wk = work_item();
+  const Work wk = work_item<true>();
   const int qb = nqb - 1 - wk.xb, h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
   const int tid = threadIdx.x, gt = tid & (NW * 64 - 1), grp = __builtin_amdgcn_readfirstlane(tid >> 8);
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane((tid >> 6) & (NW - 1)), hl = lane >> 5,
@@ -553,7 +570,7 @@ __global__ void __launch_bounds__(256 * NG) attn_dkdv_kernel(const __bf16* __res
   using C = AC<HD>;
   __shared__ __attribute__((aligned(16))) __bf16 sm[NG][2][4 * C::TILE];  // per group, stage: Qh, Ql, dOh, dOl
   __shared__ float ld_s[NG][2][2][TB];  // per group, stage: LSE·log2 e, D of the tile's queries
-  const Work wk = work_item();
+  const Work wk = work_item<false>();
   const int h = wk.h, b = wk.b, g = h / group, nkv = nh / group;
   const int tid = threadIdx.x, gt = tid & (NW * 64 - 1), grp = __builtin_amdgcn_readfirstlane(tid >> 8);
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane((tid >> 6) & (NW - 1)), hl = lane >> 5,
