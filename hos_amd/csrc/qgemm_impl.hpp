@@ -1055,7 +1055,7 @@ void launch_typed_grouped(const QWeight& w, GroupSched gs, H16 a, long long lda,
 // accumulators cost occupancy (2 waves per SIMD instead of 3 on 128×128 tiles), which the saved third of the MFMA
 // work repays only from about 64 GFLOP per launch on (measured on the MI355X, M 2048: N 8192 × K 2048 −14%,
 // N 2048 × K 8192 −15%, 4096³ −15%; N 9728 × K 896 +5%, 2048³ +8%) — else mode 3. Grouped (mixture-of-experts)
-// launches are per-expert sized and stay mode 3.
+// launches stay mode 3 (OLMoE's expert forwards, ~100-200 GFLOP each, measured 27% slower in mode 5).
 template <uint32_t QT, bool DX>
 void launch_exact(const QWeight& w, H16 a, long long lda, long long M, GemmEpi epi, float* ws, size_t ws_bytes,
                   hipStream_t st) {
