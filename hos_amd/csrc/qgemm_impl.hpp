@@ -319,7 +319,7 @@ __global__ void __launch_bounds__(BM >= 256 ? 512 : 256, (BM >= 256 && (NP == 1 
   int wid;
   const int zsp = blockIdx.z;
   if (gk.tiles) {
-    wid = blockIdx.x;  // grouped: row tile fixed above, no remap
+    wid = blockIdx.x;  // grouped: row tile fixed above, no remap (XCD runs measured 7% slower on OLMoE's step)
   } else {
     const int X = gridDim.x, Y = gridDim.y, T = X * Y, full = T & ~7;
     int t = blockIdx.x + X * blockIdx.y;
