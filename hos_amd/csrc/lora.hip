@@ -664,12 +664,17 @@ void cols_split(long long M, int gx, int* S, int* mchunk) {
 // factor fragment loaded from L2 then feeds two row tiles; at one tile the factors' L2 bytes per workgroup are
 // 2·n/16 times the activation's: Llama-3.2-1B's step, M 8192, +1.1%), else one (with fewer row blocks, two tiles per
 // workgroup would need more contraction splits: Qwen2.5-0.5B at M 2048 −1.3% with two; above 64 columns the 16
-// waves' LDS partial tiles would not fit).
+// waves' LDS partial tiles would not fit) — except for contractions from HOS_R16_RT_K on, long enough to be split
+// anyway (Qwen2.5-0.5B's gate|up du, K 9728: LoRA classes 3.80 -> 3.72 ms, +0.4% tokens/s; from K 4096 on, which
+// adds its FFN down-projection, measured no gain).
 #ifndef HOS_R16_RT
 #define HOS_R16_RT 2
 #endif
-int rows16_rt(long long M, int n) {
-  return (n <= 64 && (M + 31) / 32 >= HOS_R16_TARGET) ? HOS_R16_RT : 1;
+#ifndef HOS_R16_RT_K
+#define HOS_R16_RT_K 8192
+#endif
+int rows16_rt(long long M, int n, long long K) {
+  return (n <= 64 && ((M + 31) / 32 >= HOS_R16_TARGET || K >= HOS_R16_RT_K)) ? HOS_R16_RT : 1;
 }
 void rows16_split(long long M, long long K, int* S, int* kchunk, int rb = 16) {
   const int gx = ceil_div_i(M, rb), round = 32 * R16_NW;
@@ -681,7 +686,7 @@ void rows16_split(long long M, long long K, int* S, int* kchunk, int rb = 16) {
 size_t lora_rows_ws_bytes(long long M, long long K, int n) {
   if (M <= 0 || n <= 0) return 0;
   int S16 = 0, kc16 = 0;
-  const int rb16 = 16 * rows16_rt(M, n);
+  const int rb16 = 16 * rows16_rt(M, n, K);
   rows16_split(M, K, &S16, &kc16, rb16);
   const size_t w16 = S16 > 1 ? (size_t)S16 * ceil_div_i(M, rb16) * rb16 * ((n + 15) / 16) * 16 * 4 : 0;
   if (K <= ROWS_WIDE_KMAX) return w16;
@@ -739,7 +744,7 @@ void launch_lora_rows(long long M, long long K, float alpha, const float* X, lon
           sg.kend[t] <= K;
   if (f16) {
     HOS_REQUIRE(xh.rinv, HOS_E_INVALID, "lora_rows: the fp16 operand needs its row scales");
-    const int RT = rows16_rt(M, n), rb = 16 * RT, gx = ceil_div_i(M, rb), NJ = (n + 15) / 16;
+    const int RT = rows16_rt(M, n, K), rb = 16 * RT, gx = ceil_div_i(M, rb), NJ = (n + 15) / 16;
     int S = 0, kchunk = 0;
     rows16_split(M, K, &S, &kchunk, rb);
     HOS_REQUIRE(S == 1 || (size_t)S * gx * rb * NJ * 16 * 4 <= ws_bytes, HOS_E_INVALID, "lora_rows: workspace too small");
