@@ -195,8 +195,26 @@ def planes(w):
     return hi.astype(np.float32), lo.astype(np.float32)
 
 
+def random_kquant(rows, cols, t, seed):
+    """Q4_K (144-byte) / Q6_K (210-byte) super-blocks of random bytes with sane f16 scale fields (Q4_K: d of either
+    sign and dmin at bytes 0-3; Q6_K: d at bytes 208-209, its int8 sub-scales random of either sign): every code and
+    sub-scale combination, not only what the quantizer emits."""
+    rng = np.random.default_rng(seed)
+    nb = rows * cols // 256
+    size = 144 if t == Q4_K else 210
+    blk = rng.integers(0, 256, size=(nb, size), dtype=np.uint8)
+    d = (rng.uniform(1e-4, 4e-3, nb) * rng.choice([-1, 1], nb)).astype(np.float16)
+    if t == Q4_K:
+        dmin = rng.uniform(0, 4e-3, nb).astype(np.float16)
+        blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blk[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    else:
+        blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return blk.ravel()
+
+
 @pytest.mark.parametrize("passes", [1, 3, 4])
-@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K] + OTHER + ["q5k_random"])
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K] + OTHER + ["q5k_random", "q4k_random", "q6k_random"])
 @pytest.mark.parametrize("shape", [(576, 768), (2048, 2048)])
 def test_qgemm_weight_planes_bit_exact(gpu, t, shape, passes):
     """The weight as the qGEMM dequantizes it in registers (not the standalone dequant kernel): with one-hot
@@ -205,8 +223,13 @@ def test_qgemm_weight_planes_bit_exact(gpu, t, shape, passes):
     deq(W)'s, both on the tiles the rule picks at these sizes."""
     N, K = shape
     print(f"qgemm weight planes type {t} N={N} K={K} passes={passes}", flush=True)
-    raw = random_q5k(N, K, 9) if t == "q5k_random" else encoded(N, K, t, 60)
-    t = Q5_K if t == "q5k_random" else t
+    if t == "q5k_random":
+        raw, t = random_q5k(N, K, 9), Q5_K
+    elif t in ("q4k_random", "q6k_random"):
+        t = Q4_K if t == "q4k_random" else Q6_K
+        raw = random_kquant(N, K, t, 11)
+    else:
+        raw = encoded(N, K, t, 60)
     key = 400 + t
     gpu.upload_quant(key, raw, t, N, K)
     w = o.dequant(raw, t, N * K).reshape(N, K)
