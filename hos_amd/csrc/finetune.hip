@@ -4,11 +4,12 @@
 // the loss scaled by 1/B (the accumulation of src/main.rs:2834-2855), backward through every weight, and
 // AdamW over FtModel::params with decay on the 2-D tensors (src/main.rs:2803-2804).
 //
-// The weight GEMMs are the f32 GEMMs of the reference's GPU surface (gemm_f32.hip, fp32 MFMA): forward
-// Y = X·Wᵀ, input gradient dX = dY·W and the weight gradient dW = dYᵀ·X (the matmul_atb of
-// src/metal_be.rs:1212-1234), all on [out, in] weights kept in the GGUF layout. Norm-weight and bias
-// gradients are column sums in row order; the embedding gradient adds each token's row into its id's
-// row in token order (both deterministic).
+// The weight GEMMs, all on [out, in] weights kept in the GGUF layout: forward Y = X·Wᵀ and input gradient
+// dX = dY·W on the quantized-weight GEMM with the f32 weight as its layout (3 precision passes on fp16 MFMA), the
+// weight gradient dW = dYᵀ·X (the matmul_atb of src/metal_be.rs:1212-1234) on the f32 GEMM of the reference's GPU
+// surface (gemm_f32.hip, fp32 MFMA). Norm-weight and bias gradients are column sums, in row order within chunks
+// of rows and the chunks in order; the embedding gradient adds each token's row into its id's row in token order
+// (both deterministic).
 #include <cstring>
 #include <map>
 #include <string>
@@ -21,18 +22,31 @@ using namespace hos;
 
 namespace {
 
-// out[j] = Σ_r g[r][j]·(x ? x[r][j]·inv[r] : 1), rows in order (one thread per column).
-__global__ void colsum_kernel(const float* __restrict__ g, long long ldg, const float* __restrict__ x, long long ldx,
-                              const float* __restrict__ inv, int M, int n, float* __restrict__ out) {
+// out[j] = Σ_r g[r][j]·(x ? x[r][j]·inv[r] : 1): each workgroup row (blockIdx.y) sums one chunk of COLSUM_CH rows in
+// row order into part[chunk][j] (one thread per column, coalesced over the columns), then colsum_fold adds the
+// chunks in chunk order — deterministic, and the chunks run in parallel (one thread per column over all rows left
+// the whole GPU with a few waves, each waiting on one load per row: 0.6 ms per call at M 2048).
+constexpr int COLSUM_CH = 32;
+__global__ void colsum_part_kernel(const float* __restrict__ g, long long ldg, const float* __restrict__ x,
+                                   long long ldx, const float* __restrict__ inv, int M, int n,
+                                   float* __restrict__ part) {
 #pragma clang fp contract(off)
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n) return;
+  const int r0 = blockIdx.y * COLSUM_CH, r1 = min(M, r0 + COLSUM_CH);
   float s = 0.0f;
   if (x) {
-    for (int r = 0; r < M; r++) s += g[(long long)r * ldg + j] * x[(long long)r * ldx + j] * inv[r];
+    for (int r = r0; r < r1; r++) s += g[(long long)r * ldg + j] * x[(long long)r * ldx + j] * inv[r];
   } else {
-    for (int r = 0; r < M; r++) s += g[(long long)r * ldg + j];
+    for (int r = r0; r < r1; r++) s += g[(long long)r * ldg + j];
   }
+  part[(long long)blockIdx.y * n + j] = s;
+}
+__global__ void colsum_fold_kernel(const float* __restrict__ part, int nch, int n, float* __restrict__ out) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  float s = 0.0f;
+  for (int c = 0; c < nch; c++) s += part[(long long)c * n + j];
   out[j] = s;
 }
 
@@ -99,6 +113,9 @@ struct hos_ft {
   void* attn_planes = nullptr;  // bf16 hi/lo planes of q, k, v (attention scratch)
   size_t ws_bytes = 0;
   H16 hs{};
+  H16 ah{};  // fp16 hi/lo operand of a weight GEMM's activation (X forward, dY for the input gradient)
+  float* csp = nullptr;  // column-sum partials, one row per chunk of rows
+  size_t csp_n = 0;
   float2* rope_tab = nullptr;
   int32_t *ids = nullptr, *tgts = nullptr;
 
@@ -212,6 +229,12 @@ struct hos_ft {
     const size_t hc = std::max<size_t>({(size_t)d, 2 * (size_t)F});
     hs.data = alloc<half_t>(M * hc);  // fp16 operand the fused norm / SwiGLU kernels also write (unused here)
     hs.rinv = alloc<float>(M);
+    const size_t amax = std::max<size_t>({(size_t)d, (size_t)qd, (size_t)F, (size_t)V});
+    ah.data = alloc<half_t>(M * amax);
+    ah.lo = alloc<half_t>(M * amax);
+    ah.rinv = alloc<float>(M);
+    csp_n = (size_t)ceil_div((long long)M, COLSUM_CH) * std::max<size_t>((size_t)d, (size_t)qd);
+    csp = alloc<float>(csp_n);
     ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(V, 2 * (size_t)F) * 4, 1ull << 30));
     ws = alloc<float>(ws_bytes / 4);
     hyp = alloc<AdamHyper>(1);
@@ -304,14 +327,30 @@ struct hos_ft {
   }
 
   // ---- GEMM helpers (row-major, weights [out, in]) ----
+  // The forward and input-gradient GEMMs run on the quantized-weight GEMM with the f32 weight as its (unscaled)
+  // layout, in 3 precision passes: the activation (or dY) and the weight each split into fp16 hi + lo (~22 bits,
+  // the activation with a power-of-two row scale), A_hi·W_hi + A_lo·W_hi + A_hi·W_lo with fp32 accumulation —
+  // the f32 result to ~2^-22 relative per product, on fp16 MFMA (16× the fp32-MFMA rate per pass).
+  QWeight wview(const float* Wt, int o, int i) const {
+    QWeight w;
+    w.type = GGUF_F32;
+    w.rows = o;
+    w.cols = i;
+    w.q = (void*)Wt;
+    return w;
+  }
   // Y[M, o] (beta: 0 overwrite / 1 accumulate) = X[M, i] · Wᵀ
   void fwd(const float* X, long long ldx, const float* Wt, int o, int i, int M, float beta, float* Y, long long ldy) {
-    launch_gemm_f32(M, o, i, 1.0f, X, ldx, 1, Wt, 1, i, beta, Y, ldy, ws, ws_bytes, st);
+    launch_to_h16(X, ldx, M, i, ah, st);
+    GemmEpi e{Y, ldy, nullptr, beta != 0.0f ? 1 : 0, nullptr};
+    launch_qgemm_fwd(wview(Wt, o, i), ah, i, M, e, ws, ws_bytes, 3, st);
   }
   // dX[M, i] (+)= dY[M, o] · W
   void bwd_x(const float* dY, long long ldd, const float* Wt, int o, int i, int M, float beta, float* dX,
              long long ldx) {
-    launch_gemm_f32(M, i, o, 1.0f, dY, ldd, 1, Wt, i, 1, beta, dX, ldx, ws, ws_bytes, st);
+    launch_to_h16(dY, ldd, M, o, ah, st);
+    GemmEpi e{dX, ldx, nullptr, beta != 0.0f ? 1 : 0, nullptr};
+    launch_qgemm_dx(wview(Wt, o, i), ah, o, M, e, ws, ws_bytes, 3, st);
   }
   // dW[o, i] = dY[M, o]ᵀ · X[M, i]
   void bwd_w(const float* dY, long long ldd, const float* X, long long ldx, int o, int i, int M, float* dWt) {
@@ -319,7 +358,11 @@ struct hos_ft {
   }
   void colsum(const float* g, long long ldg, const float* x, long long ldx, const float* inv, int M, int nc,
               float* out) {
-    colsum_kernel<<<ceil_div(nc, 256), 256, 0, st>>>(g, ldg, x, ldx, inv, M, nc, out);
+    const int nch = ceil_div(M, COLSUM_CH);
+    HOS_REQUIRE((size_t)nch * nc <= csp_n, HOS_E_INVALID, "finetune: column-sum partials exceed their buffer");
+    colsum_part_kernel<<<dim3(ceil_div(nc, 256), nch), 256, 0, st>>>(g, ldg, x, ldx, inv, M, nc, csp);
+    HOS_HIP_CHECK(hipGetLastError());
+    colsum_fold_kernel<<<ceil_div(nc, 256), 256, 0, st>>>(csp, nch, nc, out);
     HOS_HIP_CHECK(hipGetLastError());
   }
   void add_bias(float* y, long long ld, int M, int nc, const float* b) {
