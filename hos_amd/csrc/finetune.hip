@@ -4,10 +4,11 @@
 // the loss scaled by 1/B (the accumulation of src/main.rs:2834-2855), backward through every weight, and
 // AdamW over FtModel::params with decay on the 2-D tensors (src/main.rs:2803-2804).
 //
-// The weight GEMMs, all on [out, in] weights kept in the GGUF layout: forward Y = X·Wᵀ and input gradient
-// dX = dY·W on the quantized-weight GEMM with the f32 weight as its layout (3 precision passes on fp16 MFMA), the
-// weight gradient dW = dYᵀ·X (the matmul_atb of src/metal_be.rs:1212-1234) on the f32 GEMM of the reference's GPU
-// surface (gemm_f32.hip, fp32 MFMA). Norm-weight and bias gradients are column sums, in row order within chunks
+// The weight GEMMs, all on [out, in] weights kept in the GGUF layout and all on the quantized-weight GEMM (3
+// precision passes on fp16 MFMA): forward Y = X·Wᵀ and input gradient dX = dY·W with the f32 weight as its layout,
+// the weight gradient dW = dYᵀ·X (the matmul_atb of src/metal_be.rs:1212-1234) in its dX form over the tokens, dYᵀ
+// the operand and X the f32 "weight" (the f32 GEMM of gemm_f32.hip, fp32 MFMA, when the token count is not a
+// multiple of 32). Norm-weight and bias gradients are column sums, in row order within chunks
 // of rows and the chunks in order; the embedding gradient adds each token's row into its id's row in token order
 // (both deterministic).
 #include <cstring>
@@ -48,6 +49,51 @@ __global__ void colsum_fold_kernel(const float* __restrict__ part, int nch, int 
   float s = 0.0f;
   for (int c = 0; c < nch; c++) s += part[(long long)c * n + j];
   out[j] = s;
+}
+
+// The weight gradient dW[o, i] = Σ_m dY[m, o]·X[m, i] runs as the quantized-weight GEMM's dX form with dYᵀ as its
+// fp16 row-scaled operand ([o][M]: one row per output column of dY, over the tokens) and X as an f32 "weight" of M
+// rows. These two kernels form that operand: the max |dY| of every column (order-free, so an atomic max of the
+// non-negative floats' bits is deterministic), then 64×64 tiles transposed through LDS and written as the scaled
+// fp16 hi / lo planes with the row scale of launch_to_h16 (a power of two putting the row max in [2^14, 2^15)).
+__global__ void colmax_kernel(const float* __restrict__ g, long long ldg, int M, int n, unsigned* __restrict__ cmax) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int r0 = blockIdx.y * COLSUM_CH, r1 = min(M, r0 + COLSUM_CH);
+  float m = 0.0f;
+  for (int r = r0; r < r1; r++) m = fmaxf(m, fabsf(g[(long long)r * ldg + j]));
+  atomicMax(cmax + j, __float_as_uint(m));
+}
+__device__ __forceinline__ int tr_row_exp(float amax) {  // the row scale exponent of launch_to_h16
+  if (!(amax > 0.0f) || amax >= 3.0e38f) return 0;
+  int ex;
+  frexpf(amax, &ex);
+  const int e = 15 - ex;
+  return e > 100 ? 100 : (e < -100 ? -100 : e);
+}
+__global__ void __launch_bounds__(256) transpose_h16_kernel(const float* __restrict__ g, long long ldg, int M, int n,
+                                                            const unsigned* __restrict__ cmax,
+                                                            _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                            float* __restrict__ rinv) {
+  __shared__ float tile[64][65];
+  const int c0 = blockIdx.x * 64, m0 = blockIdx.y * 64, tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int m = m0 + r, c = c0 + tx;
+    tile[r][tx] = (m < M && c < n) ? g[(long long)m * ldg + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int cc = ty; cc < 64; cc += 4) {
+    const int c = c0 + cc, m = m0 + tx;
+    if (c >= n) break;
+    const int e = tr_row_exp(__uint_as_float(cmax[c]));
+    if (m < M) {
+      const float v = tile[tx][cc] * ldexpf(1.0f, e);
+      const _Float16 h = (_Float16)v;
+      hi[(long long)c * M + m] = h;
+      lo[(long long)c * M + m] = (_Float16)(v - (float)h);
+    }
+    if (blockIdx.y == 0 && tx == 0) rinv[c] = ldexpf(1.0f, -e);
+  }
 }
 
 // dE[ids[t]] = Σ over the tokens with that id, in token order (the first occurrence's workgroup does the row)
@@ -116,6 +162,10 @@ struct hos_ft {
   H16 ah{};  // fp16 hi/lo operand of a weight GEMM's activation (X forward, dY for the input gradient)
   float* csp = nullptr;  // column-sum partials, one row per chunk of rows
   size_t csp_n = 0;
+  size_t ah_n = 0;             // elements of each plane of ah
+  unsigned* cmax = nullptr;    // per-column max |dY| (float bits) for the transposed operand
+  float* tr_rinv = nullptr;    // its row scales, one per column of dY
+  size_t tr_rows = 0;
   float2* rope_tab = nullptr;
   int32_t *ids = nullptr, *tgts = nullptr;
 
@@ -230,9 +280,13 @@ struct hos_ft {
     hs.data = alloc<half_t>(M * hc);  // fp16 operand the fused norm / SwiGLU kernels also write (unused here)
     hs.rinv = alloc<float>(M);
     const size_t amax = std::max<size_t>({(size_t)d, (size_t)qd, (size_t)F, (size_t)V});
-    ah.data = alloc<half_t>(M * amax);
-    ah.lo = alloc<half_t>(M * amax);
+    ah_n = M * amax;
+    ah.data = alloc<half_t>(ah_n);
+    ah.lo = alloc<half_t>(ah_n);
     ah.rinv = alloc<float>(M);
+    tr_rows = amax;
+    cmax = alloc<unsigned>(tr_rows);
+    tr_rinv = alloc<float>(tr_rows);
     csp_n = (size_t)ceil_div((long long)M, COLSUM_CH) * std::max<size_t>((size_t)d, (size_t)qd);
     csp = alloc<float>(csp_n);
     ws_bytes = std::max<size_t>(64ull << 20, std::min<size_t>(M * std::max<size_t>(V, 2 * (size_t)F) * 4, 1ull << 30));
@@ -352,9 +406,24 @@ struct hos_ft {
     GemmEpi e{dX, ldx, nullptr, beta != 0.0f ? 1 : 0, nullptr};
     launch_qgemm_dx(wview(Wt, o, i), ah, o, M, e, ws, ws_bytes, 3, st);
   }
-  // dW[o, i] = dY[M, o]ᵀ · X[M, i]
+  // dW[o, i] = dY[M, o]ᵀ · X[M, i]: the dX-form GEMM over the tokens (dYᵀ as the operand, X as an f32 weight of M
+  // rows), in 3 passes like the others; when the token count is not a multiple of 32 (the GEMM's contraction step)
+  // or X is not packed, the f32 GEMM
   void bwd_w(const float* dY, long long ldd, const float* X, long long ldx, int o, int i, int M, float* dWt) {
-    launch_gemm_f32(o, i, M, 1.0f, dY, 1, ldd, X, ldx, 1, 0.0f, dWt, i, ws, ws_bytes, st);
+    if (M % 32 != 0 || ldx != i) {
+      launch_gemm_f32(o, i, M, 1.0f, dY, 1, ldd, X, ldx, 1, 0.0f, dWt, i, ws, ws_bytes, st);
+      return;
+    }
+    HOS_REQUIRE((size_t)o <= tr_rows && (size_t)o * M <= ah_n, HOS_E_INVALID, "finetune: dYᵀ operand exceeds its buffer");
+    launch_fill((float*)cmax, o, 0.0f, st);
+    colmax_kernel<<<dim3(ceil_div(o, 256), ceil_div(M, COLSUM_CH)), 256, 0, st>>>(dY, ldd, M, o, cmax);
+    HOS_HIP_CHECK(hipGetLastError());
+    const H16 at{ah.data, tr_rinv, ah.lo};
+    transpose_h16_kernel<<<dim3(ceil_div(o, 64), ceil_div(M, 64)), 256, 0, st>>>(dY, ldd, M, o, cmax, at.data, at.lo,
+                                                                                  at.rinv);
+    HOS_HIP_CHECK(hipGetLastError());
+    GemmEpi e{dWt, i, nullptr, 0, nullptr};
+    launch_qgemm_dx(wview(X, M, i), at, M, o, e, ws, ws_bytes, 3, st);
   }
   void colsum(const float* g, long long ldg, const float* x, long long ldx, const float* inv, int M, int nc,
               float* out) {

@@ -53,12 +53,14 @@ def pair(gpu, cfg, B, T, seed):
     return ft, om, ids, tg
 
 
+# T 40: 80 tokens, the f32 weight-gradient GEMM; T 48: 96 tokens, a multiple of 32, the fp16-MFMA one over dYᵀ
+@pytest.mark.parametrize("T", [40, 48])
 @pytest.mark.parametrize("kw", [{}, dict(attn_bias=False, rope_neox=False, n_heads=6, n_kv_heads=3, dim=384,
                                         quant=8, head_quant=8, vocab=320)])
-def test_finetune_grads_match_oracle(gpu, kw):
+def test_finetune_grads_match_oracle(gpu, kw, T):
     cfg = ft_cfg(**kw)
-    print(f"finetune parity {kw}", flush=True)
-    ft, om, ids, tg = pair(gpu, cfg, B=2, T=40, seed=3)
+    print(f"finetune parity {kw} T={T}", flush=True)
+    ft, om, ids, tg = pair(gpu, cfg, B=2, T=T, seed=3)
     lg, lo = ft.loss_grad(ids, tg), om.loss_grad(ids, tg)
     assert abs(lg - lo) / abs(lo) <= TOL, (lg, lo)
     worst = 0.0
