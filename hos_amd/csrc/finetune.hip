@@ -37,8 +37,10 @@ __global__ void colsum_part_kernel(const float* __restrict__ g, long long ldg, c
   const int r0 = blockIdx.y * COLSUM_CH, r1 = min(M, r0 + COLSUM_CH);
   float s = 0.0f;
   if (x) {
+#pragma unroll 8
     for (int r = r0; r < r1; r++) s += g[(long long)r * ldg + j] * x[(long long)r * ldx + j] * inv[r];
   } else {
+#pragma unroll 8
     for (int r = r0; r < r1; r++) s += g[(long long)r * ldg + j];
   }
   part[(long long)blockIdx.y * n + j] = s;
@@ -47,6 +49,7 @@ __global__ void colsum_fold_kernel(const float* __restrict__ part, int nch, int 
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n) return;
   float s = 0.0f;
+#pragma unroll 8
   for (int c = 0; c < nch; c++) s += part[(long long)c * n + j];
   out[j] = s;
 }
@@ -61,6 +64,7 @@ __global__ void colmax_kernel(const float* __restrict__ g, long long ldg, int M,
   if (j >= n) return;
   const int r0 = blockIdx.y * COLSUM_CH, r1 = min(M, r0 + COLSUM_CH);
   float m = 0.0f;
+#pragma unroll 8
   for (int r = r0; r < r1; r++) m = fmaxf(m, fabsf(g[(long long)r * ldg + j]));
   atomicMax(cmax + j, __float_as_uint(m));
 }
@@ -393,9 +397,11 @@ struct hos_ft {
     w.q = (void*)Wt;
     return w;
   }
-  // Y[M, o] (beta: 0 overwrite / 1 accumulate) = X[M, i] · Wᵀ
-  void fwd(const float* X, long long ldx, const float* Wt, int o, int i, int M, float beta, float* Y, long long ldy) {
-    launch_to_h16(X, ldx, M, i, ah, st);
+  // Y[M, o] (beta: 0 overwrite / 1 accumulate) = X[M, i] · Wᵀ; same_x: X is the previous call's X, unchanged since,
+  // so the operand it left in ah is reused
+  void fwd(const float* X, long long ldx, const float* Wt, int o, int i, int M, float beta, float* Y, long long ldy,
+           bool same_x = false) {
+    if (!same_x) launch_to_h16(X, ldx, M, i, ah, st);
     GemmEpi e{Y, ldy, nullptr, beta != 0.0f ? 1 : 0, nullptr};
     launch_qgemm_fwd(wview(Wt, o, i), ah, i, M, e, ws, ws_bytes, 3, st);
   }
@@ -449,8 +455,8 @@ struct hos_ft {
       float* xnext = (l + 1 < L) ? act[l + 1].x : xf;
       launch_rmsnorm_fwd(a.x, Vp(l, NA), c.rms_eps, M, d, a.xn1, hs, a.inv1, st);
       fwd(a.xn1, d, W(l, WQ), qd, d, M, 0.0f, a.qkv, W3);
-      fwd(a.xn1, d, W(l, WK), kvd, d, M, 0.0f, a.qkv + qd, W3);
-      fwd(a.xn1, d, W(l, WV), kvd, d, M, 0.0f, a.qkv + qd + kvd, W3);
+      fwd(a.xn1, d, W(l, WK), kvd, d, M, 0.0f, a.qkv + qd, W3, true);
+      fwd(a.xn1, d, W(l, WV), kvd, d, M, 0.0f, a.qkv + qd + kvd, W3, true);
       if (c.attn_bias) {
         add_bias(a.qkv, W3, M, qd, Vp(l, BQ));
         add_bias(a.qkv + qd, W3, M, kvd, Vp(l, BK));
@@ -464,7 +470,7 @@ struct hos_ft {
       fwd(a.o, qd, W(l, WO), d, qd, M, 1.0f, a.x2, d);
       launch_rmsnorm_fwd(a.x2, Vp(l, NF), c.rms_eps, M, d, a.xn2, hs, a.inv2, st);
       fwd(a.xn2, d, W(l, WG), F, d, M, 0.0f, a.gu, 2LL * F);
-      fwd(a.xn2, d, W(l, WU), F, d, M, 0.0f, a.gu + F, 2LL * F);
+      fwd(a.xn2, d, W(l, WU), F, d, M, 0.0f, a.gu + F, 2LL * F, true);
       launch_swiglu_fwd(a.gu, M, F, a.h, hs, st);
       launch_copy_rows(a.x2, d, xnext, d, M, d, st);
       fwd(a.h, F, W(l, WD), d, F, M, 1.0f, xnext, d);
