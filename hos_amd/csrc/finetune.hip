@@ -56,17 +56,18 @@ __global__ void colsum_fold_kernel(const float* __restrict__ part, int nch, int 
 
 // The weight gradient dW[o, i] = Σ_m dY[m, o]·X[m, i] runs as the quantized-weight GEMM's dX form with dYᵀ as its
 // fp16 row-scaled operand ([o][M]: one row per output column of dY, over the tokens) and X as an f32 "weight" of M
-// rows. These two kernels form that operand: the max |dY| of every column (order-free, so an atomic max of the
-// non-negative floats' bits is deterministic), then 64×64 tiles transposed through LDS and written as the scaled
-// fp16 hi / lo planes with the row scale of launch_to_h16 (a power of two putting the row max in [2^14, 2^15)).
-__global__ void colmax_kernel(const float* __restrict__ g, long long ldg, int M, int n, unsigned* __restrict__ cmax) {
+// rows. These two kernels form that operand: the max |dY| of every column over each chunk of COLSUM_CH rows, then
+// 64×64 tiles transposed through LDS — each workgroup first folds its 64 columns' chunk maxima (max is
+// order-free) — and written as the scaled fp16 hi / lo planes with the row scale of launch_to_h16 (a power of two
+// putting the row max in [2^14, 2^15)).
+__global__ void colmax_kernel(const float* __restrict__ g, long long ldg, int M, int n, float* __restrict__ cpart) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n) return;
   const int r0 = blockIdx.y * COLSUM_CH, r1 = min(M, r0 + COLSUM_CH);
   float m = 0.0f;
 #pragma unroll 8
   for (int r = r0; r < r1; r++) m = fmaxf(m, fabsf(g[(long long)r * ldg + j]));
-  atomicMax(cmax + j, __float_as_uint(m));
+  cpart[(long long)blockIdx.y * n + j] = m;
 }
 __device__ __forceinline__ int tr_row_exp(float amax) {  // the row scale exponent of launch_to_h16
   if (!(amax > 0.0f) || amax >= 3.0e38f) return 0;
@@ -76,27 +77,38 @@ __device__ __forceinline__ int tr_row_exp(float amax) {  // the row scale expone
   return e > 100 ? 100 : (e < -100 ? -100 : e);
 }
 __global__ void __launch_bounds__(256) transpose_h16_kernel(const float* __restrict__ g, long long ldg, int M, int n,
-                                                            const unsigned* __restrict__ cmax,
+                                                            const float* __restrict__ cpart, int nch,
                                                             _Float16* __restrict__ hi, _Float16* __restrict__ lo,
                                                             float* __restrict__ rinv) {
   __shared__ float tile[64][65];
+  __shared__ float cm[4][64];
   const int c0 = blockIdx.x * 64, m0 = blockIdx.y * 64, tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  {
+    float mx = 0.0f;
+    if (c0 + tx < n)
+      for (int k = ty; k < nch; k += 4) mx = fmaxf(mx, cpart[(long long)k * n + c0 + tx]);
+    cm[ty][tx] = mx;
+  }
   for (int r = ty; r < 64; r += 4) {
     const int m = m0 + r, c = c0 + tx;
     tile[r][tx] = (m < M && c < n) ? g[(long long)m * ldg + c] : 0.0f;
   }
   __syncthreads();
+  if (ty == 0) {
+    const int e = tr_row_exp(fmaxf(fmaxf(cm[0][tx], cm[1][tx]), fmaxf(cm[2][tx], cm[3][tx])));
+    cm[0][tx] = (float)e;  // exact small integer
+    if (blockIdx.y == 0 && c0 + tx < n) rinv[c0 + tx] = ldexpf(1.0f, -e);
+  }
+  __syncthreads();
   for (int cc = ty; cc < 64; cc += 4) {
     const int c = c0 + cc, m = m0 + tx;
     if (c >= n) break;
-    const int e = tr_row_exp(__uint_as_float(cmax[c]));
     if (m < M) {
-      const float v = tile[tx][cc] * ldexpf(1.0f, e);
+      const float v = tile[tx][cc] * ldexpf(1.0f, (int)cm[0][cc]);
       const _Float16 h = (_Float16)v;
       hi[(long long)c * M + m] = h;
       lo[(long long)c * M + m] = (_Float16)(v - (float)h);
     }
-    if (blockIdx.y == 0 && tx == 0) rinv[c] = ldexpf(1.0f, -e);
   }
 }
 
@@ -167,7 +179,8 @@ struct hos_ft {
   float* csp = nullptr;  // column-sum partials, one row per chunk of rows
   size_t csp_n = 0;
   size_t ah_n = 0;             // elements of each plane of ah
-  unsigned* cmax = nullptr;    // per-column max |dY| (float bits) for the transposed operand
+  float* cpart = nullptr;      // per-chunk column max |dY| for the transposed operand
+  size_t cpart_n = 0;
   float* tr_rinv = nullptr;    // its row scales, one per column of dY
   size_t tr_rows = 0;
   float2* rope_tab = nullptr;
@@ -289,7 +302,8 @@ struct hos_ft {
     ah.lo = alloc<half_t>(ah_n);
     ah.rinv = alloc<float>(M);
     tr_rows = amax;
-    cmax = alloc<unsigned>(tr_rows);
+    cpart_n = (size_t)ceil_div((long long)M, COLSUM_CH) * tr_rows;
+    cpart = alloc<float>(cpart_n);
     tr_rinv = alloc<float>(tr_rows);
     csp_n = (size_t)ceil_div((long long)M, COLSUM_CH) * std::max<size_t>((size_t)d, (size_t)qd);
     csp = alloc<float>(csp_n);
@@ -421,12 +435,13 @@ struct hos_ft {
       return;
     }
     HOS_REQUIRE((size_t)o <= tr_rows && (size_t)o * M <= ah_n, HOS_E_INVALID, "finetune: dYᵀ operand exceeds its buffer");
-    launch_fill((float*)cmax, o, 0.0f, st);
-    colmax_kernel<<<dim3(ceil_div(o, 256), ceil_div(M, COLSUM_CH)), 256, 0, st>>>(dY, ldd, M, o, cmax);
+    const int nch = ceil_div(M, COLSUM_CH);
+    HOS_REQUIRE((size_t)nch * o <= cpart_n, HOS_E_INVALID, "finetune: column maxima exceed their buffer");
+    colmax_kernel<<<dim3(ceil_div(o, 256), nch), 256, 0, st>>>(dY, ldd, M, o, cpart);
     HOS_HIP_CHECK(hipGetLastError());
     const H16 at{ah.data, tr_rinv, ah.lo};
-    transpose_h16_kernel<<<dim3(ceil_div(o, 64), ceil_div(M, 64)), 256, 0, st>>>(dY, ldd, M, o, cmax, at.data, at.lo,
-                                                                                  at.rinv);
+    transpose_h16_kernel<<<dim3(ceil_div(o, 64), ceil_div(M, 64)), 256, 0, st>>>(dY, ldd, M, o, cpart, nch, at.data,
+                                                                                  at.lo, at.rinv);
     HOS_HIP_CHECK(hipGetLastError());
     GemmEpi e{dWt, i, nullptr, 0, nullptr};
     launch_qgemm_dx(wview(X, M, i), at, M, o, e, ws, ws_bytes, 3, st);
