@@ -918,6 +918,14 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
     bm = 128;
     bn = 64;
   }
+  // An f32 weight (the full finetune's trainable weights and its dW, whose "weight" is the f32 activation) costs 4
+  // bytes per element, so the weight strip each tile re-reads weighs more: 128×128 tiles from 256 of them on (its
+  // dW of a 4864-row weight over 2048 tokens, 896 columns: 116 -> 102 µs on the MI355X).
+  const bool f32w = QT == GGUF_F32;
+  if (f32w && bm * bn < 128 * 128 && ntiles(128, 128) >= 256) {
+    bm = 128;
+    bn = 128;
+  }
   // A long contraction over a narrow output (the stacked gate|up dX, the FFN down projection forward): big
   // tiles split over the contraction beat small unsplit tiles (measured on the MI355X at M 2048: dX 9728 -> 896
   // 155 vs 210 us, forward 4864 -> 896 81 vs 108 us).
@@ -932,7 +940,7 @@ void launch_typed(const QWeight& w, H16 a, long long lda, long long M, GemmEpi e
   // Llama-3.2-1B's q|k|v and o dX, the step's dX −2.4%), else 32 (equal or faster at the other step shapes: split
   // 9728 -> 896 148 vs 155 us, 2048 -> 8192 897 vs 912 us).
   const bool deep_fwd = !DX && (NP == 2 || NP == 3) && (C >= 2048 || split_big);
-  const bool deep_dx = DX && (NP == 2 || NP == 3) && C >= 2048 && Nout <= 4096 && !split_big;
+  const bool deep_dx = DX && (NP == 2 || NP == 3) && C >= 2048 && Nout <= 4096 && !split_big && !f32w;
   if (C % 64 == 0 &&
       ((bm == 64 && bn == 64) || ((NP == 1 || longc || deep_fwd || deep_dx) && bm == 128 && bn == 128)))
     bk = 64;
