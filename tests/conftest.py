@@ -12,8 +12,8 @@ def pytest_configure(config):
 
 class heartbeat:
     """Context manager for long host-side computations inside a test (the oracle's step at the benchmark's shapes):
-    every `period` seconds it prints a progress line to stderr and rewrites gpurun_out/heartbeat.txt under the
-    repository root, so a runner watching for output sees the test is alive even when pytest captures stdout."""
+    every `period` seconds it prints a progress line to stderr and rewrites heartbeat.txt in the output folder under
+    the repository root, so a runner watching for output sees the test is alive even when pytest captures stdout."""
 
     def __init__(self, what, period=30.0):
         self.what, self.period = what, period
